@@ -1,0 +1,310 @@
+"""Benchmark of the fused residual-add + RMSNorm path on one MI355X.
+
+Workload (BASELINE.json's metric): bf16 fused add+RMSNorm at (4096, H) for
+every H of configs[1] (1024 ... 12288 step 1024) and configs[2] (13312 ...
+32768).  One step = one call at each of those H, in order.  Inputs are
+resident in HBM before timing starts; every H has two buffer sets used
+alternately, and one step moves ~3.8 GB, so no call finds its rows in the
+256 MB Infinity Cache left over from its previous use.
+
+value      = algorithmic bytes of a step / time of a step (GB/s), where a
+             call at (B, H) moves (4*B*H + H) * 2 bytes: input and residual
+             read, residual and output written, weight read once.
+per_shape  = per-H microseconds per call and GB/s, from HIP events recorded
+             around every call inside the timed region (on the stream the
+             kernels run on).
+roofline   = the kernel instantiation with the largest share of the step
+             time, against MI355X's 8 TB/s HBM peak.
+cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
+                  on the host cores, on a bounded sample of the same shapes.
+cpu_torch_eager = the reference test's torch formula on the CPU, same sample.
+extra      = the other BASELINE configs (decode, fp16, streamer), µs/call.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "µs/call + achieved HBM GB/s, fused add+RMSNorm bf16 (4096,H), H=1K–32K"
+PEAK_GBS = 8000.0
+B = 4096
+H_SWEEP = list(range(1024, 12288 + 1, 1024)) + [13312, 14336, 16384, 20480, 24576, 28672, 32768]
+EPS = 1e-6
+
+
+def fused_bytes(rows, hidden, elem=2):
+    return (4 * rows * hidden + hidden) * elem
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_set(torch, rows, hidden, dtype, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn((rows, hidden), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    r = torch.randn((rows, hidden), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    return x, r
+
+
+def make_weight(torch, hidden, dtype, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (1 + 0.1 * torch.randn((hidden,), generator=g, device=dev)).to(dtype)
+
+
+def kernel_key(abi, rows, hidden, dtype_code):
+    c = abi.select_config(rows, hidden, dtype_code)
+    return c.as_tuple()
+
+
+def time_shapes(torch, op, shapes, steps, warmup, nsets=2):
+    """shapes: list of (rows, hidden, dtype, dist).  Returns per-shape lists of
+    call durations (ms) from the timed steps, and the mean step time (ms)."""
+    dev = "cuda:0"
+    bufs = []
+    for i, (rows, hidden, dtype, dist) in enumerate(shapes):
+        sets = [make_set(torch, rows, hidden, dtype, 1000 * i + s, dev) for s in range(nsets)]
+        if dist == "outliers":
+            for x, _ in sets:
+                g = torch.Generator(device=dev).manual_seed(7 + i)
+                m = torch.rand(x.shape, generator=g, device=dev) < 0.01
+                x.copy_(torch.where(m, x.float() * 50, x.float()).to(dtype))
+        bufs.append((sets, make_weight(torch, hidden, dtype, i, dev)))
+    torch.cuda.synchronize()
+    for it in range(warmup):
+        for sets, w in bufs:
+            x, r = sets[it % nsets]
+            op(x, w, r, EPS)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in shapes] for _ in range(steps)]
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_begin.record(stream)
+    for it in range(steps):
+        for j, (sets, w) in enumerate(bufs):
+            x, r = sets[(warmup + it) % nsets]
+            evs[it][j][0].record(stream)
+            op(x, w, r, EPS)
+            evs[it][j][1].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    per = [[evs[it][j][0].elapsed_time(evs[it][j][1]) for it in range(steps)] for j in range(len(shapes))]
+    step_ms = t_begin.elapsed_time(t_end) / steps
+    del bufs
+    torch.cuda.empty_cache()
+    return per, step_ms
+
+
+def cpu_baselines(torch, budget_s=12.0):
+    """The CPU oracle (kind "port") and the torch eager formula, on the box's
+    host cores, over a bounded sample: rows of (4096, H) for H in the sweep,
+    taken as a fixed number of rows per H so each leg stays within budget."""
+    import numpy as np
+
+    from oracle import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    sample_rows = 256
+    shapes = [(sample_rows, h) for h in H_SWEEP]
+    g = torch.Generator().manual_seed(0)
+    data = []
+    for rows, h in shapes:
+        x = torch.randn((rows, h), generator=g).to(torch.bfloat16)
+        r = torch.randn((rows, h), generator=g).to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn((h,), generator=g)).to(torch.bfloat16)
+        data.append((x, r, w))
+    sample_bytes = sum(fused_bytes(rows, h) for rows, h in shapes)
+
+    def bitsnp(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def oracle_pass():
+        for x, r, w in data:
+            xo, ro = bitsnp(x).copy(), bitsnp(r).copy()
+            t0 = time.perf_counter()
+            oracle.fused_add_rmsnorm_(xo, bitsnp(w), ro, EPS, oracle.BF16, threads=threads)
+            yield time.perf_counter() - t0
+
+    def torch_pass():
+        for x, r, w in data:
+            t0 = time.perf_counter()
+            s = x + r
+            torch.rms_norm(s, (x.shape[-1],), weight=w, eps=EPS)
+            yield time.perf_counter() - t0
+
+    out = {}
+    for name, fn in (("oracle", oracle_pass), ("torch", torch_pass)):
+        sum(fn())  # warm-up pass
+        reps, t_start = [], time.perf_counter()
+        while len(reps) < 3 or (time.perf_counter() - t_start < budget_s / 2 and len(reps) < 50):
+            reps.append(sum(fn()))
+        med = statistics.median(reps)
+        out[name] = {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s",
+                     "us_per_4096_row_call": round(med / len(shapes) * (B / sample_rows) * 1e6, 1),
+                     "reps": len(reps), "seconds_per_pass": round(med, 4)}
+    sample = (f"{sample_rows} rows x each H in the 1024..32768 sweep (bf16, {len(shapes)} shapes, "
+              f"{sample_bytes / 1e6:.0f} MB algorithmic per pass), median of repeated passes")
+    return out, threads, sample
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the op has no cross-GPU step (rows are independent), and this "
+              f"build runs on single-GPU boxes; --gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import hp_rms_norm_amd
+    from hp_rms_norm_amd import abi
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    abi.lib()
+    op = hp_rms_norm_amd.hp_rms_norm
+
+    shapes = [(B, h, torch.bfloat16, "bench") for h in H_SWEEP]
+    log(f"bench: timing {len(shapes)} shapes x {args.steps} steps (warmup {args.warmup})")
+    per, step_ms = time_shapes(torch, op, shapes, args.steps, args.warmup)
+    step_bytes = sum(fused_bytes(B, h) for h in H_SWEEP)
+    value = step_bytes / (step_ms * 1e-3) / 1e9
+
+    per_shape, by_kernel = [], {}
+    for (rows, h, _, _), ms in zip(shapes, per):
+        us = statistics.median(ms) * 1e3
+        key = kernel_key(abi, rows, h, 0)
+        per_shape.append({"rows": rows, "hidden": h, "us_per_call": round(us, 2),
+                          "gbs": round(fused_bytes(rows, h) / (us * 1e-6) / 1e9, 1),
+                          "kernel": {"lanes_per_row": key[1], "vec_per_lane": key[2],
+                                     "lds_vec_per_lane": key[3], "block": key[4]}})
+        k = by_kernel.setdefault(key, {"ms": 0.0, "bytes": 0, "launches": 0, "hidden": []})
+        k["ms"] += sum(ms)
+        k["bytes"] += fused_bytes(rows, h) * len(ms)
+        k["launches"] += len(ms)
+        k["hidden"].append(h)
+    dom_key, dom = max(by_kernel.items(), key=lambda kv: kv[1]["ms"])
+    achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                "kernel": (f"fused_vec_kernel<bf16, fused, lanes_per_row={dom_key[1]}, vec_per_lane={dom_key[2]}, "
+                           f"lds_vec_per_lane={dom_key[3]}, block={dom_key[4]}, flags={dom_key[6]}>"),
+                "kernel_hidden": dom["hidden"],
+                "avg_launch_us": round(dom["ms"] / dom["launches"] * 1e3, 2),
+                "algorithmic_bytes_per_launch": dom["bytes"] // dom["launches"]}
+    traffic = load_traffic(dom_key)
+    if traffic is not None:
+        roofline["traffic"] = traffic
+
+    extra = {}
+    if not args.no_extra:
+        extra = run_extra(torch, hp_rms_norm_amd, args)
+
+    cpu = None
+    torch_cpu = None
+    if not args.no_cpu:
+        log("bench: CPU baselines")
+        res, threads, sample = cpu_baselines(torch)
+        cpu = {"value": res["oracle"]["value"], "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": sample, "us_per_4096_row_call": res["oracle"]["us_per_4096_row_call"]}
+        torch_cpu = {"value": res["torch"]["value"], "unit": "GB/s", "cores": threads,
+                     "sample": sample, "us_per_4096_row_call": res["torch"]["us_per_4096_row_call"],
+                     "formula": "x + r; torch.rms_norm(s, (H,), weight=w, eps=eps) on CPU (test/test_hp_rms_norm.py:6-19)"}
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "fused add+RMSNorm bf16 (4096, H), H in configs[1] (1024..12288 step 1024) "
+                               "and configs[2] (13312..32768); one step = one call per H",
+                   "rows": B, "hidden": H_SWEEP, "eps": EPS,
+                   "inputs": "input, residual ~ N(0,1), weight ~ N(1,0.1), generated on device",
+                   "buffer_sets_per_shape": 2, "bytes_per_step": step_bytes},
+        "per_shape": per_shape,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "cpu_torch_eager": torch_cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def load_traffic(key):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 --pmc summary (profiles/), when one exists for this kernel."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        entry = t.get("lpr{}_vpl{}_lds{}_b{}".format(key[1], key[2], key[3], key[4]))
+        return None if entry is None else entry.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def run_extra(torch, ops, args):
+    """The other BASELINE configs, µs/call (median over timed calls)."""
+    out = {}
+    steps = max(10, args.steps)
+    # decode shapes with 1% outliers x50
+    dec = [(b, h, torch.bfloat16, "outliers") for b in (1, 8, 32, 128, 512) for h in (4096, 8192)]
+    per, _ = time_shapes(torch, ops.hp_rms_norm, dec, steps, args.warmup)
+    out["decode_bf16"] = [{"rows": b, "hidden": h, "us_per_call": round(statistics.median(ms) * 1e3, 2)}
+                          for (b, h, _, _), ms in zip(dec, per)]
+    # fp16 non-power-of-two hidden
+    f16 = [(B, 5120, torch.float16, "bench"), (B, 7168, torch.float16, "bench")]
+    per, _ = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
+    out["fp16"] = [{"rows": b, "hidden": h, "us_per_call": round(statistics.median(ms) * 1e3, 2),
+                    "gbs": round(fused_bytes(b, h) / (statistics.median(ms) * 1e-3) / 1e9, 1)}
+                   for (b, h, _, _), ms in zip(f16, per)]
+    # streamer (the reference "relu" = copy, and the true ReLU) at (4096, 14336)
+    rows, h = B, 14336
+    res = []
+    for dtype in (torch.bfloat16, torch.float16):
+        sets = [torch.randn(rows, h, device="cuda:0").to(dtype) for _ in range(4)]
+        outs = [torch.empty_like(s) for s in sets]
+        for name, fn in (("copy", ops.relu), ("relu", ops.relu_max0)):
+            for i in range(args.warmup):
+                fn(outs[i % 4], sets[i % 4])
+            torch.cuda.synchronize()
+            ms = []
+            for i in range(steps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn(outs[i % 4], sets[i % 4])
+                e1.record()
+                ms.append((e0, e1))
+            torch.cuda.synchronize()
+            us = statistics.median(a.elapsed_time(b) for a, b in ms) * 1e3
+            res.append({"op": name, "dtype": str(dtype).replace("torch.", ""), "rows": rows, "hidden": h,
+                        "us_per_call": round(us, 2), "gbs": round(2 * rows * h * 2 / (us * 1e-6) / 1e9, 1)})
+        del sets, outs
+    out["streamer"] = res
+    torch.cuda.empty_cache()
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,87 @@
+"""In-tree build of the two native libraries of hp_rms_norm_amd.
+
+    libhprms.so        the gfx950 kernels and their C ABI (hipcc)
+    libhprms_torch.so  the torch operator registration on top of it (g++)
+
+Both land next to this file, so they travel with the source tree.  Run
+``python -m hp_rms_norm_amd.build`` (or ``__graft_entry__.build()``).
+No GPU is needed: hipcc cross-compiles for gfx950.
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+KERNEL_LIB = os.path.join(PKG, "libhprms.so")
+TORCH_LIB = os.path.join(PKG, "libhprms_torch.so")
+
+ARCH = "gfx950"
+# Packed fp32 VALU ops stay off: plain fp32 code is what the kernels need, and
+# it keeps the generated arithmetic to ordinary IEEE binary32 instructions.
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"--offload-arch={ARCH}",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(line for line in p.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in line)
+    if out.strip():
+        print(out, flush=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"build step failed ({p.returncode}): {' '.join(cmd)}")
+
+
+def _atomic(dst, build_fn):
+    tmp = dst + ".tmp"
+    build_fn(tmp)
+    os.replace(tmp, dst)
+
+
+def build_kernels():
+    hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    srcs = [os.path.join(CSRC, "hprms.hip")]
+    _atomic(KERNEL_LIB, lambda out: _run(
+        [hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", out]))
+
+
+def build_torch_binding():
+    import torch
+    from torch.utils import cpp_extension
+
+    cxx = shutil.which("g++") or "c++"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [f"-I{p}" for p in cpp_extension.include_paths()] + [f"-I{INCLUDE}", f"-I{ROCM}/include"]
+    tlib = cpp_extension.library_paths()[0]
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           *incs, os.path.join(CSRC, "torch_binding.cpp"),
+           f"-L{PKG}", "-lhprms", f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}", "-Wl,--no-as-needed"]
+    _atomic(TORCH_LIB, lambda out: _run(cmd + ["-o", out]))
+
+
+def build_oracle():
+    oracle_dir = os.path.join(ROOT, "oracle")
+    if os.path.exists(os.path.join(oracle_dir, "Makefile")):
+        _run(["make", "-s", "-B", "-C", oracle_dir])
+
+
+def build_all():
+    build_kernels()
+    build_torch_binding()
+    build_oracle()
+
+
+if __name__ == "__main__":
+    what = sys.argv[1:] or ["all"]
+    for w in what:
+        {"all": build_all, "kernels": build_kernels, "torch": build_torch_binding,
+         "oracle": build_oracle}[w]()

@@ -1,0 +1,386 @@
+// hprms.hip - C ABI of libhprms.so: argument checks, the gfx950 dispatch table
+// and the kernel launches.  Kernels live in hprms_kernels.h.
+//
+// Reference interfaces replaced (paths under the reference repository):
+//   hprms_fused_add_rmsnorm  <- rms_norm()  hp_rms_norm/csrc/cuda/hp_rms_norm.cu:7-50
+//                               launch_rms_norm<T>()  hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618
+//   hprms_streamer           <- relu()  hp_rms_norm/csrc/cuda/activation_kernels.cu:7-39
+//                               launch_relu<T>()  hp_rms_norm/csrc/cuda/activation_kernels.cuh:122-145
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "hp_rms_norm_amd.h"
+#include "hprms_kernels.h"
+
+namespace hprms {
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(HPRMS_E_LAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+  return HPRMS_OK;
+}
+
+// ---- per-device facts, queried once per device ------------------------------------
+constexpr int kMaxDevices = 64;
+std::once_flag g_dev_once[kMaxDevices];
+int g_dev_cus[kMaxDevices];
+
+int device_cus(int* cus) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HPRMS_E_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(HPRMS_E_RANGE, "device index %d out of range", dev);
+  std::call_once(g_dev_once[dev], [dev] {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 0;
+    g_dev_cus[dev] = n;
+  });
+  if (g_dev_cus[dev] <= 0) return fail(HPRMS_E_LAUNCH, "could not query the CU count of device %d", dev);
+  *cus = g_dev_cus[dev];
+  return HPRMS_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// ---- fused kernel registry -------------------------------------------------------
+typedef void (*fused_fn)(FusedArgs);
+
+struct FusedEntry {
+  int dtype, mode, lpr, vpl, ldsv, block, flags;
+  fused_fn fn;
+};
+
+#define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS, &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS>},
+
+// (lanes per row, vectors per lane, of which in LDS, block, flags)
+#define HPRMS_SHAPES(X, DT, MODE)                                                           \
+  X(DT, MODE, 16, 1, 0, 256, 2) X(DT, MODE, 32, 1, 0, 256, 2) X(DT, MODE, 64, 1, 0, 256, 2) \
+  X(DT, MODE, 64, 2, 0, 256, 2) X(DT, MODE, 64, 4, 0, 256, 2) X(DT, MODE, 64, 8, 0, 256, 2) \
+  X(DT, MODE, 128, 2, 0, 256, 2) X(DT, MODE, 128, 4, 0, 256, 2)                             \
+  X(DT, MODE, 256, 2, 0, 256, 2) X(DT, MODE, 256, 3, 0, 256, 2)                             \
+  X(DT, MODE, 256, 4, 0, 256, 2) X(DT, MODE, 256, 5, 0, 256, 2)                             \
+  X(DT, MODE, 256, 6, 0, 256, 2) X(DT, MODE, 256, 8, 0, 256, 2)                             \
+  X(DT, MODE, 512, 2, 0, 512, 2) X(DT, MODE, 512, 3, 0, 512, 2)                             \
+  X(DT, MODE, 512, 4, 0, 512, 2) X(DT, MODE, 512, 6, 0, 512, 2)                             \
+  X(DT, MODE, 512, 8, 0, 512, 2) X(DT, MODE, 1024, 2, 0, 1024, 2)                           \
+  X(DT, MODE, 1024, 4, 0, 1024, 2) X(DT, MODE, 1024, 8, 0, 1024, 2)                         \
+  X(DT, MODE, 256, 8, 4, 256, 2) X(DT, MODE, 256, 16, 8, 256, 2)                            \
+  X(DT, MODE, 512, 8, 4, 512, 2)
+
+#define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                    \
+  X(DT, MODE, 64, 4, 0, 256, 0) X(DT, MODE, 64, 4, 0, 256, 3)                               \
+  X(DT, MODE, 128, 4, 0, 256, 0) X(DT, MODE, 128, 4, 0, 256, 3)                             \
+  X(DT, MODE, 256, 4, 0, 256, 0) X(DT, MODE, 256, 4, 0, 256, 3)                             \
+  X(DT, MODE, 512, 4, 0, 512, 0) X(DT, MODE, 512, 4, 0, 512, 3)                             \
+  X(DT, MODE, 64, 4, 0, 64, 2) X(DT, MODE, 128, 4, 0, 128, 2) X(DT, MODE, 64, 2, 0, 64, 2)  \
+  X(DT, MODE, 64, 8, 0, 64, 2) X(DT, MODE, 128, 2, 0, 128, 2) X(DT, MODE, 64, 1, 0, 64, 2)
+
+const FusedEntry kFused[] = {
+    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
+    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_TUNING_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+};
+
+const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
+  for (const FusedEntry& e : kFused)
+    if (e.dtype == dtype && e.mode == mode && e.lpr == c.lanes_per_row && e.vpl == c.vec_per_lane &&
+        e.ldsv == c.lds_vec_per_lane && e.block == c.block_threads && e.flags == c.flags)
+      return &e;
+  return nullptr;
+}
+
+// ---- the gfx950 table -------------------------------------------------------------
+// Chosen from (hidden); rows only matter through the grid size.  See the
+// tuning notes in the design document for the measurements behind it.
+void table_config(int64_t hidden, hprms_config* c) {
+  const int64_t nvec = hidden / 8;
+  *c = hprms_config{1, 0, 0, 0, 0, 0, 2};
+  struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block; };
+  static const Row rows[] = {
+      {16, 16, 1, 0, 256},     // H <= 128
+      {32, 32, 1, 0, 256},     // H <= 256
+      {64, 64, 1, 0, 256},     // H <= 512
+      {128, 64, 2, 0, 256},    // H <= 1024
+      {256, 64, 4, 0, 256},    // H <= 2048
+      {512, 128, 4, 0, 256},   // H <= 4096
+      {768, 256, 3, 0, 256},   // H <= 6144
+      {1024, 256, 4, 0, 256},  // H <= 8192
+      {1280, 256, 5, 0, 256},  // H <= 10240
+      {1536, 256, 6, 0, 256},  // H <= 12288
+      {2048, 512, 4, 0, 512},  // H <= 16384
+      {3072, 512, 6, 0, 512},  // H <= 24576
+      {4096, 1024, 4, 0, 1024},  // H <= 32768
+      {8192, 1024, 8, 0, 1024},  // H <= 65536
+  };
+  for (const Row& r : rows) {
+    if (nvec <= r.max_nvec) {
+      c->lanes_per_row = r.lpr;
+      c->vec_per_lane = r.vpl;
+      c->lds_vec_per_lane = r.ldsv;
+      c->block_threads = r.block;
+      c->tier = r.ldsv > 0 ? 2 : 1;
+      return;
+    }
+  }
+  c->tier = 3;
+  c->lanes_per_row = 256;
+  c->block_threads = 256;
+}
+
+constexpr int64_t kMaxHidden = int64_t(1) << 24;
+constexpr int64_t kMaxGrid = 0x7fffffff;
+
+struct Problem {
+  int mode;  // 0 fused, 1 plain
+  void* x;
+  void* out;
+  void* res;
+  const void* w;
+  int64_t rows, hidden, x_stride, out_stride, res_stride;
+  int dtype;
+  double eps;
+};
+
+int check_problem(const Problem& p) {
+  if (p.dtype != HPRMS_DTYPE_BF16 && p.dtype != HPRMS_DTYPE_FP16)
+    return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", p.dtype);
+  if (p.rows < 0) return fail(HPRMS_E_INVALID, "rows must be >= 0 (got %lld)", (long long)p.rows);
+  if (p.hidden < 1) return fail(HPRMS_E_INVALID, "hidden must be >= 1 (got %lld)", (long long)p.hidden);
+  if (p.hidden > kMaxHidden)
+    return fail(HPRMS_E_RANGE, "hidden %lld exceeds the supported maximum %lld", (long long)p.hidden,
+                (long long)kMaxHidden);
+  if (p.x_stride < p.hidden) return fail(HPRMS_E_INVALID, "input row stride %lld < hidden %lld",
+                                         (long long)p.x_stride, (long long)p.hidden);
+  if (p.mode == 0 && p.res_stride < p.hidden)
+    return fail(HPRMS_E_INVALID, "residual row stride %lld < hidden %lld", (long long)p.res_stride,
+                (long long)p.hidden);
+  if (p.mode == 1 && p.out_stride < p.hidden)
+    return fail(HPRMS_E_INVALID, "output row stride %lld < hidden %lld", (long long)p.out_stride,
+                (long long)p.hidden);
+  if (!(p.eps >= 0.0)) return fail(HPRMS_E_INVALID, "eps must be >= 0");
+  if (p.rows == 0) return HPRMS_OK;
+  if (!p.x || !p.w || (p.mode == 0 && !p.res) || (p.mode == 1 && !p.out))
+    return fail(HPRMS_E_INVALID, "null tensor pointer");
+  if (p.mode == 0 && p.x == p.res) return fail(HPRMS_E_INVALID, "input and residual must not alias");
+  return HPRMS_OK;
+}
+
+// Can the vector tiers take this problem with configuration c?
+bool vec_fits(const Problem& p, const hprms_config& c) {
+  if (p.hidden % 8 != 0) return false;
+  if (!aligned16(p.x) || !aligned16(p.w)) return false;
+  if (p.x_stride % 8 != 0) return false;
+  if (p.mode == 0 && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
+  if (p.mode == 1 && (!aligned16(p.out) || p.out_stride % 8 != 0)) return false;
+  if ((int64_t)c.lanes_per_row * c.vec_per_lane * 8 < p.hidden) return false;
+  // every buffer resource of a row group spans < 2^31 bytes
+  const int64_t rpb = c.block_threads / c.lanes_per_row;
+  const int64_t smax = p.x_stride > (p.mode == 0 ? p.res_stride : p.out_stride)
+                           ? p.x_stride : (p.mode == 0 ? p.res_stride : p.out_stride);
+  if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
+    return false;
+  return true;
+}
+
+template <int DT>
+int launch_general(const Problem& p, hipStream_t stream) {
+  GeneralArgs a;
+  a.x = (const uint16_t*)p.x;
+  a.out = (uint16_t*)(p.mode == 0 ? p.x : p.out);
+  a.res = (uint16_t*)p.res;
+  a.w = (const uint16_t*)p.w;
+  a.rows = p.rows;
+  a.x_stride = p.x_stride;
+  a.out_stride = p.mode == 0 ? p.x_stride : p.out_stride;
+  a.res_stride = p.res_stride;
+  a.hidden = p.hidden;
+  a.hidden_f = (float)p.hidden;
+  a.eps = (float)p.eps;
+  const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
+  if (p.mode == 0)
+    fused_general_kernel<DT, 0><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
+  else
+    fused_general_kernel<DT, 1><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
+  return check_launch("general rmsnorm kernel");
+}
+
+// Validates, picks the configuration and the kernel, then launches.  With
+// rows == 0 everything but the launch still runs (pointers may be null), so a
+// caller can check that a configuration exists without a device.
+int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
+  int rc = check_problem(p);
+  if (rc != HPRMS_OK) return rc;
+
+  hprms_config c;
+  if (forced && forced->tier != 0) {
+    c = *forced;
+  } else {
+    table_config(p.hidden, &c);
+  }
+  if (c.tier != 3 && !vec_fits(p, c)) {
+    if (forced && forced->tier != 0)
+      return fail(HPRMS_E_INVALID,
+                  "configuration (lanes_per_row %d, vec_per_lane %d) does not fit hidden %lld with "
+                  "this alignment/stride", c.lanes_per_row, c.vec_per_lane, (long long)p.hidden);
+    c.tier = 3;
+  }
+  if (c.tier == 3) {
+    if (p.rows == 0) return HPRMS_OK;
+    return p.dtype == HPRMS_DTYPE_BF16 ? launch_general<HPRMS_DTYPE_BF16>(p, stream)
+                                       : launch_general<HPRMS_DTYPE_FP16>(p, stream);
+  }
+
+  const FusedEntry* e = find_fused(p.dtype, p.mode, c);
+  if (!e)
+    return fail(HPRMS_E_INVALID,
+                "no kernel built for (lanes_per_row %d, vec_per_lane %d, lds_vec_per_lane %d, "
+                "block_threads %d, flags %d)", c.lanes_per_row, c.vec_per_lane, c.lds_vec_per_lane,
+                c.block_threads, c.flags);
+  if (p.rows == 0) return HPRMS_OK;
+
+  FusedArgs a;
+  a.x = (const uint16_t*)p.x;
+  a.out = (uint16_t*)(p.mode == 0 ? p.x : p.out);
+  a.res = (uint16_t*)p.res;
+  a.w = (const uint16_t*)p.w;
+  a.rows = p.rows;
+  const int64_t rpb = c.block_threads / c.lanes_per_row;
+  a.ngroups = (p.rows + rpb - 1) / rpb;
+  a.x_stride = p.x_stride;
+  a.out_stride = p.mode == 0 ? p.x_stride : p.out_stride;
+  a.res_stride = p.res_stride;
+  a.hidden = (int32_t)p.hidden;
+  a.nvec = (int32_t)(p.hidden / 8);
+  a.hidden_f = (float)p.hidden;
+  a.eps = (float)p.eps;
+
+  int64_t grid = a.ngroups;
+  if (c.grid_blocks > 0 && c.grid_blocks < grid) grid = c.grid_blocks;
+  if (grid > kMaxGrid) grid = kMaxGrid;
+  hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(c.block_threads), 0, stream, a);
+  return check_launch("fused rmsnorm kernel");
+}
+
+// ---- streamer ---------------------------------------------------------------------
+template <int DT, int OP>
+int launch_stream(const StreamArgs& base, bool flat, hipStream_t stream) {
+  StreamArgs a = base;
+  if (flat) {
+    constexpr int kBlock = 256, kUnroll = 4;
+    int cus = 0;
+    int rc = device_cus(&cus);
+    if (rc != HPRMS_OK) return rc;
+    a.nvec = (a.rows * a.hidden) / 8;
+    int64_t want = (a.nvec + (int64_t)kBlock * kUnroll - 1) / ((int64_t)kBlock * kUnroll);
+    const int64_t cap = (int64_t)cus * 8;
+    int64_t grid = want < cap ? want : cap;
+    if (grid < 1) grid = 1;
+    stream_flat_kernel<DT, OP, kUnroll, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(a);
+  } else {
+    const int64_t grid = a.rows < kMaxGrid ? a.rows : kMaxGrid;
+    stream_rows_kernel<DT, OP><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
+  }
+  return check_launch("streamer kernel");
+}
+
+}  // namespace
+}  // namespace hprms
+
+using namespace hprms;
+
+extern "C" {
+
+int hprms_fused_add_rmsnorm(void* input, const void* weight, void* residual, int64_t rows, int64_t hidden,
+                            int64_t input_row_stride, int64_t residual_row_stride, int dtype, double eps,
+                            hipStream_t stream) {
+  Problem p{0, input, input, residual, weight, rows, hidden, input_row_stride, input_row_stride,
+            residual_row_stride, dtype, eps};
+  return run(p, nullptr, stream);
+}
+
+int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual, int64_t rows,
+                                   int64_t hidden, int64_t input_row_stride, int64_t residual_row_stride,
+                                   int dtype, double eps, const hprms_config* config, hipStream_t stream) {
+  if (!config) return fail(HPRMS_E_INVALID, "config is null");
+  Problem p{0, input, input, residual, weight, rows, hidden, input_row_stride, input_row_stride,
+            residual_row_stride, dtype, eps};
+  return run(p, config, stream);
+}
+
+int hprms_rmsnorm(void* out, const void* in, const void* weight, int64_t rows, int64_t hidden,
+                  int64_t out_row_stride, int64_t in_row_stride, int dtype, double eps, hipStream_t stream) {
+  Problem p{1, const_cast<void*>(in), out, nullptr, weight, rows, hidden, in_row_stride, out_row_stride,
+            0, dtype, eps};
+  return run(p, nullptr, stream);
+}
+
+int hprms_select_config(int64_t rows, int64_t hidden, int dtype, hprms_config* config) {
+  if (!config) return fail(HPRMS_E_INVALID, "config is null");
+  if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
+    return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
+  if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
+  table_config(hidden, config);
+  if (hidden % 8 != 0) config->tier = 3;
+  return HPRMS_OK;
+}
+
+int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                   int64_t in_row_stride, int dtype, int op, hipStream_t stream) {
+  if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
+    return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
+  if (op != HPRMS_STREAM_COPY && op != HPRMS_STREAM_RELU)
+    return fail(HPRMS_E_INVALID, "op must be HPRMS_STREAM_COPY or HPRMS_STREAM_RELU (got %d)", op);
+  if (rows < 0) return fail(HPRMS_E_INVALID, "rows must be >= 0 (got %lld)", (long long)rows);
+  if (hidden < 1) return fail(HPRMS_E_INVALID, "hidden must be >= 1 (got %lld)", (long long)hidden);
+  if (out_row_stride < hidden || in_row_stride < hidden)
+    return fail(HPRMS_E_INVALID, "row strides must be >= hidden");
+  if (rows == 0) return HPRMS_OK;
+  if (!out || !in) return fail(HPRMS_E_INVALID, "null tensor pointer");
+  StreamArgs a{(uint16_t*)out, (const uint16_t*)in, rows, hidden, out_row_stride, in_row_stride, 0};
+  const bool flat = out_row_stride == hidden && in_row_stride == hidden && aligned16(out) && aligned16(in);
+  if (dtype == HPRMS_DTYPE_BF16)
+    return op == HPRMS_STREAM_COPY ? launch_stream<HPRMS_DTYPE_BF16, HPRMS_STREAM_COPY>(a, flat, stream)
+                                   : launch_stream<HPRMS_DTYPE_BF16, HPRMS_STREAM_RELU>(a, flat, stream);
+  return op == HPRMS_STREAM_COPY ? launch_stream<HPRMS_DTYPE_FP16, HPRMS_STREAM_COPY>(a, flat, stream)
+                                 : launch_stream<HPRMS_DTYPE_FP16, HPRMS_STREAM_RELU>(a, flat, stream);
+}
+
+int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
+  if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
+    return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
+  if (mode != 0 && mode != 1) return fail(HPRMS_E_INVALID, "mode must be 0 or 1 (got %d)", mode);
+  if (capacity < 0 || (capacity > 0 && !out)) return fail(HPRMS_E_INVALID, "bad output array");
+  int n = 0;
+  for (const FusedEntry& e : kFused) {
+    if (e.dtype != dtype || e.mode != mode) continue;
+    if (n < capacity)
+      out[n] = hprms_config{e.ldsv > 0 ? 2 : 1, e.lpr, e.vpl, e.ldsv, e.block, 0, e.flags};
+    ++n;
+  }
+  return n;
+}
+
+const char* hprms_last_error(void) { return g_err; }
+
+int hprms_abi_version(void) { return HPRMS_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// hprms_device.h - device-side building blocks for gfx950 (CDNA4, wave64).
+//
+//   * 16-byte buffer loads/stores through a per-workgroup buffer resource, so
+//     that out-of-range lanes read zeros and drop their stores in hardware
+//     instead of branching (raw buffers: a lane is out of range when its
+//     byte offset >= num_records).
+//   * bfloat16 / binary16 pack and unpack.  Packing uses gfx950's
+//     v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 (round to nearest even).
+//   * wave64 sum reduction: DPP quad_perm and row mirrors inside each 16-lane
+//     row, ds_swizzle across the two rows of a 32-lane half, readlane across
+//     the halves.  Every lane of a group ends with the same bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hp_rms_norm_amd.h"
+
+namespace hprms {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Word 3 of a raw (unswizzled, stride 0) buffer resource on gfx9 parts.
+constexpr int kRsrcWord3 = 0x00020000;
+// A byte offset past every num_records the kernels build (they stay < 2^31).
+constexpr uint32_t kOOB = 0x80000000u;
+// Cache-policy field of buffer instructions on gfx940+: nt (streaming) = 2.
+constexpr int kAuxNT = 2;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+
+template <int AUX>
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+}
+
+template <int AUX>
+__device__ __forceinline__ void store16(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, AUX);
+}
+
+// ---- element formats --------------------------------------------------------
+template <int DT>
+struct Fmt;
+
+template <>
+struct Fmt<HPRMS_DTYPE_BF16> {
+  __device__ static __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  }
+  __device__ static __forceinline__ float one(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+  __device__ static __forceinline__ uint16_t pack1(float a) { return (uint16_t)(pack(a, 0.0f) & 0xffffu); }
+};
+
+template <>
+struct Fmt<HPRMS_DTYPE_FP16> {
+  __device__ static __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, w)[0];
+  }
+  __device__ static __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, w)[1];
+  }
+  __device__ static __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  }
+  __device__ static __forceinline__ float one(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+  __device__ static __forceinline__ uint16_t pack1(float a) { return (uint16_t)(pack(a, 0.0f) & 0xffffu); }
+};
+
+// ---- reductions ---------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+
+// Sum over aligned groups of WIDTH lanes (16, 32 or 64).  Must be called with
+// every lane of the wave active.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group width");
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror: quads 0<->1 of each 8
+  v += dpp_f32<0x140>(v);  // row_mirror: halves of each 16-lane row
+  if constexpr (WIDTH >= 32) {
+    // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  }
+  if constexpr (WIDTH == 64) {
+    v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  }
+  return v;
+}
+
+}  // namespace hprms

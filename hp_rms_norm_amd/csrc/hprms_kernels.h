@@ -1,0 +1,289 @@
+// hprms_kernels.h - the gfx950 kernels of libhprms.so.
+//
+// Fused residual-add + RMSNorm, "vector" tiers (hidden % 8 == 0, 16-byte
+// aligned rows).  A row of H elements is nvec = H/8 16-byte vectors.  A
+// workgroup of BLOCK lanes works on RPB = BLOCK/LPR rows at a time, LPR lanes
+// per row; lane l of a row owns vectors l, l+LPR, ..., l+(VPL-1)*LPR, so every
+// load instruction of a wave covers 1 KiB of contiguous bytes.  The row is
+// read from HBM once: the rounded sum stays on the CU (VPL-LDSV vectors in
+// VGPRs, LDSV vectors in per-lane LDS slots) until the output is written.
+//
+//   per row:  load x, r (16 B each per vector)          global -> VGPR
+//             s = rne(x + r); store s to residual; ss += s^2 (fp32)
+//             row sum of ss: DPP/swizzle inside the wave, then one LDS
+//             exchange + barrier when the row spans several waves
+//             inv = 1 / sqrt(ss / H + eps)
+//             out = rne((s * inv) * w); store out to input
+//
+// The weight vectors a lane needs are loaded once per workgroup and kept in
+// VGPRs across the persistent row loop.
+//
+// MODE 0 is the fused op (in place on input and residual); MODE 1 is the
+// plain RMSNorm (reads `input`, writes `out`, no residual stream).
+#pragma once
+
+#include "hprms_device.h"
+
+namespace hprms {
+
+struct FusedArgs {
+  const uint16_t* x;     // input rows (MODE 0: also the output)
+  uint16_t* out;         // output rows (MODE 0: == x)
+  uint16_t* res;         // residual rows (MODE 0 only)
+  const uint16_t* w;     // weight [hidden]
+  int64_t rows;
+  int64_t ngroups;       // ceil(rows / RPB)
+  int64_t x_stride;      // elements
+  int64_t out_stride;
+  int64_t res_stride;
+  int32_t hidden;
+  int32_t nvec;          // hidden / 8
+  float hidden_f;
+  float eps;
+};
+
+template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS>
+__global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
+  static_assert(LPR >= 16 && (LPR & (LPR - 1)) == 0 && BLOCK % LPR == 0 && BLOCK % 64 == 0, "shape");
+  static_assert(LDSV >= 0 && LDSV <= VPL, "LDS share");
+  using F = Fmt<DT>;
+  constexpr int RPB = BLOCK / LPR;
+  constexpr int GW = LPR < 64 ? LPR : 64;
+  constexpr int WPR = LPR > 64 ? LPR / 64 : 1;
+  constexpr int NW = BLOCK / 64;
+  constexpr int VREG = VPL - LDSV;
+  constexpr int LAUX = (FLAGS & 1) ? kAuxNT : 0;
+  constexpr int SAUX = (FLAGS & 2) ? kAuxNT : 0;
+  constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
+
+  __shared__ float red[2][WPR > 1 ? NW : 1];
+  __shared__ u32x4 spill[LDSV > 0 ? LDSV * BLOCK : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (LPR - 1);
+  const int rib = tid / LPR;
+  const int wave = tid >> 6;
+
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)a.hidden * 2u);
+  u32x4 wv[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
+
+  bool vec_ok[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < a.nvec;
+
+  int buf = 0;
+  for (int64_t g = blockIdx.x; g < a.ngroups; g += gridDim.x) {
+    const int64_t row0 = g * RPB;
+    const int64_t left = a.rows - row0;
+    const int nrows = left < RPB ? (int)left : RPB;
+    const bool row_ok = rib < nrows;
+
+    const uint32_t xbytes = (uint32_t)(((int64_t)(nrows - 1) * a.x_stride + a.hidden) * 2);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row0 * a.x_stride, xbytes);
+    const uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + (uint32_t)lane * 16u;
+
+    __amdgpu_buffer_rsrc_t rrs = xrs, ors = xrs;
+    uint32_t roff = 0, ooff = xoff;
+    if constexpr (MODE == 0) {
+      const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_stride + a.hidden) * 2);
+      rrs = make_rsrc(a.res + row0 * a.res_stride, rbytes);
+      roff = (uint32_t)rib * (uint32_t)a.res_stride * 2u + (uint32_t)lane * 16u;
+    } else {
+      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + a.hidden) * 2);
+      ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
+      ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
+    }
+
+    u32x4 xv[VPL], rv[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const bool ok = row_ok && vec_ok[k];
+      xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
+      if constexpr (MODE == 0) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+    }
+
+    float ss0 = 0.0f, ss1 = 0.0f;
+    u32x4 sv[VREG > 0 ? VREG : 1];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      u32x4 s;
+      if constexpr (MODE == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t p = F::pack(F::lo(xv[k][j]) + F::lo(rv[k][j]), F::hi(xv[k][j]) + F::hi(rv[k][j]));
+          s[j] = p;
+          const float b0 = F::lo(p), b1 = F::hi(p);
+          ss0 = __builtin_fmaf(b0, b0, ss0);
+          ss1 = __builtin_fmaf(b1, b1, ss1);
+        }
+        const bool ok = row_ok && vec_ok[k];
+        store16<SAUX>(s, rrs, ok ? roff + k * CH : kOOB);
+      } else {
+        s = xv[k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float b0 = F::lo(s[j]), b1 = F::hi(s[j]);
+          ss0 = __builtin_fmaf(b0, b0, ss0);
+          ss1 = __builtin_fmaf(b1, b1, ss1);
+        }
+      }
+      if (k < VREG) sv[k < VREG ? k : 0] = s;
+      else spill[(k - VREG) * BLOCK + tid] = s;
+    }
+
+    float tot = group_sum<GW>(ss0 + ss1);
+    if constexpr (WPR > 1) {
+      if ((tid & 63) == 0) red[buf][wave] = tot;
+      __syncthreads();
+      const int w0 = (wave / WPR) * WPR;
+      tot = red[buf][w0];
+#pragma unroll
+      for (int j = 1; j < WPR; ++j) tot += red[buf][w0 + j];
+      buf ^= 1;
+    }
+    const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
+
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+      const bool ok = row_ok && vec_ok[k];
+      store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
+    }
+  }
+}
+
+// General kernel: any hidden, any alignment, any row strides.  One workgroup
+// per row (grid-stride), element-wise 2-byte accesses; the second pass
+// re-reads the residual row this same thread has just written (program order
+// makes its own store visible), so nothing limits hidden.
+struct GeneralArgs {
+  const uint16_t* x;
+  uint16_t* out;
+  uint16_t* res;
+  const uint16_t* w;
+  int64_t rows;
+  int64_t x_stride;
+  int64_t out_stride;
+  int64_t res_stride;
+  int64_t hidden;
+  float hidden_f;
+  float eps;
+};
+
+template <int DT, int MODE>
+__global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
+  using F = Fmt<DT>;
+  __shared__ float red[2][4];
+  const int tid = threadIdx.x;
+  int buf = 0;
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const uint16_t* x = a.x + row * a.x_stride;
+    uint16_t* o = a.out + row * a.out_stride;
+    uint16_t* r = MODE == 0 ? a.res + row * a.res_stride : nullptr;
+    float ss = 0.0f;
+    for (int64_t j = tid; j < a.hidden; j += 256) {
+      float v;
+      if constexpr (MODE == 0) {
+        const uint16_t s = F::pack1(F::one(x[j]) + F::one(r[j]));
+        r[j] = s;
+        v = F::one(s);
+      } else {
+        v = F::one(x[j]);
+      }
+      ss = __builtin_fmaf(v, v, ss);
+    }
+    float tot = group_sum<64>(ss);
+    if ((tid & 63) == 0) red[buf][tid >> 6] = tot;
+    __syncthreads();
+    tot = ((red[buf][0] + red[buf][1]) + red[buf][2]) + red[buf][3];
+    buf ^= 1;
+    const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
+    for (int64_t j = tid; j < a.hidden; j += 256) {
+      const float v = MODE == 0 ? F::one(r[j]) : F::one(x[j]);
+      o[j] = F::pack1((v * inv) * F::one(a.w[j]));
+    }
+  }
+}
+
+// ---- streamer ------------------------------------------------------------------
+struct StreamArgs {
+  uint16_t* out;
+  const uint16_t* in;
+  int64_t rows;
+  int64_t hidden;
+  int64_t out_stride;
+  int64_t in_stride;
+  int64_t nvec;  // flat kernel: total 16-byte vectors; row kernel: vectors per row
+};
+
+template <int DT, int OP>
+__device__ __forceinline__ uint32_t stream_op2(uint32_t w) {
+  if constexpr (OP == HPRMS_STREAM_COPY) {
+    return w;
+  } else {
+    // ReLU on two 16-bit lanes: strictly negative (sign set, magnitude in
+    // (0, inf]) becomes +0; -0 and NaN pass through.
+    constexpr uint32_t inf = DT == HPRMS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
+    const uint32_t m0 = w & 0x7fffu, m1 = (w >> 16) & 0x7fffu;
+    const bool z0 = (w & 0x8000u) && m0 != 0 && m0 <= inf;
+    const bool z1 = (w & 0x80000000u) && m1 != 0 && m1 <= inf;
+    return (z0 ? 0u : (w & 0xffffu)) | (z1 ? 0u : (w & 0xffff0000u));
+  }
+}
+
+template <int DT, int OP>
+__device__ __forceinline__ uint16_t stream_op1(uint16_t h) {
+  return (uint16_t)(stream_op2<DT, OP>((uint32_t)h) & 0xffffu);
+}
+
+// Flat kernel: out and in are both contiguous [rows*hidden], 16-byte aligned.
+// Each thread moves UNROLL vectors per trip, all loads before all stores.
+template <int DT, int OP, int UNROLL, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void stream_flat_kernel(StreamArgs a) {
+  const u32x4* in = reinterpret_cast<const u32x4*>(a.in);
+  u32x4* out = reinterpret_cast<u32x4*>(a.out);
+  const int64_t nthreads = (int64_t)gridDim.x * BLOCK;
+  const int64_t step = nthreads * UNROLL;
+  for (int64_t base = (int64_t)blockIdx.x * BLOCK + threadIdx.x; base < a.nvec; base += step) {
+    u32x4 v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t i = base + u * nthreads;
+      if (i < a.nvec) v[u] = __builtin_nontemporal_load(in + i);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t i = base + u * nthreads;
+      if (i < a.nvec) {
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = stream_op2<DT, OP>(v[u][j]);
+        __builtin_nontemporal_store(o, out + i);
+      }
+    }
+  }
+  // elements past the last whole vector (rows*hidden % 8), by the first block
+  if (blockIdx.x == 0) {
+    const int64_t total = a.rows * a.hidden;
+    for (int64_t e = a.nvec * 8 + threadIdx.x; e < total; e += BLOCK)
+      a.out[e] = stream_op1<DT, OP>(a.in[e]);
+  }
+}
+
+// General streamer: any strides and alignment; one workgroup per row.
+template <int DT, int OP>
+__global__ __launch_bounds__(256) void stream_rows_kernel(StreamArgs a) {
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const uint16_t* in = a.in + row * a.in_stride;
+    uint16_t* out = a.out + row * a.out_stride;
+    for (int64_t j = threadIdx.x; j < a.hidden; j += 256) out[j] = stream_op1<DT, OP>(in[j]);
+  }
+}
+
+}  // namespace hprms

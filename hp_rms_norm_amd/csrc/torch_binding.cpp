@@ -1,0 +1,192 @@
+// torch_binding.cpp - registers torch.ops.hp_rms_norm.* on top of the C ABI of
+// libhprms.so.  This is the only host layer between PyTorch and the kernels:
+// it checks tensors, flattens them to [rows, hidden] with a row stride, picks
+// the current HIP stream of the tensor's device and calls the C ABI.
+//
+// Schemas follow the reference's registration
+// (hp_rms_norm/csrc/hp_rms_norm.cpp:35-38) with the same names and argument
+// order, plus alias annotations that declare the in-place writes, so that
+// functionalisation and torch.compile see them.  Messages of the shape checks
+// are the reference's (hp_rms_norm/csrc/cuda/hp_rms_norm.cu:12-24,48 and
+// activation_kernels.cu:11-15,38).
+#include <ATen/MemoryOverlap.h>
+#include <ATen/core/Tensor.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "hp_rms_norm_amd.h"
+
+namespace {
+
+int dtype_code(const at::Tensor& t) {
+  if (t.scalar_type() == at::kBFloat16) return HPRMS_DTYPE_BF16;
+  if (t.scalar_type() == at::kHalf) return HPRMS_DTYPE_FP16;
+  TORCH_CHECK(false, "dtype must be kFloat16 or kBFloat16");
+  return -1;
+}
+
+// Rows and row stride of a [..., hidden] tensor whose leading dims collapse
+// into one (the reference flattens with view({-1, hidden}),
+// hp_rms_norm/csrc/cuda/hp_rms_norm.cu:26).
+void rows_of(const at::Tensor& t, int64_t hidden, int64_t* rows, int64_t* stride) {
+  at::Tensor flat = t.view({-1, hidden});
+  *rows = flat.size(0);
+  *stride = *rows <= 1 ? hidden : flat.stride(0);
+  TORCH_CHECK(*stride >= hidden, "rows of the tensor overlap (row stride ", *stride, " < hidden ", hidden, ")");
+}
+
+void check_status(int rc) {
+  TORCH_CHECK(rc == HPRMS_OK, "hp_rms_norm: ", hprms_last_error(), " (status ", rc, ")");
+}
+
+struct FusedShape {
+  int64_t rows, hidden, in_stride, res_stride;
+  int dtype;
+};
+
+FusedShape check_fused(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& residual) {
+  TORCH_CHECK(input.dim() >= 2, "input.dim() >= 2");
+  TORCH_CHECK(input.dim() == residual.dim(), "input.dim() == residual.dim()");
+  for (int64_t i = 0; i < input.dim(); ++i)
+    TORCH_CHECK(input.size(i) == residual.size(i), "input.size(i) == residual.size(i)");
+  TORCH_CHECK(weight.dim() == 1, "weight.dim() == 1");
+  const int64_t hidden = weight.size(0);
+  TORCH_CHECK(input.size(-1) == hidden, "input.size(-1) == hidden_dim");
+  TORCH_CHECK(input.stride(-1) == 1, "input.stride(-1) == 1");
+  TORCH_CHECK(residual.stride(-1) == 1, "residual.stride(-1) == 1");
+  TORCH_CHECK(weight.stride(0) == 1 || hidden == 1, "weight.stride(0) == 1");
+  FusedShape s;
+  s.dtype = dtype_code(input);
+  TORCH_CHECK(residual.scalar_type() == input.scalar_type(), "residual.dtype() == input.dtype()");
+  TORCH_CHECK(weight.scalar_type() == input.scalar_type(), "weight.dtype() == input.dtype()");
+  TORCH_CHECK(residual.device() == input.device() && weight.device() == input.device(),
+              "input, weight and residual must be on the same device");
+  s.hidden = hidden;
+  rows_of(input, hidden, &s.rows, &s.in_stride);
+  int64_t rrows = 0;
+  rows_of(residual, hidden, &rrows, &s.res_stride);
+  if (s.rows > 0) at::assert_no_overlap(input, residual);
+  return s;
+}
+
+void rms_norm_hip(at::Tensor& input, const at::Tensor& weight, at::Tensor& residual, double eps) {
+  const FusedShape s = check_fused(input, weight, residual);
+  if (s.rows == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm(input.data_ptr(), weight.data_ptr(), residual.data_ptr(), s.rows,
+                                       s.hidden, s.in_stride, s.res_stride, s.dtype, eps, stream));
+}
+
+void rms_norm_meta(at::Tensor& input, const at::Tensor& weight, at::Tensor& residual, double eps) {
+  (void)check_fused(input, weight, residual);
+  (void)eps;
+}
+
+struct StreamShape {
+  int64_t rows, hidden, out_stride, in_stride;
+  int dtype;
+};
+
+StreamShape check_stream(const at::Tensor& out, const at::Tensor& input) {
+  TORCH_CHECK(input.dim() >= 2, "input.dim() >= 2");
+  TORCH_CHECK(input.dim() == out.dim(), "input.dim() == out.dim()");
+  for (int64_t i = 0; i < input.dim(); ++i)
+    TORCH_CHECK(input.size(i) == out.size(i), "input.size(i) == out.size(i)");
+  TORCH_CHECK(input.stride(-1) == 1, "input.stride(-1) == 1");
+  TORCH_CHECK(out.stride(-1) == 1, "out.stride(-1) == 1");
+  StreamShape s;
+  s.dtype = dtype_code(input);
+  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out.dtype() == input.dtype()");
+  TORCH_CHECK(out.device() == input.device(), "out and input must be on the same device");
+  s.hidden = input.size(-1);
+  int64_t orows = 0;
+  rows_of(input, s.hidden, &s.rows, &s.in_stride);
+  rows_of(out, s.hidden, &orows, &s.out_stride);
+  if (s.rows > 0 && s.hidden > 0) at::assert_no_partial_overlap(out, input);
+  return s;
+}
+
+void stream_hip(at::Tensor& out, const at::Tensor& input, int op) {
+  const StreamShape s = check_stream(out, input);
+  if (s.rows == 0 || s.hidden == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_streamer(out.data_ptr(), input.data_ptr(), s.rows, s.hidden, s.out_stride, s.in_stride,
+                              s.dtype, op, stream));
+}
+
+void relu_hip(at::Tensor& out, const at::Tensor& input) { stream_hip(out, input, HPRMS_STREAM_COPY); }
+void relu_max0_hip(at::Tensor& out, const at::Tensor& input) { stream_hip(out, input, HPRMS_STREAM_RELU); }
+void stream_meta(at::Tensor& out, const at::Tensor& input) { (void)check_stream(out, input); }
+
+struct PlainShape {
+  int64_t rows, hidden, out_stride, in_stride;
+  int dtype;
+};
+
+PlainShape check_plain(const at::Tensor& out, const at::Tensor& input, const at::Tensor& weight) {
+  TORCH_CHECK(input.dim() >= 2, "input.dim() >= 2");
+  TORCH_CHECK(input.dim() == out.dim(), "input.dim() == out.dim()");
+  for (int64_t i = 0; i < input.dim(); ++i)
+    TORCH_CHECK(input.size(i) == out.size(i), "input.size(i) == out.size(i)");
+  TORCH_CHECK(weight.dim() == 1, "weight.dim() == 1");
+  const int64_t hidden = weight.size(0);
+  TORCH_CHECK(input.size(-1) == hidden, "input.size(-1) == hidden_dim");
+  TORCH_CHECK(input.stride(-1) == 1, "input.stride(-1) == 1");
+  TORCH_CHECK(out.stride(-1) == 1, "out.stride(-1) == 1");
+  TORCH_CHECK(weight.stride(0) == 1 || hidden == 1, "weight.stride(0) == 1");
+  PlainShape s;
+  s.dtype = dtype_code(input);
+  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out.dtype() == input.dtype()");
+  TORCH_CHECK(weight.scalar_type() == input.scalar_type(), "weight.dtype() == input.dtype()");
+  TORCH_CHECK(out.device() == input.device() && weight.device() == input.device(),
+              "out, input and weight must be on the same device");
+  s.hidden = hidden;
+  int64_t orows = 0;
+  rows_of(input, hidden, &s.rows, &s.in_stride);
+  rows_of(out, hidden, &orows, &s.out_stride);
+  if (s.rows > 0) at::assert_no_partial_overlap(out, input);
+  return s;
+}
+
+void rms_norm_plain_hip(at::Tensor& out, const at::Tensor& input, const at::Tensor& weight, double eps) {
+  const PlainShape s = check_plain(out, input, weight);
+  if (s.rows == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_rmsnorm(out.data_ptr(), input.data_ptr(), weight.data_ptr(), s.rows, s.hidden,
+                             s.out_stride, s.in_stride, s.dtype, eps, stream));
+}
+
+void rms_norm_plain_meta(at::Tensor& out, const at::Tensor& input, const at::Tensor& weight, double eps) {
+  (void)check_plain(out, input, weight);
+  (void)eps;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(hp_rms_norm, m) {
+  m.def("rms_norm(Tensor(a!) input, Tensor weight, Tensor(b!) residual, float eps) -> ()");
+  m.def("relu(Tensor(a!) out, Tensor input) -> ()");
+  m.def("relu_max0(Tensor(a!) out, Tensor input) -> ()");
+  m.def("rms_norm_plain(Tensor(a!) out, Tensor input, Tensor weight, float eps) -> ()");
+}
+
+// ROCm builds of PyTorch expose HIP devices under the CUDA dispatch key.
+TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
+  m.impl("rms_norm", &rms_norm_hip);
+  m.impl("relu", &relu_hip);
+  m.impl("relu_max0", &relu_max0_hip);
+  m.impl("rms_norm_plain", &rms_norm_plain_hip);
+}
+
+// Shape checks only, for fake tensors / torch.compile tracing.  Meta tensors
+// carry no data, so nothing is computed here.
+TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
+  m.impl("rms_norm", &rms_norm_meta);
+  m.impl("relu", &stream_meta);
+  m.impl("relu_max0", &stream_meta);
+  m.impl("rms_norm_plain", &rms_norm_plain_meta);
+}

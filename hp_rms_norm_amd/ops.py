@@ -1,0 +1,44 @@
+"""Python surface of the ops; the first two are drop-ins for the reference's
+``hp_rms_norm.ops`` (hp_rms_norm/ops.py:4-24): same names, positional
+argument order, in-place semantics and ``None`` return."""
+import torch
+
+__all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm"]
+
+
+def hp_rms_norm(input, weight, residual, eps):
+    """Fused residual-add + RMSNorm, in place (reference: hp_rms_norm/ops.py:4-15).
+
+    ``residual <- input + residual`` (rounded to the tensor dtype) and
+    ``input <- rms_norm(input + residual) * weight`` with fp32 accumulation.
+    Tensors: ``input``/``residual`` [..., H] bf16 or fp16 on a HIP device,
+    ``weight`` [H] of the same dtype.  Returns None.
+    """
+    torch.ops.hp_rms_norm.rms_norm.default(input, weight, residual, eps)
+
+
+def relu(output, input):
+    """The reference's "relu" (hp_rms_norm/ops.py:17-24): its kernel is an
+    identity copy (activation_kernels.cuh:99-119), so ``output <- input``."""
+    torch.ops.hp_rms_norm.relu.default(output, input)
+
+
+def relu_max0(output, input):
+    """A true ReLU on the same streamer: ``output <- max(input, 0)``,
+    matching ``torch.relu`` (-0 and NaN pass through).  No reference counterpart."""
+    torch.ops.hp_rms_norm.relu_max0.default(output, input)
+
+
+def rms_norm(output, input, weight, eps):
+    """Plain RMSNorm without a residual stream: ``output <- rms_norm(input) *
+    weight``; ``output`` may be ``input``.  No reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_plain.default(output, input, weight, eps)
+
+
+def fused_add_rms_norm(input, residual, weight, eps):
+    """Out-of-place form of ``hp_rms_norm``: returns ``(normed, input +
+    residual)`` as new tensors and leaves the arguments untouched."""
+    out = input.clone()
+    res = residual.clone()
+    torch.ops.hp_rms_norm.rms_norm.default(out, weight, res, eps)
+    return out, res

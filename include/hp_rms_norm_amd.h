@@ -1,0 +1,134 @@
+/*
+ * hp_rms_norm_amd.h - C ABI of the MI355X (gfx950) fused residual-add + RMSNorm
+ * library `libhprms.so`.
+ *
+ * Every entry point takes plain device pointers, element counts, element
+ * strides, a dtype code and a HIP stream.  No entry point allocates device
+ * memory, synchronises the stream or throws: each returns HPRMS_OK (0) or a
+ * negative HPRMS_E* code, and the message of the calling thread's last failure
+ * is available from hprms_last_error().  Launches are asynchronous on `stream`
+ * (NULL = the null stream of the current device).  The kernels run on the
+ * device that owns the pointers; the caller makes that device current.
+ *
+ * Storage is row-major [rows, hidden] with a row stride (in elements) per
+ * tensor; elements inside a row are contiguous.
+ */
+#ifndef HP_RMS_NORM_AMD_H_
+#define HP_RMS_NORM_AMD_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HPRMS_ABI_VERSION 1
+
+/* element types (the reference accepts exactly these two:
+ * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
+typedef enum {
+  HPRMS_DTYPE_BF16 = 0,
+  HPRMS_DTYPE_FP16 = 1
+} hprms_dtype;
+
+/* status codes */
+#define HPRMS_OK 0
+#define HPRMS_E_INVALID (-22)  /* bad argument: null pointer, size, stride, dtype */
+#define HPRMS_E_LAUNCH (-5)    /* the HIP runtime rejected a launch or query */
+#define HPRMS_E_RANGE (-34)    /* a size or stride does not fit the kernel's index width */
+
+/* streamer operations for hprms_streamer() */
+#define HPRMS_STREAM_COPY 0   /* out = in (the reference "relu": activation_kernels.cuh:99-119) */
+#define HPRMS_STREAM_RELU 1   /* out = max(in, +0), NaN propagates */
+
+/*
+ * Fused residual-add + RMSNorm, in place.
+ *   residual[r, :] <- rne(f32(input) + f32(residual))
+ *   input[r, :]    <- rne((f32(residual_new) * rsqrt(mean(f32(residual_new)^2) + eps)) * f32(weight))
+ * with fp32 accumulation of the mean of squares.
+ *
+ * Replaces the reference's host entry `void rms_norm(Tensor& input, const
+ * Tensor& weight, Tensor& residual, double eps)` (hp_rms_norm/csrc/cuda/hp_rms_norm.cu:7-50)
+ * and its launcher `launch_rms_norm<T>(T* input, const T* weight, T* residual,
+ * size_t tokens, int hidden_dim, double eps, cudaStream_t)`
+ * (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618); the two row strides are new
+ * (the reference assumes contiguous rows).  rows == 0 is a no-op.
+ * hidden may be any value in [1, 2^24]; the fast tiers need hidden % 8 == 0,
+ * row strides % 8 == 0 and 16-byte aligned pointers, other shapes take a
+ * slower general kernel with the same results.
+ */
+int hprms_fused_add_rmsnorm(void* input, const void* weight, void* residual,
+                            int64_t rows, int64_t hidden,
+                            int64_t input_row_stride, int64_t residual_row_stride,
+                            int dtype, double eps, hipStream_t stream);
+
+/*
+ * Row-wise streamer: out[r, :] = op(in[r, :]).
+ * Replaces `void relu(Tensor& out, const Tensor& input)`
+ * (hp_rms_norm/csrc/cuda/activation_kernels.cu:7-39) and `launch_relu<T>(const T*
+ * input, T* out, int64_t tokens, int dim, int sm_count, cudaStream_t)`
+ * (hp_rms_norm/csrc/cuda/activation_kernels.cuh:122-145).  HPRMS_STREAM_COPY
+ * is the reference's observable behaviour (an identity copy); HPRMS_STREAM_RELU
+ * is a true ReLU offered beside it.  `out` and `in` must not partially overlap.
+ */
+int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden,
+                   int64_t out_row_stride, int64_t in_row_stride,
+                   int dtype, int op, hipStream_t stream);
+
+/*
+ * Plain (residual-free) RMSNorm, out of place: out = rne((f32(in) * rsqrt(mean(f32(in)^2) + eps)) * f32(weight)).
+ * No counterpart in the reference; it is the same kernel family without the
+ * residual stream, for the first and last norm of a layer stack.
+ * `out` may equal `in` (in place).
+ */
+int hprms_rmsnorm(void* out, const void* in, const void* weight,
+                  int64_t rows, int64_t hidden,
+                  int64_t out_row_stride, int64_t in_row_stride,
+                  int dtype, double eps, hipStream_t stream);
+
+/*
+ * Kernel configuration of the fused add+RMSNorm family.  Used by the tuning
+ * sweep and by tests that exercise every tier at every shape; normal callers
+ * use hprms_fused_add_rmsnorm(), which picks the configuration from the
+ * gfx950 table.  No counterpart in the reference (its tier choice is internal
+ * to launch_rms_norm, hp_rms_norm.cuh:573).
+ */
+typedef struct {
+  int32_t tier;             /* 0 = table, 1 = register tier, 2 = register+LDS tier, 3 = general kernel */
+  int32_t lanes_per_row;    /* 16, 32, 64, 128, 256, 512 or 1024 */
+  int32_t vec_per_lane;     /* 16-byte vectors of the row held by each lane */
+  int32_t lds_vec_per_lane; /* of those, how many are kept in LDS (tier 2) */
+  int32_t block_threads;    /* workgroup size: 64 ... 1024 */
+  int32_t grid_blocks;      /* 0 = one workgroup per row group; >0 = persistent grid of this many */
+  int32_t flags;            /* bit 0: non-temporal loads; bit 1: non-temporal stores */
+} hprms_config;
+
+int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
+                                   int64_t rows, int64_t hidden,
+                                   int64_t input_row_stride, int64_t residual_row_stride,
+                                   int dtype, double eps, const hprms_config* config,
+                                   hipStream_t stream);
+
+/* The configuration hprms_fused_add_rmsnorm() would use for (rows, hidden,
+ * dtype), written to *config (tier 3 when only the general kernel fits
+ * hidden).  Pure function of its arguments; touches no device. */
+int hprms_select_config(int64_t rows, int64_t hidden, int dtype, hprms_config* config);
+
+/* Lists the vector-tier configurations built into the library for (dtype,
+ * mode: 0 fused add+RMSNorm, 1 plain RMSNorm).  Writes up to `capacity`
+ * entries to `out` (may be NULL when capacity is 0) and returns how many
+ * exist, or a negative status.  Touches no device. */
+int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity);
+
+/* Message of the calling thread's most recent failure ("" if none). */
+const char* hprms_last_error(void);
+
+/* HPRMS_ABI_VERSION of the built library. */
+int hprms_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HP_RMS_NORM_AMD_H_ */

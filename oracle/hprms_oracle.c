@@ -1,0 +1,248 @@
+/*
+ * hprms_oracle.c - CPU restatement of hp_rms_norm's fused residual-add + RMSNorm
+ * path and of its streamer.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * or the timed CPU baseline.  The product (hp_rms_norm_amd, libhprms.so) never
+ * links, loads or calls it.
+ *
+ * Algorithm followed (paths under the reference repository):
+ *   - the reference's own test oracle, test/test_hp_rms_norm.py:6-19:
+ *       inp_res = inp + res                         (bf16/fp16 tensor add)
+ *       out = torch.rms_norm(inp_res, (H,), weight, eps)
+ *   - the in-place contract of the op: residual <- inp_res, input <- out
+ *     (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:207,251; hp_rms_norm/ops.py:4-15)
+ *   - the streamer's observable behaviour, an identity copy
+ *     (hp_rms_norm/csrc/cuda/activation_kernels.cuh:99-119, test/test_relu.py:24)
+ *
+ * Arithmetic, element by element, in IEEE binary32 with round-to-nearest-even:
+ *   s   = rne16(f32(x) + f32(r))                 stored to residual
+ *   ms  = fp32 mean of f32(s)^2 over the row     (summed in binary64, then
+ *                                                 rounded once to binary32:
+ *                                                 no reduction-order error)
+ *   inv = 1 / sqrt(ms + (float)eps)              two correctly rounded ops
+ *   out = rne16((f32(s) * inv) * f32(w))          stored to input
+ * The 16-bit conversions below are written from the IEEE 754 definitions
+ * (bfloat16 = the top half of a binary32; binary16 with subnormals).
+ *
+ * Parity pins (tests/test_oracle.py): golden vectors made by the reference's
+ * own formula in torch (tests/golden/), the live torch formula, a binary64
+ * brute force, closed forms (constant rows, power-of-two scaling), numpy's
+ * binary16 conversion, and planted mistakes (the `mutation` argument) that
+ * each pin must reject.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORACLE_BF16 0
+#define ORACLE_FP16 1
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---- 16-bit <-> binary32 conversions --------------------------------------- */
+
+float hprms_oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* Round-to-nearest-even of a binary32 to bfloat16.  NaN -> 0x7FC0. */
+uint16_t hprms_oracle_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float hprms_oracle_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu;
+  uint32_t m = h & 0x3ffu;
+  if (e == 0x1f) return u2f(sign | 0x7f800000u | (m << 13));   /* inf / NaN */
+  if (e == 0) {                                                /* zero / subnormal: m * 2^-24 */
+    float v = (float)m * 5.9604644775390625e-08f;
+    return sign ? -v : v;
+  }
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* Round-to-nearest-even of a binary32 to binary16, with subnormals and
+ * overflow to infinity.  NaN -> 0x7E00 with the input's sign. */
+uint16_t hprms_oracle_f32_to_f16(float f) {
+  uint32_t u = f2u(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7E00;
+  if (a >= 0x477FF000u) return sign | 0x7C00;      /* |f| >= 65520 rounds to inf */
+  if (a >= 0x38800000u) {                          /* normal result, |f| >= 2^-14 */
+    uint32_t t = a - 0x38000000u;                  /* rebias 127 -> 15 */
+    t += 0xFFFu + ((t >> 13) & 1u);
+    return sign | (uint16_t)(t >> 13);
+  }
+  if (a <= 0x33000000u) return sign;               /* |f| <= 2^-25 rounds to 0 */
+  /* subnormal result: round(mant * 2^(e-150) / 2^-24) */
+  uint32_t e = a >> 23;
+  uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+  uint32_t shift = 126u - e;                       /* 14 .. 24 */
+  uint32_t q = mant >> shift;
+  uint32_t rem = mant & ((1u << shift) - 1u);
+  uint32_t half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (q & 1u))) q += 1u;
+  return sign | (uint16_t)q;
+}
+
+static inline float to_f32(uint16_t h, int dtype) {
+  return dtype == ORACLE_BF16 ? hprms_oracle_bf16_to_f32(h) : hprms_oracle_f16_to_f32(h);
+}
+static inline uint16_t from_f32(float f, int dtype) {
+  return dtype == ORACLE_BF16 ? hprms_oracle_f32_to_bf16(f) : hprms_oracle_f32_to_f16(f);
+}
+/* rounding by truncation: only for the planted-mistake mode */
+static inline uint16_t from_f32_trunc(float f, int dtype) {
+  if (dtype == ORACLE_BF16) return (uint16_t)(f2u(f) >> 16);
+  return hprms_oracle_f32_to_f16(u2f(f2u(f) & 0xffffe000u));
+}
+
+/* ---- planted mistakes (tests only; 0 = the algorithm) ---------------------- */
+enum {
+  MUT_NONE = 0,
+  MUT_DROP_EPS = 1,        /* rsqrt(mean) */
+  MUT_MEAN_H_MINUS_1 = 2,  /* divide the sum of squares by H-1 */
+  MUT_WEIGHT_REVERSED = 3, /* weight[H-1-j] */
+  MUT_TRUNC_RESIDUAL = 4,  /* residual rounded by truncation */
+  MUT_NORM_INPUT = 5,      /* normalise the pre-add input instead of the sum */
+  MUT_L1_MEAN = 6,         /* mean of |s| instead of s^2 (then squared) */
+  MUT_UNROUNDED_SQUARES = 7, /* squares of the unrounded fp32 sum (the reference kernel's order) */
+  MUT_WEIGHT_TWICE = 8     /* (s * inv) * w * w */
+};
+
+static int check_rows(int64_t rows, int64_t hidden, int64_t s0, int64_t s1) {
+  return rows >= 0 && hidden >= 1 && s0 >= hidden && s1 >= hidden;
+}
+
+/* One row of the fused op.  x: input row (overwritten with the output),
+ * r: residual row (overwritten with the rounded sum). */
+static void fused_row(uint16_t* x, const uint16_t* w, uint16_t* r, int64_t H,
+                      int dtype, float epsf, int mutation) {
+  double acc = 0.0;
+  for (int64_t j = 0; j < H; ++j) {
+    float sum = to_f32(x[j], dtype) + to_f32(r[j], dtype);
+    uint16_t s = mutation == MUT_TRUNC_RESIDUAL ? from_f32_trunc(sum, dtype) : from_f32(sum, dtype);
+    float sf = to_f32(s, dtype);
+    if (mutation == MUT_UNROUNDED_SQUARES) sf = sum;
+    if (mutation == MUT_NORM_INPUT) sf = to_f32(x[j], dtype);
+    if (mutation == MUT_L1_MEAN) acc += fabs((double)sf);
+    else acc += (double)sf * (double)sf;
+    r[j] = s;
+  }
+  if (mutation == MUT_L1_MEAN) acc = (acc / (double)H) * (acc / (double)H) * (double)H;
+  double denom = mutation == MUT_MEAN_H_MINUS_1 && H > 1 ? (double)(H - 1) : (double)H;
+  float ms = (float)(acc / denom);
+  float v = mutation == MUT_DROP_EPS ? ms : ms + epsf;
+  float inv = 1.0f / sqrtf(v);
+  for (int64_t j = 0; j < H; ++j) {
+    float sf = to_f32(mutation == MUT_NORM_INPUT ? x[j] : r[j], dtype);
+    float wf = to_f32(w[mutation == MUT_WEIGHT_REVERSED ? H - 1 - j : j], dtype);
+    float y = (sf * inv) * wf;
+    if (mutation == MUT_WEIGHT_TWICE) y = y * wf;
+    x[j] = from_f32(y, dtype);
+  }
+}
+
+/* Fused residual-add + RMSNorm over [rows, hidden], in place.
+ * Returns 0, or -22 on a bad argument. */
+int hprms_oracle_fused_add_rmsnorm(uint16_t* input, const uint16_t* weight, uint16_t* residual,
+                                   int64_t rows, int64_t hidden,
+                                   int64_t input_row_stride, int64_t residual_row_stride,
+                                   int dtype, double eps, int threads, int mutation) {
+  if (!check_rows(rows, hidden, input_row_stride, residual_row_stride)) return -22;
+  if (dtype != ORACLE_BF16 && dtype != ORACLE_FP16) return -22;
+  if (rows == 0) return 0;
+  if (!input || !weight || !residual) return -22;
+  float epsf = (float)eps;
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+  for (int64_t i = 0; i < rows; ++i)
+    fused_row(input + i * input_row_stride, weight, residual + i * residual_row_stride,
+              hidden, dtype, epsf, mutation);
+  (void)threads;
+  return 0;
+}
+
+/* Plain RMSNorm, out = rne16((f32(in) * inv) * f32(w)); out may equal in. */
+int hprms_oracle_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* weight,
+                         int64_t rows, int64_t hidden, int64_t out_row_stride,
+                         int64_t in_row_stride, int dtype, double eps, int threads) {
+  if (!check_rows(rows, hidden, out_row_stride, in_row_stride)) return -22;
+  if (dtype != ORACLE_BF16 && dtype != ORACLE_FP16) return -22;
+  if (rows == 0) return 0;
+  if (!out || !in || !weight) return -22;
+  float epsf = (float)eps;
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+  for (int64_t i = 0; i < rows; ++i) {
+    const uint16_t* x = in + i * in_row_stride;
+    uint16_t* o = out + i * out_row_stride;
+    double acc = 0.0;
+    for (int64_t j = 0; j < hidden; ++j) {
+      double v = (double)to_f32(x[j], dtype);
+      acc += v * v;
+    }
+    float inv = 1.0f / sqrtf((float)(acc / (double)hidden) + epsf);
+    for (int64_t j = 0; j < hidden; ++j)
+      o[j] = from_f32((to_f32(x[j], dtype) * inv) * to_f32(weight[j], dtype), dtype);
+  }
+  (void)threads;
+  return 0;
+}
+
+/* Streamer: op 0 = identity copy, op 1 = ReLU: strictly negative values
+ * (sign set, nonzero magnitude, not NaN) become +0; -0, NaN and everything
+ * else pass through unchanged, as torch.relu does. */
+int hprms_oracle_streamer(uint16_t* out, const uint16_t* in, int64_t rows, int64_t hidden,
+                          int64_t out_row_stride, int64_t in_row_stride, int dtype, int op,
+                          int threads) {
+  if (!check_rows(rows, hidden, out_row_stride, in_row_stride)) return -22;
+  if ((dtype != ORACLE_BF16 && dtype != ORACLE_FP16) || (op != 0 && op != 1)) return -22;
+  if (rows == 0) return 0;
+  if (!out || !in) return -22;
+  uint16_t nan_floor = dtype == ORACLE_BF16 ? 0x7f80u : 0x7c00u; /* |h| above this is NaN */
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+  for (int64_t i = 0; i < rows; ++i) {
+    const uint16_t* x = in + i * in_row_stride;
+    uint16_t* o = out + i * out_row_stride;
+    for (int64_t j = 0; j < hidden; ++j) {
+      uint16_t h = x[j];
+      if (op == 1 && (h & 0x8000u) && (h & 0x7fffu) != 0 && (h & 0x7fffu) <= nan_floor) h = 0;
+      o[j] = h;
+    }
+  }
+  (void)threads;
+  return 0;
+}
+
+int hprms_oracle_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* Array forms of the conversions, for the conversion pins. */
+void hprms_oracle_from_f32(const float* src, uint16_t* dst, int64_t n, int dtype) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = from_f32(src[i], dtype);
+}
+void hprms_oracle_to_f32(const uint16_t* src, float* dst, int64_t n, int dtype) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = to_f32(src[i], dtype);
+}

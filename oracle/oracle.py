@@ -1,0 +1,154 @@
+"""ctypes wrapper of the CPU oracle ``oracle/libhprms_oracle.so``.
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py``, as the checker or the timed CPU
+baseline.  The product package ``hp_rms_norm_amd`` never imports it.
+
+Arrays are numpy ``uint16`` holding bfloat16 / binary16 bit patterns, 2-D
+``[rows, hidden]`` with contiguous rows (any row stride).  The arithmetic and
+the reference lines it restates are documented in ``oracle/hprms_oracle.c``.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+BF16, FP16 = 0, 1
+COPY, RELU = 0, 1
+
+# planted mistakes understood by the C oracle (tests/test_oracle.py shows that
+# the pins reject each of them)
+MUTATIONS = {
+    "drop_eps": 1,
+    "mean_h_minus_1": 2,
+    "weight_reversed": 3,
+    "trunc_residual": 4,
+    "norm_input": 5,
+    "l1_mean": 6,
+    "unrounded_squares": 7,
+    "weight_twice": 8,
+}
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhprms_oracle.so")
+_lib = None
+
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i64 = ctypes.c_int64
+
+
+def build():
+    """Compile the oracle with its Makefile (gcc, OpenMP)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `make -C oracle` (or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        L.hprms_oracle_fused_add_rmsnorm.argtypes = [_u16p, _u16p, _u16p, _i64, _i64, _i64, _i64,
+                                                     ctypes.c_int, ctypes.c_double, ctypes.c_int, ctypes.c_int]
+        L.hprms_oracle_rmsnorm.argtypes = [_u16p, _u16p, _u16p, _i64, _i64, _i64, _i64,
+                                           ctypes.c_int, ctypes.c_double, ctypes.c_int]
+        L.hprms_oracle_streamer.argtypes = [_u16p, _u16p, _i64, _i64, _i64, _i64,
+                                            ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.hprms_oracle_from_f32.argtypes = [_f32p, _u16p, _i64, ctypes.c_int]
+        L.hprms_oracle_to_f32.argtypes = [_u16p, _f32p, _i64, ctypes.c_int]
+        L.hprms_oracle_max_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p16(a):
+    return a.ctypes.data_as(_u16p)
+
+
+def _rows(a):
+    assert a.dtype == np.uint16 and a.ndim == 2 and a.strides[1] == 2, "2-D uint16 rows expected"
+    assert a.strides[0] % 2 == 0
+    return a.shape[0], a.shape[1], a.strides[0] // 2
+
+
+def max_threads():
+    return lib().hprms_oracle_max_threads()
+
+
+def fused_add_rmsnorm_(x, w, r, eps, dtype, threads=1, mutation=0):
+    """In place, like the op: r <- rne(x + r); x <- normalised output."""
+    rows, hidden, sx = _rows(x)
+    rows_r, hidden_r, sr = _rows(r)
+    assert (rows, hidden) == (rows_r, hidden_r) and w.shape == (hidden,) and w.dtype == np.uint16
+    w = np.ascontiguousarray(w)
+    if isinstance(mutation, str):
+        mutation = MUTATIONS[mutation]
+    rc = lib().hprms_oracle_fused_add_rmsnorm(_p16(x), _p16(w), _p16(r), rows, hidden, max(sx, hidden),
+                                              max(sr, hidden), dtype, float(eps), threads, mutation)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+
+
+def fused_add_rmsnorm(x, w, r, eps, dtype, threads=1, mutation=0):
+    """Out of place: returns (output, new_residual) as fresh arrays."""
+    xo = np.array(x, dtype=np.uint16, copy=True, order="C")
+    ro = np.array(r, dtype=np.uint16, copy=True, order="C")
+    fused_add_rmsnorm_(xo, w, ro, eps, dtype, threads, mutation)
+    return xo, ro
+
+
+def rmsnorm(x, w, eps, dtype, threads=1):
+    xc = np.ascontiguousarray(x)
+    rows, hidden, sx = _rows(xc)
+    out = np.empty_like(xc)
+    rc = lib().hprms_oracle_rmsnorm(_p16(out), _p16(xc), _p16(np.ascontiguousarray(w)), rows, hidden,
+                                    hidden, sx, dtype, float(eps), threads)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+    return out
+
+
+def streamer(x, dtype, op, threads=1):
+    xc = np.ascontiguousarray(x)
+    rows, hidden, sx = _rows(xc)
+    out = np.empty_like(xc)
+    rc = lib().hprms_oracle_streamer(_p16(out), _p16(xc), rows, hidden, hidden, sx, dtype, op, threads)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+    return out
+
+
+def from_f32(a, dtype):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().hprms_oracle_from_f32(a.ctypes.data_as(_f32p), _p16(out), a.size, dtype)
+    return out
+
+
+def to_f32(a, dtype):
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().hprms_oracle_to_f32(_p16(a), out.ctypes.data_as(_f32p), a.size, dtype)
+    return out
+
+
+def ulp_distance(a, b, dtype):
+    """Distance in units of the last place between two arrays of 16-bit
+    patterns (bf16 or fp16), on the ordered-integer line; NaN pairs count 0,
+    NaN against a number counts as a large distance."""
+    a = np.asarray(a, dtype=np.uint16).astype(np.int32)
+    b = np.asarray(b, dtype=np.uint16).astype(np.int32)
+
+    def ordered(v):
+        mag = v & 0x7FFF
+        return np.where(v & 0x8000, -mag, mag)
+
+    nan_floor = 0x7F80 if dtype == BF16 else 0x7C00
+    na = (a & 0x7FFF) > nan_floor
+    nb = (b & 0x7FFF) > nan_floor
+    d = np.abs(ordered(a) - ordered(b))
+    d = np.where(na & nb, 0, d)
+    d = np.where(na ^ nb, 1 << 20, d)
+    return d

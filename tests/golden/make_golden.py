@@ -1,0 +1,106 @@
+"""Writes tests/golden/golden.npz + golden.json: seeded input/output vectors of
+the reference's own test oracle, evaluated with torch on the CPU.
+
+The formula is the reference's test oracle (test/test_hp_rms_norm.py:6-19):
+    inp_res = inp + res
+    out = torch.rms_norm(inp_res, normalized_shape=(H,), weight=weight, eps=eps)
+and the streamer's pinned behaviour (test/test_relu.py:24: out == inp), plus
+torch.relu for the true-ReLU variant.  The reference package itself is not
+imported (it needs its CUDA extension); only torch runs here.
+
+Run from the repository root:  python tests/golden/make_golden.py
+"""
+import json
+import os
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def fused_case(name, rows, hidden, dtype, eps, dist, seed, special=None):
+    g = torch.Generator().manual_seed(seed)
+    if dist == "reference_test":          # test/test_hp_rms_norm.py:29-31: all N(0, 0.1)
+        x = torch.normal(0, 0.1, (rows, hidden), generator=g)
+        r = torch.normal(0, 0.1, (rows, hidden), generator=g)
+        w = torch.normal(0, 0.1, (hidden,), generator=g)
+    else:                                  # the benchmark distribution: N(0,1), N(0,1), N(1, 0.1)
+        x = torch.randn((rows, hidden), generator=g)
+        r = torch.randn((rows, hidden), generator=g)
+        w = 1 + 0.1 * torch.randn((hidden,), generator=g)
+        if dist == "outliers":             # 1% of input entries scaled by 50
+            m = torch.rand((rows, hidden), generator=g) < 0.01
+            x = torch.where(m, x * 50, x)
+    x, r, w = x.to(dtype), r.to(dtype), w.to(dtype)
+    if special is not None:
+        special(x, r, w)
+    inp_res = x + r
+    out = torch.rms_norm(inp_res, normalized_shape=(hidden,), weight=w, eps=eps)
+    return name, {"kind": "fused", "dtype": "bf16" if dtype == torch.bfloat16 else "fp16",
+                  "eps": eps, "rows": rows, "hidden": hidden}, \
+        {"x": bits(x), "r": bits(r), "w": bits(w), "out": bits(out), "res": bits(inp_res)}
+
+
+def sp_zero_and_huge(x, r, w):
+    x[0].zero_(); r[0].zero_()             # all-zero row: out = 0
+    x[1].fill_(1e30); r[1].fill_(1e30)     # squares overflow fp32: inv = 0
+    x[2, 5] = float("nan")                 # NaN poisons one row's output
+
+
+def sp_fp16_overflow(x, r, w):
+    x[0, :4] = 60000.0; r[0, :4] = 60000.0   # sum rounds to inf
+    x[1].fill_(2.0 ** -20); r[1].fill_(2.0 ** -20)  # subnormal sums
+
+
+def sp_constant_rows(x, r, w):
+    x.zero_(); r.zero_()
+    for i in range(x.shape[0]):
+        x[i].fill_(2.0 ** (i - 3) * (-1) ** i)
+
+
+def stream_case(name, rows, hidden, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((rows, hidden), generator=g).to(dtype)
+    specials = [0.0, -0.0, float("nan"), float("inf"), -float("inf"), 1e-40, -1e-40, -1.0, 1.0]
+    x[0, :len(specials)] = torch.tensor(specials).to(dtype)
+    return name, {"kind": "stream", "dtype": "bf16" if dtype == torch.bfloat16 else "fp16",
+                  "rows": rows, "hidden": hidden}, \
+        {"x": bits(x), "copy": bits(x.clone()), "relu": bits(torch.relu(x))}
+
+
+def main():
+    bf, hf = torch.bfloat16, torch.float16
+    cases = [
+        fused_case("bf16_4x4096_bench", 4, 4096, bf, 1e-6, "bench", 1),
+        fused_case("bf16_3x1024_reftest", 3, 1024, bf, 2.0 ** -7, "reference_test", 2),
+        fused_case("bf16_5x128_reftest", 5, 128, bf, 2.0 ** -7, "reference_test", 3),
+        fused_case("fp16_3x5120_bench", 3, 5120, hf, 1e-6, "bench", 4),
+        fused_case("fp16_2x7168_bench", 2, 7168, hf, 1e-6, "bench", 5),
+        fused_case("bf16_1x32768_bench", 1, 32768, bf, 1e-6, "bench", 6),
+        fused_case("bf16_2x8192_outliers", 2, 8192, bf, 1e-6, "outliers", 7),
+        fused_case("bf16_3x1000_tail", 3, 1000, bf, 1e-6, "bench", 8),
+        fused_case("fp16_2x13_tail", 2, 13, hf, 1e-6, "bench", 9),
+        fused_case("bf16_4x256_special", 4, 256, bf, 1e-6, "bench", 10, sp_zero_and_huge),
+        fused_case("fp16_2x256_special", 2, 256, hf, 1e-6, "bench", 11, sp_fp16_overflow),
+        fused_case("bf16_6x512_constant_eps0", 6, 512, bf, 0.0, "bench", 12, sp_constant_rows),
+        stream_case("stream_bf16_3x384", 3, 384, bf, 13),
+        stream_case("stream_fp16_2x1000", 2, 1000, hf, 14),
+    ]
+    arrays, meta = {}, {"torch": torch.__version__, "cases": {}}
+    for name, m, arrs in cases:
+        meta["cases"][name] = m
+        for k, v in arrs.items():
+            arrays[f"{name}/{k}"] = v
+    np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)
+    with open(os.path.join(HERE, "golden.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+    print("wrote", len(cases), "cases")
+
+
+if __name__ == "__main__":
+    main()

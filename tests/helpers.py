@@ -1,0 +1,68 @@
+"""Shared helpers of the test suite: seeded inputs of the benchmark
+distributions, bit views and the parity assertions (residual bit-exact,
+output within 1 ulp and atol/rtol 1e-2 of the oracle)."""
+import numpy as np
+import torch
+
+from oracle import oracle
+
+DT = {torch.bfloat16: oracle.BF16, torch.float16: oracle.FP16}
+# Tolerance of the normalised output against the oracle (the target's bar):
+# at most 1 unit in the last place, and assert_close(atol=1e-2, rtol=1e-2).
+MAX_ULP = 1
+ATOL = RTOL = 1e-2
+
+
+def bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def from_bits(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(dtype)
+
+
+def make_inputs(rows, hidden, dtype, seed, dist="bench"):
+    """input, residual ~ N(0,1), weight ~ N(1, 0.1) (dist "bench"); "outliers"
+    scales a seeded 1% of input entries by 50; "reference_test" is the
+    reference test's N(0, 0.1) for all three (test/test_hp_rms_norm.py:29-31)."""
+    g = torch.Generator().manual_seed(seed)
+    if dist == "reference_test":
+        x = torch.normal(0, 0.1, (rows, hidden), generator=g)
+        r = torch.normal(0, 0.1, (rows, hidden), generator=g)
+        w = torch.normal(0, 0.1, (hidden,), generator=g)
+    else:
+        x = torch.randn((rows, hidden), generator=g)
+        r = torch.randn((rows, hidden), generator=g)
+        w = 1 + 0.1 * torch.randn((hidden,), generator=g)
+        if dist == "outliers":
+            m = torch.rand((rows, hidden), generator=g) < 0.01
+            x = torch.where(m, x * 50, x)
+    return x.to(dtype), r.to(dtype), w.to(dtype)
+
+
+def oracle_fused(x, r, w, eps, dtype, threads=None):
+    if threads is None:
+        threads = min(16, oracle.max_threads())
+    return oracle.fused_add_rmsnorm(bits(x).reshape(-1, x.shape[-1]), bits(w), bits(r).reshape(-1, x.shape[-1]),
+                                    eps, DT[dtype], threads=threads)
+
+
+def assert_residual_exact(got_bits, want_bits, dtype, what="residual"):
+    got = np.asarray(got_bits).reshape(-1)
+    want = np.asarray(want_bits).reshape(-1)
+    d = oracle.ulp_distance(got, want, DT[dtype])   # NaN vs NaN counts as equal
+    bad = np.nonzero((got != want) & (d != 0))[0]
+    assert bad.size == 0, (f"{what} not bit-exact at {bad.size} elements; first index {bad[0]}: "
+                           f"got 0x{got[bad[0]]:04x} want 0x{want[bad[0]]:04x}")
+
+
+def assert_output_close(got_bits, want_bits, dtype, what="output"):
+    got = np.asarray(got_bits).reshape(-1)
+    want = np.asarray(want_bits).reshape(-1)
+    d = oracle.ulp_distance(got, want, DT[dtype])
+    worst = int(d.max()) if d.size else 0
+    assert worst <= MAX_ULP, f"{what}: {int((d > MAX_ULP).sum())} elements beyond {MAX_ULP} ulp (max {worst})"
+    gt = from_bits(got, dtype).float()
+    wt = from_bits(want, dtype).float()
+    torch.testing.assert_close(gt, wt, atol=ATOL, rtol=RTOL, equal_nan=True)
+    return d

@@ -1,0 +1,304 @@
+"""GPU parity of the fused residual-add + RMSNorm kernels against the CPU oracle.
+
+Bar (from the target): the residual is bit-exact, the normalised output is
+within 1 ulp (and atol = rtol = 1e-2) of the oracle, fp32 accumulation.
+Most tests call the kernels through the C ABI (hp_rms_norm_amd.abi, ctypes);
+the drop-in torch op is covered by the golden, sweep and graph tests.
+"""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (DT, assert_output_close, assert_residual_exact, bits, from_bits, make_inputs,
+                     oracle_fused)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def abi():
+    assert torch.cuda.is_available(), "the gpu tests need a HIP device"
+    import hp_rms_norm_amd  # noqa: F401  (registers the torch ops; fails loudly if unbuilt)
+    from hp_rms_norm_amd import abi as a
+    a.lib()
+    return a
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def run_abi(abi, x, w, r, eps, config=None):
+    """x, r: device tensors viewed as [rows, hidden] with unit inner stride."""
+    hidden = x.shape[-1]
+    x2, r2 = x.view(-1, hidden), r.view(-1, hidden)
+    abi.fused_add_rmsnorm(x2.data_ptr(), w.data_ptr(), r2.data_ptr(), x2.shape[0], hidden,
+                          x2.stride(0) if x2.shape[0] > 1 else hidden,
+                          r2.stride(0) if r2.shape[0] > 1 else hidden,
+                          DT[x.dtype], eps, _stream(), config)
+
+
+def check_case(abi, rows, hidden, dtype, eps=1e-6, seed=0, dist="bench", config=None, via="abi"):
+    x, r, w = make_inputs(rows, hidden, dtype, seed, dist)
+    want_out, want_res = oracle_fused(x, r, w, eps, dtype)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    if via == "abi":
+        run_abi(abi, xd, wd, rd, eps, config)
+    else:
+        import hp_rms_norm_amd
+        hp_rms_norm_amd.hp_rms_norm(xd, wd, rd, eps)
+    torch.cuda.synchronize()
+    tag = f"{rows}x{hidden} {dtype} seed {seed} {dist} cfg {config.as_tuple() if config else 'table'}"
+    assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
+    return assert_output_close(bits(xd), want_out, dtype, "output " + tag)
+
+
+# ---- golden vectors (the reference's own formula, evaluated by torch on CPU) ----
+def test_golden_fused_through_torch_op(abi, golden):
+    import hp_rms_norm_amd
+    for name, c in golden.items():
+        if c["kind"] != "fused":
+            continue
+        dtype = torch.bfloat16 if c["dtype"] == "bf16" else torch.float16
+        x, r, w = (from_bits(c[k], dtype).to(DEV) for k in ("x", "r", "w"))
+        print("golden", name, flush=True)
+        hp_rms_norm_amd.hp_rms_norm(x, w, r, c["eps"])
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(r), c["res"], dtype, name + " residual")
+        assert_output_close(bits(x), c["out"], dtype, name + " output")
+
+
+# ---- the BASELINE configurations --------------------------------------------------
+C1 = [(4096, 4096, torch.bfloat16, "bench")]
+C2 = [(4096, h, torch.bfloat16, "bench") for h in range(1024, 12288 + 1, 1024)]
+C3 = [(4096, h, torch.bfloat16, "bench") for h in (13312, 14336, 16384, 20480, 24576, 28672, 32768)]
+C4 = [(b, h, torch.bfloat16, "outliers") for b in (1, 8, 32, 128, 512) for h in (4096, 8192)]
+C5 = [(4096, 5120, torch.float16, "bench"), (4096, 7168, torch.float16, "bench")]
+
+
+@pytest.mark.parametrize("rows,hidden,dtype,dist", C1 + C2 + C3 + C4 + C5,
+                         ids=lambda v: str(v).replace("torch.", ""))
+def test_baseline_configs(abi, rows, hidden, dtype, dist):
+    print("case", rows, hidden, dtype, dist, flush=True)
+    d = check_case(abi, rows, hidden, dtype, seed=rows * 7 + hidden, dist=dist)
+    # the only differences left are fp32 reduction order: rare 1-ulp flips
+    assert (d != 0).mean() < 1e-3
+
+
+def test_reference_sweep_through_torch_op(abi):
+    """The reference test's sweep (test/test_hp_rms_norm.py:49-60): H = 128 ...
+    32768 step 128, random token counts, eps = bf16 eps, N(0, 0.1) inputs; here
+    seeded, smaller token counts, and both dtypes (the reference's loop only
+    ever ran bf16)."""
+    rng = random.Random(1234)
+    eps = torch.finfo(torch.bfloat16).eps
+    for dtype in (torch.bfloat16, torch.float16):
+        for hidden in range(128, 32768 + 128, 128):
+            rows = rng.randint(1, 48)
+            check_case(abi, rows, hidden, dtype, eps=eps, seed=hidden, dist="reference_test", via="torch")
+
+
+# ---- every built kernel configuration, with ragged row groups and tails -------------
+def _configs(abi, dtype, mode=0):
+    return abi.kernel_configs(DT[dtype], mode)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_every_kernel_config(abi, dtype):
+    for cfg in _configs(abi, dtype):
+        cover = cfg.lanes_per_row * cfg.vec_per_lane * 8
+        rpb = cfg.block_threads // cfg.lanes_per_row
+        hiddens = {cover, max(8, cover - 8), max(8, cover - cfg.lanes_per_row * 8 + 8)}
+        for hidden in sorted(hiddens):
+            rows = 3 * rpb + 1
+            print("config", cfg.as_tuple(), "hidden", hidden, "rows", rows, flush=True)
+            check_case(abi, rows, hidden, dtype, seed=hidden + rows, config=cfg)
+
+
+def test_persistent_grid(abi):
+    from hp_rms_norm_amd.abi import Config
+    base = abi.select_config(1000, 4096, DT[torch.bfloat16])
+    for grid in (1, 7, 64):
+        cfg = Config(*base.as_tuple())
+        cfg.grid_blocks = grid
+        check_case(abi, 1000, 4096, torch.bfloat16, seed=grid, config=cfg)
+
+
+# ---- general kernel: tails, misalignment, row strides ---------------------------------
+@pytest.mark.parametrize("hidden", [1, 7, 13, 100, 1000, 4097, 40000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_hidden_not_multiple_of_8(abi, hidden, dtype):
+    check_case(abi, 37, hidden, dtype, seed=hidden)
+
+
+def test_general_tier_forced(abi):
+    from hp_rms_norm_amd.abi import Config
+    cfg = Config(3, 256, 0, 0, 256, 0, 0)
+    for hidden in (8, 4096, 32768):
+        check_case(abi, 19, hidden, torch.bfloat16, seed=hidden, config=cfg)
+
+
+@pytest.mark.parametrize("pad", [3, 8, 24])
+def test_strided_and_misaligned_rows(abi, pad):
+    """Rows inside a wider buffer (row stride = hidden + pad) and, for odd pads,
+    16-byte misaligned row starts; both tensors offset by one element."""
+    rows, hidden, eps, dtype = 50, 2048, 1e-6, torch.bfloat16
+    x, r, w = make_inputs(rows, hidden, dtype, pad)
+    want_out, want_res = oracle_fused(x, r, w, eps, dtype)
+    for offset in (0, 1):
+        bx = torch.zeros(rows, hidden + pad + offset, dtype=dtype, device=DEV)
+        br = torch.zeros(rows, hidden + pad + offset, dtype=dtype, device=DEV)
+        xd = bx[:, offset:offset + hidden]
+        rd = br[:, offset:offset + hidden]
+        xd.copy_(x.to(DEV))
+        rd.copy_(r.to(DEV))
+        wd = w.to(DEV)
+        abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden, xd.stride(0),
+                              rd.stride(0), DT[dtype], eps, _stream())
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(rd), want_res, dtype)
+        assert_output_close(bits(xd), want_out, dtype)
+        # the padding around the rows is untouched
+        assert torch.count_nonzero(bx[:, :offset]) == 0 and torch.count_nonzero(bx[:, offset + hidden:]) == 0
+        assert torch.count_nonzero(br[:, offset + hidden:]) == 0
+
+
+def test_3d_input_and_empty(abi):
+    import hp_rms_norm_amd
+    x, r, w = make_inputs(6, 4096, torch.bfloat16, 5)
+    want_out, want_res = oracle_fused(x, r, w, 1e-6, torch.bfloat16)
+    xd = x.to(DEV).view(2, 3, 4096)
+    rd = r.to(DEV).view(2, 3, 4096)
+    hp_rms_norm_amd.hp_rms_norm(xd, w.to(DEV), rd, 1e-6)
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rd), want_res, torch.bfloat16)
+    assert_output_close(bits(xd), want_out, torch.bfloat16)
+    e = torch.empty(0, 4096, dtype=torch.bfloat16, device=DEV)
+    hp_rms_norm_amd.hp_rms_norm(e, w.to(DEV), e.clone(), 1e-6)
+
+
+# ---- size-independent properties at the largest configuration ---------------------------
+def test_full_size_properties(abi):
+    """At (4096, 32768): the residual equals torch's own HIP bf16 add
+    bit-for-bit, the output is within 1 ulp of a float32 torch evaluation of
+    the reference formula on the GPU, and permuting rows permutes outputs
+    bit-for-bit (rows are independent)."""
+    import hp_rms_norm_amd
+    rows, hidden, eps, dtype = 4096, 32768, 1e-6, torch.bfloat16
+    x, r, w = make_inputs(rows, hidden, dtype, 99)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    s_ref = xd + rd
+    sf = s_ref.float()
+    o_ref = ((sf * torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + eps)) * wd.float()).to(dtype)
+    perm = torch.randperm(rows, generator=torch.Generator().manual_seed(3)).to(DEV)
+    xp, rp = xd[perm].contiguous(), rd[perm].contiguous()
+    hp_rms_norm_amd.hp_rms_norm(xd, wd, rd, eps)
+    hp_rms_norm_amd.hp_rms_norm(xp, wd, rp, eps)
+    torch.cuda.synchronize()
+    assert torch.equal(rd.view(torch.int16), s_ref.view(torch.int16))
+    assert_output_close(bits(xd), bits(o_ref), dtype)
+    assert torch.equal(xp.view(torch.int16), xd[perm].view(torch.int16))
+    assert torch.equal(rp.view(torch.int16), rd[perm].view(torch.int16))
+
+
+# ---- streams and graphs ------------------------------------------------------------------
+def test_runs_on_current_stream(abi):
+    import hp_rms_norm_amd
+    x, r, w = make_inputs(512, 8192, torch.bfloat16, 11)
+    want_out, want_res = oracle_fused(x, r, w, 1e-6, torch.bfloat16)
+    s = torch.cuda.Stream()
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        hp_rms_norm_amd.hp_rms_norm(xd, wd, rd, 1e-6)
+    s.synchronize()
+    assert_residual_exact(bits(rd), want_res, torch.bfloat16)
+    assert_output_close(bits(xd), want_out, torch.bfloat16)
+
+
+def test_hip_graph_capture_and_replay(abi):
+    """The op allocates nothing and issues no memset, so it can be captured;
+    each replay (fresh inputs copied in between, with eager work and syncs
+    around it) must match the eager result."""
+    import hp_rms_norm_amd
+    rows, hidden, eps, dtype = 256, 4096, 1e-6, torch.bfloat16
+    xs = torch.empty(rows, hidden, dtype=dtype, device=DEV)
+    rs = torch.empty_like(xs)
+    wd = make_inputs(1, hidden, dtype, 0)[2].to(DEV)
+    xs.normal_()
+    rs.normal_()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hp_rms_norm_amd.hp_rms_norm(xs, wd, rs, eps)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hp_rms_norm_amd.hp_rms_norm(xs, wd, rs, eps)
+    for rep in range(4):
+        x, r, _ = make_inputs(rows, hidden, dtype, 100 + rep)
+        xs.copy_(x.to(DEV))
+        rs.copy_(r.to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_x, got_r = xs.clone(), rs.clone()
+        xe, re_ = x.to(DEV), r.to(DEV)
+        hp_rms_norm_amd.hp_rms_norm(xe, wd, re_, eps)
+        torch.cuda.synchronize()
+        assert torch.equal(got_x.view(torch.int16), xe.view(torch.int16)), f"replay {rep} output"
+        assert torch.equal(got_r.view(torch.int16), re_.view(torch.int16)), f"replay {rep} residual"
+
+
+# ---- plain RMSNorm ---------------------------------------------------------------------
+@pytest.mark.parametrize("hidden", [128, 1000, 4096, 12288, 32768])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_plain_rmsnorm(abi, hidden, dtype):
+    import hp_rms_norm_amd
+    x, _, w = make_inputs(33, hidden, dtype, hidden)
+    want = oracle.rmsnorm(bits(x), bits(w), 1e-6, DT[dtype], threads=8)
+    xd, wd = x.to(DEV), w.to(DEV)
+    out = torch.empty_like(xd)
+    hp_rms_norm_amd.rms_norm(out, xd, wd, 1e-6)
+    torch.cuda.synchronize()
+    assert_output_close(bits(out), want, dtype)
+    assert torch.equal(xd.cpu().view(torch.int16), x.view(torch.int16))  # input untouched
+    hp_rms_norm_amd.rms_norm(xd, xd, wd, 1e-6)                           # in place
+    torch.cuda.synchronize()
+    assert torch.equal(xd.view(torch.int16), out.view(torch.int16))
+
+
+def test_functional_form(abi):
+    import hp_rms_norm_amd
+    x, r, w = make_inputs(64, 4096, torch.bfloat16, 8)
+    want_out, want_res = oracle_fused(x, r, w, 1e-6, torch.bfloat16)
+    xd, rd = x.to(DEV), r.to(DEV)
+    out, res = hp_rms_norm_amd.fused_add_rms_norm(xd, rd, w.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(res), want_res, torch.bfloat16)
+    assert_output_close(bits(out), want_out, torch.bfloat16)
+    assert torch.equal(xd.cpu().view(torch.int16), x.view(torch.int16))
+    assert torch.equal(rd.cpu().view(torch.int16), r.view(torch.int16))
+
+
+# ---- errors raised on the GPU path --------------------------------------------------------
+def test_errors_on_device_tensors(abi):
+    import hp_rms_norm_amd
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(256, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="input.dim"):
+        hp_rms_norm_amd.hp_rms_norm(x[0], w, x[0].clone(), 1e-6)
+    with pytest.raises(RuntimeError, match="dtype must be kFloat16 or kBFloat16"):
+        hp_rms_norm_amd.hp_rms_norm(x.float(), w.float(), x.float().clone(), 1e-6)
+    with pytest.raises(RuntimeError, match="weight.dtype"):
+        hp_rms_norm_amd.hp_rms_norm(x, w.half(), x.clone(), 1e-6)
+    with pytest.raises(RuntimeError):
+        hp_rms_norm_amd.hp_rms_norm(x, w, x, 1e-6)  # input aliases residual
+    with pytest.raises(RuntimeError, match="same device"):
+        hp_rms_norm_amd.hp_rms_norm(x, w.cpu(), x.clone(), 1e-6)
+    xt = torch.zeros(256, 4, dtype=torch.bfloat16, device=DEV).t()   # [4, 256], inner stride 4
+    with pytest.raises(RuntimeError, match=r"input.stride\(-1\) == 1"):
+        hp_rms_norm_amd.hp_rms_norm(xt, w, x.clone(), 1e-6)
