@@ -10,9 +10,11 @@ alternately, and one step moves ~3.8 GB, so no call finds its rows in the
 value      = algorithmic bytes of a step / time of a step (GB/s), where a
              call at (B, H) moves (4*B*H + H) * 2 bytes: input and residual
              read, residual and output written, weight read once.
-per_shape  = per-H microseconds per call and GB/s, from HIP events recorded
-             around every call inside the timed region (on the stream the
-             kernels run on).
+per_shape  = per-H microseconds per call and GB/s: back-to-back calls over
+             rotating buffer sets spanning >= 1 GiB (so every call is cold in
+             the Infinity Cache), one HIP event pair around them on the
+             stream the kernels run on.  Each timed region starts behind a
+             short spin kernel so the host's launch rate is not measured.
 roofline   = the kernel instantiation with the largest share of the step
              time, against MI355X's 8 TB/s HBM peak.
 cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
@@ -65,13 +67,29 @@ def kernel_key(abi, rows, hidden, dtype_code):
     return c.as_tuple()
 
 
-def time_shapes(torch, op, shapes, steps, warmup, nsets=2):
-    """shapes: list of (rows, hidden, dtype, dist).  Returns per-shape lists of
-    call durations (ms) from the timed steps, and the mean step time (ms)."""
-    dev = "cuda:0"
+_SLEEP_CYCLES_PER_MS = None
+
+
+def prefill(torch, ms):
+    """Queue a spin kernel of about `ms` so the host gets ahead of the GPU:
+    the launches that follow are queued while it runs, and the timed region
+    measures the GPU, not Python's launch rate."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        torch.cuda._sleep(1_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS * ms))
+
+
+def make_bufs(torch, shapes, nsets_for, dev="cuda:0"):
     bufs = []
     for i, (rows, hidden, dtype, dist) in enumerate(shapes):
-        sets = [make_set(torch, rows, hidden, dtype, 1000 * i + s, dev) for s in range(nsets)]
+        sets = [make_set(torch, rows, hidden, dtype, 1000 * i + s, dev) for s in range(nsets_for(rows, hidden))]
         if dist == "outliers":
             for x, _ in sets:
                 g = torch.Generator(device=dev).manual_seed(7 + i)
@@ -79,31 +97,65 @@ def time_shapes(torch, op, shapes, steps, warmup, nsets=2):
                 x.copy_(torch.where(m, x.float() * 50, x.float()).to(dtype))
         bufs.append((sets, make_weight(torch, hidden, dtype, i, dev)))
     torch.cuda.synchronize()
+    return bufs
+
+
+def time_step(torch, op, shapes, steps, warmup):
+    """One step = one call per shape, in order; two buffer sets per shape used
+    alternately.  Returns the mean step time (ms) over `steps` timed steps."""
+    bufs = make_bufs(torch, shapes, lambda r, h: 2)
     for it in range(warmup):
         for sets, w in bufs:
-            x, r = sets[it % nsets]
+            x, r = sets[it % 2]
             op(x, w, r, EPS)
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in shapes] for _ in range(steps)]
-    t_begin = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t_begin.record(stream)
+    prefill(torch, 20)
+    t0.record(stream)
     for it in range(steps):
-        for j, (sets, w) in enumerate(bufs):
-            x, r = sets[(warmup + it) % nsets]
-            evs[it][j][0].record(stream)
+        for sets, w in bufs:
+            x, r = sets[(warmup + it) % 2]
             op(x, w, r, EPS)
-            evs[it][j][1].record(stream)
-    t_end.record(stream)
+    t1.record(stream)
     torch.cuda.synchronize()
-    per = [[evs[it][j][0].elapsed_time(evs[it][j][1]) for it in range(steps)] for j in range(len(shapes))]
-    step_ms = t_begin.elapsed_time(t_end) / steps
     del bufs
     torch.cuda.empty_cache()
-    return per, step_ms
+    return t0.elapsed_time(t1) / steps
+
+
+def cold_sets(rows, hidden, elem=2, floor=2, span=1 << 30):
+    """Buffer sets so that one pass over them spans >= 1 GiB (4x the MALL)."""
+    return max(floor, min(256, -(-span // (2 * rows * hidden * elem))))
+
+
+def time_shapes(torch, op, shapes, calls, warmup):
+    """Per shape: `calls` back-to-back calls over rotating buffer sets spanning
+    >= 1 GiB, one HIP event pair around them.  Returns µs per call."""
+    out = []
+    for shape in shapes:
+        rows, hidden = shape[0], shape[1]
+        bufs = make_bufs(torch, [shape], lambda r, h: cold_sets(r, h))
+        sets, w = bufs[0]
+        n = len(sets)
+        for it in range(warmup):
+            x, r = sets[it % n]
+            op(x, w, r, EPS)
+        stream = torch.cuda.current_stream()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ncalls = max(calls, n)
+        torch.cuda.synchronize()
+        prefill(torch, 10)
+        t0.record(stream)
+        for it in range(ncalls):
+            x, r = sets[(warmup + it) % n]
+            op(x, w, r, EPS)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        out.append(t0.elapsed_time(t1) * 1e3 / ncalls)
+        del bufs, sets
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baselines(torch, budget_s=12.0):
@@ -185,31 +237,32 @@ def main():
 
     shapes = [(B, h, torch.bfloat16, "bench") for h in H_SWEEP]
     log(f"bench: timing {len(shapes)} shapes x {args.steps} steps (warmup {args.warmup})")
-    per, step_ms = time_shapes(torch, op, shapes, args.steps, args.warmup)
+    step_ms = time_step(torch, op, shapes, args.steps, args.warmup)
     step_bytes = sum(fused_bytes(B, h) for h in H_SWEEP)
     value = step_bytes / (step_ms * 1e-3) / 1e9
+    log("bench: per-shape timing")
+    per_us = time_shapes(torch, op, shapes, args.steps, args.warmup)
 
     per_shape, by_kernel = [], {}
-    for (rows, h, _, _), ms in zip(shapes, per):
-        us = statistics.median(ms) * 1e3
+    for (rows, h, _, _), us in zip(shapes, per_us):
         key = kernel_key(abi, rows, h, 0)
         per_shape.append({"rows": rows, "hidden": h, "us_per_call": round(us, 2),
                           "gbs": round(fused_bytes(rows, h) / (us * 1e-6) / 1e9, 1),
                           "kernel": {"lanes_per_row": key[1], "vec_per_lane": key[2],
-                                     "lds_vec_per_lane": key[3], "block": key[4]}})
-        k = by_kernel.setdefault(key, {"ms": 0.0, "bytes": 0, "launches": 0, "hidden": []})
-        k["ms"] += sum(ms)
-        k["bytes"] += fused_bytes(rows, h) * len(ms)
-        k["launches"] += len(ms)
+                                     "lds_vec_per_lane": key[3], "block": key[4], "flags": key[6]}})
+        k = by_kernel.setdefault(key, {"us": 0.0, "bytes": 0, "launches": 0, "hidden": []})
+        k["us"] += us
+        k["bytes"] += fused_bytes(rows, h)
+        k["launches"] += 1
         k["hidden"].append(h)
-    dom_key, dom = max(by_kernel.items(), key=lambda kv: kv[1]["ms"])
-    achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+    dom_key, dom = max(by_kernel.items(), key=lambda kv: kv[1]["us"])
+    achieved = dom["bytes"] / (dom["us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
                 "kernel": (f"fused_vec_kernel<bf16, fused, lanes_per_row={dom_key[1]}, vec_per_lane={dom_key[2]}, "
                            f"lds_vec_per_lane={dom_key[3]}, block={dom_key[4]}, flags={dom_key[6]}>"),
                 "kernel_hidden": dom["hidden"],
-                "avg_launch_us": round(dom["ms"] / dom["launches"] * 1e3, 2),
+                "avg_launch_us": round(dom["us"] / dom["launches"], 2),
                 "algorithmic_bytes_per_launch": dom["bytes"] // dom["launches"]}
     traffic = load_traffic(dom_key)
     if traffic is not None:
@@ -239,7 +292,8 @@ def main():
                                "and configs[2] (13312..32768); one step = one call per H",
                    "rows": B, "hidden": H_SWEEP, "eps": EPS,
                    "inputs": "input, residual ~ N(0,1), weight ~ N(1,0.1), generated on device",
-                   "buffer_sets_per_shape": 2, "bytes_per_step": step_bytes},
+                   "buffer_sets_per_shape": 2, "bytes_per_step": step_bytes,
+                   "per_shape_timing": "back-to-back calls over buffer sets spanning >= 1 GiB"},
         "per_shape": per_shape,
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -270,34 +324,33 @@ def run_extra(torch, ops, args):
     steps = max(10, args.steps)
     # decode shapes with 1% outliers x50
     dec = [(b, h, torch.bfloat16, "outliers") for b in (1, 8, 32, 128, 512) for h in (4096, 8192)]
-    per, _ = time_shapes(torch, ops.hp_rms_norm, dec, steps, args.warmup)
-    out["decode_bf16"] = [{"rows": b, "hidden": h, "us_per_call": round(statistics.median(ms) * 1e3, 2)}
-                          for (b, h, _, _), ms in zip(dec, per)]
+    us = time_shapes(torch, ops.hp_rms_norm, dec, steps, args.warmup)
+    out["decode_bf16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2)} for (b, h, _, _), u in zip(dec, us)]
     # fp16 non-power-of-two hidden
     f16 = [(B, 5120, torch.float16, "bench"), (B, 7168, torch.float16, "bench")]
-    per, _ = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
-    out["fp16"] = [{"rows": b, "hidden": h, "us_per_call": round(statistics.median(ms) * 1e3, 2),
-                    "gbs": round(fused_bytes(b, h) / (statistics.median(ms) * 1e-3) / 1e9, 1)}
-                   for (b, h, _, _), ms in zip(f16, per)]
+    us = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
+    out["fp16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2),
+                    "gbs": round(fused_bytes(b, h) / (u * 1e-6) / 1e9, 1)} for (b, h, _, _), u in zip(f16, us)]
     # streamer (the reference "relu" = copy, and the true ReLU) at (4096, 14336)
     rows, h = B, 14336
     res = []
     for dtype in (torch.bfloat16, torch.float16):
-        sets = [torch.randn(rows, h, device="cuda:0").to(dtype) for _ in range(4)]
-        outs = [torch.empty_like(s) for s in sets]
+        n = cold_sets(rows, h)
+        sets = [torch.randn(rows, h, device="cuda:0").to(dtype) for _ in range(n)]
+        outs = [torch.empty_like(t) for t in sets]
         for name, fn in (("copy", ops.relu), ("relu", ops.relu_max0)):
             for i in range(args.warmup):
-                fn(outs[i % 4], sets[i % 4])
+                fn(outs[i % n], sets[i % n])
+            ncalls = max(steps, n)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
-            ms = []
-            for i in range(steps):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                fn(outs[i % 4], sets[i % 4])
-                e1.record()
-                ms.append((e0, e1))
+            prefill(torch, 10)
+            e0.record()
+            for i in range(ncalls):
+                fn(outs[i % n], sets[i % n])
+            e1.record()
             torch.cuda.synchronize()
-            us = statistics.median(a.elapsed_time(b) for a, b in ms) * 1e3
+            us = e0.elapsed_time(e1) * 1e3 / ncalls
             res.append({"op": name, "dtype": str(dtype).replace("torch.", ""), "rows": rows, "hidden": h,
                         "us_per_call": round(us, 2), "gbs": round(2 * rows * h * 2 / (us * 1e-6) / 1e9, 1)})
         del sets, outs

@@ -66,31 +66,33 @@ struct FusedEntry {
   fused_fn fn;
 };
 
-#define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
-  {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS, &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS>},
+// flags: bits 0-1 = non-temporal loads / stores, bit 2 = weight loaded late
+#define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
+  {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
+   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 3, ((FLAGS) >> 2) & 1>},
 
-// (lanes per row, vectors per lane, of which in LDS, block, flags)
+// (lanes per row, vectors per lane, of which in LDS, block, flags): the shapes
+// every dtype and mode gets.
 #define HPRMS_SHAPES(X, DT, MODE)                                                           \
-  X(DT, MODE, 16, 1, 0, 256, 2) X(DT, MODE, 32, 1, 0, 256, 2) X(DT, MODE, 64, 1, 0, 256, 2) \
-  X(DT, MODE, 64, 2, 0, 256, 2) X(DT, MODE, 64, 4, 0, 256, 2) X(DT, MODE, 64, 8, 0, 256, 2) \
-  X(DT, MODE, 128, 2, 0, 256, 2) X(DT, MODE, 128, 4, 0, 256, 2)                             \
-  X(DT, MODE, 256, 2, 0, 256, 2) X(DT, MODE, 256, 3, 0, 256, 2)                             \
-  X(DT, MODE, 256, 4, 0, 256, 2) X(DT, MODE, 256, 5, 0, 256, 2)                             \
-  X(DT, MODE, 256, 6, 0, 256, 2) X(DT, MODE, 256, 8, 0, 256, 2)                             \
-  X(DT, MODE, 512, 2, 0, 512, 2) X(DT, MODE, 512, 3, 0, 512, 2)                             \
-  X(DT, MODE, 512, 4, 0, 512, 2) X(DT, MODE, 512, 6, 0, 512, 2)                             \
-  X(DT, MODE, 512, 8, 0, 512, 2) X(DT, MODE, 1024, 2, 0, 1024, 2)                           \
-  X(DT, MODE, 1024, 4, 0, 1024, 2) X(DT, MODE, 1024, 8, 0, 1024, 2)                         \
-  X(DT, MODE, 256, 8, 4, 256, 2) X(DT, MODE, 256, 16, 8, 256, 2)                            \
-  X(DT, MODE, 512, 8, 4, 512, 2)
+  X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3) \
+  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 3) X(DT, MODE, 128, 4, 0, 256, 3) \
+  X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 4, 0, 512, 3)                             \
+  X(DT, MODE, 1024, 4, 0, 1024, 3) X(DT, MODE, 1024, 8, 0, 1024, 3)                         \
+  X(DT, MODE, 64, 2, 0, 256, 7) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 4, 0, 256, 7) \
+  X(DT, MODE, 256, 4, 0, 256, 7) X(DT, MODE, 512, 4, 0, 512, 7)                             \
+  X(DT, MODE, 1024, 4, 0, 1024, 7) X(DT, MODE, 1024, 8, 0, 1024, 7)                         \
+  X(DT, MODE, 512, 8, 4, 512, 3) X(DT, MODE, 512, 8, 4, 512, 7)                             \
+  X(DT, MODE, 256, 16, 8, 256, 7) X(DT, MODE, 1024, 8, 4, 1024, 7)
 
+// extra bf16 fused shapes kept for the tuning sweep
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                    \
-  X(DT, MODE, 64, 4, 0, 256, 0) X(DT, MODE, 64, 4, 0, 256, 3)                               \
-  X(DT, MODE, 128, 4, 0, 256, 0) X(DT, MODE, 128, 4, 0, 256, 3)                             \
-  X(DT, MODE, 256, 4, 0, 256, 0) X(DT, MODE, 256, 4, 0, 256, 3)                             \
-  X(DT, MODE, 512, 4, 0, 512, 0) X(DT, MODE, 512, 4, 0, 512, 3)                             \
-  X(DT, MODE, 64, 4, 0, 64, 2) X(DT, MODE, 128, 4, 0, 128, 2) X(DT, MODE, 64, 2, 0, 64, 2)  \
-  X(DT, MODE, 64, 8, 0, 64, 2) X(DT, MODE, 128, 2, 0, 128, 2) X(DT, MODE, 64, 1, 0, 64, 2)
+  X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 64, 4, 0, 64, 7) X(DT, MODE, 128, 4, 0, 128, 7)  \
+  X(DT, MODE, 128, 2, 0, 256, 7) X(DT, MODE, 256, 2, 0, 256, 7) X(DT, MODE, 256, 3, 0, 256, 7) \
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 3, 0, 512, 7) X(DT, MODE, 512, 6, 0, 512, 7) \
+  X(DT, MODE, 256, 8, 0, 256, 7) X(DT, MODE, 512, 8, 0, 512, 7) X(DT, MODE, 128, 4, 0, 256, 0) \
+  X(DT, MODE, 256, 4, 0, 256, 2) X(DT, MODE, 512, 4, 0, 512, 2) X(DT, MODE, 128, 8, 0, 256, 7) \
+  X(DT, MODE, 64, 8, 0, 256, 7) X(DT, MODE, 256, 8, 4, 256, 7) X(DT, MODE, 512, 12, 6, 512, 7) \
+  X(DT, MODE, 512, 16, 8, 512, 7)
 
 const FusedEntry kFused[] = {
     HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
@@ -113,23 +115,19 @@ const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
 // tuning notes in the design document for the measurements behind it.
 void table_config(int64_t hidden, hprms_config* c) {
   const int64_t nvec = hidden / 8;
-  *c = hprms_config{1, 0, 0, 0, 0, 0, 2};
-  struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block; };
+  *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
+  struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row rows[] = {
-      {16, 16, 1, 0, 256},     // H <= 128
-      {32, 32, 1, 0, 256},     // H <= 256
-      {64, 64, 1, 0, 256},     // H <= 512
-      {128, 64, 2, 0, 256},    // H <= 1024
-      {256, 64, 4, 0, 256},    // H <= 2048
-      {512, 128, 4, 0, 256},   // H <= 4096
-      {768, 256, 3, 0, 256},   // H <= 6144
-      {1024, 256, 4, 0, 256},  // H <= 8192
-      {1280, 256, 5, 0, 256},  // H <= 10240
-      {1536, 256, 6, 0, 256},  // H <= 12288
-      {2048, 512, 4, 0, 512},  // H <= 16384
-      {3072, 512, 6, 0, 512},  // H <= 24576
-      {4096, 1024, 4, 0, 1024},  // H <= 32768
-      {8192, 1024, 8, 0, 1024},  // H <= 65536
+      {16, 16, 1, 0, 256, 3},        // H <= 128
+      {32, 32, 1, 0, 256, 3},        // H <= 256
+      {64, 64, 1, 0, 256, 3},        // H <= 512
+      {128, 64, 2, 0, 256, 3},       // H <= 1024
+      {256, 64, 4, 0, 256, 3},       // H <= 2048
+      {512, 128, 4, 0, 256, 3},      // H <= 4096
+      {1024, 256, 4, 0, 256, 3},     // H <= 8192
+      {2048, 512, 4, 0, 512, 3},     // H <= 16384
+      {4096, 1024, 4, 0, 1024, 3},   // H <= 32768
+      {8192, 1024, 8, 0, 1024, 7},   // H <= 65536
   };
   for (const Row& r : rows) {
     if (nvec <= r.max_nvec) {
@@ -137,6 +135,7 @@ void table_config(int64_t hidden, hprms_config* c) {
       c->vec_per_lane = r.vpl;
       c->lds_vec_per_lane = r.ldsv;
       c->block_threads = r.block;
+      c->flags = r.flags;
       c->tier = r.ldsv > 0 ? 2 : 1;
       return;
     }

@@ -15,8 +15,13 @@
 //             inv = 1 / sqrt(ss / H + eps)
 //             out = rne((s * inv) * w); store out to input
 //
-// The weight vectors a lane needs are loaded once per workgroup and kept in
-// VGPRs across the persistent row loop.
+// The weight vectors a lane needs are re-read per row group (they stay hot in
+// L2): either together with the row (WLATE = 0) or after the residual has
+// been stored (WLATE = 1), when the residual registers are free again, which
+// keeps the peak VGPR count low enough for 8 waves per SIMD at VPL = 4.
+//
+// FLAGS bit 0 marks the row loads non-temporal, bit 1 the stores: the rows
+// are touched once, so they should not displace the weight from the caches.
 //
 // MODE 0 is the fused op (in place on input and residual); MODE 1 is the
 // plain RMSNorm (reads `input`, writes `out`, no residual stream).
@@ -42,7 +47,7 @@ struct FusedArgs {
   float eps;
 };
 
-template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS>
+template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
 __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   static_assert(LPR >= 16 && (LPR & (LPR - 1)) == 0 && BLOCK % LPR == 0 && BLOCK % 64 == 0, "shape");
   static_assert(LDSV >= 0 && LDSV <= VPL, "LDS share");
@@ -65,9 +70,6 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   const int wave = tid >> 6;
 
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)a.hidden * 2u);
-  u32x4 wv[VPL];
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
 
   bool vec_ok[VPL];
 #pragma unroll
@@ -96,12 +98,16 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
     }
 
-    u32x4 xv[VPL], rv[VPL];
+    u32x4 xv[VPL], rv[VPL], wv[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       const bool ok = row_ok && vec_ok[k];
       xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
       if constexpr (MODE == 0) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+    }
+    if constexpr (!WLATE) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
     }
 
     float ss0 = 0.0f, ss1 = 0.0f;
@@ -131,6 +137,11 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
       }
       if (k < VREG) sv[k < VREG ? k : 0] = s;
       else spill[(k - VREG) * BLOCK + tid] = s;
+    }
+
+    if constexpr (WLATE) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
     }
 
     float tot = group_sum<GW>(ss0 + ss1);

@@ -101,7 +101,8 @@ typedef struct {
   int32_t lds_vec_per_lane; /* of those, how many are kept in LDS (tier 2) */
   int32_t block_threads;    /* workgroup size: 64 ... 1024 */
   int32_t grid_blocks;      /* 0 = one workgroup per row group; >0 = persistent grid of this many */
-  int32_t flags;            /* bit 0: non-temporal loads; bit 1: non-temporal stores */
+  int32_t flags;            /* bit 0: non-temporal row loads; bit 1: non-temporal stores;
+                               bit 2: weight loaded after the residual is stored */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,

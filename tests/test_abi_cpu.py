@@ -1,0 +1,147 @@
+"""The C ABI of libhprms.so, on the CPU: the library loads, exports every
+function include/hp_rms_norm_amd.h declares, rejects bad arguments with a
+status and a message before touching a device, and its dispatch table maps
+every hidden size to a kernel that is built."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from hp_rms_norm_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hp_rms_norm_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hprms_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) >= 7
+    lib = abi.lib()
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert set(names) == set(abi.SYMBOLS)
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define HPRMS_ABI_VERSION (\d+)", open(HEADER).read())
+    assert abi.lib().hprms_abi_version() == int(m.group(1))
+
+
+def test_status_codes_match_header():
+    text = open(HEADER).read()
+    for name, val in (("HPRMS_E_INVALID", abi.HPRMS_E_INVALID), ("HPRMS_E_LAUNCH", abi.HPRMS_E_LAUNCH),
+                      ("HPRMS_E_RANGE", abi.HPRMS_E_RANGE)):
+        assert re.search(rf"#define {name} \({val}\)", text), name
+
+
+def fused(**kw):
+    a = dict(input=0x1000, weight=0x2000, residual=0x3000, rows=4, hidden=4096, si=4096, sr=4096,
+             dtype=abi.DTYPE_BF16, eps=1e-6)
+    a.update(kw)
+    return abi.lib().hprms_fused_add_rmsnorm(a["input"], a["weight"], a["residual"], a["rows"], a["hidden"],
+                                             a["si"], a["sr"], a["dtype"], a["eps"], None)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dtype=2), "dtype"),
+    (dict(rows=-1), "rows"),
+    (dict(hidden=0), "hidden"),
+    (dict(si=100), "input row stride"),
+    (dict(sr=100), "residual row stride"),
+    (dict(eps=-1.0), "eps"),
+    (dict(input=0), "null"),
+    (dict(residual=0), "null"),
+    (dict(weight=0), "null"),
+    (dict(residual=0x1000), "alias"),
+])
+def test_fused_rejects_bad_arguments(kw, msg):
+    assert fused(**kw) == abi.HPRMS_E_INVALID
+    assert msg in abi.last_error()
+
+
+def test_fused_rejects_hidden_beyond_maximum():
+    assert fused(hidden=(1 << 24) + 8, si=(1 << 24) + 8, sr=(1 << 24) + 8) == abi.HPRMS_E_RANGE
+
+
+def test_zero_rows_is_a_no_op_without_pointers():
+    assert fused(rows=0, input=0, weight=0, residual=0) == abi.HPRMS_OK
+
+
+def test_streamer_and_plain_reject_bad_arguments():
+    L = abi.lib()
+    assert L.hprms_streamer(0x1000, 0x2000, 4, 64, 64, 64, 0, 5, None) == abi.HPRMS_E_INVALID
+    assert "op" in abi.last_error()
+    assert L.hprms_streamer(0x1000, 0x2000, 4, 64, 32, 64, 0, 0, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_streamer(0, 0, 0, 64, 64, 64, 0, 0, None) == abi.HPRMS_OK
+    assert L.hprms_rmsnorm(0x1000, 0x2000, 0, 4, 64, 64, 64, 0, 1e-6, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_rmsnorm(0x1000, 0x2000, 0x3000, 4, 64, 63, 64, 0, 1e-6, None) == abi.HPRMS_E_INVALID
+
+
+def test_errors_are_thread_local():
+    import threading
+    assert fused(dtype=9) == abi.HPRMS_E_INVALID
+    seen = {}
+
+    def other():
+        seen["msg"] = abi.last_error()
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "dtype" in abi.last_error()
+
+
+def test_table_covers_every_hidden_with_a_built_kernel():
+    """Every hidden size maps either to a built vector-tier kernel that covers
+    it, or to the general kernel; checked through the config entry point with
+    rows = 0 (validates and looks the kernel up, launches nothing)."""
+    L = abi.lib()
+    for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+        for hidden in list(range(8, 70000, 8)) + [1, 3, 1001, 4097]:
+            c = abi.select_config(4096, hidden, dtype)
+            if hidden % 8:
+                assert c.tier == 3
+                continue
+            if c.tier == 3:
+                assert hidden > 65536
+                continue
+            assert c.lanes_per_row * c.vec_per_lane * 8 >= hidden
+            assert c.block_threads % c.lanes_per_row == 0
+            rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
+                                                  ctypes.byref(c), None)
+            assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
+            rc = L.hprms_rmsnorm(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6, None)
+            assert rc == abi.HPRMS_OK
+
+
+def test_config_entry_rejects_unbuilt_and_misfit_configs():
+    L = abi.lib()
+    c = abi.Config(1, 128, 3, 0, 256, 0, 3)  # not instantiated
+    assert L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, 3072, 3072, 3072, 0, 1e-6, ctypes.byref(c),
+                                            None) == abi.HPRMS_E_INVALID
+    assert "no kernel built" in abi.last_error()
+    c = abi.Config(1, 64, 1, 0, 256, 0, 3)   # covers 512 elements only
+    assert L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, 4096, 4096, 4096, 0, 1e-6, ctypes.byref(c),
+                                            None) == abi.HPRMS_E_INVALID
+    assert "does not fit" in abi.last_error()
+
+
+def test_every_built_config_is_well_formed():
+    for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+        for mode in (0, 1):
+            cfgs = abi.kernel_configs(dtype, mode)
+            assert cfgs
+            for c in cfgs:
+                assert c.lanes_per_row in (16, 32, 64, 128, 256, 512, 1024)
+                assert c.block_threads % 64 == 0 and c.block_threads % c.lanes_per_row == 0
+                assert 0 <= c.lds_vec_per_lane <= c.vec_per_lane
+                assert c.tier == (2 if c.lds_vec_per_lane else 1)
+                # LDS spill of a workgroup fits the 160 KiB of a gfx950 CU
+                assert c.lds_vec_per_lane * c.block_threads * 16 <= 160 * 1024

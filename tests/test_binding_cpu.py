@@ -1,0 +1,102 @@
+"""The torch binding, on the CPU: schemas, the drop-in Python surface, the
+reference's shape checks and messages (hp_rms_norm/csrc/cuda/hp_rms_norm.cu:12-24,48,
+activation_kernels.cu:11-15) exercised through the Meta kernels, and no CPU
+fallback (CPU tensors are refused by the dispatcher)."""
+import inspect
+
+import pytest
+import torch
+
+import hp_rms_norm_amd
+from hp_rms_norm_amd import ops
+
+M = "meta"
+
+
+def t(*shape, dtype=torch.bfloat16):
+    return torch.empty(*shape, dtype=dtype, device=M)
+
+
+def test_schemas_keep_reference_names_and_order_with_alias_annotations():
+    s = str(torch.ops.hp_rms_norm.rms_norm.default._schema)
+    assert s == "hp_rms_norm::rms_norm(Tensor(a!) input, Tensor weight, Tensor(b!) residual, float eps) -> ()"
+    s = str(torch.ops.hp_rms_norm.relu.default._schema)
+    assert s == "hp_rms_norm::relu(Tensor(a!) out, Tensor input) -> ()"
+
+
+def test_python_surface_matches_reference_ops():
+    # hp_rms_norm/ops.py:4-24
+    assert list(inspect.signature(ops.hp_rms_norm).parameters) == ["input", "weight", "residual", "eps"]
+    assert list(inspect.signature(ops.relu).parameters) == ["output", "input"]
+    import hp_rms_norm  # the import-compatible alias package
+    assert hp_rms_norm.hp_rms_norm is ops.hp_rms_norm and hp_rms_norm.relu is ops.relu
+    assert hp_rms_norm.ops.hp_rms_norm is ops.hp_rms_norm
+
+
+def test_meta_accepts_valid_shapes():
+    assert ops.hp_rms_norm(t(4, 4096), t(4096), t(4, 4096), 1e-6) is None
+    assert ops.hp_rms_norm(t(2, 3, 128), t(128), t(2, 3, 128), 1e-6) is None
+    assert ops.relu(t(4, 256), t(4, 256)) is None
+    assert ops.relu_max0(t(4, 256, dtype=torch.float16), t(4, 256, dtype=torch.float16)) is None
+    assert ops.rms_norm(t(4, 256), t(4, 256), t(256), 1e-6) is None
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((t(4096), t(4096), t(4096)), r"input.dim\(\) >= 2"),
+    ((t(4, 4096), t(4096), t(1, 4, 4096)), r"input.dim\(\) == residual.dim\(\)"),
+    ((t(4, 4096), t(4096), t(5, 4096)), r"input.size\(i\) == residual.size\(i\)"),
+    ((t(4, 4096), t(1, 4096), t(4, 4096)), r"weight.dim\(\) == 1"),
+    ((t(4, 4096), t(2048), t(4, 4096)), r"input.size\(-1\) == hidden_dim"),
+    ((t(4096, 4).t(), t(4096), t(4, 4096)), r"input.stride\(-1\) == 1"),
+    ((t(4, 4096), t(4096), t(4096, 4).t()), r"residual.stride\(-1\) == 1"),
+    ((t(4, 4096, dtype=torch.float32), t(4096, dtype=torch.float32), t(4, 4096, dtype=torch.float32)),
+     "dtype must be kFloat16 or kBFloat16"),
+    ((t(4, 4096), t(4096, dtype=torch.float16), t(4, 4096)), r"weight.dtype\(\) == input.dtype\(\)"),
+    ((t(4, 4096), t(4096), t(4, 4096, dtype=torch.float16)), r"residual.dtype\(\) == input.dtype\(\)"),
+])
+def test_meta_rejects_like_the_reference(args, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        ops.hp_rms_norm(*args, 1e-6)
+
+
+def test_meta_rejects_rows_that_cannot_be_flattened():
+    base = t(4, 8, 256)
+    x = base.transpose(0, 1)      # [8, 4, 256]: leading dims do not collapse
+    with pytest.raises(RuntimeError):
+        ops.hp_rms_norm(x, t(256), t(8, 4, 256), 1e-6)
+
+
+def test_streamer_meta_rejects_like_the_reference():
+    with pytest.raises(RuntimeError, match=r"input.dim\(\) >= 2"):
+        ops.relu(t(256), t(256))
+    with pytest.raises(RuntimeError, match=r"input.size\(i\) == out.size\(i\)"):
+        ops.relu(t(4, 128), t(4, 256))
+    with pytest.raises(RuntimeError, match="dtype must be kFloat16 or kBFloat16"):
+        ops.relu(t(4, 256, dtype=torch.float32), t(4, 256, dtype=torch.float32))
+
+
+def test_no_cpu_fallback():
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    w = torch.ones(256, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        ops.hp_rms_norm(x, w, x.clone(), 1e-6)
+    with pytest.raises(NotImplementedError):
+        ops.relu(x.clone(), x)
+
+
+def test_package_points_at_in_tree_libraries():
+    import os
+    assert os.path.dirname(hp_rms_norm_amd.TORCH_LIB) == os.path.dirname(os.path.abspath(hp_rms_norm_amd.__file__))
+    assert os.path.exists(hp_rms_norm_amd.KERNEL_LIB)
+
+
+def test_fake_tensor_tracing_sees_the_mutation():
+    """Alias annotations make the in-place writes visible to functionalisation."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(8, 512, dtype=torch.bfloat16, device=M)
+        r = torch.empty(8, 512, dtype=torch.bfloat16, device=M)
+        w = torch.empty(512, dtype=torch.bfloat16, device=M)
+        ops.hp_rms_norm(x, w, r, 1e-6)
+    schema = torch.ops.hp_rms_norm.rms_norm.default._schema
+    assert [a.alias_info.is_write if a.alias_info else False for a in schema.arguments] == [True, False, True, False]

@@ -1,0 +1,249 @@
+"""Pins of the CPU oracle (oracle/hprms_oracle.c), on the CPU.
+
+Each check is independent of the oracle's own code:
+  * golden vectors written by the reference's test formula in torch
+    (tests/golden/, test/test_hp_rms_norm.py:6-19 and test/test_relu.py:24),
+  * the same formula evaluated live by torch at other shapes,
+  * a binary64 brute force written with numpy's own reductions,
+  * closed forms: constant rows of powers of two with eps = 0 give +-w
+    exactly; scaling a row by a power of two leaves the output unchanged,
+  * the 16-bit conversions against numpy's binary16 and torch's bfloat16
+    conversions on exhaustive and random bit patterns,
+and every planted mistake the oracle can be asked to make is rejected by at
+least one of these pins.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+BF, HF = oracle.BF16, oracle.FP16
+TDT = {BF: torch.bfloat16, HF: torch.float16}
+
+
+def tbits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def tfrom(a, code):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(TDT[code])
+
+
+def seeded(rows, hidden, code, seed, dist="bench"):
+    g = torch.Generator().manual_seed(seed)
+    if dist == "reference_test":
+        x, r, w = (torch.normal(0, 0.1, s, generator=g) for s in ((rows, hidden), (rows, hidden), (hidden,)))
+    else:
+        x = torch.randn((rows, hidden), generator=g)
+        r = torch.randn((rows, hidden), generator=g)
+        w = 1 + 0.1 * torch.randn((hidden,), generator=g)
+    dt = TDT[code]
+    return tbits(x.to(dt)), tbits(r.to(dt)), tbits(w.to(dt))
+
+
+def torch_formula(x, r, w, eps, code):
+    """The reference test's oracle (test/test_hp_rms_norm.py:6-19), run by torch."""
+    xt, rt, wt = tfrom(x, code), tfrom(r, code), tfrom(w, code)
+    s = xt + rt
+    out = torch.rms_norm(s, normalized_shape=(xt.shape[-1],), weight=wt, eps=eps)
+    return tbits(out), tbits(s)
+
+
+def to_16(v64, code):
+    """binary64 -> 16-bit pattern, through numpy / torch conversions only."""
+    if code == HF:
+        return v64.astype(np.float16).view(np.uint16)   # binary64 -> binary16 directly, RNE
+    return tbits(torch.from_numpy(v64).to(torch.bfloat16))  # torch: binary64 -> bfloat16
+
+
+def brute_force(x, r, w, eps, code):
+    """binary64 evaluation with numpy's reductions; the residual is rounded to
+    the 16-bit type first (the op stores it), everything after is binary64."""
+    f = (lambda a: a.view(np.float16).astype(np.float64)) if code == HF else \
+        (lambda a: (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64))
+    s16 = to_16(f(x) + f(r), code)
+    s = f(s16)
+    rms = np.sqrt(np.mean(s * s, axis=-1, keepdims=True) + eps)
+    return to_16(s / rms * f(w)[None, :], code), s16
+
+
+# ---- the pins, each returning a failure message or None ----------------------------------
+def pin_golden(golden, mutation=0):
+    for name, c in golden.items():
+        if c["kind"] != "fused":
+            continue
+        code = BF if c["dtype"] == "bf16" else HF
+        out, res = oracle.fused_add_rmsnorm(c["x"], c["w"], c["r"], c["eps"], code, mutation=mutation)
+        dr = oracle.ulp_distance(res, c["res"], code)
+        if dr.max() != 0:
+            return f"{name}: residual differs"
+        d = oracle.ulp_distance(out, c["out"], code)
+        if d.max() > 1:
+            return f"{name}: output {d.max()} ulp"
+        if (d != 0).mean() > 1e-3:
+            return f"{name}: {(d != 0).mean():.1e} of outputs off by one ulp"
+    return None
+
+
+LIVE = [(64, 4096, BF, 1e-6, "bench"), (48, 5120, HF, 1e-6, "bench"), (16, 1000, BF, 2 ** -7, "reference_test"),
+        (8, 32768, BF, 1e-6, "bench"), (32, 768, HF, 2 ** -7, "reference_test"), (200, 64, BF, 1e-5, "bench")]
+
+
+def pin_torch_live(mutation=0):
+    for i, (rows, hidden, code, eps, dist) in enumerate(LIVE):
+        x, r, w = seeded(rows, hidden, code, 50 + i, dist)
+        want_out, want_res = torch_formula(x, r, w, eps, code)
+        out, res = oracle.fused_add_rmsnorm(x, w, r, eps, code, mutation=mutation)
+        if not np.array_equal(res, want_res):
+            return f"live {rows}x{hidden}: residual differs"
+        d = oracle.ulp_distance(out, want_out, code)
+        if d.max() > 1 or (d != 0).mean() > 1e-3:
+            return f"live {rows}x{hidden}: output max {d.max()} ulp, {(d != 0).mean():.1e} off"
+    return None
+
+
+def pin_brute_force(mutation=0):
+    for i, (rows, hidden, code) in enumerate([(16, 96, BF), (16, 130, HF), (4, 2048, BF), (9, 7, HF)]):
+        x, r, w = seeded(rows, hidden, code, 90 + i)
+        want_out, want_res = brute_force(x, r, w, 1e-6, code)
+        out, res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, code, mutation=mutation)
+        if not np.array_equal(res, want_res):
+            return f"brute {rows}x{hidden}: residual differs"
+        if oracle.ulp_distance(out, want_out, code).max() > 1:
+            return f"brute {rows}x{hidden}: output beyond 1 ulp of binary64"
+    return None
+
+
+def pin_closed_forms(mutation=0):
+    for code in (BF, HF):
+        rows, hidden = 6, 256
+        _, _, w = seeded(1, hidden, code, 7)
+        # constant rows c = +-2^k (x = c, r = 0) with eps = 0: out = sign(c) * w exactly
+        cs = np.array([2.0 ** (k - 3) * (-1) ** k for k in range(rows)])
+        x = to_16(np.repeat(cs[:, None], hidden, axis=1), code)
+        r = np.zeros_like(x)
+        out, res = oracle.fused_add_rmsnorm(x, w, r, 0.0, code, mutation=mutation)
+        if not np.array_equal(res, x):
+            return "constant rows: residual != x + 0"
+        want = np.where(cs[:, None] < 0, w[None, :] ^ 0x8000, w[None, :]).astype(np.uint16)
+        if not np.array_equal(out, want):
+            return "constant rows: output != +-w"
+        # power-of-two scaling of a row leaves the output unchanged (eps = 0)
+        x, r, w2 = seeded(4, 512, code, 8)
+        base, _ = oracle.fused_add_rmsnorm(x, w2, r, 0.0, code, mutation=mutation)
+        f = oracle.to_f32(x, code).astype(np.float64) * 4.0
+        g = oracle.to_f32(r, code).astype(np.float64) * 4.0
+        scaled, _ = oracle.fused_add_rmsnorm(to_16(f, code), w2, to_16(g, code), 0.0, code, mutation=mutation)
+        if not np.array_equal(base, scaled):
+            return "scaling a row by 4 changed the output"
+    return None
+
+
+def all_pins(golden, mutation=0):
+    return [m for m in (pin_golden(golden, mutation), pin_torch_live(mutation), pin_brute_force(mutation),
+                        pin_closed_forms(mutation)) if m]
+
+
+# ---- tests ---------------------------------------------------------------------------------
+def test_oracle_matches_golden_vectors(golden):
+    assert pin_golden(golden) is None
+
+
+def test_oracle_matches_live_torch_formula():
+    assert pin_torch_live() is None
+
+
+def test_oracle_matches_binary64_brute_force():
+    assert pin_brute_force() is None
+
+
+def test_oracle_closed_forms():
+    assert pin_closed_forms() is None
+
+
+@pytest.mark.parametrize("name", sorted(oracle.MUTATIONS))
+def test_planted_mistake_is_rejected(golden, name):
+    failures = all_pins(golden, oracle.MUTATIONS[name])
+    assert failures, f"no pin rejects the planted mistake {name!r}"
+
+
+def test_streamer_golden(golden):
+    for name, c in golden.items():
+        if c["kind"] != "stream":
+            continue
+        code = BF if c["dtype"] == "bf16" else HF
+        assert np.array_equal(oracle.streamer(c["x"], code, oracle.COPY), c["copy"]), name
+        got = oracle.streamer(c["x"], code, oracle.RELU)
+        # torch's bf16 relu canonicalises NaN payloads; compare NaN-ness there
+        assert oracle.ulp_distance(got, c["relu"], code).max() == 0, name
+
+
+def test_streamer_relu_matches_torch_cpu():
+    for code in (BF, HF):
+        allbits = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(64, 1024)
+        got = oracle.streamer(allbits, code, oracle.RELU)
+        want = tbits(torch.relu(tfrom(allbits, code)))
+        assert oracle.ulp_distance(got, want, code).max() == 0
+        nonnan = (allbits & 0x7FFF) <= (0x7F80 if code == BF else 0x7C00)
+        assert np.array_equal(got[nonnan], want[nonnan])   # incl. -0 kept as -0
+
+
+def test_fp16_conversion_exhaustive_and_random():
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = oracle.to_f32(allh, HF)
+    want = allh.view(np.float16).astype(np.float32)
+    same = (f.view(np.uint32) == want.view(np.uint32)) | (np.isnan(f) & np.isnan(want))
+    assert same.all()
+    rng = np.random.default_rng(0)
+    u = rng.integers(0, 2 ** 32, size=4_000_000, dtype=np.uint64).astype(np.uint32)
+    edges = np.array([0x477FEFFF, 0x477FF000, 0x477FF001, 0x33000000, 0x33000001, 0x33800000, 0x387FE000,
+                      0x387FF000, 0x38800000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x00000001, 0x80000000],
+                     dtype=np.uint32)
+    vals = np.concatenate([u, edges]).view(np.float32)
+    got = oracle.from_f32(vals, HF)
+    with np.errstate(over="ignore"):   # values beyond binary16's range become inf, as intended
+        want = vals.astype(np.float16).view(np.uint16)
+    nan = np.isnan(vals)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert ((got[nan] & 0x7FFF) > 0x7C00).all()
+
+
+def test_bf16_conversion_random():
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    assert np.array_equal(oracle.to_f32(allh, BF).view(np.uint32), allh.astype(np.uint32) << 16)
+    rng = np.random.default_rng(1)
+    u = rng.integers(0, 2 ** 32, size=4_000_000, dtype=np.uint64).astype(np.uint32)
+    ties = (rng.integers(0, 2 ** 16, size=100_000, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000
+    vals = np.concatenate([u, ties, np.array([0x7F7FFFFF, 0x7F7F8000, 0xFF7F8000], np.uint32)]).view(np.float32)
+    got = oracle.from_f32(vals, BF)
+    want = tbits(torch.from_numpy(vals.copy()).to(torch.bfloat16))
+    nan = np.isnan(vals)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert ((got[nan] & 0x7FFF) > 0x7F80).all()
+
+
+def test_oracle_rmsnorm_plain_matches_torch():
+    for code in (BF, HF):
+        x, _, w = seeded(32, 1536, code, 3)
+        want = tbits(torch.rms_norm(tfrom(x, code), (1536,), weight=tfrom(w, code), eps=1e-6))
+        d = oracle.ulp_distance(oracle.rmsnorm(x, w, 1e-6, code), want, code)
+        assert d.max() <= 1 and (d != 0).mean() < 1e-3
+
+
+def test_oracle_strided_rows_and_threads():
+    x, r, w = seeded(40, 1000, BF, 4)
+    want_out, want_res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, BF)
+    bx = np.zeros((40, 1024), np.uint16)
+    br = np.zeros((40, 1030), np.uint16)
+    bx[:, :1000] = x
+    br[:, 3:1003] = r
+    oracle.fused_add_rmsnorm_(bx[:, :1000], w, br[:, 3:1003], 1e-6, BF, threads=4)
+    assert np.array_equal(bx[:, :1000], want_out) and np.array_equal(br[:, 3:1003], want_res)
+    assert not bx[:, 1000:].any() and not br[:, :3].any() and not br[:, 1003:].any()
+
+
+def test_oracle_rejects_bad_arguments():
+    x = np.zeros((2, 8), np.uint16)
+    with pytest.raises(ValueError):
+        oracle.fused_add_rmsnorm(x, np.zeros(8, np.uint16), x, 1e-6, 7)
