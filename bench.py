@@ -218,6 +218,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--profile", type=int, default=0, metavar="H",
+                    help="profiling driver: only run (4096, H) bf16 calls, then a 1 GiB device copy "
+                         "(the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--profile-config", default="",
+                    help="with --profile: force lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the op has no cross-GPU step (rows are independent), and this "
@@ -234,6 +239,8 @@ def main():
         sys.exit(1)
     abi.lib()
     op = hp_rms_norm_amd.hp_rms_norm
+    if args.profile:
+        return profile_driver(torch, abi, op, args)
 
     shapes = [(B, h, torch.bfloat16, "bench") for h in H_SWEEP]
     log(f"bench: timing {len(shapes)} shapes x {args.steps} steps (warmup {args.warmup})")
@@ -301,6 +308,28 @@ def main():
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+
+
+def profile_driver(torch, abi, op, args):
+    """A short, fixed workload for rocprofv3 counter runs: `steps` cold calls
+    of (4096, H) bf16, then `steps` copies of a 1 GiB bf16 tensor."""
+    hidden = args.profile
+    if args.profile_config:
+        lpr, vpl, ldsv, block, flags = (int(v) for v in args.profile_config.split(","))
+        cfg = abi.Config(2 if ldsv else 1, lpr, vpl, ldsv, block, 0, flags)
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def op(x, w, r, eps):  # noqa: F811  (the forced configuration, through the C ABI)
+            abi.fused_add_rmsnorm(x.data_ptr(), w.data_ptr(), r.data_ptr(), x.shape[0], x.shape[1],
+                                  x.stride(0), r.stride(0), abi.DTYPE_BF16, eps, stream, cfg)
+    us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup)[0]
+    n = 1 << 29
+    src = torch.empty(n, dtype=torch.bfloat16, device="cuda:0").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile: (4096, {hidden}) {us:.2f} us/call; then {args.steps} copies of {2 * n} bytes")
 
 
 def load_traffic(key):
