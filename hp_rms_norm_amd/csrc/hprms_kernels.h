@@ -253,34 +253,33 @@ __device__ __forceinline__ uint16_t stream_op1(uint16_t h) {
   return (uint16_t)(stream_op2<DT, OP>((uint32_t)h) & 0xffffu);
 }
 
-// Flat kernel: out and in are both contiguous [rows*hidden], 16-byte aligned.
-// Each thread moves UNROLL vectors per trip, all loads before all stores.
+// Chunked kernel: out and in are both contiguous [rows*hidden], 16-byte
+// aligned.  Workgroup g moves the UNROLL*BLOCK vectors starting at vector
+// g*UNROLL*BLOCK (lane t takes t, t+BLOCK, ...: each wave instruction covers
+// 1 KiB), all loads before all stores, non-temporal both ways.  One
+// workgroup per chunk, no grid-stride loop.
 template <int DT, int OP, int UNROLL, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void stream_flat_kernel(StreamArgs a) {
+__global__ __launch_bounds__(BLOCK) void stream_chunk_kernel(StreamArgs a) {
   const u32x4* in = reinterpret_cast<const u32x4*>(a.in);
   u32x4* out = reinterpret_cast<u32x4*>(a.out);
-  const int64_t nthreads = (int64_t)gridDim.x * BLOCK;
-  const int64_t step = nthreads * UNROLL;
-  for (int64_t base = (int64_t)blockIdx.x * BLOCK + threadIdx.x; base < a.nvec; base += step) {
-    u32x4 v[UNROLL];
+  const int64_t base = (int64_t)blockIdx.x * (UNROLL * BLOCK) + threadIdx.x;
+  u32x4 v[UNROLL];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int64_t i = base + u * nthreads;
-      if (i < a.nvec) v[u] = __builtin_nontemporal_load(in + i);
-    }
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t i = base + u * BLOCK;
+    if (i < a.nvec) v[u] = __builtin_nontemporal_load(in + i);
+  }
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int64_t i = base + u * nthreads;
-      if (i < a.nvec) {
-        u32x4 o;
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t i = base + u * BLOCK;
+    if (i < a.nvec) {
+      u32x4 o;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = stream_op2<DT, OP>(v[u][j]);
-        __builtin_nontemporal_store(o, out + i);
-      }
+      for (int j = 0; j < 4; ++j) o[j] = stream_op2<DT, OP>(v[u][j]);
+      __builtin_nontemporal_store(o, out + i);
     }
   }
-  // elements past the last whole vector (rows*hidden % 8), by the first block
-  if (blockIdx.x == 0) {
+  if (blockIdx.x == gridDim.x - 1) {  // elements past the last whole vector
     const int64_t total = a.rows * a.hidden;
     for (int64_t e = a.nvec * 8 + threadIdx.x; e < total; e += BLOCK)
       a.out[e] = stream_op1<DT, OP>(a.in[e]);
