@@ -27,8 +27,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 constexpr int kRsrcWord3 = 0x00020000;
 // A byte offset past every num_records the kernels build (they stay < 2^31).
 constexpr uint32_t kOOB = 0x80000000u;
-// Cache-policy field of buffer instructions on gfx940+: nt (streaming) = 2.
+// Cache-policy field of buffer instructions on gfx940+: sc0 = 1, nt
+// (streaming) = 2, sc1 = 16.
 constexpr int kAuxNT = 2;
+constexpr int kAuxSC1 = 16;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
