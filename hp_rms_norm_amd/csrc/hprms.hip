@@ -45,30 +45,31 @@ struct FusedEntry {
 };
 
 // flags: bits 0-1 = non-temporal loads / stores, bit 2 = weight loaded late,
-// bit 3 = sc1 policy bit on the row accesses
+// bits 3-4 = sc1 policy bit on the row loads / stores
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
-   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 11, ((FLAGS) >> 2) & 1>},
+   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 27, ((FLAGS) >> 2) & 1>},
 
 // (lanes per row, vectors per lane, of which in LDS, block, flags): the shapes
 // every dtype and mode gets -- the table's entries first, then alternatives
-// that the tests run and the sweep compares against.  flags 11 = nt + sc1 on
-// the row accesses, 15 = the same with the weight loaded late.
+// that the tests run and the sweep compares against.  flags 3 = nt on the row
+// loads and stores, 7 = the same with the weight loaded late, 27 / 31 = nt
+// plus sc1 on loads and stores (without / with the late weight).
 #define HPRMS_SHAPES(X, DT, MODE)                                                              \
-  X(DT, MODE, 16, 1, 0, 256, 11) X(DT, MODE, 32, 1, 0, 256, 11) X(DT, MODE, 64, 1, 0, 256, 11) \
-  X(DT, MODE, 32, 4, 0, 256, 11) X(DT, MODE, 64, 4, 0, 256, 15) X(DT, MODE, 128, 3, 0, 256, 15) \
-  X(DT, MODE, 128, 4, 0, 256, 11) X(DT, MODE, 256, 4, 0, 256, 11) X(DT, MODE, 512, 3, 0, 512, 15) \
-  X(DT, MODE, 256, 8, 4, 256, 11) X(DT, MODE, 1024, 3, 0, 1024, 15)                             \
-  X(DT, MODE, 1024, 4, 0, 1024, 15) X(DT, MODE, 1024, 8, 4, 1024, 15)                           \
-  X(DT, MODE, 64, 2, 0, 256, 11) X(DT, MODE, 256, 2, 0, 256, 15) X(DT, MODE, 1024, 2, 0, 1024, 15) \
-  X(DT, MODE, 256, 8, 0, 256, 11) X(DT, MODE, 512, 8, 4, 512, 15) X(DT, MODE, 1024, 8, 0, 1024, 15)
+  X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
+  X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 3, 0, 256, 7)   \
+  X(DT, MODE, 128, 4, 0, 256, 3) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
+  X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 3, 0, 1024, 31)                             \
+  X(DT, MODE, 1024, 4, 0, 1024, 31) X(DT, MODE, 1024, 8, 4, 1024, 31)                           \
+  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 2, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
+  X(DT, MODE, 256, 8, 0, 256, 27) X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
 
-// extra bf16 fused shapes kept for the tuning sweep (nt only, no sc1, ...)
+// extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
-  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 3) X(DT, MODE, 128, 4, 0, 256, 3)    \
-  X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 4, 0, 512, 3) X(DT, MODE, 1024, 4, 0, 1024, 3) \
-  X(DT, MODE, 512, 4, 0, 512, 11) X(DT, MODE, 256, 16, 8, 256, 15) X(DT, MODE, 128, 4, 0, 256, 0) \
-  X(DT, MODE, 1024, 4, 2, 1024, 15) X(DT, MODE, 256, 6, 3, 256, 15)
+  X(DT, MODE, 64, 2, 0, 256, 11) X(DT, MODE, 128, 4, 0, 256, 27) X(DT, MODE, 256, 4, 0, 256, 27) \
+  X(DT, MODE, 512, 4, 0, 512, 3) X(DT, MODE, 1024, 4, 0, 1024, 7) X(DT, MODE, 512, 4, 0, 512, 27) \
+  X(DT, MODE, 256, 16, 8, 256, 31) X(DT, MODE, 128, 4, 0, 256, 0) X(DT, MODE, 1024, 4, 2, 1024, 31) \
+  X(DT, MODE, 256, 6, 3, 256, 31) X(DT, MODE, 256, 8, 4, 256, 3)
 
 const FusedEntry kFused[] = {
     HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
@@ -91,22 +92,22 @@ const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
 // tuning notes in the design document for the measurements behind it.
 void table_config(int64_t hidden, hprms_config* c) {
   const int64_t nvec = hidden / 8;
-  *c = hprms_config{1, 0, 0, 0, 0, 0, 11};
+  *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row rows[] = {
-      {16, 16, 1, 0, 256, 11},       // H <= 128:   16 rows per workgroup
-      {32, 32, 1, 0, 256, 11},       // H <= 256
-      {64, 64, 1, 0, 256, 11},       // H <= 512:   one row per wave
-      {128, 32, 4, 0, 256, 11},      // H <= 1024:  two rows per wave
-      {256, 64, 4, 0, 256, 15},      // H <= 2048
-      {384, 128, 3, 0, 256, 15},     // H <= 3072:  two waves per row
-      {512, 128, 4, 0, 256, 11},     // H <= 4096
-      {1024, 256, 4, 0, 256, 11},    // H <= 8192:  one row per 4-wave workgroup
-      {1536, 512, 3, 0, 512, 15},    // H <= 12288
-      {2048, 256, 8, 4, 256, 11},    // H <= 16384: LDS tier, half the row in LDS
-      {3072, 1024, 3, 0, 1024, 15},  // H <= 24576
-      {4096, 1024, 4, 0, 1024, 15},  // H <= 32768
-      {8192, 1024, 8, 4, 1024, 15},  // H <= 65536: LDS tier
+      {16, 16, 1, 0, 256, 3},        // H <= 128:   16 rows per workgroup
+      {32, 32, 1, 0, 256, 3},        // H <= 256
+      {64, 64, 1, 0, 256, 3},        // H <= 512:   one row per wave
+      {128, 32, 4, 0, 256, 3},       // H <= 1024:  two rows per wave
+      {256, 64, 4, 0, 256, 7},       // H <= 2048
+      {384, 128, 3, 0, 256, 7},      // H <= 3072:  two waves per row
+      {512, 128, 4, 0, 256, 3},      // H <= 4096
+      {1024, 256, 4, 0, 256, 3},     // H <= 8192:  one row per 4-wave workgroup
+      {1536, 512, 3, 0, 512, 31},    // H <= 12288
+      {2048, 256, 8, 4, 256, 27},    // H <= 16384: LDS tier, half the row in LDS
+      {3072, 1024, 3, 0, 1024, 31},  // H <= 24576
+      {4096, 1024, 4, 0, 1024, 31},  // H <= 32768
+      {8192, 1024, 8, 4, 1024, 31},  // H <= 65536: LDS tier
   };
   for (const Row& r : rows) {
     if (nvec <= r.max_nvec) {

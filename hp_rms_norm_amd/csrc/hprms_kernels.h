@@ -22,7 +22,8 @@
 //
 // FLAGS bit 0 marks the row loads non-temporal, bit 1 the stores: the rows
 // are touched once, so they should not displace the weight from the caches.
-// Bit 3 adds the sc1 (system-scope) policy bit to both.
+// Bits 3 and 4 add the sc1 (device-scope) policy bit to the loads and to the
+// stores respectively.
 //
 // MODE 0 is the fused op (in place on input and residual); MODE 1 is the
 // plain RMSNorm (reads `input`, writes `out`, no residual stream).
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   constexpr int NW = BLOCK / 64;
   constexpr int VREG = VPL - LDSV;
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
-  constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
+  constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
 
   __shared__ float red[2][WPR > 1 ? NW : 1];

@@ -103,7 +103,7 @@ typedef struct {
   int32_t grid_blocks;      /* 0 = one workgroup per row group; >0 = persistent grid of this many */
   int32_t flags;            /* bit 0: non-temporal row loads; bit 1: non-temporal stores;
                                bit 2: weight loaded after the residual is stored;
-                               bit 3: sc1 cache-policy bit on the row loads and stores */
+                               bit 3 / bit 4: sc1 cache-policy bit on the row loads / stores */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
