@@ -62,7 +62,9 @@ struct FusedEntry {
   X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 3, 0, 1024, 31)                             \
   X(DT, MODE, 1024, 4, 0, 1024, 31) X(DT, MODE, 1024, 8, 4, 1024, 31)                           \
   X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 2, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
-  X(DT, MODE, 256, 8, 0, 256, 27) X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
+  X(DT, MODE, 256, 8, 0, 256, 27) X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31) \
+  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 512, 2, 0, 512, 7)    \
+  X(DT, MODE, 512, 4, 0, 512, 7)
 
 // extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
@@ -88,13 +90,29 @@ const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
 }
 
 // ---- the gfx950 table -------------------------------------------------------------
-// Chosen from (hidden); rows only matter through the grid size.  See the
-// tuning notes in the design document for the measurements behind it.
-void table_config(int64_t hidden, hprms_config* c) {
+// Chosen from (rows, hidden) by measurement on MI355X.  With few rows (at most
+// one per CU) the kernel is latency-bound: one row per workgroup and at most
+// two vectors per lane shortens each wave's serial work.  Otherwise the
+// bandwidth table below applies.
+bool latency_config(int64_t rows, int64_t nvec, hprms_config* c) {
+  if (rows > 256 || nvec <= 64 || nvec > 2048) return false;
+  struct Row { int64_t max_nvec; int lpr, vpl; };
+  static const Row lat[] = {{128, 64, 2}, {256, 128, 2}, {512, 256, 2}, {1024, 512, 2}, {2048, 512, 4}};
+  for (const Row& r : lat) {
+    if (nvec <= r.max_nvec) {
+      *c = hprms_config{1, r.lpr, r.vpl, 0, r.lpr, 0, 7};
+      return true;
+    }
+  }
+  return false;
+}
+
+void table_config(int64_t rows, int64_t hidden, hprms_config* c) {
   const int64_t nvec = hidden / 8;
+  if (latency_config(rows, nvec, c)) return;
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
-  static const Row rows[] = {
+  static const Row table[] = {
       {16, 16, 1, 0, 256, 3},        // H <= 128:   16 rows per workgroup
       {32, 32, 1, 0, 256, 3},        // H <= 256
       {64, 64, 1, 0, 256, 3},        // H <= 512:   one row per wave
@@ -109,7 +127,7 @@ void table_config(int64_t hidden, hprms_config* c) {
       {4096, 1024, 4, 0, 1024, 31},  // H <= 32768
       {8192, 1024, 8, 4, 1024, 31},  // H <= 65536: LDS tier
   };
-  for (const Row& r : rows) {
+  for (const Row& r : table) {
     if (nvec <= r.max_nvec) {
       c->lanes_per_row = r.lpr;
       c->vec_per_lane = r.vpl;
@@ -213,7 +231,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   if (forced && forced->tier != 0) {
     c = *forced;
   } else {
-    table_config(p.hidden, &c);
+    table_config(p.rows, p.hidden, &c);
   }
   if (c.tier != 3 && !vec_fits(p, c)) {
     if (forced && forced->tier != 0)
@@ -317,7 +335,7 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, hprms_config* c
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
-  table_config(hidden, config);
+  table_config(rows, hidden, config);
   if (hidden % 8 != 0) config->tier = 3;
   return HPRMS_OK;
 }

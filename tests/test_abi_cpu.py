@@ -103,9 +103,9 @@ def test_table_covers_every_hidden_with_a_built_kernel():
     it, or to the general kernel; checked through the config entry point with
     rows = 0 (validates and looks the kernel up, launches nothing)."""
     L = abi.lib()
-    for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+    for dtype, rows in ((abi.DTYPE_BF16, 4096), (abi.DTYPE_FP16, 4096), (abi.DTYPE_BF16, 1), (abi.DTYPE_FP16, 256)):
         for hidden in list(range(8, 70000, 8)) + [1, 3, 1001, 4097]:
-            c = abi.select_config(4096, hidden, dtype)
+            c = abi.select_config(rows, hidden, dtype)
             if hidden % 8:
                 assert c.tier == 3
                 continue

@@ -205,6 +205,61 @@ def test_full_size_properties(abi):
     assert torch.equal(rp.view(torch.int16), rd[perm].view(torch.int16))
 
 
+def test_batch_beyond_2_pow_31_elements(abi):
+    """(2^19 + 5, 4096) bf16: 2.15e9 elements per tensor, so row offsets pass
+    2^31 elements.  The whole residual must equal torch's HIP add bit-for-bit
+    and the whole output must be within 1 ulp of a float32 torch evaluation
+    (checked in row chunks); the first and last rows are also checked against
+    the CPU oracle."""
+    import hp_rms_norm_amd
+    rows, hidden, eps, dtype = (1 << 19) + 5, 4096, 1e-6, torch.bfloat16
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn((rows, hidden), generator=g, device=DEV, dtype=torch.float32).to(dtype)
+    r = torch.randn((rows, hidden), generator=g, device=DEV, dtype=torch.float32).to(dtype)
+    w = make_inputs(1, hidden, dtype, 3)[2].to(DEV)
+    ends = torch.cat([torch.arange(0, 64), torch.arange(rows - 64, rows)]).to(DEV)
+    xe, re_ = x[ends].cpu(), r[ends].cpu()
+    s_ref = x + r
+    hp_rms_norm_amd.hp_rms_norm(x, w, r, eps)
+    torch.cuda.synchronize()
+    assert torch.equal(r.view(torch.int16), s_ref.view(torch.int16))
+    del s_ref
+    wf = w.float()
+
+    def ordered(t):  # bf16 bits on the ordered-integer line (no NaNs occur here)
+        i = t.view(torch.int16).to(torch.int32)
+        mag = i & 0x7FFF
+        return torch.where(i < 0, -mag, mag)
+
+    for c0 in range(0, rows, 65536):
+        sf = r[c0:c0 + 65536].float()
+        o = ((sf * torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + eps)) * wf).to(dtype)
+        d = int((ordered(x[c0:c0 + 65536]) - ordered(o)).abs().max())
+        assert d <= 1, f"rows {c0}..: {d} ulp"
+    want_out, want_res = oracle_fused(xe, re_, w.cpu(), eps, dtype)
+    assert_residual_exact(bits(r[ends]), want_res, dtype)
+    assert_output_close(bits(x[ends]), want_out, dtype)
+
+
+def test_torch_compile_functionalises_the_in_place_op(abi):
+    """torch.compile (aot_eager: no codegen) traces the op through its Meta
+    kernel and functionalises its declared in-place writes; the compiled
+    function must give the eager result bit-for-bit."""
+    import hp_rms_norm_amd
+
+    def f(x, w, r):
+        y = x * 2
+        hp_rms_norm_amd.hp_rms_norm(y, w, r, 1e-6)
+        return y + 0, r + 0
+
+    x, r, w = (t.to(DEV) for t in make_inputs(64, 4096, torch.bfloat16, 21))
+    want_y, want_r = f(x.clone(), w, r.clone())
+    got_y, got_r = torch.compile(f, backend="aot_eager", fullgraph=True)(x.clone(), w, r.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(got_y.view(torch.int16), want_y.view(torch.int16))
+    assert torch.equal(got_r.view(torch.int16), want_r.view(torch.int16))
+
+
 # ---- streams and graphs ------------------------------------------------------------------
 def test_runs_on_current_stream(abi):
     import hp_rms_norm_amd
