@@ -21,6 +21,7 @@ STREAM_COPY, STREAM_RELU = 0, 1
 # every symbol the header declares
 SYMBOLS = (
     "hprms_fused_add_rmsnorm",
+    "hprms_fused_add_rmsnorm_fp8",
     "hprms_streamer",
     "hprms_rmsnorm",
     "hprms_fused_add_rmsnorm_config",
@@ -67,6 +68,7 @@ def lib():
         L.hprms_fused_add_rmsnorm_config.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd,
                                                      ctypes.POINTER(Config), vp]
         L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
+        L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
         L.hprms_streamer.argtypes = [vp, vp, i64, i64, i64, i64, ci, ci, vp]
         L.hprms_select_config.argtypes = [i64, i64, ci, ctypes.POINTER(Config)]
         L.hprms_kernel_configs.argtypes = [ci, ci, ctypes.POINTER(Config), ci]
@@ -74,6 +76,7 @@ def lib():
         L.hprms_last_error.argtypes = []
         L.hprms_abi_version.restype = ci
         for name in ("hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
+                     "hprms_fused_add_rmsnorm_fp8",
                      "hprms_streamer", "hprms_select_config", "hprms_kernel_configs"):
             getattr(L, name).restype = ci
         _lib = L
@@ -98,6 +101,13 @@ def fused_add_rmsnorm(input_ptr, weight_ptr, residual_ptr, rows, hidden, input_s
     return _check(lib().hprms_fused_add_rmsnorm_config(input_ptr, weight_ptr, residual_ptr, rows, hidden,
                                                        input_stride, residual_stride, dtype, eps,
                                                        ctypes.byref(config), stream))
+
+
+def fused_add_rmsnorm_fp8(out_ptr, scale_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride,
+                          input_stride, residual_stride, dtype, eps, stream=0):
+    return _check(lib().hprms_fused_add_rmsnorm_fp8(out_ptr, scale_ptr, input_ptr, weight_ptr, residual_ptr, rows,
+                                                    hidden, out_stride, input_stride, residual_stride, dtype, eps,
+                                                    stream))
 
 
 def rmsnorm(out_ptr, in_ptr, weight_ptr, rows, hidden, out_stride, in_stride, dtype, eps, stream=0):

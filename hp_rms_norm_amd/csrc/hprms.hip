@@ -50,21 +50,23 @@ struct FusedEntry {
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 27, ((FLAGS) >> 2) & 1>},
 
-// (lanes per row, vectors per lane, of which in LDS, block, flags): the shapes
-// every dtype and mode gets -- the table's entries first, then alternatives
-// that the tests run and the sweep compares against.  flags 3 = nt on the row
-// loads and stores, 7 = the same with the weight loaded late, 27 / 31 = nt
-// plus sc1 on loads and stores (without / with the late weight).
-#define HPRMS_SHAPES(X, DT, MODE)                                                              \
+// (lanes per row, vectors per lane, of which in LDS, block, flags).  flags 3 =
+// nt on the row loads and stores, 7 = the same with the weight loaded late,
+// 27 / 31 = nt plus sc1 on loads and stores (without / with the late weight).
+// The table's entries (bandwidth rows, then the latency rows for few rows):
+#define HPRMS_TABLE_SHAPES(X, DT, MODE)                                                        \
   X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
   X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 3, 0, 256, 7)   \
   X(DT, MODE, 128, 4, 0, 256, 3) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
   X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 3, 0, 1024, 31)                             \
   X(DT, MODE, 1024, 4, 0, 1024, 31) X(DT, MODE, 1024, 8, 4, 1024, 31)                           \
-  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 2, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
-  X(DT, MODE, 256, 8, 0, 256, 27) X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31) \
-  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 512, 2, 0, 512, 7)    \
-  X(DT, MODE, 512, 4, 0, 512, 7)
+  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
+
+// alternatives of the fused op that the tests run and the sweep compares against
+#define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
+  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 0, 256, 27) \
+  X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
 
 // extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
@@ -74,11 +76,15 @@ struct FusedEntry {
   X(DT, MODE, 256, 6, 3, 256, 31) X(DT, MODE, 256, 8, 4, 256, 3)
 
 const FusedEntry kFused[] = {
-    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
-    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
+    HPRMS_ALT_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_ALT_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
     HPRMS_TUNING_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 2)
 };
 
 const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
@@ -147,14 +153,15 @@ constexpr int64_t kMaxHidden = int64_t(1) << 24;
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
 struct Problem {
-  int mode;  // 0 fused, 1 plain
+  int mode;  // 0 fused, 1 plain, 2 fused with FP8 output
   void* x;
-  void* out;
+  void* out;  // mode 1: 16-bit output; mode 2: FP8 output
   void* res;
   const void* w;
   int64_t rows, hidden, x_stride, out_stride, res_stride;
   int dtype;
   double eps;
+  float* scale;  // mode 2
 };
 
 int check_problem(const Problem& p) {
@@ -167,17 +174,17 @@ int check_problem(const Problem& p) {
                 (long long)kMaxHidden);
   if (p.x_stride < p.hidden) return fail(HPRMS_E_INVALID, "input row stride %lld < hidden %lld",
                                          (long long)p.x_stride, (long long)p.hidden);
-  if (p.mode == 0 && p.res_stride < p.hidden)
+  if (p.mode != 1 && p.res_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "residual row stride %lld < hidden %lld", (long long)p.res_stride,
                 (long long)p.hidden);
-  if (p.mode == 1 && p.out_stride < p.hidden)
+  if (p.mode != 0 && p.out_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "output row stride %lld < hidden %lld", (long long)p.out_stride,
                 (long long)p.hidden);
   if (!(p.eps >= 0.0)) return fail(HPRMS_E_INVALID, "eps must be >= 0");
   if (p.rows == 0) return HPRMS_OK;
-  if (!p.x || !p.w || (p.mode == 0 && !p.res) || (p.mode == 1 && !p.out))
+  if (!p.x || !p.w || (p.mode != 1 && !p.res) || (p.mode != 0 && !p.out) || (p.mode == 2 && !p.scale))
     return fail(HPRMS_E_INVALID, "null tensor pointer");
-  if (p.mode == 0 && p.x == p.res) return fail(HPRMS_E_INVALID, "input and residual must not alias");
+  if (p.mode != 1 && p.x == p.res) return fail(HPRMS_E_INVALID, "input and residual must not alias");
   return HPRMS_OK;
 }
 
@@ -186,13 +193,14 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   if (p.hidden % 8 != 0) return false;
   if (!aligned16(p.x) || !aligned16(p.w)) return false;
   if (p.x_stride % 8 != 0) return false;
-  if (p.mode == 0 && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
+  if (p.mode != 1 && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
   if (p.mode == 1 && (!aligned16(p.out) || p.out_stride % 8 != 0)) return false;
+  if (p.mode == 2 && (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0)) return false;
   if ((int64_t)c.lanes_per_row * c.vec_per_lane * 8 < p.hidden) return false;
   // every buffer resource of a row group spans < 2^31 bytes
   const int64_t rpb = c.block_threads / c.lanes_per_row;
-  const int64_t smax = p.x_stride > (p.mode == 0 ? p.res_stride : p.out_stride)
-                           ? p.x_stride : (p.mode == 0 ? p.res_stride : p.out_stride);
+  int64_t smax = p.x_stride > p.out_stride ? p.x_stride : p.out_stride;
+  if (p.mode != 1 && p.res_stride > smax) smax = p.res_stride;
   if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
     return false;
   return true;
@@ -202,21 +210,26 @@ template <int DT>
 int launch_general(const Problem& p, hipStream_t stream) {
   GeneralArgs a;
   a.x = (const uint16_t*)p.x;
-  a.out = (uint16_t*)(p.mode == 0 ? p.x : p.out);
+  a.out = (uint16_t*)(p.mode == 1 ? p.out : p.x);
   a.res = (uint16_t*)p.res;
   a.w = (const uint16_t*)p.w;
   a.rows = p.rows;
   a.x_stride = p.x_stride;
-  a.out_stride = p.mode == 0 ? p.x_stride : p.out_stride;
+  a.out_stride = p.mode == 1 ? p.out_stride : p.x_stride;
   a.res_stride = p.res_stride;
   a.hidden = p.hidden;
   a.hidden_f = (float)p.hidden;
   a.eps = (float)p.eps;
+  a.q = p.mode == 2 ? (uint8_t*)p.out : nullptr;
+  a.scale = p.scale;
+  a.q_stride = p.mode == 2 ? p.out_stride : 0;
   const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
   if (p.mode == 0)
     fused_general_kernel<DT, 0><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
-  else
+  else if (p.mode == 1)
     fused_general_kernel<DT, 1><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
+  else
+    fused_general_kernel<DT, 2><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
   return check_launch("general rmsnorm kernel");
 }
 
@@ -256,14 +269,17 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
 
   FusedArgs a;
   a.x = (const uint16_t*)p.x;
-  a.out = (uint16_t*)(p.mode == 0 ? p.x : p.out);
+  a.out = (uint16_t*)(p.mode == 1 ? p.out : p.x);
   a.res = (uint16_t*)p.res;
   a.w = (const uint16_t*)p.w;
   a.rows = p.rows;
+  a.q = p.mode == 2 ? (uint8_t*)p.out : nullptr;
+  a.scale = p.scale;
+  a.q_stride = p.mode == 2 ? p.out_stride : 0;
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   a.ngroups = (p.rows + rpb - 1) / rpb;
   a.x_stride = p.x_stride;
-  a.out_stride = p.mode == 0 ? p.x_stride : p.out_stride;
+  a.out_stride = p.mode == 1 ? p.out_stride : p.x_stride;
   a.res_stride = p.res_stride;
   a.hidden = (int32_t)p.hidden;
   a.nvec = (int32_t)(p.hidden / 8);
@@ -310,7 +326,15 @@ int hprms_fused_add_rmsnorm(void* input, const void* weight, void* residual, int
                             int64_t input_row_stride, int64_t residual_row_stride, int dtype, double eps,
                             hipStream_t stream) {
   Problem p{0, input, input, residual, weight, rows, hidden, input_row_stride, input_row_stride,
-            residual_row_stride, dtype, eps};
+            residual_row_stride, dtype, eps, nullptr};
+  return run(p, nullptr, stream);
+}
+
+int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, const void* weight, void* residual,
+                                int64_t rows, int64_t hidden, int64_t out_row_stride, int64_t input_row_stride,
+                                int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
+  Problem p{2, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
+            residual_row_stride, dtype, eps, scale};
   return run(p, nullptr, stream);
 }
 
@@ -319,14 +343,14 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
                                    int dtype, double eps, const hprms_config* config, hipStream_t stream) {
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
   Problem p{0, input, input, residual, weight, rows, hidden, input_row_stride, input_row_stride,
-            residual_row_stride, dtype, eps};
+            residual_row_stride, dtype, eps, nullptr};
   return run(p, config, stream);
 }
 
 int hprms_rmsnorm(void* out, const void* in, const void* weight, int64_t rows, int64_t hidden,
                   int64_t out_row_stride, int64_t in_row_stride, int dtype, double eps, hipStream_t stream) {
   Problem p{1, const_cast<void*>(in), out, nullptr, weight, rows, hidden, in_row_stride, out_row_stride,
-            0, dtype, eps};
+            0, dtype, eps, nullptr};
   return run(p, nullptr, stream);
 }
 
@@ -364,7 +388,7 @@ int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int6
 int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode != 0 && mode != 1) return fail(HPRMS_E_INVALID, "mode must be 0 or 1 (got %d)", mode);
+  if (mode < 0 || mode > 2) return fail(HPRMS_E_INVALID, "mode must be 0, 1 or 2 (got %d)", mode);
   if (capacity < 0 || (capacity > 0 && !out)) return fail(HPRMS_E_INVALID, "bad output array");
   int n = 0;
   for (const FusedEntry& e : kFused) {

@@ -76,6 +76,28 @@ struct Fmt<HPRMS_DTYPE_FP16> {
   __device__ static __forceinline__ uint16_t pack1(float a) { return (uint16_t)(pack(a, 0.0f) & 0xffffu); }
 };
 
+// ---- FP8 ----------------------------------------------------------------------
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Four binary32 values to four OCP e4m3fn bytes (gfx950 v_cvt_pk_fp8_f32:
+// round to nearest even; callers clamp to +-448 first).  Byte i of the result
+// holds value i.
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// Clamp to the e4m3fn range; NaN passes through (both compares are false).
+__device__ __forceinline__ float clamp_e4m3(float v) {
+  return v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
+}
+
+template <int AUX>
+__device__ __forceinline__ void store8(u32x2 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, AUX);
+}
+
 // ---- reductions ---------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -100,6 +122,27 @@ __device__ __forceinline__ float group_sum(float v) {
     v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
   }
+  return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// Unsigned maximum over aligned groups of WIDTH lanes, same lane pattern as
+// group_sum.  Must be called with every lane of the wave active.
+template <int WIDTH>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+  static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group width");
+  v = __builtin_elementwise_max(v, dpp_u32<0xB1>(v));
+  v = __builtin_elementwise_max(v, dpp_u32<0x4E>(v));
+  v = __builtin_elementwise_max(v, dpp_u32<0x141>(v));
+  v = __builtin_elementwise_max(v, dpp_u32<0x140>(v));
+  if constexpr (WIDTH >= 32) v = __builtin_elementwise_max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));
+  if constexpr (WIDTH == 64)
+    v = __builtin_elementwise_max((uint32_t)__builtin_amdgcn_readlane((int)v, 0),
+                                  (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
   return v;
 }
 

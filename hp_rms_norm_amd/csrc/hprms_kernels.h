@@ -26,7 +26,12 @@
 // stores respectively.
 //
 // MODE 0 is the fused op (in place on input and residual); MODE 1 is the
-// plain RMSNorm (reads `input`, writes `out`, no residual stream).
+// plain RMSNorm (reads `input`, writes `out`, no residual stream); MODE 2 is
+// the fused op with an FP8 output: the 16-bit output y is quantised per row
+// (scale = max(amax|y| / 448, FLT_MIN) to scale[row], q = e4m3fn(clamp(y /
+// scale)) to q), the residual is updated in place and `input` is only read.
+// The row maximum is a second DPP/LDS reduction over the 16-bit magnitudes
+// (sign-magnitude bit patterns order like their values, NaN above inf).
 #pragma once
 
 #include "hprms_device.h"
@@ -47,6 +52,9 @@ struct FusedArgs {
   int32_t nvec;          // hidden / 8
   float hidden_f;
   float eps;
+  uint8_t* q;            // MODE 2: FP8 output rows
+  float* scale;          // MODE 2: per-row scales
+  int64_t q_stride;      // MODE 2: bytes between FP8 rows
 };
 
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
@@ -90,11 +98,16 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
 
     __amdgpu_buffer_rsrc_t rrs = xrs, ors = xrs;
     uint32_t roff = 0, ooff = xoff;
-    if constexpr (MODE == 0) {
+    if constexpr (MODE == 0 || MODE == 2) {
       const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_stride + a.hidden) * 2);
       rrs = make_rsrc(a.res + row0 * a.res_stride, rbytes);
       roff = (uint32_t)rib * (uint32_t)a.res_stride * 2u + (uint32_t)lane * 16u;
-    } else {
+    }
+    if constexpr (MODE == 2) {
+      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + a.hidden);
+      ors = make_rsrc(a.q + row0 * a.q_stride, qbytes);
+      ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)lane * 8u;
+    } else if constexpr (MODE == 1) {
       const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + a.hidden) * 2);
       ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
@@ -105,7 +118,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     for (int k = 0; k < VPL; ++k) {
       const bool ok = row_ok && vec_ok[k];
       xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
-      if constexpr (MODE == 0) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+      if constexpr (MODE != 1) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
     }
     if constexpr (!WLATE) {
 #pragma unroll
@@ -117,7 +130,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       u32x4 s;
-      if constexpr (MODE == 0) {
+      if constexpr (MODE != 1) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t p = F::pack(F::lo(xv[k][j]) + F::lo(rv[k][j]), F::hi(xv[k][j]) + F::hi(rv[k][j]));
@@ -158,15 +171,62 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     }
     const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
 
+    if constexpr (MODE != 2) {
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
-      u32x4 o;
+      for (int k = 0; k < VPL; ++k) {
+        const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
+        u32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        o[j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
-      const bool ok = row_ok && vec_ok[k];
-      store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
+        for (int j = 0; j < 4; ++j)
+          o[j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+        const bool ok = row_ok && vec_ok[k];
+        store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
+      }
+    } else {
+      // y in 16-bit form, kept in the registers x came in; the row maximum of
+      // |y| over the valid vectors, as packed 16-bit magnitudes
+      uint32_t m2 = 0;
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xv[k][j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+        if (row_ok && vec_ok[k]) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t mag = xv[k][j] & 0x7fff7fffu;
+            const uint32_t lo = mag & 0xffffu, hi = mag >> 16;
+            m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(lo, hi));
+          }
+        }
+      }
+      uint32_t mx = group_max_u32<GW>(m2);
+      if constexpr (WPR > 1) {
+        if ((tid & 63) == 0) red[buf][wave] = __builtin_bit_cast(float, mx);
+        __syncthreads();
+        const int w0 = (wave / WPR) * WPR;
+#pragma unroll
+        for (int j = 0; j < WPR; ++j) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w0 + j]));
+        buf ^= 1;
+      }
+      const float amax = F::one((uint16_t)mx);
+      float sc = amax / 448.0f;
+      if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+      const float isc = 1.0f / sc;
+      if (row_ok && lane == 0) a.scale[row0 + rib] = sc;
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        u32x2 q;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t y0 = xv[k][2 * h], y1 = xv[k][2 * h + 1];
+          q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * isc), clamp_e4m3(F::hi(y0) * isc),
+                             clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
+        }
+        const bool ok = row_ok && vec_ok[k];
+        store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
+      }
     }
   }
 }
@@ -187,6 +247,9 @@ struct GeneralArgs {
   int64_t hidden;
   float hidden_f;
   float eps;
+  uint8_t* q;        // MODE 2
+  float* scale;      // MODE 2
+  int64_t q_stride;  // MODE 2
 };
 
 template <int DT, int MODE>
@@ -198,11 +261,11 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
   for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
     const uint16_t* x = a.x + row * a.x_stride;
     uint16_t* o = a.out + row * a.out_stride;
-    uint16_t* r = MODE == 0 ? a.res + row * a.res_stride : nullptr;
+    uint16_t* r = MODE != 1 ? a.res + row * a.res_stride : nullptr;
     float ss = 0.0f;
     for (int64_t j = tid; j < a.hidden; j += 256) {
       float v;
-      if constexpr (MODE == 0) {
+      if constexpr (MODE != 1) {
         const uint16_t s = F::pack1(F::one(x[j]) + F::one(r[j]));
         r[j] = s;
         v = F::one(s);
@@ -217,9 +280,31 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
     tot = ((red[buf][0] + red[buf][1]) + red[buf][2]) + red[buf][3];
     buf ^= 1;
     const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
-    for (int64_t j = tid; j < a.hidden; j += 256) {
-      const float v = MODE == 0 ? F::one(r[j]) : F::one(x[j]);
-      o[j] = F::pack1((v * inv) * F::one(a.w[j]));
+    if constexpr (MODE != 2) {
+      for (int64_t j = tid; j < a.hidden; j += 256) {
+        const float v = MODE == 0 ? F::one(r[j]) : F::one(x[j]);
+        o[j] = F::pack1((v * inv) * F::one(a.w[j]));
+      }
+    } else {
+      // y is recomputed in each pass from the residual this thread wrote, so
+      // both passes see the same bits
+      uint32_t m = 0;
+      for (int64_t j = tid; j < a.hidden; j += 256)
+        m = __builtin_elementwise_max(m, (uint32_t)(F::pack1((F::one(r[j]) * inv) * F::one(a.w[j])) & 0x7fffu));
+      uint32_t mx = group_max_u32<64>(m);
+      if ((tid & 63) == 0) red[buf][tid >> 6] = __builtin_bit_cast(float, mx);
+      __syncthreads();
+      for (int j = 0; j < 4; ++j) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][j]));
+      buf ^= 1;
+      float sc = F::one((uint16_t)mx) / 448.0f;
+      if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+      const float isc = 1.0f / sc;
+      if (tid == 0) a.scale[row] = sc;
+      uint8_t* qr = a.q + row * a.q_stride;
+      for (int64_t j = tid; j < a.hidden; j += 256) {
+        const float y = F::one(F::pack1((F::one(r[j]) * inv) * F::one(a.w[j])));
+        qr[j] = (uint8_t)(pack_e4m3x4(clamp_e4m3(y * isc), 0.0f, 0.0f, 0.0f) & 0xffu);
+      }
     }
   }
 }

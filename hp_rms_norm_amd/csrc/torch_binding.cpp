@@ -165,6 +165,46 @@ void rms_norm_plain_meta(at::Tensor& out, const at::Tensor& input, const at::Ten
   (void)eps;
 }
 
+struct Fp8Shape {
+  FusedShape f;
+  int64_t out_stride;
+};
+
+Fp8Shape check_fp8(const at::Tensor& out, const at::Tensor& scale, const at::Tensor& input,
+                   const at::Tensor& weight, const at::Tensor& residual) {
+  Fp8Shape s;
+  s.f = check_fused(input, weight, residual);
+  TORCH_CHECK(out.scalar_type() == at::kFloat8_e4m3fn, "out.dtype() == float8_e4m3fn");
+  TORCH_CHECK(scale.scalar_type() == at::kFloat, "scale.dtype() == float32");
+  TORCH_CHECK(out.dim() == input.dim(), "out.dim() == input.dim()");
+  for (int64_t i = 0; i < input.dim(); ++i) TORCH_CHECK(out.size(i) == input.size(i), "out.size(i) == input.size(i)");
+  TORCH_CHECK(out.stride(-1) == 1, "out.stride(-1) == 1");
+  TORCH_CHECK(scale.numel() == s.f.rows, "scale.numel() == number of rows");
+  TORCH_CHECK(scale.is_contiguous(), "scale must be contiguous");
+  TORCH_CHECK(out.device() == input.device() && scale.device() == input.device(),
+              "out, scale and input must be on the same device");
+  int64_t orows = 0;
+  rows_of(out, s.f.hidden, &orows, &s.out_stride);
+  return s;
+}
+
+void rms_norm_fp8_hip(at::Tensor& out, at::Tensor& scale, const at::Tensor& input, const at::Tensor& weight,
+                      at::Tensor& residual, double eps) {
+  const Fp8Shape s = check_fp8(out, scale, input, weight, residual);
+  if (s.f.rows == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm_fp8(out.data_ptr(), scale.data_ptr<float>(), input.data_ptr(),
+                                           weight.data_ptr(), residual.data_ptr(), s.f.rows, s.f.hidden,
+                                           s.out_stride, s.f.in_stride, s.f.res_stride, s.f.dtype, eps, stream));
+}
+
+void rms_norm_fp8_meta(at::Tensor& out, at::Tensor& scale, const at::Tensor& input, const at::Tensor& weight,
+                       at::Tensor& residual, double eps) {
+  (void)check_fp8(out, scale, input, weight, residual);
+  (void)eps;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(hp_rms_norm, m) {
@@ -172,6 +212,8 @@ TORCH_LIBRARY(hp_rms_norm, m) {
   m.def("relu(Tensor(a!) out, Tensor input) -> ()");
   m.def("relu_max0(Tensor(a!) out, Tensor input) -> ()");
   m.def("rms_norm_plain(Tensor(a!) out, Tensor input, Tensor weight, float eps) -> ()");
+  m.def("rms_norm_fp8_quant(Tensor(a!) out, Tensor(b!) scale, Tensor input, Tensor weight, Tensor(c!) residual, "
+        "float eps) -> ()");
 }
 
 // ROCm builds of PyTorch expose HIP devices under the CUDA dispatch key.
@@ -180,6 +222,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
   m.impl("relu", &relu_hip);
   m.impl("relu_max0", &relu_max0_hip);
   m.impl("rms_norm_plain", &rms_norm_plain_hip);
+  m.impl("rms_norm_fp8_quant", &rms_norm_fp8_hip);
 }
 
 // Shape checks only, for fake tensors / torch.compile tracing.  Meta tensors
@@ -189,4 +232,5 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
   m.impl("relu", &stream_meta);
   m.impl("relu_max0", &stream_meta);
   m.impl("rms_norm_plain", &rms_norm_plain_meta);
+  m.impl("rms_norm_fp8_quant", &rms_norm_fp8_meta);
 }

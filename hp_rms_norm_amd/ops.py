@@ -3,7 +3,8 @@
 argument order, in-place semantics and ``None`` return."""
 import torch
 
-__all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm"]
+__all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "hp_rms_norm_fp8",
+           "fused_add_rms_norm_fp8"]
 
 
 def hp_rms_norm(input, weight, residual, eps):
@@ -42,3 +43,23 @@ def fused_add_rms_norm(input, residual, weight, eps):
     res = residual.clone()
     torch.ops.hp_rms_norm.rms_norm.default(out, weight, res, eps)
     return out, res
+
+
+def hp_rms_norm_fp8(output, scale, input, weight, residual, eps):
+    """Fused residual-add + RMSNorm with an FP8 output, dynamic per row:
+    ``residual <- input + residual`` in place; with ``y`` the op's 16-bit
+    output, ``scale[r] = max(amax|y[r]| / 448, FLT_MIN)`` and ``output[r] =
+    float8_e4m3fn(clamp(y[r] * (1 / scale[r]), -448, 448))``.  ``input`` is
+    only read.  ``output``: float8_e4m3fn, same shape as ``input``; ``scale``:
+    float32 with one element per row.  No reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(output, scale, input, weight, residual, eps)
+
+
+def fused_add_rms_norm_fp8(input, residual, weight, eps):
+    """Allocating form of ``hp_rms_norm_fp8``: returns ``(q, scale)`` with
+    ``q`` float8_e4m3fn shaped like ``input`` and ``scale`` float32 of shape
+    ``input.shape[:-1] + (1,)``; ``residual`` is updated in place."""
+    q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
+    scale = torch.empty(input.shape[:-1] + (1,), dtype=torch.float32, device=input.device)
+    torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(q, scale, input, weight, residual, eps)
+    return q, scale

@@ -88,6 +88,25 @@ int hprms_rmsnorm(void* out, const void* in, const void* weight,
                   int dtype, double eps, hipStream_t stream);
 
 /*
+ * Fused residual-add + RMSNorm with an FP8 (OCP e4m3fn) output and one scale
+ * per row (dynamic per-token quantisation of the op's 16-bit output y):
+ *   residual[r, :] <- rne16(f32(input) + f32(residual))        (in place)
+ *   y              =  the 16-bit output of hprms_fused_add_rmsnorm
+ *   scale[r]       =  max(max_j |y[r, j]| / 448, FLT_MIN)      (float32)
+ *   out[r, :]      =  e4m3fn(clamp(y / scale[r] computed as y * (1 / scale[r]), -448, 448))
+ * `input` is only read; `out` is [rows, hidden] bytes with its own row stride
+ * (in bytes).  A row containing NaN gets a NaN scale and NaN outputs.  No
+ * counterpart in the reference: it is the fused op followed by the
+ * quantisation step that feeds an FP8 GEMM, with one write of H bytes
+ * instead of 2H.  Fast tiers additionally need out 8-byte aligned and
+ * out_row_stride % 8 == 0.
+ */
+int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, const void* weight,
+                                void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                                int64_t input_row_stride, int64_t residual_row_stride,
+                                int dtype, double eps, hipStream_t stream);
+
+/*
  * Kernel configuration of the fused add+RMSNorm family.  Used by the tuning
  * sweep and by tests that exercise every tier at every shape; normal callers
  * use hprms_fused_add_rmsnorm(), which picks the configuration from the
@@ -118,7 +137,7 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, hprms_config* config);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
- * mode: 0 fused add+RMSNorm, 1 plain RMSNorm).  Writes up to `capacity`
+ * mode: 0 fused add+RMSNorm, 1 plain RMSNorm, 2 fused with FP8 output).  Writes up to `capacity`
  * entries to `out` (may be NULL when capacity is 0) and returns how many
  * exist, or a negative status.  Touches no device. */
 int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity);

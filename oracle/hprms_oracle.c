@@ -26,14 +26,21 @@
  * The 16-bit conversions below are written from the IEEE 754 definitions
  * (bfloat16 = the top half of a binary32; binary16 with subnormals).
  *
+ * With the FP8 output (hprms_oracle_fused_add_rmsnorm_fp8) the 16-bit output
+ * y is quantised per row: scale = max(amax|y| / 448, FLT_MIN),
+ * q = e4m3fn(clamp(y * (1 / scale), +-448)); this is the composition of the op
+ * with per-token dynamic FP8 quantisation as torch evaluates it.
+ *
  * Parity pins (tests/test_oracle.py): golden vectors made by the reference's
  * own formula in torch (tests/golden/), the live torch formula, a binary64
  * brute force, closed forms (constant rows, power-of-two scaling), numpy's
  * binary16 conversion, and planted mistakes (the `mutation` argument) that
  * each pin must reject.
  */
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -237,6 +244,97 @@ int hprms_oracle_max_threads(void) {
 #else
   return 1;
 #endif
+}
+
+/* ---- FP8 (OCP e4m3fn) quantised output ---------------------------------------- */
+
+/* Round-to-nearest-even of a binary32 to OCP FP8 e4m3fn (bias 7, 3 mantissa
+ * bits, subnormals m * 2^-9, no infinities, 0x7F / 0xFF = NaN, max 448).  Not
+ * saturating: magnitudes that round past 448 become NaN, as torch's
+ * float8_e4m3fn conversion does; callers clamp first. */
+uint8_t hprms_oracle_f32_to_e4m3(float f) {
+  uint32_t u = f2u(f);
+  uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x43E80000u) return sign | 0x7F;          /* NaN, inf, or rounds past 448 */
+  if (a >= 0x3C800000u) {                           /* normal result, |f| >= 2^-6 */
+    uint32_t t = a - 0x3C000000u;                   /* rebias 127 -> 7 */
+    t += 0x7FFFFu + ((t >> 20) & 1u);
+    return sign | (uint8_t)(t >> 20);
+  }
+  if (a <= 0x3A800000u) return sign;                /* |f| <= 2^-10 rounds to 0 */
+  uint32_t e = a >> 23;                             /* subnormal: round(|f| / 2^-9) */
+  uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+  uint32_t shift = 141u - e;                        /* 21 .. 24 */
+  uint32_t q = mant >> shift;
+  uint32_t rem = mant & ((1u << shift) - 1u);
+  uint32_t half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (q & 1u))) q += 1u;
+  return sign | (uint8_t)q;
+}
+
+float hprms_oracle_e4m3_to_f32(uint8_t h) {
+  float sgn = (h & 0x80) ? -1.0f : 1.0f;
+  uint32_t e = (h >> 3) & 0xFu, m = h & 7u;
+  if (e == 0xF && m == 7) return sgn * NAN;
+  if (e == 0) return sgn * (float)m * 0.001953125f;            /* m * 2^-9 */
+  return sgn * ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
+}
+
+/* Fused residual-add + RMSNorm with a per-row FP8 output (the op's 16-bit
+ * output y, then dynamic per-token quantisation):
+ *   residual <- rne16(x + r)                      (in place; input untouched)
+ *   y        = the 16-bit output of the fused op  (as above)
+ *   amax     = max |y| over the row               (NaN if any y is NaN)
+ *   scale    = max(amax / 448, FLT_MIN)           -> scale[row]
+ *   q        = e4m3fn(clamp(y * (1 / scale), -448, 448)) -> q[row, :]
+ * q has its own row stride in bytes (elements). */
+int hprms_oracle_fused_add_rmsnorm_fp8(uint8_t* q, float* scale, const uint16_t* input,
+                                       const uint16_t* weight, uint16_t* residual,
+                                       int64_t rows, int64_t hidden, int64_t q_row_stride,
+                                       int64_t input_row_stride, int64_t residual_row_stride,
+                                       int dtype, double eps, int threads) {
+  if (!check_rows(rows, hidden, input_row_stride, residual_row_stride) || q_row_stride < hidden) return -22;
+  if (dtype != ORACLE_BF16 && dtype != ORACLE_FP16) return -22;
+  if (rows == 0) return 0;
+  if (!q || !scale || !input || !weight || !residual) return -22;
+  float epsf = (float)eps;
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+  for (int64_t i = 0; i < rows; ++i) {
+    const uint16_t* xr = input + i * input_row_stride;
+    uint16_t* rr = residual + i * residual_row_stride;
+    uint8_t* qr = q + i * q_row_stride;
+    uint16_t* y = (uint16_t*)malloc((size_t)hidden * sizeof(uint16_t));
+    if (!y) continue;
+    for (int64_t j = 0; j < hidden; ++j) y[j] = xr[j];
+    fused_row(y, weight, rr, hidden, dtype, epsf, MUT_NONE);
+    float amax = 0.0f;
+    int nan = 0;
+    for (int64_t j = 0; j < hidden; ++j) {
+      float v = fabsf(to_f32(y[j], dtype));
+      if (v != v) nan = 1;
+      else if (v > amax) amax = v;
+    }
+    float sc = nan ? NAN : amax / 448.0f;
+    if (sc < FLT_MIN) sc = FLT_MIN;                 /* NaN compares false and stays */
+    float inv = 1.0f / sc;
+    scale[i] = sc;
+    for (int64_t j = 0; j < hidden; ++j) {
+      float v = to_f32(y[j], dtype) * inv;
+      v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
+      qr[j] = hprms_oracle_f32_to_e4m3(v);
+    }
+    free(y);
+  }
+  (void)threads;
+  return 0;
+}
+
+void hprms_oracle_e4m3_from_f32(const float* src, uint8_t* dst, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = hprms_oracle_f32_to_e4m3(src[i]);
 }
 
 /* Array forms of the conversions, for the conversion pins. */

@@ -59,6 +59,10 @@ def lib():
         L.hprms_oracle_from_f32.argtypes = [_f32p, _u16p, _i64, ctypes.c_int]
         L.hprms_oracle_to_f32.argtypes = [_u16p, _f32p, _i64, ctypes.c_int]
         L.hprms_oracle_max_threads.restype = ctypes.c_int
+        _u8p = ctypes.POINTER(ctypes.c_uint8)
+        L.hprms_oracle_fused_add_rmsnorm_fp8.argtypes = [_u8p, _f32p, _u16p, _u16p, _u16p, _i64, _i64, _i64,
+                                                         _i64, _i64, ctypes.c_int, ctypes.c_double, ctypes.c_int]
+        L.hprms_oracle_e4m3_from_f32.argtypes = [_f32p, _u8p, _i64]
         _lib = L
     return _lib
 
@@ -152,3 +156,42 @@ def ulp_distance(a, b, dtype):
     d = np.where(na & nb, 0, d)
     d = np.where(na ^ nb, 1 << 20, d)
     return d
+
+
+def fused_add_rmsnorm_fp8(x, w, r, eps, dtype, threads=1):
+    """FP8 form: returns (q uint8 [rows, hidden] of e4m3fn bits, scale float32
+    [rows], new residual); x is not modified."""
+    xc = np.ascontiguousarray(x)
+    rows, hidden, sx = _rows(xc)
+    ro = np.array(r, dtype=np.uint16, copy=True, order="C")
+    q = np.empty((rows, hidden), dtype=np.uint8)
+    sc = np.empty(rows, dtype=np.float32)
+    rc = lib().hprms_oracle_fused_add_rmsnorm_fp8(
+        q.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), sc.ctypes.data_as(_f32p), _p16(xc),
+        _p16(np.ascontiguousarray(w)), _p16(ro), rows, hidden, hidden, sx, hidden, dtype, float(eps), threads)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+    return q, sc, ro
+
+
+def e4m3_from_f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint8)
+    lib().hprms_oracle_e4m3_from_f32(a.ctypes.data_as(_f32p), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
+                                     a.size)
+    return out
+
+
+def e4m3_ulp_distance(a, b):
+    """Distance between FP8 e4m3fn bit patterns on the ordered line; NaN pairs 0."""
+    a = np.asarray(a, dtype=np.uint8).astype(np.int32)
+    b = np.asarray(b, dtype=np.uint8).astype(np.int32)
+
+    def ordered(v):
+        mag = v & 0x7F
+        return np.where(v & 0x80, -mag, mag)
+
+    na, nb = (a & 0x7F) == 0x7F, (b & 0x7F) == 0x7F
+    d = np.abs(ordered(a) - ordered(b))
+    d = np.where(na & nb, 0, d)
+    return np.where(na ^ nb, 1 << 20, d)

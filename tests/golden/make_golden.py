@@ -63,6 +63,28 @@ def sp_constant_rows(x, r, w):
         x[i].fill_(2.0 ** (i - 3) * (-1) ** i)
 
 
+def fp8_case(name, rows, hidden, dtype, eps, seed, special=None):
+    """The fused op's output quantised per row to float8_e4m3fn, as torch
+    evaluates it: scale = max(amax|y| / 448, FLT_MIN); q = e4m3fn(clamp(y *
+    (1 / scale), -448, 448)).  Input x is not modified by the FP8 variant."""
+    name, meta, arrs = fused_case(name, rows, hidden, dtype, eps, "bench", seed, special)
+    y = torch.from_numpy(arrs["out"].view(np.int16)).view(dtype)
+    yf = y.float()
+    amax = yf.abs().amax(-1, keepdim=True)
+    scale = torch.clamp(amax / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (yf * (1.0 / scale)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    meta["kind"] = "fp8"
+    arrs["q"] = q.view(torch.uint8).numpy().copy()
+    arrs["scale"] = scale.reshape(-1).numpy().copy()
+    return name, meta, arrs
+
+
+def sp_fp8_rows(x, r, w):
+    x[0].zero_(); r[0].zero_()             # all-zero row: scale = FLT_MIN, q = 0
+    x[1, 3] = float("nan")                 # NaN row: NaN scale, NaN outputs
+    x[2] *= 1e-3; r[2] *= 1e-3             # small row: same q as a scaled row
+
+
 def stream_case(name, rows, hidden, dtype, seed):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn((rows, hidden), generator=g).to(dtype)
@@ -88,6 +110,9 @@ def main():
         fused_case("bf16_4x256_special", 4, 256, bf, 1e-6, "bench", 10, sp_zero_and_huge),
         fused_case("fp16_2x256_special", 2, 256, hf, 1e-6, "bench", 11, sp_fp16_overflow),
         fused_case("bf16_6x512_constant_eps0", 6, 512, bf, 0.0, "bench", 12, sp_constant_rows),
+        fp8_case("fp8_bf16_4x4096", 4, 4096, bf, 1e-6, 15),
+        fp8_case("fp8_fp16_3x5120", 3, 5120, hf, 1e-6, 16),
+        fp8_case("fp8_bf16_4x1000_tail", 4, 1000, bf, 1e-6, 17, sp_fp8_rows),
         stream_case("stream_bf16_3x384", 3, 384, bf, 13),
         stream_case("stream_fp16_2x1000", 2, 1000, hf, 14),
     ]

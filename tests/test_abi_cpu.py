@@ -119,6 +119,8 @@ def test_table_covers_every_hidden_with_a_built_kernel():
             assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
             rc = L.hprms_rmsnorm(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6, None)
             assert rc == abi.HPRMS_OK
+            rc = L.hprms_fused_add_rmsnorm_fp8(0, 0, 0, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
+            assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
 
 
 def test_config_entry_rejects_unbuilt_and_misfit_configs():
@@ -145,3 +147,17 @@ def test_every_built_config_is_well_formed():
                 assert c.tier == (2 if c.lds_vec_per_lane else 1)
                 # LDS spill of a workgroup fits the 160 KiB of a gfx950 CU
                 assert c.lds_vec_per_lane * c.block_threads * 16 <= 160 * 1024
+
+
+def test_fp8_entry_rejects_bad_arguments():
+    L = abi.lib()
+    ok = dict(out=0x4000, scale=0x5000, x=0x1000, w=0x2000, r=0x3000, so=4096)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.hprms_fused_add_rmsnorm_fp8(a["out"], a["scale"], a["x"], a["w"], a["r"], 4, 4096, a["so"],
+                                             4096, 4096, 0, 1e-6, None)
+    assert call(scale=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
+    assert call(out=0) == abi.HPRMS_E_INVALID
+    assert call(so=100) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
+    assert call(r=0x1000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()

@@ -100,3 +100,21 @@ def test_fake_tensor_tracing_sees_the_mutation():
         ops.hp_rms_norm(x, w, r, 1e-6)
     schema = torch.ops.hp_rms_norm.rms_norm.default._schema
     assert [a.alias_info.is_write if a.alias_info else False for a in schema.arguments] == [True, False, True, False]
+
+
+def test_fp8_op_schema_and_meta_checks():
+    s = str(torch.ops.hp_rms_norm.rms_norm_fp8_quant.default._schema)
+    assert s == ("hp_rms_norm::rms_norm_fp8_quant(Tensor(a!) out, Tensor(b!) scale, Tensor input, Tensor weight, "
+                 "Tensor(c!) residual, float eps) -> ()")
+    x, w, r = t(4, 256), t(256), t(4, 256)
+    q = t(4, 256, dtype=torch.float8_e4m3fn)
+    sc = torch.empty(4, 1, device=M)
+    assert ops.hp_rms_norm_fp8(q, sc, x, w, r, 1e-6) is None
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        ops.hp_rms_norm_fp8(t(4, 256), sc, x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="float32"):
+        ops.hp_rms_norm_fp8(q, torch.empty(4, 1, device=M, dtype=torch.float16), x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="number of rows"):
+        ops.hp_rms_norm_fp8(q, torch.empty(3, device=M), x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match=r"input.size\(-1\) == hidden_dim"):
+        ops.hp_rms_norm_fp8(q, sc, x, t(128), r, 1e-6)

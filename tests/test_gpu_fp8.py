@@ -1,0 +1,136 @@
+"""GPU parity of the fused add+RMSNorm with FP8 (OCP e4m3fn) per-row output.
+
+Pins: the residual is bit-exact against the oracle; q and scale equal, bit
+for bit, torch's quantisation of the 16-bit output the same kernel family
+produces for the same inputs (the bf16 op run on a copy); against the CPU
+oracle q is within one FP8 step (rows whose 16-bit output matches the
+oracle's bit-for-bit are exact) and scale within one 16-bit ulp of amax.
+`input` is not modified.  NaN encodings differ (hardware 0xFF, torch 0x7F):
+NaN compares equal to NaN here.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, assert_residual_exact, bits, from_bits, make_inputs
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    assert torch.cuda.is_available(), "the gpu tests need a HIP device"
+    import hp_rms_norm_amd
+    return hp_rms_norm_amd
+
+
+def torch_quantise(y):
+    yf = y.float()
+    scale = torch.clamp(yf.abs().amax(-1, keepdim=True) / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (yf * (1.0 / scale)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, scale
+
+
+def q_bits(q):
+    return q.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6):
+    x, r, w = make_inputs(rows, hidden, dtype, seed, dist)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    q, sc = ops.fused_add_rms_norm_fp8(xd, rd, wd, eps)
+    # the same inputs through the 16-bit op
+    y, r16 = ops.fused_add_rms_norm(x.to(DEV), r.to(DEV), wd, eps)
+    torch.cuda.synchronize()
+    tag = f"{rows}x{hidden} {dtype} seed {seed}"
+    assert torch.equal(xd.cpu().view(torch.int16), x.view(torch.int16)), "input modified " + tag
+    assert torch.equal(rd.view(torch.int16), r16.view(torch.int16)), "residual differs from the 16-bit op " + tag
+    tq, tsc = torch_quantise(y)
+    assert torch.equal(sc.reshape(-1).view(torch.int32), tsc.reshape(-1).view(torch.int32)) or \
+        torch.allclose(sc.reshape(-1), tsc.reshape(-1), rtol=0, atol=0, equal_nan=True), "scale " + tag
+    d = oracle.e4m3_ulp_distance(q_bits(q), q_bits(tq))
+    assert d.max() == 0, f"q differs from torch's quantisation of y: {tag}"
+    # against the CPU oracle
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8(bits(x), bits(w), bits(r), eps, DT[dtype],
+                                                 threads=min(16, oracle.max_threads()))
+    assert_residual_exact(bits(rd), ores, dtype, "residual " + tag)
+    do = oracle.e4m3_ulp_distance(q_bits(q).reshape(oq.shape), oq)
+    assert do.max() <= 1, tag
+    np.testing.assert_allclose(sc.reshape(-1).cpu().numpy(), osc, rtol=2.0 ** -7, equal_nan=True)
+    return q, sc
+
+
+def test_fp8_golden_through_torch_op(ops, golden):
+    for name, c in golden.items():
+        if c["kind"] != "fp8":
+            continue
+        dtype = torch.bfloat16 if c["dtype"] == "bf16" else torch.float16
+        x, r, w = (from_bits(c[k], dtype).to(DEV) for k in ("x", "r", "w"))
+        q, sc = ops.fused_add_rms_norm_fp8(x, r, w, c["eps"])
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(r), c["res"], dtype, name)
+        d = oracle.e4m3_ulp_distance(q_bits(q), c["q"])
+        assert d.max() <= 1 and (d != 0).mean() < 1e-3, name
+        np.testing.assert_allclose(sc.reshape(-1).cpu().numpy(), c["scale"], rtol=2.0 ** -7, equal_nan=True)
+
+
+@pytest.mark.parametrize("rows,hidden,dtype", [
+    (4096, 4096, torch.bfloat16), (4096, 8192, torch.bfloat16), (4096, 16384, torch.bfloat16),
+    (4096, 32768, torch.bfloat16), (4096, 5120, torch.float16), (4096, 7168, torch.float16),
+    (1, 4096, torch.bfloat16), (32, 8192, torch.bfloat16), (512, 4096, torch.bfloat16)],
+    ids=lambda v: str(v).replace("torch.", ""))
+def test_fp8_baseline_shapes(ops, rows, hidden, dtype):
+    print("fp8 case", rows, hidden, dtype, flush=True)
+    run_case(ops, rows, hidden, dtype, seed=rows + hidden, dist="outliers" if rows <= 512 else "bench")
+
+
+def test_fp8_every_table_entry(ops):
+    """H at every breakpoint of the table (and one below), with 300 rows (the
+    bandwidth rows) and 7 rows (the latency rows)."""
+    for hidden in (128, 256, 512, 1024, 2048, 3072, 4096, 8192, 12288, 16384, 24576, 32768, 65536, 520, 4088):
+        for rows in (300, 7):
+            print("fp8 table", rows, hidden, flush=True)
+            run_case(ops, rows, hidden, torch.bfloat16, seed=hidden + rows)
+
+
+@pytest.mark.parametrize("hidden", [1, 13, 1000, 4097])
+def test_fp8_general_kernel(ops, hidden):
+    run_case(ops, 37, hidden, torch.bfloat16, seed=hidden)
+    run_case(ops, 5, hidden, torch.float16, seed=hidden + 1)
+
+
+def test_fp8_strided_misaligned_output_and_special_rows(ops):
+    from hp_rms_norm_amd import abi
+    rows, hidden, eps, dtype = 40, 2048, 1e-6, torch.bfloat16
+    x, r, w = make_inputs(rows, hidden, dtype, 77)
+    x[0].zero_()
+    r[0].zero_()
+    x[1, 5] = float("nan")
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8(bits(x), bits(w), bits(r), eps, oracle.BF16)
+    assert osc[0] == np.finfo(np.float32).tiny and np.isnan(osc[1])
+    for offset, pad in ((0, 64), (1, 3)):
+        xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+        buf = torch.zeros(rows, hidden + pad + offset, dtype=torch.uint8, device=DEV)
+        qv = buf[:, offset:offset + hidden]
+        sc = torch.full((rows,), 7.0, device=DEV)
+        abi.fused_add_rmsnorm_fp8(qv.data_ptr(), sc.data_ptr(), xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows,
+                                  hidden, qv.stride(0), hidden, hidden, abi.DTYPE_BF16, eps,
+                                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(rd), ores, dtype)
+        assert oracle.e4m3_ulp_distance(qv.cpu().numpy(), oq).max() <= 1
+        np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7, equal_nan=True)
+        assert not buf[:, :offset].any() and not buf[:, offset + hidden:].any()
+        assert not qv[0].any()                                   # zero row -> zero codes
+        assert ((qv[1].cpu().numpy() & 0x7F) == 0x7F).all()       # NaN row -> NaN codes
+
+
+def test_fp8_bytes_move_less(ops):
+    """FP8 output: the op writes H bytes per row instead of 2H, and still
+    updates the residual; checks the written sizes through the returned tensors."""
+    x, r, w = (t.to(DEV) for t in make_inputs(8, 4096, torch.bfloat16, 3))
+    q, sc = ops.fused_add_rms_norm_fp8(x, r, w, 1e-6)
+    assert q.dtype == torch.float8_e4m3fn and q.shape == x.shape and q.element_size() == 1
+    assert sc.shape == (8, 1) and sc.dtype == torch.float32

@@ -247,3 +247,72 @@ def test_oracle_rejects_bad_arguments():
     x = np.zeros((2, 8), np.uint16)
     with pytest.raises(ValueError):
         oracle.fused_add_rmsnorm(x, np.zeros(8, np.uint16), x, 1e-6, 7)
+
+
+# ---- FP8 (e4m3fn) output --------------------------------------------------------------------
+def torch_quantise(y_bits, code):
+    """Per-row dynamic quantisation of a 16-bit output as torch evaluates it."""
+    y = tfrom(y_bits, code).float()
+    scale = torch.clamp(y.abs().amax(-1, keepdim=True) / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (y * (1.0 / scale)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).numpy(), scale.reshape(-1).numpy()
+
+
+def test_e4m3_conversion_matches_torch():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    pts = np.unique(codes[np.isfinite(codes)])
+    mids = ((pts[:-1].astype(np.float64) + pts[1:]) / 2).astype(np.float32)
+    u = np.concatenate([pts.astype(np.float32), mids]).view(np.uint32).astype(np.int64)
+    near = np.concatenate([u + k for k in range(-3, 4)])
+    near = near[(near >= 0) & (near < 2 ** 32)].astype(np.uint32).view(np.float32)
+    rng = np.random.default_rng(2)
+    vals = np.concatenate([near, rng.uniform(-600, 600, 2_000_000).astype(np.float32),
+                           (rng.standard_normal(1_000_000) * 1e-2).astype(np.float32),
+                           np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 464.0, 480.0], np.float32)])
+    got = oracle.e4m3_from_f32(vals)
+    want = torch.from_numpy(vals).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+
+
+def test_oracle_fp8_quantisation_stage_matches_torch():
+    """The oracle's q and scale equal torch's quantisation of the oracle's own
+    16-bit output (so the FP8 stage is pinned independently of y)."""
+    cases = [(64, 4096, BF, "bench"), (32, 5120, HF, "bench"), (16, 1000, BF, "reference_test"), (8, 13, HF, "bench")]
+    for i, (rows, hidden, code, dist) in enumerate(cases):
+        x, r, w = seeded(rows, hidden, code, 300 + i, dist)
+        x[0, :] = 0
+        r[0, :] = 0                                  # zero row
+        y, res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, code)
+        q, sc, res8 = oracle.fused_add_rmsnorm_fp8(x, w, r, 1e-6, code)
+        assert np.array_equal(res8, res)
+        tq, tsc = torch_quantise(y, code)
+        assert np.array_equal(sc, tsc)
+        assert oracle.e4m3_ulp_distance(q, tq).max() == 0
+
+
+def test_oracle_fp8_matches_golden(golden):
+    for name, c in golden.items():
+        if c["kind"] != "fp8":
+            continue
+        code = BF if c["dtype"] == "bf16" else HF
+        q, sc, res = oracle.fused_add_rmsnorm_fp8(c["x"], c["w"], c["r"], c["eps"], code)
+        assert oracle.ulp_distance(res, c["res"], code).max() == 0, name
+        y, _ = oracle.fused_add_rmsnorm(c["x"], c["w"], c["r"], c["eps"], code)
+        same = np.all(oracle.ulp_distance(y, c["out"], code) == 0, axis=1)
+        assert same.mean() >= 0.5, name
+        d = oracle.e4m3_ulp_distance(q, c["q"])
+        assert d[same].max(initial=0) == 0, name          # rows whose y matches: bit-exact
+        assert np.array_equal(sc[same], c["scale"][same], equal_nan=True), name
+        assert d.max() <= 1, name                          # elsewhere within one FP8 step
+
+
+def test_planted_fp8_mistake_is_rejected():
+    """Quantising with a scale of amax / 240 (the e4m3fnuz maximum) instead of
+    448 fails the torch pin of the quantisation stage."""
+    x, r, w = seeded(16, 512, BF, 9)
+    y, _ = oracle.fused_add_rmsnorm(x, w, r, 1e-6, BF)
+    tq, tsc = torch_quantise(y, BF)
+    yf = oracle.to_f32(y, BF)
+    bad_scale = np.maximum(np.abs(yf).max(-1) / np.float32(240.0), np.finfo(np.float32).tiny).astype(np.float32)
+    bad_q = oracle.e4m3_from_f32(np.clip(yf * (np.float32(1.0) / bad_scale)[:, None], -448, 448))
+    assert not np.array_equal(bad_scale, tsc) and oracle.e4m3_ulp_distance(bad_q, tq).max() > 0
