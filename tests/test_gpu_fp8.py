@@ -27,7 +27,9 @@ def ops():
 
 
 def torch_quantise(y):
-    yf = y.float()
+    # on the CPU: ATen's HIP kernels turn division by a scalar into a
+    # multiplication by its reciprocal, the CPU path divides
+    yf = y.detach().cpu().float()
     scale = torch.clamp(yf.abs().amax(-1, keepdim=True) / 448.0, min=torch.finfo(torch.float32).tiny)
     q = (yf * (1.0 / scale)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
     return q, scale
@@ -48,8 +50,9 @@ def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6):
     assert torch.equal(xd.cpu().view(torch.int16), x.view(torch.int16)), "input modified " + tag
     assert torch.equal(rd.view(torch.int16), r16.view(torch.int16)), "residual differs from the 16-bit op " + tag
     tq, tsc = torch_quantise(y)
-    assert torch.equal(sc.reshape(-1).view(torch.int32), tsc.reshape(-1).view(torch.int32)) or \
-        torch.allclose(sc.reshape(-1), tsc.reshape(-1), rtol=0, atol=0, equal_nan=True), "scale " + tag
+    sc_c, tsc_c = sc.reshape(-1).cpu(), tsc.reshape(-1)
+    assert torch.equal(sc_c.view(torch.int32), tsc_c.view(torch.int32)) or \
+        torch.allclose(sc_c, tsc_c, rtol=0, atol=0, equal_nan=True), "scale " + tag
     d = oracle.e4m3_ulp_distance(q_bits(q), q_bits(tq))
     assert d.max() == 0, f"q differs from torch's quantisation of y: {tag}"
     # against the CPU oracle
