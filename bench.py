@@ -365,6 +365,32 @@ def run_extra(torch, ops, args):
     us = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
     out["fp16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2),
                     "gbs": round(fused_bytes(b, h) / (u * 1e-6) / 1e9, 1)} for (b, h, _, _), u in zip(f16, us)]
+    # fused add+RMSNorm with FP8 output (reads x, r, w; writes r and H bytes + a scale per row)
+    fp8 = []
+    for h in (4096, 8192, 16384, 32768):
+        n = cold_sets(B, h)
+        sets = [make_set(torch, B, h, torch.bfloat16, 7000 + i, "cuda:0") for i in range(n)]
+        w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+        qs = [torch.empty(B, h, dtype=torch.float8_e4m3fn, device="cuda:0") for _ in range(n)]
+        sc = torch.empty(B, 1, dtype=torch.float32, device="cuda:0")
+        for i in range(args.warmup):
+            ops.hp_rms_norm_fp8(qs[i % n], sc, sets[i % n][0], w, sets[i % n][1], EPS)
+        ncalls = max(steps, n)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        prefill(torch, 10)
+        e0.record()
+        for i in range(ncalls):
+            ops.hp_rms_norm_fp8(qs[i % n], sc, sets[i % n][0], w, sets[i % n][1], EPS)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / ncalls
+        nbytes = 7 * B * h + 2 * h + 4 * B
+        fp8.append({"rows": B, "hidden": h, "us_per_call": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "bytes_per_call": nbytes})
+        del sets, qs
+        torch.cuda.empty_cache()
+    out["fp8_output_bf16"] = fp8
     # streamer (the reference "relu" = copy, and the true ReLU) at (4096, 14336)
     rows, h = B, 14336
     res = []
