@@ -70,7 +70,7 @@ def lib():
         L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
         L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
         L.hprms_streamer.argtypes = [vp, vp, i64, i64, i64, i64, ci, ci, vp]
-        L.hprms_select_config.argtypes = [i64, i64, ci, ctypes.POINTER(Config)]
+        L.hprms_select_config.argtypes = [i64, i64, ci, ci, ctypes.POINTER(Config)]
         L.hprms_kernel_configs.argtypes = [ci, ci, ctypes.POINTER(Config), ci]
         L.hprms_last_error.restype = ctypes.c_char_p
         L.hprms_last_error.argtypes = []
@@ -120,9 +120,10 @@ def streamer(out_ptr, in_ptr, rows, hidden, out_stride, in_stride, dtype, op, st
                                        stream))
 
 
-def select_config(rows, hidden, dtype):
+def select_config(rows, hidden, dtype, mode=0):
+    """The table's configuration; mode 0 fused, 1 plain RMSNorm, 2 FP8 output."""
     c = Config()
-    _check(lib().hprms_select_config(rows, hidden, dtype, ctypes.byref(c)))
+    _check(lib().hprms_select_config(rows, hidden, dtype, mode, ctypes.byref(c)))
     return c
 
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 1
+#define HPRMS_ABI_VERSION 2
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -131,10 +131,12 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
                                    int dtype, double eps, const hprms_config* config,
                                    hipStream_t stream);
 
-/* The configuration hprms_fused_add_rmsnorm() would use for (rows, hidden,
- * dtype), written to *config (tier 3 when only the general kernel fits
- * hidden).  Pure function of its arguments; touches no device. */
-int hprms_select_config(int64_t rows, int64_t hidden, int dtype, hprms_config* config);
+/* The configuration the library would use for (rows, hidden, dtype) and
+ * `mode` (0: hprms_fused_add_rmsnorm, 1: hprms_rmsnorm, 2:
+ * hprms_fused_add_rmsnorm_fp8), written to *config (tier 3 when only the
+ * general kernel fits hidden).  Pure function of its arguments; touches no
+ * device. */
+int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
  * mode: 0 fused add+RMSNorm, 1 plain RMSNorm, 2 fused with FP8 output).  Writes up to `capacity`

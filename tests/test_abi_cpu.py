@@ -121,6 +121,13 @@ def test_table_covers_every_hidden_with_a_built_kernel():
             assert rc == abi.HPRMS_OK
             rc = L.hprms_fused_add_rmsnorm_fp8(0, 0, 0, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
             assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
+            # the FP8 table's choice also exists as a fused (mode 0) kernel, so the
+            # 16-bit op can be run with the same lane mapping
+            c8 = abi.select_config(rows, hidden, dtype, 2)
+            assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
+            rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
+                                                  ctypes.byref(c8), None)
+            assert rc == abi.HPRMS_OK, (hidden, c8.as_tuple(), abi.last_error())
 
 
 def test_config_entry_rejects_unbuilt_and_misfit_configs():
