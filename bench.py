@@ -223,6 +223,8 @@ def main():
                          "(the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--profile-config", default="",
                     help="with --profile: force lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags")
+    ap.add_argument("--profile-op", default="fused", choices=("fused", "fp8"),
+                    help="with --profile: the 16-bit fused op or its FP8-output form")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the op has no cross-GPU step (rows are independent), and this "
@@ -328,6 +330,13 @@ def profile_driver(torch, abi, op, args):
         def op(x, w, r, eps):  # noqa: F811  (the forced configuration, through the C ABI)
             abi.fused_add_rmsnorm(x.data_ptr(), w.data_ptr(), r.data_ptr(), x.shape[0], x.shape[1],
                                   x.stride(0), r.stride(0), abi.DTYPE_BF16, eps, stream, cfg)
+    if args.profile_op == "fp8":
+        import hp_rms_norm_amd
+        q = torch.empty(B, hidden, dtype=torch.float8_e4m3fn, device="cuda:0")
+        sc = torch.empty(B, 1, dtype=torch.float32, device="cuda:0")
+
+        def op(x, w, r, eps):  # noqa: F811  (FP8 output; the input row is only read)
+            hp_rms_norm_amd.hp_rms_norm_fp8(q, sc, x, w, r, eps)
     us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup)[0]
     n = 1 << 29
     src = torch.empty(n, dtype=torch.bfloat16, device="cuda:0").normal_()

@@ -275,6 +275,44 @@ def test_runs_on_current_stream(abi):
     assert_output_close(bits(xd), want_out, torch.bfloat16)
 
 
+def test_concurrent_threads_and_streams(abi):
+    """Four host threads, each on its own stream with its own tensors, call
+    the op repeatedly; every result matches the oracle."""
+    import threading
+
+    import hp_rms_norm_amd
+    shapes = [(300, 4096), (17, 8192), (1000, 1024), (64, 32768)]
+    data = []
+    for i, (rows, hidden) in enumerate(shapes):
+        x, r, w = make_inputs(rows, hidden, torch.bfloat16, 600 + i)
+        data.append((x, r, w, oracle_fused(x, r, w, 1e-6, torch.bfloat16)))
+    results, errors = {}, []
+
+    def worker(i):
+        try:
+            x, r, w, _ = data[i]
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(5):
+                    xd, rd, wd = x.to(DEV, non_blocking=False), r.to(DEV), w.to(DEV)
+                    hp_rms_norm_amd.hp_rms_norm(xd, wd, rd, 1e-6)
+            s.synchronize()
+            results[i] = (bits(xd), bits(rd))
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(shapes))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(len(shapes)):
+        want_out, want_res = data[i][3]
+        assert_residual_exact(results[i][1], want_res, torch.bfloat16)
+        assert_output_close(results[i][0], want_out, torch.bfloat16)
+
+
 def test_hip_graph_capture_and_replay(abi):
     """The op allocates nothing and issues no memset, so it can be captured;
     each replay (fresh inputs copied in between, with eager work and syncs
