@@ -23,7 +23,9 @@
 // FLAGS bit 0 marks the row loads non-temporal, bit 1 the stores: the rows
 // are touched once, so they should not displace the weight from the caches.
 // Bits 3 and 4 add the sc1 (device-scope) policy bit to the loads and to the
-// stores respectively.
+// stores respectively.  The residual is stored as soon as it is formed:
+// deferring it to the output phase (one write burst per workgroup) measured
+// up to 5% slower.
 //
 // MODE 0 is the fused op (in place on input and residual); MODE 1 is the
 // plain RMSNorm (reads `input`, writes `out`, no residual stream); MODE 2 is
