@@ -318,6 +318,22 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def time_rotating(torch, call, n, steps, warmup):
+    """µs per call of call(i % n) over max(steps, n) back-to-back calls."""
+    for i in range(warmup):
+        call(i % n)
+    ncalls = max(steps, n)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    prefill(torch, 10)
+    e0.record()
+    for i in range(ncalls):
+        call(i % n)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / ncalls
+
+
 def profile_driver(torch, abi, op, args):
     """A short, fixed workload for rocprofv3 counter runs: `steps` cold calls
     of (4096, H) bf16, then `steps` copies of a 1 GiB bf16 tensor."""
@@ -400,6 +416,44 @@ def run_extra(torch, ops, args):
         del sets, qs
         torch.cuda.empty_cache()
     out["fp8_output_bf16"] = fp8
+    # out-of-place fused op (input and residual only read): the same 4 rows of bytes per row
+    oop = []
+    for h in (4096, 8192, 16384, 32768):
+        n = cold_sets(B, h, floor=2, span=1 << 30)
+        sets = [make_set(torch, B, h, torch.bfloat16, 8000 + i, "cuda:0") for i in range(n)]
+        outs = [(torch.empty_like(x), torch.empty_like(r)) for x, r in sets]
+        w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+
+        def call(i, sets=sets, outs=outs, w=w):
+            ops.fused_add_rms_norm_out(outs[i][0], outs[i][1], sets[i][0], w, sets[i][1], EPS)
+        us = time_rotating(torch, call, n, steps, args.warmup)
+        oop.append({"rows": B, "hidden": h, "us_per_call": round(us, 2),
+                    "gbs": round(fused_bytes(B, h) / (us * 1e-6) / 1e9, 1)})
+        del sets, outs
+        torch.cuda.empty_cache()
+    out["out_of_place_bf16"] = oop
+    # partial sums + fused op: P parts read, residual read and written, output written
+    red = []
+    h = 8192
+    for nparts in (2, 4, 8):
+        per_set = (nparts + 2) * B * h * 2
+        n = max(2, -(-(1 << 30) // per_set))
+        g = torch.Generator(device="cuda:0").manual_seed(nparts)
+        sets = [([torch.randn(B, h, device="cuda:0", generator=g).to(torch.bfloat16) for _ in range(nparts)],
+                 torch.randn(B, h, device="cuda:0", generator=g).to(torch.bfloat16),
+                 torch.empty(B, h, dtype=torch.bfloat16, device="cuda:0")) for _ in range(n)]
+        w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+
+        def call(i, sets=sets, w=w):
+            parts, r, o = sets[i]
+            ops.reduce_add_rms_norm(o, parts, w, r, EPS)
+        us = time_rotating(torch, call, n, steps, args.warmup)
+        nbytes = (nparts + 3) * B * h * 2 + 2 * h
+        red.append({"parts": nparts, "rows": B, "hidden": h, "us_per_call": round(us, 2),
+                    "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_call": nbytes})
+        del sets
+        torch.cuda.empty_cache()
+    out["reduce_parts_bf16"] = red
     # streamer (the reference "relu" = copy, and the true ReLU) at (4096, 14336)
     rows, h = B, 14336
     res = []

@@ -17,11 +17,16 @@ HPRMS_E_LAUNCH = -5
 HPRMS_E_RANGE = -34
 DTYPE_BF16, DTYPE_FP16 = 0, 1
 STREAM_COPY, STREAM_RELU = 0, 1
+MAX_PARTS = 8
+# the `mode` numbering of hprms_select_config / hprms_kernel_configs
+MODE_FUSED, MODE_PLAIN, MODE_FP8, MODE_OUT, MODE_REDUCE = 0, 1, 2, 3, 4
 
 # every symbol the header declares
 SYMBOLS = (
     "hprms_fused_add_rmsnorm",
     "hprms_fused_add_rmsnorm_fp8",
+    "hprms_fused_add_rmsnorm_out",
+    "hprms_reduce_add_rmsnorm",
     "hprms_streamer",
     "hprms_rmsnorm",
     "hprms_fused_add_rmsnorm_config",
@@ -69,6 +74,9 @@ def lib():
                                                      ctypes.POINTER(Config), vp]
         L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
         L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
+        L.hprms_fused_add_rmsnorm_out.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
+        L.hprms_reduce_add_rmsnorm.argtypes = [vp, ctypes.POINTER(vp), ci, vp, vp, i64, i64, i64, i64, i64, ci,
+                                               cd, vp]
         L.hprms_streamer.argtypes = [vp, vp, i64, i64, i64, i64, ci, ci, vp]
         L.hprms_select_config.argtypes = [i64, i64, ci, ci, ctypes.POINTER(Config)]
         L.hprms_kernel_configs.argtypes = [ci, ci, ctypes.POINTER(Config), ci]
@@ -76,7 +84,7 @@ def lib():
         L.hprms_last_error.argtypes = []
         L.hprms_abi_version.restype = ci
         for name in ("hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
-                     "hprms_fused_add_rmsnorm_fp8",
+                     "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_out", "hprms_reduce_add_rmsnorm",
                      "hprms_streamer", "hprms_select_config", "hprms_kernel_configs"):
             getattr(L, name).restype = ci
         _lib = L
@@ -110,6 +118,23 @@ def fused_add_rmsnorm_fp8(out_ptr, scale_ptr, input_ptr, weight_ptr, residual_pt
                                                     stream))
 
 
+def fused_add_rmsnorm_out(out_ptr, residual_out_ptr, input_ptr, residual_ptr, weight_ptr, rows, hidden,
+                          out_stride, residual_out_stride, input_stride, residual_stride, dtype, eps, stream=0):
+    return _check(lib().hprms_fused_add_rmsnorm_out(out_ptr, residual_out_ptr, input_ptr, residual_ptr, weight_ptr,
+                                                    rows, hidden, out_stride, residual_out_stride, input_stride,
+                                                    residual_stride, dtype, eps, stream))
+
+
+def reduce_add_rmsnorm(out_ptr, part_ptrs, weight_ptr, residual_ptr, rows, hidden, out_stride, part_stride,
+                       residual_stride, dtype, eps, stream=0):
+    """``part_ptrs``: a sequence of device pointers (1 ... MAX_PARTS); a
+    ``None`` sequence passes a null array."""
+    arr = None if part_ptrs is None else (ctypes.c_void_p * max(1, len(part_ptrs)))(*part_ptrs)
+    n = 0 if part_ptrs is None else len(part_ptrs)
+    return _check(lib().hprms_reduce_add_rmsnorm(out_ptr, arr, n, weight_ptr, residual_ptr, rows, hidden, out_stride,
+                                                 part_stride, residual_stride, dtype, eps, stream))
+
+
 def rmsnorm(out_ptr, in_ptr, weight_ptr, rows, hidden, out_stride, in_stride, dtype, eps, stream=0):
     return _check(lib().hprms_rmsnorm(out_ptr, in_ptr, weight_ptr, rows, hidden, out_stride, in_stride,
                                       dtype, eps, stream))
@@ -121,7 +146,7 @@ def streamer(out_ptr, in_ptr, rows, hidden, out_stride, in_stride, dtype, op, st
 
 
 def select_config(rows, hidden, dtype, mode=0):
-    """The table's configuration; mode 0 fused, 1 plain RMSNorm, 2 FP8 output."""
+    """The table's configuration for a MODE_* entry point."""
     c = Config()
     _check(lib().hprms_select_config(rows, hidden, dtype, mode, ctypes.byref(c)))
     return c

@@ -6,6 +6,8 @@
 //                               launch_rms_norm<T>()  hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618
 //   hprms_streamer           <- relu()  hp_rms_norm/csrc/cuda/activation_kernels.cu:7-39
 //                               launch_relu<T>()  hp_rms_norm/csrc/cuda/activation_kernels.cuh:122-145
+// The other entry points (plain RMSNorm, FP8 output, out of place, partial-sum
+// reduction) have no reference counterpart and share the fused kernels.
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -90,6 +92,10 @@ const FusedEntry kFused[] = {
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 2)
     HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
     HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 2)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 3)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 3)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 4)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 4)
 };
 
 const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
@@ -176,16 +182,23 @@ constexpr int64_t kMaxHidden = int64_t(1) << 24;
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
 struct Problem {
-  int mode;  // 0 fused, 1 plain, 2 fused with FP8 output
-  void* x;
-  void* out;  // mode 1: 16-bit output; mode 2: FP8 output
+  int mode;  // 0 fused, 1 plain, 2 fused with FP8 output, 3 fused out of place, 4 parts reduced first
+  void* x;    // mode 4: parts[0]
+  void* out;  // modes 1, 3, 4: 16-bit output; mode 2: FP8 output
   void* res;
   const void* w;
   int64_t rows, hidden, x_stride, out_stride, res_stride;
   int dtype;
   double eps;
-  float* scale;  // mode 2
+  float* scale = nullptr;      // mode 2
+  void* res_out = nullptr;     // mode 3
+  int64_t res_out_stride = 0;  // mode 3
+  int nparts = 1;              // mode 4
+  const void* const* parts = nullptr;
 };
+
+bool has_res(int mode) { return mode != 1; }
+bool has_out(int mode) { return mode != 0; }
 
 int check_problem(const Problem& p) {
   if (p.dtype != HPRMS_DTYPE_BF16 && p.dtype != HPRMS_DTYPE_FP16)
@@ -197,17 +210,43 @@ int check_problem(const Problem& p) {
                 (long long)kMaxHidden);
   if (p.x_stride < p.hidden) return fail(HPRMS_E_INVALID, "input row stride %lld < hidden %lld",
                                          (long long)p.x_stride, (long long)p.hidden);
-  if (p.mode != 1 && p.res_stride < p.hidden)
+  if (has_res(p.mode) && p.res_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "residual row stride %lld < hidden %lld", (long long)p.res_stride,
                 (long long)p.hidden);
-  if (p.mode != 0 && p.out_stride < p.hidden)
+  if (has_out(p.mode) && p.out_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "output row stride %lld < hidden %lld", (long long)p.out_stride,
                 (long long)p.hidden);
+  if (p.mode == 3 && p.res_out_stride < p.hidden)
+    return fail(HPRMS_E_INVALID, "residual output row stride %lld < hidden %lld", (long long)p.res_out_stride,
+                (long long)p.hidden);
+  if (p.mode == 4 && (p.nparts < 1 || p.nparts > HPRMS_MAX_PARTS))
+    return fail(HPRMS_E_INVALID, "nparts must be in [1, %d] (got %d)", HPRMS_MAX_PARTS, p.nparts);
   if (!(p.eps >= 0.0)) return fail(HPRMS_E_INVALID, "eps must be >= 0");
   if (p.rows == 0) return HPRMS_OK;
-  if (!p.x || !p.w || (p.mode != 1 && !p.res) || (p.mode != 0 && !p.out) || (p.mode == 2 && !p.scale))
+  if (p.mode == 4 && !p.parts) return fail(HPRMS_E_INVALID, "null parts array");
+  if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) || (p.mode == 2 && !p.scale) ||
+      (p.mode == 3 && !p.res_out))
     return fail(HPRMS_E_INVALID, "null tensor pointer");
-  if (p.mode != 1 && p.x == p.res) return fail(HPRMS_E_INVALID, "input and residual must not alias");
+  if (p.mode == 4) {
+    for (int g = 0; g < p.nparts; ++g) {
+      if (!p.parts[g]) return fail(HPRMS_E_INVALID, "null tensor pointer (part %d)", g);
+      if (p.parts[g] == p.res) return fail(HPRMS_E_INVALID, "part %d and residual must not alias", g);
+    }
+    if (p.out == p.res) return fail(HPRMS_E_INVALID, "output and residual must not alias");
+    for (int g = 0; g < p.nparts; ++g)
+      if (p.parts[g] == p.out && p.out_stride != p.x_stride)
+        return fail(HPRMS_E_INVALID, "output aliases part %d with a different row stride", g);
+    return HPRMS_OK;
+  }
+  if (p.mode == 3) {
+    if (p.out == p.res_out) return fail(HPRMS_E_INVALID, "output and residual output must not alias");
+    if (p.out == p.res || p.res_out == p.x)
+      return fail(HPRMS_E_INVALID, "output and residual output may only alias input and residual respectively");
+    if ((p.out == p.x && p.out_stride != p.x_stride) || (p.res_out == p.res && p.res_out_stride != p.res_stride))
+      return fail(HPRMS_E_INVALID, "an in-place alias needs equal row strides");
+    return HPRMS_OK;
+  }
+  if (has_res(p.mode) && p.x == p.res) return fail(HPRMS_E_INVALID, "input and residual must not alias");
   return HPRMS_OK;
 }
 
@@ -216,14 +255,22 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   if (p.hidden % 8 != 0) return false;
   if (!aligned16(p.x) || !aligned16(p.w)) return false;
   if (p.x_stride % 8 != 0) return false;
-  if (p.mode != 1 && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
-  if (p.mode == 1 && (!aligned16(p.out) || p.out_stride % 8 != 0)) return false;
-  if (p.mode == 2 && (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0)) return false;
+  if (has_res(p.mode) && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
+  if (p.mode == 2) {
+    if (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0) return false;
+  } else if (has_out(p.mode) && (!aligned16(p.out) || p.out_stride % 8 != 0)) {
+    return false;
+  }
+  if (p.mode == 3 && (!aligned16(p.res_out) || p.res_out_stride % 8 != 0)) return false;
+  if (p.mode == 4 && p.parts)  // null only with rows == 0 (a configuration check)
+    for (int g = 0; g < p.nparts; ++g)
+      if (!aligned16(p.parts[g])) return false;
   if ((int64_t)c.lanes_per_row * c.vec_per_lane * 8 < p.hidden) return false;
   // every buffer resource of a row group spans < 2^31 bytes
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   int64_t smax = p.x_stride > p.out_stride ? p.x_stride : p.out_stride;
-  if (p.mode != 1 && p.res_stride > smax) smax = p.res_stride;
+  if (has_res(p.mode) && p.res_stride > smax) smax = p.res_stride;
+  if (p.mode == 3 && p.res_out_stride > smax) smax = p.res_out_stride;
   if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
     return false;
   return true;
@@ -231,15 +278,19 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
 
 template <int DT>
 int launch_general(const Problem& p, hipStream_t stream) {
-  GeneralArgs a;
+  GeneralArgs a = {};
   a.x = (const uint16_t*)p.x;
-  a.out = (uint16_t*)(p.mode == 1 ? p.out : p.x);
+  a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 ? p.x : p.out);
   a.res = (uint16_t*)p.res;
   a.w = (const uint16_t*)p.w;
   a.rows = p.rows;
   a.x_stride = p.x_stride;
-  a.out_stride = p.mode == 1 ? p.out_stride : p.x_stride;
+  a.out_stride = p.mode == 0 || p.mode == 2 ? p.x_stride : p.out_stride;
   a.res_stride = p.res_stride;
+  a.res_out = (uint16_t*)p.res_out;
+  a.res_out_stride = p.res_out_stride;
+  a.nparts = p.nparts;
+  for (int g = 0; g < p.nparts && p.parts; ++g) a.parts[g] = (const uint16_t*)p.parts[g];
   a.hidden = p.hidden;
   a.hidden_f = (float)p.hidden;
   a.eps = (float)p.eps;
@@ -247,12 +298,13 @@ int launch_general(const Problem& p, hipStream_t stream) {
   a.scale = p.scale;
   a.q_stride = p.mode == 2 ? p.out_stride : 0;
   const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
-  if (p.mode == 0)
-    fused_general_kernel<DT, 0><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
-  else if (p.mode == 1)
-    fused_general_kernel<DT, 1><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
-  else
-    fused_general_kernel<DT, 2><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
+  switch (p.mode) {
+    case 0: fused_general_kernel<DT, 0><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
+    case 1: fused_general_kernel<DT, 1><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
+    case 2: fused_general_kernel<DT, 2><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
+    case 3: fused_general_kernel<DT, 3><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
+    default: fused_general_kernel<DT, 4><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
+  }
   return check_launch("general rmsnorm kernel");
 }
 
@@ -290,9 +342,13 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
                 c.block_threads, c.flags);
   if (p.rows == 0) return HPRMS_OK;
 
-  FusedArgs a;
+  FusedArgs a = {};
   a.x = (const uint16_t*)p.x;
-  a.out = (uint16_t*)(p.mode == 1 ? p.out : p.x);
+  a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 ? p.x : p.out);
+  a.res_out = (uint16_t*)p.res_out;
+  a.res_out_stride = p.res_out_stride;
+  a.nparts = p.nparts;
+  for (int g = 0; g < p.nparts && p.parts; ++g) a.parts[g] = (const uint16_t*)p.parts[g];
   a.res = (uint16_t*)p.res;
   a.w = (const uint16_t*)p.w;
   a.rows = p.rows;
@@ -302,7 +358,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   a.ngroups = (p.rows + rpb - 1) / rpb;
   a.x_stride = p.x_stride;
-  a.out_stride = p.mode == 1 ? p.out_stride : p.x_stride;
+  a.out_stride = p.mode == 0 || p.mode == 2 ? p.x_stride : p.out_stride;
   a.res_stride = p.res_stride;
   a.hidden = (int32_t)p.hidden;
   a.nvec = (int32_t)(p.hidden / 8);
@@ -370,6 +426,28 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
   return run(p, config, stream);
 }
 
+int hprms_fused_add_rmsnorm_out(void* out, void* residual_out, const void* input, const void* residual,
+                                const void* weight, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                                int64_t residual_out_row_stride, int64_t input_row_stride,
+                                int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
+  Problem p{3, const_cast<void*>(input), out, const_cast<void*>(residual), weight, rows, hidden, input_row_stride,
+            out_row_stride, residual_row_stride, dtype, eps};
+  p.res_out = residual_out;
+  p.res_out_stride = residual_out_row_stride;
+  return run(p, nullptr, stream);
+}
+
+int hprms_reduce_add_rmsnorm(void* out, const void* const* parts, int nparts, const void* weight, void* residual,
+                             int64_t rows, int64_t hidden, int64_t out_row_stride, int64_t part_row_stride,
+                             int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
+  Problem p{4, nullptr, out, residual, weight, rows, hidden, part_row_stride, out_row_stride,
+            residual_row_stride, dtype, eps};
+  p.nparts = nparts;
+  p.parts = parts;
+  if (parts && nparts >= 1) p.x = const_cast<void*>(parts[0]);
+  return run(p, nullptr, stream);
+}
+
 int hprms_rmsnorm(void* out, const void* in, const void* weight, int64_t rows, int64_t hidden,
                   int64_t out_row_stride, int64_t in_row_stride, int dtype, double eps, hipStream_t stream) {
   Problem p{1, const_cast<void*>(in), out, nullptr, weight, rows, hidden, in_row_stride, out_row_stride,
@@ -381,7 +459,7 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode < 0 || mode > 2) return fail(HPRMS_E_INVALID, "mode must be 0, 1 or 2 (got %d)", mode);
+  if (mode < 0 || mode > 4) return fail(HPRMS_E_INVALID, "mode must be in [0, 4] (got %d)", mode);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
   table_config(rows, hidden, mode, config);
   if (hidden % 8 != 0) config->tier = 3;
@@ -412,7 +490,7 @@ int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int6
 int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode < 0 || mode > 2) return fail(HPRMS_E_INVALID, "mode must be 0, 1 or 2 (got %d)", mode);
+  if (mode < 0 || mode > 4) return fail(HPRMS_E_INVALID, "mode must be in [0, 4] (got %d)", mode);
   if (capacity < 0 || (capacity > 0 && !out)) return fail(HPRMS_E_INVALID, "bad output array");
   int n = 0;
   for (const FusedEntry& e : kFused) {

@@ -34,6 +34,11 @@
 // scale)) to q), the residual is updated in place and `input` is only read.
 // The row maximum is a second DPP/LDS reduction over the 16-bit magnitudes
 // (sign-magnitude bit patterns order like their values, NaN above inf).
+// MODE 3 is the fused op out of place: input and residual are only read, the
+// sum goes to res_out and the output to out.  MODE 4 adds nparts partial rows
+// first (the buffers of a tensor-parallel all-reduce): a = rne(p0 + p1 + ...)
+// summed in fp32 left to right and rounded once, then the fused op on a, with
+// the residual updated in place and the output written to out.
 #pragma once
 
 #include "hprms_device.h"
@@ -57,6 +62,10 @@ struct FusedArgs {
   uint8_t* q;            // MODE 2: FP8 output rows
   float* scale;          // MODE 2: per-row scales
   int64_t q_stride;      // MODE 2: bytes between FP8 rows
+  uint16_t* res_out;     // MODE 3: residual output rows
+  int64_t res_out_stride;
+  int32_t nparts;        // MODE 4: number of partial rows summed (x is part 0)
+  const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
 };
 
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
@@ -69,6 +78,8 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;
   constexpr int NW = BLOCK / 64;
   constexpr int VREG = VPL - LDSV;
+  constexpr bool RES = MODE != 1;                                  // residual stream read
+  constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
@@ -98,18 +109,26 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row0 * a.x_stride, xbytes);
     const uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + (uint32_t)lane * 16u;
 
-    __amdgpu_buffer_rsrc_t rrs = xrs, ors = xrs;
-    uint32_t roff = 0, ooff = xoff;
-    if constexpr (MODE == 0 || MODE == 2) {
+    // rrs/roff: residual loads; srs/soff: residual stores; ors/ooff: output
+    __amdgpu_buffer_rsrc_t rrs = xrs, srs = xrs, ors = xrs;
+    uint32_t roff = 0, soff = 0, ooff = xoff;
+    if constexpr (RES) {
       const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_stride + a.hidden) * 2);
       rrs = make_rsrc(a.res + row0 * a.res_stride, rbytes);
       roff = (uint32_t)rib * (uint32_t)a.res_stride * 2u + (uint32_t)lane * 16u;
+      srs = rrs;
+      soff = roff;
+    }
+    if constexpr (MODE == 3) {
+      const uint32_t sbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_out_stride + a.hidden) * 2);
+      srs = make_rsrc(a.res_out + row0 * a.res_out_stride, sbytes);
+      soff = (uint32_t)rib * (uint32_t)a.res_out_stride * 2u + (uint32_t)lane * 16u;
     }
     if constexpr (MODE == 2) {
       const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + a.hidden);
       ors = make_rsrc(a.q + row0 * a.q_stride, qbytes);
       ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)lane * 8u;
-    } else if constexpr (MODE == 1) {
+    } else if constexpr (OUT16) {
       const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + a.hidden) * 2);
       ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
@@ -120,11 +139,43 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     for (int k = 0; k < VPL; ++k) {
       const bool ok = row_ok && vec_ok[k];
       xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
-      if constexpr (MODE != 1) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+      if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
     }
     if constexpr (!WLATE) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
+    }
+
+    if constexpr (MODE == 4) {
+      // x := rne(sum of the parts), accumulated in fp32 in part order; the
+      // unrolled loop keeps every parts[] index a constant
+      float acc[VPL][8];
+#pragma unroll
+      for (int k = 0; k < VPL; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[k][2 * j] = F::lo(xv[k][j]);
+          acc[k][2 * j + 1] = F::hi(xv[k][j]);
+        }
+#pragma unroll
+      for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+        if (g >= a.nparts) break;
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * a.x_stride, xbytes);
+        u32x4 pv[VPL];
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) pv[k] = load16<LAUX>(prs, (row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[k][2 * j] += F::lo(pv[k][j]);
+            acc[k][2 * j + 1] += F::hi(pv[k][j]);
+          }
+      }
+#pragma unroll
+      for (int k = 0; k < VPL; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[k][j] = F::pack(acc[k][2 * j], acc[k][2 * j + 1]);
     }
 
     float ss0 = 0.0f, ss1 = 0.0f;
@@ -132,7 +183,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       u32x4 s;
-      if constexpr (MODE != 1) {
+      if constexpr (RES) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t p = F::pack(F::lo(xv[k][j]) + F::lo(rv[k][j]), F::hi(xv[k][j]) + F::hi(rv[k][j]));
@@ -142,7 +193,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
           ss1 = __builtin_fmaf(b1, b1, ss1);
         }
         const bool ok = row_ok && vec_ok[k];
-        store16<SAUX>(s, rrs, ok ? roff + k * CH : kOOB);
+        store16<SAUX>(s, srs, ok ? soff + k * CH : kOOB);
       } else {
         s = xv[k];
 #pragma unroll
@@ -252,6 +303,10 @@ struct GeneralArgs {
   uint8_t* q;        // MODE 2
   float* scale;      // MODE 2
   int64_t q_stride;  // MODE 2
+  uint16_t* res_out;  // MODE 3
+  int64_t res_out_stride;
+  int32_t nparts;    // MODE 4
+  const uint16_t* parts[HPRMS_MAX_PARTS];
 };
 
 template <int DT, int MODE>
@@ -263,13 +318,25 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
   for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
     const uint16_t* x = a.x + row * a.x_stride;
     uint16_t* o = a.out + row * a.out_stride;
-    uint16_t* r = MODE != 1 ? a.res + row * a.res_stride : nullptr;
+    const uint16_t* r = MODE != 1 ? a.res + row * a.res_stride : nullptr;
+    // where the rounded sum goes (and is read back from by the output pass)
+    uint16_t* rs = MODE == 3 ? a.res_out + row * a.res_out_stride
+                   : MODE != 1 ? a.res + row * a.res_stride : nullptr;
     float ss = 0.0f;
     for (int64_t j = tid; j < a.hidden; j += 256) {
       float v;
       if constexpr (MODE != 1) {
-        const uint16_t s = F::pack1(F::one(x[j]) + F::one(r[j]));
-        r[j] = s;
+        float xj = F::one(x[j]);
+        if constexpr (MODE == 4) {
+#pragma unroll
+          for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+            if (g >= a.nparts) break;
+            xj += F::one(a.parts[g][row * a.x_stride + j]);
+          }
+          xj = F::one(F::pack1(xj));
+        }
+        const uint16_t s = F::pack1(xj + F::one(r[j]));
+        rs[j] = s;
         v = F::one(s);
       } else {
         v = F::one(x[j]);
@@ -284,7 +351,7 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
     const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
     if constexpr (MODE != 2) {
       for (int64_t j = tid; j < a.hidden; j += 256) {
-        const float v = MODE == 0 ? F::one(r[j]) : F::one(x[j]);
+        const float v = MODE == 1 ? F::one(x[j]) : F::one(rs[j]);
         o[j] = F::pack1((v * inv) * F::one(a.w[j]));
       }
     } else {
@@ -292,7 +359,7 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
       // both passes see the same bits
       uint32_t m = 0;
       for (int64_t j = tid; j < a.hidden; j += 256)
-        m = __builtin_elementwise_max(m, (uint32_t)(F::pack1((F::one(r[j]) * inv) * F::one(a.w[j])) & 0x7fffu));
+        m = __builtin_elementwise_max(m, (uint32_t)(F::pack1((F::one(rs[j]) * inv) * F::one(a.w[j])) & 0x7fffu));
       uint32_t mx = group_max_u32<64>(m);
       if ((tid & 63) == 0) red[buf][tid >> 6] = __builtin_bit_cast(float, mx);
       __syncthreads();
@@ -304,7 +371,7 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
       if (tid == 0) a.scale[row] = sc;
       uint8_t* qr = a.q + row * a.q_stride;
       for (int64_t j = tid; j < a.hidden; j += 256) {
-        const float y = F::one(F::pack1((F::one(r[j]) * inv) * F::one(a.w[j])));
+        const float y = F::one(F::pack1((F::one(rs[j]) * inv) * F::one(a.w[j])));
         qr[j] = (uint8_t)(pack_e4m3x4(clamp_e4m3(y * isc), 0.0f, 0.0f, 0.0f) & 0xffu);
       }
     }

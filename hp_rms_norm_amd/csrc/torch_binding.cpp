@@ -205,6 +205,134 @@ void rms_norm_fp8_meta(at::Tensor& out, at::Tensor& scale, const at::Tensor& inp
   (void)eps;
 }
 
+// ---- fused op out of place ----------------------------------------------------------
+FusedShape check_fused_out(const at::Tensor& out, const at::Tensor& residual_out, const at::Tensor& input,
+                           const at::Tensor& weight, const at::Tensor& residual) {
+  TORCH_CHECK(input.dim() >= 2, "input.dim() >= 2");
+  const int64_t hidden = weight.dim() == 1 ? weight.size(0) : -1;
+  for (const at::Tensor* t : {&residual, &out, &residual_out}) {
+    TORCH_CHECK(t->dim() == input.dim(), "all row tensors must have input.dim() dimensions");
+    for (int64_t i = 0; i < input.dim(); ++i) TORCH_CHECK(t->size(i) == input.size(i), "input.size(i) == residual.size(i)");
+    TORCH_CHECK(t->stride(-1) == 1, "rows must be contiguous (stride(-1) == 1)");
+    TORCH_CHECK(t->scalar_type() == input.scalar_type(), "all tensors must have input.dtype()");
+    TORCH_CHECK(t->device() == input.device(), "all tensors must be on input's device");
+  }
+  TORCH_CHECK(weight.dim() == 1, "weight.dim() == 1");
+  TORCH_CHECK(input.size(-1) == hidden, "input.size(-1) == hidden_dim");
+  TORCH_CHECK(input.stride(-1) == 1, "input.stride(-1) == 1");
+  TORCH_CHECK(weight.stride(0) == 1 || hidden == 1, "weight.stride(0) == 1");
+  TORCH_CHECK(weight.scalar_type() == input.scalar_type(), "weight.dtype() == input.dtype()");
+  TORCH_CHECK(weight.device() == input.device(), "weight must be on input's device");
+  FusedShape s;
+  s.dtype = dtype_code(input);
+  s.hidden = hidden;
+  rows_of(input, hidden, &s.rows, &s.in_stride);
+  int64_t r = 0, st = 0;
+  rows_of(residual, hidden, &r, &s.res_stride);
+  rows_of(out, hidden, &r, &st);
+  rows_of(residual_out, hidden, &r, &st);
+  if (s.rows > 0) {
+    // out may be input and residual_out may be residual (in place); no other sharing
+    at::assert_no_overlap(out, residual_out);
+    at::assert_no_overlap(out, residual);
+    at::assert_no_overlap(residual_out, input);
+    at::assert_no_partial_overlap(out, input);
+    at::assert_no_partial_overlap(residual_out, residual);
+  }
+  return s;
+}
+
+void rms_norm_out_hip(at::Tensor& out, at::Tensor& residual_out, const at::Tensor& input, const at::Tensor& weight,
+                      const at::Tensor& residual, double eps) {
+  const FusedShape s = check_fused_out(out, residual_out, input, weight, residual);
+  if (s.rows == 0) return;
+  int64_t r = 0, out_stride = 0, res_out_stride = 0;
+  rows_of(out, s.hidden, &r, &out_stride);
+  rows_of(residual_out, s.hidden, &r, &res_out_stride);
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm_out(out.data_ptr(), residual_out.data_ptr(), input.data_ptr(),
+                                           residual.data_ptr(), weight.data_ptr(), s.rows, s.hidden, out_stride,
+                                           res_out_stride, s.in_stride, s.res_stride, s.dtype, eps, stream));
+}
+
+void rms_norm_out_meta(at::Tensor& out, at::Tensor& residual_out, const at::Tensor& input, const at::Tensor& weight,
+                       const at::Tensor& residual, double eps) {
+  (void)check_fused_out(out, residual_out, input, weight, residual);
+  (void)eps;
+}
+
+// ---- partial-sum reduction + fused op ----------------------------------------------------
+struct ReduceShape {
+  int64_t rows, hidden, out_stride, part_stride, res_stride;
+  int dtype;
+};
+
+ReduceShape check_reduce(const at::Tensor& out, at::TensorList parts, const at::Tensor& weight,
+                         const at::Tensor& residual) {
+  TORCH_CHECK(!parts.empty() && (int64_t)parts.size() <= HPRMS_MAX_PARTS, "parts must hold 1 to ",
+              HPRMS_MAX_PARTS, " tensors (got ", parts.size(), ")");
+  TORCH_CHECK(residual.dim() >= 2, "input.dim() >= 2");
+  TORCH_CHECK(weight.dim() == 1, "weight.dim() == 1");
+  const int64_t hidden = weight.size(0);
+  TORCH_CHECK(residual.size(-1) == hidden, "input.size(-1) == hidden_dim");
+  TORCH_CHECK(weight.stride(0) == 1 || hidden == 1, "weight.stride(0) == 1");
+  ReduceShape s;
+  s.dtype = dtype_code(residual);
+  s.hidden = hidden;
+  TORCH_CHECK(weight.scalar_type() == residual.scalar_type(), "weight.dtype() == input.dtype()");
+  TORCH_CHECK(weight.device() == residual.device(), "weight must be on residual's device");
+  for (const at::Tensor* t : {&out, &parts[0]}) {
+    TORCH_CHECK(t->dim() == residual.dim(), "all row tensors must have residual.dim() dimensions");
+    for (int64_t i = 0; i < residual.dim(); ++i)
+      TORCH_CHECK(t->size(i) == residual.size(i), "input.size(i) == residual.size(i)");
+  }
+  for (const at::Tensor* t : {&residual, &out}) {
+    TORCH_CHECK(t->stride(-1) == 1, "rows must be contiguous (stride(-1) == 1)");
+    TORCH_CHECK(t->scalar_type() == residual.scalar_type(), "all tensors must have residual.dtype()");
+    TORCH_CHECK(t->device() == residual.device(), "all tensors must be on residual's device");
+  }
+  rows_of(residual, hidden, &s.rows, &s.res_stride);
+  int64_t r = 0;
+  rows_of(out, hidden, &r, &s.out_stride);
+  for (size_t g = 0; g < parts.size(); ++g) {
+    const at::Tensor& p = parts[g];
+    TORCH_CHECK(p.sizes() == parts[0].sizes(), "every part must have the shape of the residual");
+    TORCH_CHECK(p.stride(-1) == 1, "rows must be contiguous (stride(-1) == 1)");
+    TORCH_CHECK(p.scalar_type() == residual.scalar_type(), "all tensors must have residual.dtype()");
+    TORCH_CHECK(p.device() == residual.device(), "all tensors must be on residual's device");
+    int64_t st = 0;
+    rows_of(p, hidden, &r, &st);
+    if (g == 0) s.part_stride = st;
+    TORCH_CHECK(st == s.part_stride, "all parts must share one row stride");
+    if (s.rows > 0) {
+      at::assert_no_overlap(p, residual);
+      at::assert_no_partial_overlap(out, p);
+    }
+  }
+  if (s.rows > 0) at::assert_no_overlap(out, residual);
+  return s;
+}
+
+void reduce_rms_norm_hip(at::Tensor& out, at::TensorList parts, const at::Tensor& weight, at::Tensor& residual,
+                         double eps) {
+  const ReduceShape s = check_reduce(out, parts, weight, residual);
+  if (s.rows == 0) return;
+  const void* ptrs[HPRMS_MAX_PARTS];
+  for (size_t g = 0; g < parts.size(); ++g) ptrs[g] = parts[g].data_ptr();
+  c10::DeviceGuard guard(residual.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(residual.device().index()).stream();
+  check_status(hprms_reduce_add_rmsnorm(out.data_ptr(), ptrs, (int)parts.size(), weight.data_ptr(),
+                                        residual.data_ptr(), s.rows, s.hidden, s.out_stride, s.part_stride,
+                                        s.res_stride, s.dtype, eps, stream));
+}
+
+void reduce_rms_norm_meta(at::Tensor& out, at::TensorList parts, const at::Tensor& weight, at::Tensor& residual,
+                          double eps) {
+  (void)check_reduce(out, parts, weight, residual);
+  (void)eps;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(hp_rms_norm, m) {
@@ -214,6 +342,9 @@ TORCH_LIBRARY(hp_rms_norm, m) {
   m.def("rms_norm_plain(Tensor(a!) out, Tensor input, Tensor weight, float eps) -> ()");
   m.def("rms_norm_fp8_quant(Tensor(a!) out, Tensor(b!) scale, Tensor input, Tensor weight, Tensor(c!) residual, "
         "float eps) -> ()");
+  m.def("rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, Tensor residual, "
+        "float eps) -> ()");
+  m.def("reduce_add_rms_norm(Tensor(a!) out, Tensor[] parts, Tensor weight, Tensor(b!) residual, float eps) -> ()");
 }
 
 // ROCm builds of PyTorch expose HIP devices under the CUDA dispatch key.
@@ -223,6 +354,8 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
   m.impl("relu_max0", &relu_max0_hip);
   m.impl("rms_norm_plain", &rms_norm_plain_hip);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_hip);
+  m.impl("rms_norm_out", &rms_norm_out_hip);
+  m.impl("reduce_add_rms_norm", &reduce_rms_norm_hip);
 }
 
 // Shape checks only, for fake tensors / torch.compile tracing.  Meta tensors
@@ -233,4 +366,6 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
   m.impl("relu_max0", &stream_meta);
   m.impl("rms_norm_plain", &rms_norm_plain_meta);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_meta);
+  m.impl("rms_norm_out", &rms_norm_out_meta);
+  m.impl("reduce_add_rms_norm", &reduce_rms_norm_meta);
 }

@@ -3,8 +3,8 @@
 argument order, in-place semantics and ``None`` return."""
 import torch
 
-__all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "hp_rms_norm_fp8",
-           "fused_add_rms_norm_fp8"]
+__all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "fused_add_rms_norm_out",
+           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "reduce_add_rms_norm"]
 
 
 def hp_rms_norm(input, weight, residual, eps):
@@ -36,12 +36,21 @@ def rms_norm(output, input, weight, eps):
     torch.ops.hp_rms_norm.rms_norm_plain.default(output, input, weight, eps)
 
 
+def fused_add_rms_norm_out(out, residual_out, input, weight, residual, eps):
+    """Out-of-place ``hp_rms_norm``: ``residual_out <- input + residual`` and
+    ``out <- rms_norm(residual_out) * weight``; ``input`` and ``residual`` are
+    only read.  ``out`` may be ``input`` and ``residual_out`` may be
+    ``residual``.  The same kernel as the in-place op (2 reads and 2 writes
+    per element).  No reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_out.default(out, residual_out, input, weight, residual, eps)
+
+
 def fused_add_rms_norm(input, residual, weight, eps):
-    """Out-of-place form of ``hp_rms_norm``: returns ``(normed, input +
-    residual)`` as new tensors and leaves the arguments untouched."""
-    out = input.clone()
-    res = residual.clone()
-    torch.ops.hp_rms_norm.rms_norm.default(out, weight, res, eps)
+    """Allocating out-of-place form of ``hp_rms_norm``: returns ``(normed,
+    input + residual)`` as new tensors and leaves the arguments untouched."""
+    out = torch.empty_like(input)
+    res = torch.empty_like(residual)
+    torch.ops.hp_rms_norm.rms_norm_out.default(out, res, input, weight, residual, eps)
     return out, res
 
 
@@ -63,3 +72,14 @@ def fused_add_rms_norm_fp8(input, residual, weight, eps):
     scale = torch.empty(input.shape[:-1] + (1,), dtype=torch.float32, device=input.device)
     torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(q, scale, input, weight, residual, eps)
     return q, scale
+
+
+def reduce_add_rms_norm(out, parts, weight, residual, eps):
+    """Partial sums fused with ``hp_rms_norm``: with ``a = sum(parts)`` added
+    in fp32 in list order and rounded once to the tensor dtype,
+    ``residual <- a + residual`` in place and ``out <- rms_norm(residual) *
+    weight``.  ``parts``: 1 to 8 tensors shaped like ``residual`` that share one
+    row stride (the buffers of a tensor-parallel all-reduce); they are only
+    read, and ``out`` may be one of them.  With one part this is
+    ``hp_rms_norm`` writing its output to ``out``.  No reference counterpart."""
+    torch.ops.hp_rms_norm.reduce_add_rms_norm.default(out, list(parts), weight, residual, eps)

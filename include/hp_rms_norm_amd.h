@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 2
+#define HPRMS_ABI_VERSION 3
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -37,6 +37,9 @@ typedef enum {
 #define HPRMS_E_INVALID (-22)  /* bad argument: null pointer, size, stride, dtype */
 #define HPRMS_E_LAUNCH (-5)    /* the HIP runtime rejected a launch or query */
 #define HPRMS_E_RANGE (-34)    /* a size or stride does not fit the kernel's index width */
+
+/* most partial buffers hprms_reduce_add_rmsnorm() sums */
+#define HPRMS_MAX_PARTS 8
 
 /* streamer operations for hprms_streamer() */
 #define HPRMS_STREAM_COPY 0   /* out = in (the reference "relu": activation_kernels.cuh:99-119) */
@@ -107,6 +110,44 @@ int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, cons
                                 int dtype, double eps, hipStream_t stream);
 
 /*
+ * Fused residual-add + RMSNorm out of place: the arithmetic of
+ * hprms_fused_add_rmsnorm() with `input` and `residual` only read,
+ *   residual_out[r, :] <- rne(f32(input) + f32(residual))
+ *   out[r, :]          <- the normalised output
+ * No counterpart in the reference (its op is in place only,
+ * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:33,42); it moves the same 4 rows of
+ * bytes per row as the in-place op, where a clone followed by the in-place op
+ * moves 8.  `out` may equal `input` and `residual_out` may equal `residual`
+ * (exact aliases with equal strides, i.e. in place); `out` and
+ * `residual_out` must differ.  Buffers must not otherwise overlap.
+ */
+int hprms_fused_add_rmsnorm_out(void* out, void* residual_out, const void* input, const void* residual,
+                                const void* weight, int64_t rows, int64_t hidden,
+                                int64_t out_row_stride, int64_t residual_out_row_stride,
+                                int64_t input_row_stride, int64_t residual_row_stride,
+                                int dtype, double eps, hipStream_t stream);
+
+/*
+ * Partial-sum reduction fused with residual-add + RMSNorm: the on-device half
+ * of a tensor-parallel "all-reduce + residual + RMSNorm".  With P = nparts
+ * (1 ... HPRMS_MAX_PARTS) buffers of the same shape and row stride,
+ *   a[r, :]        =  rne(((f32(parts[0]) + f32(parts[1])) + ...) + f32(parts[P-1]))
+ *   residual[r, :] <- rne(f32(a) + f32(residual))                 (in place)
+ *   out[r, :]      <- rne((f32(residual_new) * rsqrt(mean(f32(residual_new)^2) + eps)) * f32(weight))
+ * i.e. an all-reduce that sums in fp32 in rank order and rounds once, followed
+ * by hprms_fused_add_rmsnorm() on its result; with P = 1 it equals that op
+ * writing to `out`.  The parts are only read: in a deployment they are the
+ * peer buffers of the ranks (device pointers mapped from the other GPUs) or
+ * the chunks a reduce-scatter received.  No counterpart in the reference.
+ * `out` may be one of the parts (exact alias, same row stride); `residual`
+ * must not alias `out` or a part.
+ */
+int hprms_reduce_add_rmsnorm(void* out, const void* const* parts, int nparts, const void* weight,
+                             void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                             int64_t part_row_stride, int64_t residual_row_stride,
+                             int dtype, double eps, hipStream_t stream);
+
+/*
  * Kernel configuration of the fused add+RMSNorm family.  Used by the tuning
  * sweep and by tests that exercise every tier at every shape; normal callers
  * use hprms_fused_add_rmsnorm(), which picks the configuration from the
@@ -133,13 +174,14 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
 
 /* The configuration the library would use for (rows, hidden, dtype) and
  * `mode` (0: hprms_fused_add_rmsnorm, 1: hprms_rmsnorm, 2:
- * hprms_fused_add_rmsnorm_fp8), written to *config (tier 3 when only the
+ * hprms_fused_add_rmsnorm_fp8, 3: hprms_fused_add_rmsnorm_out, 4:
+ * hprms_reduce_add_rmsnorm), written to *config (tier 3 when only the
  * general kernel fits hidden).  Pure function of its arguments; touches no
  * device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
- * mode: 0 fused add+RMSNorm, 1 plain RMSNorm, 2 fused with FP8 output).  Writes up to `capacity`
+ * mode, numbered as for hprms_select_config).  Writes up to `capacity`
  * entries to `out` (may be NULL when capacity is 0) and returns how many
  * exist, or a negative status.  Touches no device. */
 int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity);

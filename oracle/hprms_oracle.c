@@ -31,6 +31,12 @@
  * q = e4m3fn(clamp(y * (1 / scale), +-448)); this is the composition of the op
  * with per-token dynamic FP8 quantisation as torch evaluates it.
  *
+ * The partial-sum form (hprms_oracle_reduce_add_rmsnorm) first forms
+ * a = rne16(((f32(p0) + f32(p1)) + ...) + f32(p[P-1])), summed in binary32 in
+ * part order and rounded once (an all-reduce of the parts), then applies the
+ * fused op to a with the output written to `out`.  It has no counterpart in
+ * the reference; with P = 1 it is the fused op.
+ *
  * Parity pins (tests/test_oracle.py): golden vectors made by the reference's
  * own formula in torch (tests/golden/), the live torch formula, a binary64
  * brute force, closed forms (constant rows, power-of-two scaling), numpy's
@@ -328,6 +334,57 @@ int hprms_oracle_fused_add_rmsnorm_fp8(uint8_t* q, float* scale, const uint16_t*
       qr[j] = hprms_oracle_f32_to_e4m3(v);
     }
     free(y);
+  }
+  (void)threads;
+  return 0;
+}
+
+/* planted mistakes of the partial-sum step (tests only; 0 = the algorithm) */
+enum {
+  RMUT_STEP_ROUNDING = 1, /* round to 16 bits after every addition (a ring all-reduce in bf16) */
+  RMUT_NO_ROUNDING = 2,   /* add the residual to the unrounded fp32 sum */
+  RMUT_REVERSED = 3       /* sum the parts in reverse order */
+};
+
+/* Partial-sum reduction + fused op: out[r] = fused output of a = rne16(sum of
+ * the parts), residual <- rne16(a + residual).  The parts share one row
+ * stride; out has its own.  Returns 0, or -22 on a bad argument. */
+int hprms_oracle_reduce_add_rmsnorm(uint16_t* out, const uint16_t* const* parts, int nparts,
+                                    const uint16_t* weight, uint16_t* residual, int64_t rows,
+                                    int64_t hidden, int64_t out_row_stride, int64_t part_row_stride,
+                                    int64_t residual_row_stride, int dtype, double eps, int threads,
+                                    int mutation) {
+  if (!check_rows(rows, hidden, out_row_stride, residual_row_stride) || part_row_stride < hidden) return -22;
+  if ((dtype != ORACLE_BF16 && dtype != ORACLE_FP16) || nparts < 1) return -22;
+  if (rows == 0) return 0;
+  if (!out || !parts || !weight || !residual) return -22;
+  for (int g = 0; g < nparts; ++g)
+    if (!parts[g]) return -22;
+  float epsf = (float)eps;
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+  for (int64_t i = 0; i < rows; ++i) {
+    uint16_t* o = out + i * out_row_stride;
+    uint16_t* rr = residual + i * residual_row_stride;
+    const int64_t off = i * part_row_stride;
+    for (int64_t j = 0; j < hidden; ++j) {
+      const int first = mutation == RMUT_REVERSED ? nparts - 1 : 0;
+      float acc = to_f32(parts[first][off + j], dtype);
+      for (int t = 1; t < nparts; ++t) {
+        const int g = mutation == RMUT_REVERSED ? nparts - 1 - t : t;
+        acc = acc + to_f32(parts[g][off + j], dtype);
+        if (mutation == RMUT_STEP_ROUNDING) acc = to_f32(from_f32(acc, dtype), dtype);
+      }
+      if (mutation == RMUT_NO_ROUNDING) {
+        /* fold the residual into the unrounded sum; fused_row then adds 0 */
+        acc = acc + to_f32(rr[j], dtype);
+        rr[j] = 0;
+      }
+      o[j] = from_f32(acc, dtype);
+    }
+    fused_row(o, weight, rr, hidden, dtype, epsf, MUT_NONE);
   }
   (void)threads;
   return 0;

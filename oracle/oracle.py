@@ -29,6 +29,13 @@ MUTATIONS = {
     "weight_twice": 8,
 }
 
+# planted mistakes of the partial-sum step (reduce_add_rmsnorm)
+REDUCE_MUTATIONS = {
+    "step_rounding": 1,
+    "no_rounding": 2,
+    "reversed": 3,
+}
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhprms_oracle.so")
 _lib = None
@@ -63,6 +70,9 @@ def lib():
         L.hprms_oracle_fused_add_rmsnorm_fp8.argtypes = [_u8p, _f32p, _u16p, _u16p, _u16p, _i64, _i64, _i64,
                                                          _i64, _i64, ctypes.c_int, ctypes.c_double, ctypes.c_int]
         L.hprms_oracle_e4m3_from_f32.argtypes = [_f32p, _u8p, _i64]
+        L.hprms_oracle_reduce_add_rmsnorm.argtypes = [_u16p, ctypes.POINTER(_u16p), ctypes.c_int, _u16p, _u16p,
+                                                      _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
+                                                      ctypes.c_double, ctypes.c_int, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -122,6 +132,27 @@ def streamer(x, dtype, op, threads=1):
     if rc != 0:
         raise ValueError(f"oracle rejected the arguments ({rc})")
     return out
+
+
+def reduce_add_rmsnorm(parts, w, r, eps, dtype, threads=1, mutation=0):
+    """Partial-sum form: a = rne(sum of ``parts`` in order, fp32), then the
+    fused op on a.  Returns (output, new_residual) as fresh arrays; the
+    arguments are not modified."""
+    ps = [np.ascontiguousarray(p, dtype=np.uint16) for p in parts]
+    assert ps and all(p.shape == ps[0].shape for p in ps)
+    rows, hidden, _ = _rows(ps[0])
+    ro = np.array(r, dtype=np.uint16, copy=True, order="C")
+    assert ro.shape == (rows, hidden)
+    out = np.empty((rows, hidden), dtype=np.uint16)
+    if isinstance(mutation, str):
+        mutation = REDUCE_MUTATIONS[mutation]
+    arr = (_u16p * len(ps))(*[_p16(p) for p in ps])
+    rc = lib().hprms_oracle_reduce_add_rmsnorm(_p16(out), arr, len(ps), _p16(np.ascontiguousarray(w)), _p16(ro),
+                                               rows, hidden, hidden, hidden, hidden, dtype, float(eps), threads,
+                                               mutation)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+    return out, ro
 
 
 def from_f32(a, dtype):

@@ -121,6 +121,11 @@ def test_table_covers_every_hidden_with_a_built_kernel():
             assert rc == abi.HPRMS_OK
             rc = L.hprms_fused_add_rmsnorm_fp8(0, 0, 0, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
             assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
+            rc = L.hprms_fused_add_rmsnorm_out(0, 0, 0, 0, 0, 0, hidden, hidden, hidden, hidden, hidden, dtype,
+                                               1e-6, None)
+            assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
+            rc = L.hprms_reduce_add_rmsnorm(0, None, 2, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
+            assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
             # the FP8 table's choice also exists as a fused (mode 0) kernel, so the
             # 16-bit op can be run with the same lane mapping
             c8 = abi.select_config(rows, hidden, dtype, 2)
@@ -144,7 +149,7 @@ def test_config_entry_rejects_unbuilt_and_misfit_configs():
 
 def test_every_built_config_is_well_formed():
     for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
-        for mode in (0, 1):
+        for mode in range(5):
             cfgs = abi.kernel_configs(dtype, mode)
             assert cfgs
             for c in cfgs:
@@ -168,3 +173,39 @@ def test_fp8_entry_rejects_bad_arguments():
     assert call(out=0) == abi.HPRMS_E_INVALID
     assert call(so=100) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
     assert call(r=0x1000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+
+
+def test_out_of_place_entry_rejects_bad_arguments():
+    L = abi.lib()
+    ok = dict(out=0x4000, ro=0x5000, x=0x1000, r=0x3000, w=0x2000, so=4096, sro=4096)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.hprms_fused_add_rmsnorm_out(a["out"], a["ro"], a["x"], a["r"], a["w"], 4, 4096, a["so"], a["sro"],
+                                             4096, 4096, 0, 1e-6, None)
+    assert call(ro=0x4000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+    assert call(out=0x3000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+    assert call(ro=0x1000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+    assert call(out=0x1000, so=8192) == abi.HPRMS_E_INVALID and "strides" in abi.last_error()
+    assert call(sro=100) == abi.HPRMS_E_INVALID and "residual output row stride" in abi.last_error()
+    assert call(ro=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
+    # zero rows: a configuration check only, every pointer may be null
+    assert L.hprms_fused_add_rmsnorm_out(0, 0, 0, 0, 0, 0, 4096, 4096, 4096, 4096, 4096, 0, 1e-6, None) == abi.HPRMS_OK
+
+
+def test_reduce_entry_rejects_bad_arguments():
+    L = abi.lib()
+    parts = (ctypes.c_void_p * 8)(*[0x10000 * (g + 1) for g in range(8)])
+
+    def call(out=0x100000, p=parts, n=2, res=0x200000, po=4096, sp=4096):
+        return L.hprms_reduce_add_rmsnorm(out, p, n, 0x300000, res, 4, 4096, po, sp, 4096, 0, 1e-6, None)
+    assert call(n=0) == abi.HPRMS_E_INVALID and "nparts" in abi.last_error()
+    assert call(n=9) == abi.HPRMS_E_INVALID and "nparts" in abi.last_error()
+    assert call(p=None) == abi.HPRMS_E_INVALID and "parts" in abi.last_error()
+    assert call(res=0x20000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+    assert call(out=0x200000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+    assert call(out=0x10000, po=8192) == abi.HPRMS_E_INVALID and "stride" in abi.last_error()
+    assert call(sp=100) == abi.HPRMS_E_INVALID and "row stride" in abi.last_error()
+    holes = (ctypes.c_void_p * 2)(0x10000, None)
+    assert call(p=holes) == abi.HPRMS_E_INVALID and "part 1" in abi.last_error()
+    assert abi.select_config(4096, 4096, abi.DTYPE_BF16, abi.MODE_REDUCE).tier in (1, 2)

@@ -118,3 +118,43 @@ def test_fp8_op_schema_and_meta_checks():
         ops.hp_rms_norm_fp8(q, torch.empty(3, device=M), x, w, r, 1e-6)
     with pytest.raises(RuntimeError, match=r"input.size\(-1\) == hidden_dim"):
         ops.hp_rms_norm_fp8(q, sc, x, t(128), r, 1e-6)
+
+
+def test_out_of_place_and_reduce_schemas():
+    s = str(torch.ops.hp_rms_norm.rms_norm_out.default._schema)
+    assert s == ("hp_rms_norm::rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, "
+                 "Tensor residual, float eps) -> ()")
+    s = str(torch.ops.hp_rms_norm.reduce_add_rms_norm.default._schema)
+    assert s == ("hp_rms_norm::reduce_add_rms_norm(Tensor(a!) out, Tensor[] parts, Tensor weight, "
+                 "Tensor(b!) residual, float eps) -> ()")
+
+
+def test_out_of_place_meta_checks():
+    x, r, w = t(4, 256), t(4, 256), t(256)
+    assert ops.fused_add_rms_norm_out(t(4, 256), t(4, 256), x, w, r, 1e-6) is None
+    assert ops.fused_add_rms_norm_out(x, r, x, w, r, 1e-6) is None          # in place is allowed
+    out, res = ops.fused_add_rms_norm(x, r, w, 1e-6)
+    assert out.shape == x.shape and res.shape == r.shape and out.device.type == M
+    with pytest.raises(RuntimeError, match=r"input.size\(-1\) == hidden_dim"):
+        ops.fused_add_rms_norm_out(t(4, 256), t(4, 256), x, t(128), r, 1e-6)
+    with pytest.raises(RuntimeError, match="dtype"):
+        ops.fused_add_rms_norm_out(t(4, 256, dtype=torch.float16), t(4, 256), x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match=r"input.size\(i\) == residual.size\(i\)"):
+        ops.fused_add_rms_norm_out(t(4, 256), t(5, 256), x, w, r, 1e-6)
+
+
+def test_reduce_meta_checks():
+    r, w = t(4, 256), t(256)
+    parts = [t(4, 256) for _ in range(3)]
+    assert ops.reduce_add_rms_norm(t(4, 256), parts, w, r, 1e-6) is None
+    assert ops.reduce_add_rms_norm(parts[0], parts, w, r, 1e-6) is None     # out may be a part
+    with pytest.raises(RuntimeError, match="1 to 8"):
+        ops.reduce_add_rms_norm(t(4, 256), [], w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="1 to 8"):
+        ops.reduce_add_rms_norm(t(4, 256), [t(4, 256) for _ in range(9)], w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="shape"):
+        ops.reduce_add_rms_norm(t(4, 256), [t(4, 256), t(2, 256)], w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="dtype"):
+        ops.reduce_add_rms_norm(t(4, 256), [t(4, 256), t(4, 256, dtype=torch.float16)], w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="one row stride"):
+        ops.reduce_add_rms_norm(t(4, 256), [t(4, 256), t(4, 512)[:, :256]], w, r, 1e-6)

@@ -1,0 +1,222 @@
+"""GPU parity of the out-of-place fused op and of the partial-sum form
+(reduce + residual-add + RMSNorm) against the CPU oracle, through the C ABI
+and the torch ops.
+
+Bar: the residual (and the residual output) bit-exact, the normalised output
+within 1 ulp and atol = rtol = 1e-2 of the oracle.  Both forms share the
+table with the in-place op, so with the same inputs their outputs must also be
+bit-identical to the in-place op's (same reduction order).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, assert_output_close, assert_residual_exact, bits, make_inputs, oracle_fused
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+# every bandwidth row of the table (rows = 513) and every latency row (rows = 64),
+# with a ragged width below each boundary
+HIDDENS = [128, 256, 512, 1000, 2048, 3064, 4096, 8192, 12280, 16384, 24576, 32768, 65536]
+
+
+@pytest.fixture(scope="module")
+def abi():
+    assert torch.cuda.is_available(), "the gpu tests need a HIP device"
+    import hp_rms_norm_amd  # noqa: F401  (registers the torch ops; fails loudly if unbuilt)
+    from hp_rms_norm_amd import abi as a
+    a.lib()
+    return a
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _stride(t):
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
+def in_place(x, r, w, eps):
+    import hp_rms_norm_amd
+    xd, rd = x.to(DEV), r.to(DEV)
+    hp_rms_norm_amd.hp_rms_norm(xd, w.to(DEV), rd, eps)
+    torch.cuda.synchronize()
+    return bits(xd), bits(rd)
+
+
+# ---- out of place ----------------------------------------------------------------------
+def run_out(abi, xd, rd, wd, od, rod, eps):
+    abi.fused_add_rmsnorm_out(od.data_ptr(), rod.data_ptr(), xd.data_ptr(), rd.data_ptr(), wd.data_ptr(),
+                              xd.shape[0], xd.shape[1], _stride(od), _stride(rod), _stride(xd), _stride(rd),
+                              DT[xd.dtype], eps, _stream())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_out_of_place_every_table_row(abi, dtype):
+    for rows in (513, 64):
+        for hidden in HIDDENS:
+            print("out", rows, hidden, dtype, flush=True)
+            x, r, w = make_inputs(rows, hidden, dtype, seed=rows + hidden)
+            want_out, want_res = oracle_fused(x, r, w, 1e-6, dtype)
+            xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+            od, rod = torch.empty_like(xd), torch.empty_like(rd)
+            run_out(abi, xd, rd, wd, od, rod, 1e-6)
+            torch.cuda.synchronize()
+            tag = f"{rows}x{hidden} {dtype}"
+            assert np.array_equal(bits(xd), bits(x)) and np.array_equal(bits(rd), bits(r)), "inputs modified " + tag
+            assert_residual_exact(bits(rod), want_res, dtype, "residual_out " + tag)
+            assert_output_close(bits(od), want_out, dtype, "out " + tag)
+            ip_out, ip_res = in_place(x, r, w, 1e-6)
+            assert np.array_equal(bits(od), ip_out), "differs from the in-place op " + tag
+
+
+def test_out_of_place_torch_ops_and_aliases(abi):
+    import hp_rms_norm_amd
+    x, r, w = make_inputs(300, 4096, torch.bfloat16, seed=5)
+    want_out, want_res = oracle_fused(x, r, w, 1e-6, torch.bfloat16)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    out, res = hp_rms_norm_amd.fused_add_rms_norm(xd, rd, wd, 1e-6)       # allocating form
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(res), want_res, torch.bfloat16)
+    assert_output_close(bits(out), want_out, torch.bfloat16)
+    assert np.array_equal(bits(xd), bits(x)) and np.array_equal(bits(rd), bits(r))
+    # the out form with out = input and residual_out = residual is the in-place op
+    hp_rms_norm_amd.fused_add_rms_norm_out(xd, rd, xd, wd, rd, 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(xd), bits(out)) and np.array_equal(bits(rd), bits(res))
+    # input and residual may be the same tensor when both are only read: s = x + x
+    y = x.to(DEV)
+    o2, s2 = hp_rms_norm_amd.fused_add_rms_norm(y, y, wd, 1e-6)
+    want_out2, want_res2 = oracle_fused(x, x, w, 1e-6, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(s2), want_res2, torch.bfloat16)
+    assert_output_close(bits(o2), want_out2, torch.bfloat16)
+
+
+@pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24), (4096, 3)])
+def test_out_of_place_strided_and_general_tier(abi, hidden, pad):
+    dtype = torch.float16
+    rows = 37
+    x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + pad)
+    want_out, want_res = oracle_fused(x, r, w, 1e-6, dtype)
+    wide = lambda: torch.zeros(rows, hidden + pad, dtype=dtype, device=DEV)   # noqa: E731
+    xb, rb, ob, rob = wide(), wide(), wide(), wide()
+    xd, rd = xb[:, pad:pad + hidden], rb[:, :hidden]
+    xd.copy_(x.to(DEV))
+    rd.copy_(r.to(DEV))
+    od, rod = ob[:, :hidden], rob[:, pad:pad + hidden]
+    run_out(abi, xd, rd, w.to(DEV), od, rod, 1e-6)
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rod), want_res, dtype)
+    assert_output_close(bits(od), want_out, dtype)
+    assert not bits(ob[:, hidden:]).any() and not bits(rob[:, :pad]).any(), "wrote outside the rows"
+
+
+# ---- partial sums ----------------------------------------------------------------------
+def make_parts(nparts, rows, hidden, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(nparts)]
+
+
+def oracle_reduce(parts, r, w, eps, dtype):
+    hidden = r.shape[-1]
+    return oracle.reduce_add_rmsnorm([bits(p).reshape(-1, hidden) for p in parts], bits(w),
+                                     bits(r).reshape(-1, hidden), eps, DT[dtype], threads=min(16, oracle.max_threads()))
+
+
+def run_reduce(abi, od, pds, wd, rd, eps):
+    abi.reduce_add_rmsnorm(od.data_ptr(), [p.data_ptr() for p in pds], wd.data_ptr(), rd.data_ptr(), rd.shape[0],
+                           rd.shape[1], _stride(od), _stride(pds[0]), _stride(rd), DT[rd.dtype], eps, _stream())
+
+
+@pytest.mark.parametrize("nparts", [1, 2, 3, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_reduce_every_table_row(abi, dtype, nparts):
+    for rows in (513, 64):
+        for hidden in HIDDENS:
+            if nparts == 8 and hidden > 16384 and rows == 513:
+                continue   # keeps the oracle's share of the test short; covered by the nparts = 3 case
+            print("reduce", nparts, rows, hidden, dtype, flush=True)
+            parts = make_parts(nparts, rows, hidden, dtype, seed=nparts * 1000 + hidden)
+            _, r, w = make_inputs(rows, hidden, dtype, seed=rows + hidden)
+            want_out, want_res = oracle_reduce(parts, r, w, 1e-6, dtype)
+            pds = [p.to(DEV) for p in parts]
+            rd, wd = r.to(DEV), w.to(DEV)
+            od = torch.empty_like(rd)
+            run_reduce(abi, od, pds, wd, rd, 1e-6)
+            torch.cuda.synchronize()
+            tag = f"P={nparts} {rows}x{hidden} {dtype}"
+            assert all(np.array_equal(bits(pd), bits(p)) for pd, p in zip(pds, parts)), "parts modified " + tag
+            assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
+            assert_output_close(bits(od), want_out, dtype, "out " + tag)
+            if nparts == 1:
+                ip_out, ip_res = in_place(parts[0], r, w, 1e-6)
+                assert np.array_equal(bits(od), ip_out), "P=1 differs from the in-place op " + tag
+
+
+def test_reduce_torch_op_out_is_a_part(abi):
+    import hp_rms_norm_amd
+    parts = make_parts(4, 200, 8192, torch.bfloat16, seed=11)
+    _, r, w = make_inputs(200, 8192, torch.bfloat16, seed=12)
+    want_out, want_res = oracle_reduce(parts, r, w, 1e-6, torch.bfloat16)
+    pds = [p.to(DEV) for p in parts]
+    rd = r.to(DEV)
+    hp_rms_norm_amd.reduce_add_rms_norm(pds[0], pds, w.to(DEV), rd, 1e-6)
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rd), want_res, torch.bfloat16)
+    assert_output_close(bits(pds[0]), want_out, torch.bfloat16)
+
+
+@pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24)])
+def test_reduce_strided_and_general_tier(abi, hidden, pad):
+    dtype = torch.bfloat16
+    rows = 29
+    parts = make_parts(3, rows, hidden, dtype, seed=hidden)
+    _, r, w = make_inputs(rows, hidden, dtype, seed=hidden + 1)
+    want_out, want_res = oracle_reduce(parts, r, w, 1e-6, dtype)
+    pbufs = [torch.zeros(rows, hidden + pad, dtype=dtype, device=DEV) for _ in parts]
+    pds = [b[:, pad:pad + hidden] for b in pbufs]
+    for pd, p in zip(pds, parts):
+        pd.copy_(p.to(DEV))
+    rb = torch.zeros(rows, hidden + pad, dtype=dtype, device=DEV)
+    rd = rb[:, :hidden]
+    rd.copy_(r.to(DEV))
+    ob = torch.zeros(rows, hidden + 2 * pad, dtype=dtype, device=DEV)
+    od = ob[:, pad:pad + hidden]
+    run_reduce(abi, od, pds, w.to(DEV), rd, 1e-6)
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rd), want_res, dtype)
+    assert_output_close(bits(od), want_out, dtype)
+    assert not bits(ob[:, :pad]).any() and not bits(ob[:, pad + hidden:]).any(), "wrote outside the rows"
+
+
+def test_reduce_full_size_identities(abi):
+    """At the benchmark's size, checks that need no oracle: parts [x, 0, 0, 0]
+    and [x/2, x/2] (exact halves) both sum to x exactly, so both must equal the
+    in-place op on x bit for bit; rows are independent, so a permutation of the
+    rows permutes the output."""
+    import hp_rms_norm_amd
+    rows, hidden = 4096, 8192
+    x, r, w = (t.to(DEV) for t in make_inputs(rows, hidden, torch.bfloat16, seed=21))
+    want_x, want_r = x.clone(), r.clone()
+    hp_rms_norm_amd.hp_rms_norm(want_x, w, want_r, 1e-6)
+    zeros = torch.zeros_like(x)
+    for parts in ([x, zeros, zeros, zeros], [x * 0.5, x * 0.5]):
+        rd = r.clone()
+        out = torch.empty_like(x)
+        hp_rms_norm_amd.reduce_add_rms_norm(out, parts, w, rd, 1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want_x.view(torch.int16))
+        assert torch.equal(rd.view(torch.int16), want_r.view(torch.int16))
+    perm = torch.randperm(rows, generator=torch.Generator().manual_seed(3)).to(DEV)
+    parts = [torch.randn(rows, hidden, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    rd, rp = r.clone(), r[perm].clone()
+    out, outp = torch.empty_like(x), torch.empty_like(x)
+    hp_rms_norm_amd.reduce_add_rms_norm(out, parts, w, rd, 1e-6)
+    hp_rms_norm_amd.reduce_add_rms_norm(outp, [p[perm].contiguous() for p in parts], w, rp, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(outp.view(torch.int16), out[perm].view(torch.int16))
+    assert torch.equal(rp.view(torch.int16), rd[perm].view(torch.int16))

@@ -316,3 +316,78 @@ def test_planted_fp8_mistake_is_rejected():
     bad_scale = np.maximum(np.abs(yf).max(-1) / np.float32(240.0), np.finfo(np.float32).tiny).astype(np.float32)
     bad_q = oracle.e4m3_from_f32(np.clip(yf * (np.float32(1.0) / bad_scale)[:, None], -448, 448))
     assert not np.array_equal(bad_scale, tsc) and oracle.e4m3_ulp_distance(bad_q, tq).max() > 0
+
+
+# ---- the partial-sum form (reduce + residual-add + RMSNorm) ---------------------------------
+def torch_reduce_formula(parts, r, w, eps, code):
+    """The all-reduce of the parts as torch evaluates it (binary32 adds in part
+    order, one conversion to the 16-bit type), followed by the reference test's
+    formula (test/test_hp_rms_norm.py:6-19)."""
+    acc = tfrom(parts[0], code).float()
+    for p in parts[1:]:
+        acc = acc + tfrom(p, code).float()
+    return torch_formula(tbits(acc.to(TDT[code])), r, w, eps, code)
+
+
+def pin_reduce_torch_live(mutation=0):
+    for code in (BF, HF):
+        for nparts in (1, 2, 3, 8):
+            parts = [seeded(16, 384, code, 200 + g)[0] for g in range(nparts)]
+            _, r, w = seeded(16, 384, code, 199)
+            out, res = oracle.reduce_add_rmsnorm(parts, w, r, 1e-6, code, mutation=mutation)
+            want_out, want_res = torch_reduce_formula(parts, r, w, 1e-6, code)
+            if oracle.ulp_distance(res, want_res, code).max() != 0:
+                return f"P={nparts}: residual differs from torch"
+            if oracle.ulp_distance(out, want_out, code).max() > 1:
+                return f"P={nparts}: output beyond 1 ulp of torch"
+    return None
+
+
+def bits16(values, code):
+    return tbits(torch.tensor(values, dtype=torch.float64).to(TDT[code]))
+
+
+def pin_reduce_closed_forms(mutation=0):
+    """Residual values fixed by the definition, with u = ulp(1) of the type:
+    1 + u/2 + u/2 = 1 + u when rounded once (rounding after each addition ties
+    to 1 twice); (1 + u/2) rounds to 1 before the residual u/2 is added, so the
+    sum is 1, not 1 + u; 2^24 + 1 - 2^24 = 0 in binary32 left to right (the
+    reversed order gives 1)."""
+    for code, u in ((BF, 2.0 ** -7), (HF, 2.0 ** -10)):
+        w = bits16([1.0] * 8, code)
+
+        def res_of(part_values, r_value):
+            parts = [bits16([[v] * 8], code) for v in part_values]
+            _, res = oracle.reduce_add_rmsnorm(parts, w, bits16([[r_value] * 8], code), 1e-6, code,
+                                               mutation=mutation)
+            return oracle.to_f32(res, code)[0]
+        if not np.all(res_of([1.0, u / 2, u / 2], 0.0) == np.float32(1 + u)):
+            return "1 + u/2 + u/2 is not rounded once"
+        if not np.all(res_of([1.0, u / 2], u / 2) == np.float32(1.0)):
+            return "the reduced sum is not rounded before the residual add"
+        # 2^24 is a bfloat16 value but not a binary16 one (max 65504)
+        if code == BF and not np.all(res_of([2.0 ** 24, 1.0, -2.0 ** 24], 0.0) == 0.0):
+            return "parts are not summed left to right"
+    return None
+
+
+def test_reduce_oracle_matches_live_torch_formula():
+    assert pin_reduce_torch_live() is None
+
+
+def test_reduce_oracle_closed_forms():
+    assert pin_reduce_closed_forms() is None
+
+
+def test_reduce_oracle_with_one_part_is_the_fused_op():
+    x, r, w = seeded(32, 520, BF, 3)
+    out, res = oracle.reduce_add_rmsnorm([x], w, r, 1e-6, BF)
+    want_out, want_res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, BF)
+    assert np.array_equal(out, want_out) and np.array_equal(res, want_res)
+
+
+@pytest.mark.parametrize("name", sorted(oracle.REDUCE_MUTATIONS))
+def test_planted_reduce_mistake_is_rejected(name):
+    m = oracle.REDUCE_MUTATIONS[name]
+    failures = [f for f in (pin_reduce_torch_live(m), pin_reduce_closed_forms(m)) if f]
+    assert failures, f"no pin rejects the planted mistake {name!r}"
