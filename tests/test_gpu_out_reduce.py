@@ -220,3 +220,45 @@ def test_reduce_full_size_identities(abi):
     torch.cuda.synchronize()
     assert torch.equal(outp.view(torch.int16), out[perm].view(torch.int16))
     assert torch.equal(rp.view(torch.int16), rd[perm].view(torch.int16))
+
+
+def test_graph_capture_and_replay_of_both_forms(abi):
+    """Both ops allocate nothing and issue no memset, so they can be captured
+    together; every replay (fresh inputs copied in, eager work and syncs in
+    between) must equal the eager result bit for bit."""
+    import hp_rms_norm_amd
+    rows, hidden, eps, dtype = 192, 8192, 1e-6, torch.bfloat16
+    w = make_inputs(1, hidden, dtype, 0)[2].to(DEV)
+    x, r = torch.empty(rows, hidden, dtype=dtype, device=DEV), torch.empty(rows, hidden, dtype=dtype, device=DEV)
+    out, res_out = torch.empty_like(x), torch.empty_like(x)
+    parts = [torch.empty_like(x) for _ in range(3)]
+    r2, out2 = torch.empty_like(x), torch.empty_like(x)
+    for t in (x, r, r2, *parts):
+        t.normal_()
+
+    def body():
+        hp_rms_norm_amd.fused_add_rms_norm_out(out, res_out, x, w, r, eps)
+        hp_rms_norm_amd.reduce_add_rms_norm(out2, parts, w, r2, eps)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    for rep in range(4):
+        g = torch.Generator(device=DEV).manual_seed(50 + rep)
+        fresh = {name: torch.randn(rows, hidden, device=DEV, generator=g).to(dtype)
+                 for name in ("x", "r", "r2", "p0", "p1", "p2")}
+        for dst, name in ((x, "x"), (r, "r"), (r2, "r2"), (parts[0], "p0"), (parts[1], "p1"), (parts[2], "p2")):
+            dst.copy_(fresh[name])
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (out, res_out, out2, r2)]
+        e_out, e_res = hp_rms_norm_amd.fused_add_rms_norm(fresh["x"], fresh["r"], w, eps)
+        e_r2, e_out2 = fresh["r2"].clone(), torch.empty_like(x)
+        hp_rms_norm_amd.reduce_add_rms_norm(e_out2, [fresh["p0"], fresh["p1"], fresh["p2"]], w, e_r2, eps)
+        torch.cuda.synchronize()
+        for a, b, what in zip(got, (e_out, e_res, e_out2, e_r2), ("out", "residual_out", "reduce out", "reduce residual")):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"replay {rep}: {what}"
