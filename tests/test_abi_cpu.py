@@ -209,3 +209,24 @@ def test_reduce_entry_rejects_bad_arguments():
     holes = (ctypes.c_void_p * 2)(0x10000, None)
     assert call(p=holes) == abi.HPRMS_E_INVALID and "part 1" in abi.last_error()
     assert abi.select_config(4096, 4096, abi.DTYPE_BF16, abi.MODE_REDUCE).tier in (1, 2)
+
+
+def test_plain_c_caller_compiles_links_and_runs(tmp_path):
+    """The header is C99 and the library answers a C program (no torch, no
+    device): tests/c_abi_caller.c, built with gcc."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    libdir = os.path.dirname(abi.KERNEL_LIB)
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    exe = str(tmp_path / "c_abi_caller")
+    cmd = [gcc, "-std=c99", "-Wall", "-Wextra", "-Werror=implicit-function-declaration", "-D__HIP_PLATFORM_AMD__",
+           f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(rocm, 'include')}",
+           os.path.join(ROOT, "tests", "c_abi_caller.c"), f"-L{libdir}", "-lhprms", f"-Wl,-rpath,{libdir}",
+           "-o", exe]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    assert p.returncode == 0, p.stderr[-2000:]
+    p = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert p.returncode == 0 and "ok" in p.stdout, p.stdout + p.stderr
