@@ -63,14 +63,14 @@ struct FusedEntry {
   X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 3, 0, 1024, 31)                             \
   X(DT, MODE, 1024, 4, 0, 1024, 31) X(DT, MODE, 1024, 8, 4, 1024, 31)                           \
   X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
-  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7) X(DT, MODE, 1024, 2, 0, 1024, 31)
 
 // entries of the FP8-output table that the other tables do not use
-#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 512, 8, 4, 512, 31)
+#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
 
 // alternatives of the fused op that the tests run and the sweep compares against
 #define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
-  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 0, 256, 27) \
+  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
   X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
 
 // extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
@@ -157,6 +157,7 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
       {512, 128, 4, 0, 256, 3},      // H <= 4096
       {1024, 256, 4, 0, 256, 3},     // H <= 8192:  one row per 4-wave workgroup
       {1536, 512, 3, 0, 512, 31},    // H <= 12288
+      {1920, 1024, 2, 0, 1024, 31},  // H <= 15360
       {2048, 256, 8, 4, 256, 27},    // H <= 16384: LDS tier, half the row in LDS
       {3072, 1024, 3, 0, 1024, 31},  // H <= 24576
       {4096, 1024, 4, 0, 1024, 31},  // H <= 32768
