@@ -60,10 +60,11 @@ struct FusedEntry {
   X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
   X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 3, 0, 256, 7)   \
   X(DT, MODE, 128, 4, 0, 256, 3) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
-  X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 3, 0, 1024, 31)                             \
-  X(DT, MODE, 1024, 4, 0, 1024, 31) X(DT, MODE, 1024, 8, 4, 1024, 31)                           \
+  X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27)                            \
+  X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)                           \
+  X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
   X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
-  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7) X(DT, MODE, 1024, 2, 0, 1024, 31)
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
 
 // entries of the FP8-output table that the other tables do not use
 #define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
