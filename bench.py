@@ -432,6 +432,22 @@ def run_extra(torch, ops, args):
         del sets, outs
         torch.cuda.empty_cache()
     out["out_of_place_bf16"] = oop
+    # plain RMSNorm (no residual): one read and one write of the row
+    plain = []
+    for h in (4096, 8192, 16384, 32768):
+        n = cold_sets(B, h, floor=2, span=1 << 30)
+        sets = [make_set(torch, B, h, torch.bfloat16, 9000 + i, "cuda:0")[0] for i in range(n)]
+        outs = [torch.empty_like(x) for x in sets]
+        w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+
+        def call(i, sets=sets, outs=outs, w=w):
+            ops.rms_norm(outs[i], sets[i], w, EPS)
+        us = time_rotating(torch, call, n, steps, args.warmup)
+        nbytes = 2 * B * h * 2 + 2 * h
+        plain.append({"rows": B, "hidden": h, "us_per_call": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        del sets, outs
+        torch.cuda.empty_cache()
+    out["plain_rmsnorm_bf16"] = plain
     # partial sums + fused op: P parts read, residual read and written, output written
     red = []
     h = 8192

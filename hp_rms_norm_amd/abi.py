@@ -19,7 +19,8 @@ DTYPE_BF16, DTYPE_FP16 = 0, 1
 STREAM_COPY, STREAM_RELU = 0, 1
 MAX_PARTS = 8
 # the `mode` numbering of hprms_select_config / hprms_kernel_configs
-MODE_FUSED, MODE_PLAIN, MODE_FP8, MODE_OUT, MODE_REDUCE = 0, 1, 2, 3, 4
+MODE_FUSED, MODE_PLAIN, MODE_FP8, MODE_OUT, MODE_REDUCE, MODE_MXFP8, MODE_MXFP4 = 0, 1, 2, 3, 4, 5, 6
+MX_FP8_E4M3, MX_FP4_E2M1 = 0, 1
 
 # every symbol the header declares
 SYMBOLS = (
@@ -27,6 +28,7 @@ SYMBOLS = (
     "hprms_fused_add_rmsnorm_fp8",
     "hprms_fused_add_rmsnorm_out",
     "hprms_reduce_add_rmsnorm",
+    "hprms_fused_add_rmsnorm_mx",
     "hprms_streamer",
     "hprms_rmsnorm",
     "hprms_fused_add_rmsnorm_config",
@@ -77,6 +79,7 @@ def lib():
         L.hprms_fused_add_rmsnorm_out.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
         L.hprms_reduce_add_rmsnorm.argtypes = [vp, ctypes.POINTER(vp), ci, vp, vp, i64, i64, i64, i64, i64, ci,
                                                cd, vp]
+        L.hprms_fused_add_rmsnorm_mx.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, cd, vp]
         L.hprms_streamer.argtypes = [vp, vp, i64, i64, i64, i64, ci, ci, vp]
         L.hprms_select_config.argtypes = [i64, i64, ci, ci, ctypes.POINTER(Config)]
         L.hprms_kernel_configs.argtypes = [ci, ci, ctypes.POINTER(Config), ci]
@@ -85,6 +88,7 @@ def lib():
         L.hprms_abi_version.restype = ci
         for name in ("hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
                      "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_out", "hprms_reduce_add_rmsnorm",
+                     "hprms_fused_add_rmsnorm_mx",
                      "hprms_streamer", "hprms_select_config", "hprms_kernel_configs"):
             getattr(L, name).restype = ci
         _lib = L
@@ -133,6 +137,13 @@ def reduce_add_rmsnorm(out_ptr, part_ptrs, weight_ptr, residual_ptr, rows, hidde
     n = 0 if part_ptrs is None else len(part_ptrs)
     return _check(lib().hprms_reduce_add_rmsnorm(out_ptr, arr, n, weight_ptr, residual_ptr, rows, hidden, out_stride,
                                                  part_stride, residual_stride, dtype, eps, stream))
+
+
+def fused_add_rmsnorm_mx(out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride,
+                         scale_stride, input_stride, residual_stride, fmt, dtype, eps, stream=0):
+    return _check(lib().hprms_fused_add_rmsnorm_mx(out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows,
+                                                   hidden, out_stride, scale_stride, input_stride, residual_stride,
+                                                   fmt, dtype, eps, stream))
 
 
 def rmsnorm(out_ptr, in_ptr, weight_ptr, rows, hidden, out_stride, in_stride, dtype, eps, stream=0):

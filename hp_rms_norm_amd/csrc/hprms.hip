@@ -97,6 +97,14 @@ const FusedEntry kFused[] = {
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 3)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 4)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 4)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 5)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 5)
+    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 5)
+    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 5)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 6)
+    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 6)
+    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 6)
+    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 6)
 };
 
 const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
@@ -128,6 +136,7 @@ bool latency_config(int64_t rows, int64_t nvec, hprms_config* c) {
 // The FP8 output adds a second row reduction (the absolute maximum) and a
 // barrier; above 4K elements it prefers more, smaller workgroups per CU, and
 // at 32K the LDS tier (measured 5.8% faster than 1024 lanes x 4 in registers).
+// The MX outputs (per-block maxima, no second barrier) start from the same rows.
 bool fp8_config(int64_t nvec, hprms_config* c) {
   struct Row { int64_t min_nvec, max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row fp8[] = {{513, 1024, 512, 2, 0, 512, 7},
@@ -145,7 +154,7 @@ bool fp8_config(int64_t nvec, hprms_config* c) {
 void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   const int64_t nvec = hidden / 8;
   if (latency_config(rows, nvec, c)) return;
-  if (mode == 2 && fp8_config(nvec, c)) return;
+  if ((mode == 2 || mode == 5 || mode == 6) && fp8_config(nvec, c)) return;
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row table[] = {
@@ -197,7 +206,13 @@ struct Problem {
   int64_t res_out_stride = 0;  // mode 3
   int nparts = 1;              // mode 4
   const void* const* parts = nullptr;
+  void* mx_scales = nullptr;   // modes 5, 6: E8M0 bytes
+  int64_t mx_scale_stride = 0; // bytes
 };
+
+bool is_mx(int mode) { return mode == 5 || mode == 6; }
+// bytes of quantised output per row (modes 2, 5, 6)
+int64_t q_row_bytes(int mode, int64_t hidden) { return mode == 6 ? hidden / 2 : hidden; }
 
 bool has_res(int mode) { return mode != 1; }
 bool has_out(int mode) { return mode != 0; }
@@ -215,9 +230,14 @@ int check_problem(const Problem& p) {
   if (has_res(p.mode) && p.res_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "residual row stride %lld < hidden %lld", (long long)p.res_stride,
                 (long long)p.hidden);
-  if (has_out(p.mode) && p.out_stride < p.hidden)
-    return fail(HPRMS_E_INVALID, "output row stride %lld < hidden %lld", (long long)p.out_stride,
-                (long long)p.hidden);
+  if (is_mx(p.mode) && p.hidden % 32 != 0)
+    return fail(HPRMS_E_INVALID, "MX output needs hidden %% 32 == 0 (got %lld)", (long long)p.hidden);
+  if (has_out(p.mode) && p.out_stride < q_row_bytes(p.mode, p.hidden))
+    return fail(HPRMS_E_INVALID, "output row stride %lld < %lld", (long long)p.out_stride,
+                (long long)q_row_bytes(p.mode, p.hidden));
+  if (is_mx(p.mode) && p.mx_scale_stride < p.hidden / 32)
+    return fail(HPRMS_E_INVALID, "scale row stride %lld < hidden / 32 = %lld", (long long)p.mx_scale_stride,
+                (long long)(p.hidden / 32));
   if (p.mode == 3 && p.res_out_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "residual output row stride %lld < hidden %lld", (long long)p.res_out_stride,
                 (long long)p.hidden);
@@ -227,7 +247,7 @@ int check_problem(const Problem& p) {
   if (p.rows == 0) return HPRMS_OK;
   if (p.mode == 4 && !p.parts) return fail(HPRMS_E_INVALID, "null parts array");
   if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) || (p.mode == 2 && !p.scale) ||
-      (p.mode == 3 && !p.res_out))
+      (p.mode == 3 && !p.res_out) || (is_mx(p.mode) && !p.mx_scales))
     return fail(HPRMS_E_INVALID, "null tensor pointer");
   if (p.mode == 4) {
     for (int g = 0; g < p.nparts; ++g) {
@@ -258,8 +278,10 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   if (!aligned16(p.x) || !aligned16(p.w)) return false;
   if (p.x_stride % 8 != 0) return false;
   if (has_res(p.mode) && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
-  if (p.mode == 2) {
+  if (p.mode == 2 || p.mode == 5) {
     if (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0) return false;
+  } else if (p.mode == 6) {
+    if (((uintptr_t)p.out & 3u) != 0 || p.out_stride % 4 != 0) return false;
   } else if (has_out(p.mode) && (!aligned16(p.out) || p.out_stride % 8 != 0)) {
     return false;
   }
@@ -323,6 +345,11 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   } else {
     table_config(p.rows, p.hidden, p.mode, &c);
   }
+  if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
+    return fail(HPRMS_E_INVALID,
+                "MX output needs 16-byte aligned input, residual and weight, row strides %% 8 == 0, and the "
+                "output %s", p.mode == 5 ? "8-byte aligned with a row stride % 8 == 0" :
+                "4-byte aligned with a row stride % 4 == 0");
   if (c.tier != 3 && !vec_fits(p, c)) {
     if (forced && forced->tier != 0)
       return fail(HPRMS_E_INVALID,
@@ -346,7 +373,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
 
   FusedArgs a = {};
   a.x = (const uint16_t*)p.x;
-  a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 ? p.x : p.out);
+  a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x : p.out);
   a.res_out = (uint16_t*)p.res_out;
   a.res_out_stride = p.res_out_stride;
   a.nparts = p.nparts;
@@ -354,13 +381,15 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   a.res = (uint16_t*)p.res;
   a.w = (const uint16_t*)p.w;
   a.rows = p.rows;
-  a.q = p.mode == 2 ? (uint8_t*)p.out : nullptr;
+  a.q = p.mode == 2 || is_mx(p.mode) ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
-  a.q_stride = p.mode == 2 ? p.out_stride : 0;
+  a.q_stride = p.mode == 2 || is_mx(p.mode) ? p.out_stride : 0;
+  a.mx_scale = (uint8_t*)p.mx_scales;
+  a.mx_scale_stride = p.mx_scale_stride;
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   a.ngroups = (p.rows + rpb - 1) / rpb;
   a.x_stride = p.x_stride;
-  a.out_stride = p.mode == 0 || p.mode == 2 ? p.x_stride : p.out_stride;
+  a.out_stride = p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x_stride : p.out_stride;
   a.res_stride = p.res_stride;
   a.hidden = (int32_t)p.hidden;
   a.nvec = (int32_t)(p.hidden / 8);
@@ -450,6 +479,19 @@ int hprms_reduce_add_rmsnorm(void* out, const void* const* parts, int nparts, co
   return run(p, nullptr, stream);
 }
 
+int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const void* weight, void* residual,
+                               int64_t rows, int64_t hidden, int64_t out_row_stride, int64_t scale_row_stride,
+                               int64_t input_row_stride, int64_t residual_row_stride, int format, int dtype,
+                               double eps, hipStream_t stream) {
+  if (format != HPRMS_MX_FP8_E4M3 && format != HPRMS_MX_FP4_E2M1)
+    return fail(HPRMS_E_INVALID, "format must be HPRMS_MX_FP8_E4M3 or HPRMS_MX_FP4_E2M1 (got %d)", format);
+  Problem p{format == HPRMS_MX_FP8_E4M3 ? 5 : 6, const_cast<void*>(input), out, residual, weight, rows, hidden,
+            input_row_stride, out_row_stride, residual_row_stride, dtype, eps};
+  p.mx_scales = scales;
+  p.mx_scale_stride = scale_row_stride;
+  return run(p, nullptr, stream);
+}
+
 int hprms_rmsnorm(void* out, const void* in, const void* weight, int64_t rows, int64_t hidden,
                   int64_t out_row_stride, int64_t in_row_stride, int dtype, double eps, hipStream_t stream) {
   Problem p{1, const_cast<void*>(in), out, nullptr, weight, rows, hidden, in_row_stride, out_row_stride,
@@ -461,7 +503,7 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode < 0 || mode > 4) return fail(HPRMS_E_INVALID, "mode must be in [0, 4] (got %d)", mode);
+  if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
   table_config(rows, hidden, mode, config);
   if (hidden % 8 != 0) config->tier = 3;
@@ -492,7 +534,7 @@ int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int6
 int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode < 0 || mode > 4) return fail(HPRMS_E_INVALID, "mode must be in [0, 4] (got %d)", mode);
+  if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
   if (capacity < 0 || (capacity > 0 && !out)) return fail(HPRMS_E_INVALID, "bad output array");
   int n = 0;
   for (const FusedEntry& e : kFused) {

@@ -98,6 +98,27 @@ __device__ __forceinline__ void store8(u32x2 v, __amdgpu_buffer_rsrc_t r, uint32
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, AUX);
 }
 
+template <int AUX>
+__device__ __forceinline__ void store4(uint32_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, AUX);
+}
+
+template <int AUX>
+__device__ __forceinline__ void store1(uint8_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, AUX);
+}
+
+// ---- OCP MX (E2M1 elements) ----------------------------------------------------------
+// binary32 -> E2M1 code (sign in bit 3): round to nearest, ties to the even
+// code, by the midpoints of the value table 0 .5 1 1.5 2 3 4 6; saturates at 6
+// (infinity included); NaN gives a zero code with NaN's sign bit.
+__device__ __forceinline__ uint32_t e2m1_code(float v) {
+  const float a = __builtin_fabsf(v);
+  const uint32_t c = (uint32_t)(a > 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a > 1.25f) +
+                     (uint32_t)(a >= 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a >= 3.5f) + (uint32_t)(a > 5.0f);
+  return c | ((__float_as_uint(v) >> 28) & 8u);
+}
+
 // ---- reductions ---------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -132,6 +153,12 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
 
 // Unsigned maximum over aligned groups of WIDTH lanes, same lane pattern as
 // group_sum.  Must be called with every lane of the wave active.
+// Unsigned maximum over each aligned quad of lanes (every lane gets it).
+__device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
+  v = __builtin_elementwise_max(v, dpp_u32<0xB1>(v));  // quad_perm [1,0,3,2]
+  return __builtin_elementwise_max(v, dpp_u32<0x4E>(v));  // quad_perm [2,3,0,1]
+}
+
 template <int WIDTH>
 __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
   static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group width");

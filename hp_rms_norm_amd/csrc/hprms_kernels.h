@@ -38,7 +38,16 @@
 // sum goes to res_out and the output to out.  MODE 4 adds nparts partial rows
 // first (the buffers of a tensor-parallel all-reduce): a = rne(p0 + p1 + ...)
 // summed in fp32 left to right and rounded once, then the fused op on a, with
-// the residual updated in place and the output written to out.
+// the residual updated in place and the output written to out.  MODES 5 and 6
+// are the fused op with an OCP MX output (MXFP8 / MXFP4): the 16-bit output y
+// is cut into blocks of 32 consecutive elements -- the 8 elements of four
+// adjacent lanes at one vector index, so a block's maximum is one DPP quad
+// reduction -- each with the scale 2^s, s = floor(log2 max|y|) - emax (8 for
+// E4M3, 2 for E2M1) clamped to [-127, 127], written as one E8M0 byte, and
+// elements y / 2^s rounded to nearest even and saturated (E4M3 bytes; E2M1
+// codes two per byte, the even element in the low nibble).  A block holding
+// NaN or infinity gets the scale byte 0xFF and unscaled elements.  The
+// residual is updated in place and `input` is only read, as in MODE 2.
 #pragma once
 
 #include "hprms_device.h"
@@ -66,6 +75,8 @@ struct FusedArgs {
   int64_t res_out_stride;
   int32_t nparts;        // MODE 4: number of partial rows summed (x is part 0)
   const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
+  uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes, hidden / 32 per row
+  int64_t mx_scale_stride;  // bytes between scale rows
 };
 
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
@@ -78,7 +89,9 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;
   constexpr int NW = BLOCK / 64;
   constexpr int VREG = VPL - LDSV;
+  static_assert(MODE >= 0 && MODE <= 6, "mode");
   constexpr bool RES = MODE != 1;                                  // residual stream read
+  constexpr bool MX = MODE == 5 || MODE == 6;                      // OCP MX output
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
@@ -124,11 +137,22 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
       srs = make_rsrc(a.res_out + row0 * a.res_out_stride, sbytes);
       soff = (uint32_t)rib * (uint32_t)a.res_out_stride * 2u + (uint32_t)lane * 16u;
     }
-    if constexpr (MODE == 2) {
-      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + a.hidden);
+    // MX: the scale bytes of the row group
+    __amdgpu_buffer_rsrc_t xsrs = xrs;
+    uint32_t xsoff = 0;
+    if constexpr (MODE == 2 || MX) {
+      constexpr uint32_t QB = MODE == 6 ? 4u : 8u;  // output bytes per 8-element vector
+      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + a.hidden * (int64_t)QB / 8);
       ors = make_rsrc(a.q + row0 * a.q_stride, qbytes);
-      ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)lane * 8u;
-    } else if constexpr (OUT16) {
+      ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)lane * QB;
+    }
+    if constexpr (MX) {
+      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * a.mx_scale_stride + a.hidden / 32);
+      xsrs = make_rsrc(a.mx_scale + row0 * a.mx_scale_stride, sbytes);
+      // one lane of each quad writes its block's scale byte
+      xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)a.mx_scale_stride + (uint32_t)lane / 4u : kOOB;
+    }
+    if constexpr (OUT16) {
       const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + a.hidden) * 2);
       ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
@@ -224,7 +248,47 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     }
     const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
 
-    if constexpr (MODE != 2) {
+    if constexpr (MX) {
+      constexpr int EMAX = MODE == 5 ? 8 : 2;
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
+        u32x4 y;
+        uint32_t m2 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          y[j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+          const uint32_t mag = y[j] & 0x7fff7fffu;
+          m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(mag & 0xffffu, mag >> 16));
+        }
+        // the block maximum as binary32: its exponent field is floor(log2) + 127
+        // (0 for zero and for bf16 subnormals, which clamp; 255 for NaN / inf)
+        const uint32_t e32 = __float_as_uint(F::one((uint16_t)quad_max_u32(m2))) >> 23;
+        int sexp = (int)e32 - 127 - EMAX;
+        if (e32 == 0 || sexp < -127) sexp = -127;
+        const bool bad = e32 == 255u;
+        const float mul = bad ? 1.0f : __uint_as_float((uint32_t)(127 - sexp) << 23);
+        const bool ok = row_ok && vec_ok[k];
+        store1<SAUX>((uint8_t)(bad ? 0xFFu : (uint32_t)(sexp + 127)), xsrs,
+                     ok && xsoff != kOOB ? xsoff + (uint32_t)(k * (LPR / 4)) : kOOB);
+        if constexpr (MODE == 5) {
+          u32x2 q;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t y0 = y[2 * h], y1 = y[2 * h + 1];
+            q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * mul), clamp_e4m3(F::hi(y0) * mul),
+                               clamp_e4m3(F::lo(y1) * mul), clamp_e4m3(F::hi(y1) * mul));
+          }
+          store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
+        } else {
+          uint32_t q = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            q |= (e2m1_code(F::lo(y[j]) * mul) | (e2m1_code(F::hi(y[j]) * mul) << 4)) << (8 * j);
+          store4<SAUX>(q, ors, ok ? ooff + k * (LPR * 4u) : kOOB);
+        }
+      }
+    } else if constexpr (MODE != 2) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];

@@ -333,6 +333,63 @@ void reduce_rms_norm_meta(at::Tensor& out, at::TensorList parts, const at::Tenso
   (void)eps;
 }
 
+// ---- fused op with an OCP MX output ---------------------------------------------------
+struct MxShape {
+  FusedShape f;
+  int64_t out_stride, scale_stride;
+};
+
+MxShape check_mx(const at::Tensor& out, const at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,
+                 const at::Tensor& residual, int64_t format) {
+  TORCH_CHECK(format == HPRMS_MX_FP8_E4M3 || format == HPRMS_MX_FP4_E2M1,
+              "format must be 0 (MXFP8, E4M3) or 1 (MXFP4, E2M1)");
+  MxShape s;
+  s.f = check_fused(input, weight, residual);
+  TORCH_CHECK(s.f.hidden % 32 == 0, "MX output needs hidden_dim % 32 == 0");
+  const bool fp8 = format == HPRMS_MX_FP8_E4M3;
+  TORCH_CHECK(out.scalar_type() == at::kByte ||
+                  out.scalar_type() == (fp8 ? at::kFloat8_e4m3fn : at::kFloat4_e2m1fn_x2),
+              fp8 ? "out.dtype() must be float8_e4m3fn or uint8" : "out.dtype() must be float4_e2m1fn_x2 or uint8");
+  TORCH_CHECK(scales.scalar_type() == at::kByte || scales.scalar_type() == at::kFloat8_e8m0fnu,
+              "scales.dtype() must be float8_e8m0fnu or uint8");
+  const int64_t qw = fp8 ? s.f.hidden : s.f.hidden / 2;
+  for (const at::Tensor* t : {&out, &scales}) {
+    TORCH_CHECK(t->dim() == input.dim(), "out and scales must have input.dim() dimensions");
+    for (int64_t i = 0; i + 1 < input.dim(); ++i)
+      TORCH_CHECK(t->size(i) == input.size(i), "out and scales must match input in the leading dimensions");
+    TORCH_CHECK(t->stride(-1) == 1, "out and scales must be contiguous in the last dimension");
+    TORCH_CHECK(t->device() == input.device(), "out, scales and input must be on the same device");
+  }
+  TORCH_CHECK(out.size(-1) == qw, "out.size(-1) must be ", qw, " (", fp8 ? "hidden" : "hidden / 2", ")");
+  TORCH_CHECK(scales.size(-1) == s.f.hidden / 32, "scales.size(-1) must be hidden / 32 = ", s.f.hidden / 32);
+  int64_t r = 0;
+  rows_of(out, qw, &r, &s.out_stride);
+  rows_of(scales, s.f.hidden / 32, &r, &s.scale_stride);
+  if (s.f.rows > 0) {
+    at::assert_no_overlap(out, scales);
+    at::assert_no_overlap(out, residual);
+    at::assert_no_overlap(scales, residual);
+  }
+  return s;
+}
+
+void rms_norm_mx_hip(at::Tensor& out, at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,
+                     at::Tensor& residual, int64_t format, double eps) {
+  const MxShape s = check_mx(out, scales, input, weight, residual, format);
+  if (s.f.rows == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm_mx(out.data_ptr(), scales.data_ptr(), input.data_ptr(), weight.data_ptr(),
+                                          residual.data_ptr(), s.f.rows, s.f.hidden, s.out_stride, s.scale_stride,
+                                          s.f.in_stride, s.f.res_stride, (int)format, s.f.dtype, eps, stream));
+}
+
+void rms_norm_mx_meta(at::Tensor& out, at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,
+                      at::Tensor& residual, int64_t format, double eps) {
+  (void)check_mx(out, scales, input, weight, residual, format);
+  (void)eps;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(hp_rms_norm, m) {
@@ -345,6 +402,8 @@ TORCH_LIBRARY(hp_rms_norm, m) {
   m.def("rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, Tensor residual, "
         "float eps) -> ()");
   m.def("reduce_add_rms_norm(Tensor(a!) out, Tensor[] parts, Tensor weight, Tensor(b!) residual, float eps) -> ()");
+  m.def("rms_norm_mx_quant(Tensor(a!) out, Tensor(b!) scales, Tensor input, Tensor weight, Tensor(c!) residual, "
+        "int format, float eps) -> ()");
 }
 
 // ROCm builds of PyTorch expose HIP devices under the CUDA dispatch key.
@@ -356,6 +415,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_hip);
   m.impl("rms_norm_out", &rms_norm_out_hip);
   m.impl("reduce_add_rms_norm", &reduce_rms_norm_hip);
+  m.impl("rms_norm_mx_quant", &rms_norm_mx_hip);
 }
 
 // Shape checks only, for fake tensors / torch.compile tracing.  Meta tensors
@@ -368,4 +428,5 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_meta);
   m.impl("rms_norm_out", &rms_norm_out_meta);
   m.impl("reduce_add_rms_norm", &reduce_rms_norm_meta);
+  m.impl("rms_norm_mx_quant", &rms_norm_mx_meta);
 }

@@ -4,7 +4,10 @@ argument order, in-place semantics and ``None`` return."""
 import torch
 
 __all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "fused_add_rms_norm_out",
-           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "reduce_add_rms_norm"]
+           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "reduce_add_rms_norm", "hp_rms_norm_mx",
+           "fused_add_rms_norm_mxfp8", "fused_add_rms_norm_mxfp4", "MXFP8", "MXFP4"]
+
+MXFP8, MXFP4 = 0, 1  # element formats of the OCP MX output
 
 
 def hp_rms_norm(input, weight, residual, eps):
@@ -83,3 +86,43 @@ def reduce_add_rms_norm(out, parts, weight, residual, eps):
     read, and ``out`` may be one of them.  With one part this is
     ``hp_rms_norm`` writing its output to ``out``.  No reference counterpart."""
     torch.ops.hp_rms_norm.reduce_add_rms_norm.default(out, list(parts), weight, residual, eps)
+
+
+def hp_rms_norm_mx(output, scales, input, weight, residual, eps, format):
+    """Fused residual-add + RMSNorm with an OCP MX block-scaled output
+    (``format`` MXFP8: E4M3 elements, MXFP4: E2M1 elements two per byte, even
+    element in the low nibble).  ``residual <- input + residual`` in place;
+    with ``y`` the op's 16-bit output, each block of 32 consecutive elements
+    of a row gets ``scales = floor(log2(max|y|)) - emax`` as an E8M0 byte
+    (emax 8 / 2; 0xFF for a block holding NaN or inf) and ``output = y / 2^s``
+    rounded to nearest even, saturated.  ``output``: ``[..., H]``
+    float8_e4m3fn (MXFP8) or ``[..., H // 2]`` float4_e2m1fn_x2 (MXFP4), or
+    uint8; ``scales``: ``[..., H // 32]`` float8_e8m0fnu or uint8.  ``input``
+    is only read.  Needs ``H % 32 == 0``.  No reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_mx_quant.default(output, scales, input, weight, residual, format, eps)
+
+
+def _mx_alloc(input, format):
+    h = input.shape[-1]
+    if format == MXFP8:
+        q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
+    else:
+        q = torch.empty(input.shape[:-1] + (h // 2,), dtype=torch.float4_e2m1fn_x2, device=input.device)
+    scales = torch.empty(input.shape[:-1] + (h // 32,), dtype=torch.float8_e8m0fnu, device=input.device)
+    return q, scales
+
+
+def fused_add_rms_norm_mxfp8(input, residual, weight, eps):
+    """Allocating MXFP8 form of ``hp_rms_norm_mx``: returns ``(q, scales)``;
+    ``residual`` is updated in place."""
+    q, scales = _mx_alloc(input, MXFP8)
+    hp_rms_norm_mx(q, scales, input, weight, residual, eps, MXFP8)
+    return q, scales
+
+
+def fused_add_rms_norm_mxfp4(input, residual, weight, eps):
+    """Allocating MXFP4 form of ``hp_rms_norm_mx``: returns ``(q, scales)``
+    with ``q`` packed two E2M1 codes per byte; ``residual`` is updated in place."""
+    q, scales = _mx_alloc(input, MXFP4)
+    hp_rms_norm_mx(q, scales, input, weight, residual, eps, MXFP4)
+    return q, scales

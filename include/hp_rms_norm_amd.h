@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 3
+#define HPRMS_ABI_VERSION 4
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -40,6 +40,10 @@ typedef enum {
 
 /* most partial buffers hprms_reduce_add_rmsnorm() sums */
 #define HPRMS_MAX_PARTS 8
+
+/* element formats of hprms_fused_add_rmsnorm_mx() (OCP Microscaling Formats v1.0) */
+#define HPRMS_MX_FP8_E4M3 0   /* MXFP8: one E4M3 byte per element */
+#define HPRMS_MX_FP4_E2M1 1   /* MXFP4: two E2M1 codes per byte, the even element in the low nibble */
 
 /* streamer operations for hprms_streamer() */
 #define HPRMS_STREAM_COPY 0   /* out = in (the reference "relu": activation_kernels.cuh:99-119) */
@@ -148,6 +152,30 @@ int hprms_reduce_add_rmsnorm(void* out, const void* const* parts, int nparts, co
                              int dtype, double eps, hipStream_t stream);
 
 /*
+ * Fused residual-add + RMSNorm with an OCP MX block-scaled output (the input
+ * format of gfx950's scaled MFMA instructions):
+ *   residual[r, :] <- rne16(f32(input) + f32(residual))        (in place)
+ *   y              =  the 16-bit output of hprms_fused_add_rmsnorm
+ *   per block of 32 consecutive elements of a row:
+ *     s          = clamp(floor(log2(max |y|)) - emax, -127, 127)   (emax 8 for E4M3, 2 for E2M1)
+ *     scales[b]  = s + 127 (E8M0; 0xFF if the block holds a NaN or an infinity)
+ *     out        = y / 2^s rounded to nearest even in the element format,
+ *                  saturated to +-448 (E4M3) or +-6 (E2M1)
+ * `format` is HPRMS_MX_FP8_E4M3 (out: hidden bytes per row) or
+ * HPRMS_MX_FP4_E2M1 (out: hidden / 2 bytes per row); `scales` holds hidden / 32
+ * bytes per row; both row strides are in bytes.  `input` is only read.  Needs
+ * hidden % 32 == 0, 16-byte aligned input, residual and weight with row
+ * strides % 8 == 0, and `out` 8-byte (E4M3) or 4-byte (E2M1) aligned with a
+ * row stride that is a multiple of that; there is no general-tier fallback.
+ * No counterpart in the reference.
+ */
+int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const void* weight,
+                               void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                               int64_t scale_row_stride, int64_t input_row_stride,
+                               int64_t residual_row_stride, int format, int dtype, double eps,
+                               hipStream_t stream);
+
+/*
  * Kernel configuration of the fused add+RMSNorm family.  Used by the tuning
  * sweep and by tests that exercise every tier at every shape; normal callers
  * use hprms_fused_add_rmsnorm(), which picks the configuration from the
@@ -175,7 +203,8 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
 /* The configuration the library would use for (rows, hidden, dtype) and
  * `mode` (0: hprms_fused_add_rmsnorm, 1: hprms_rmsnorm, 2:
  * hprms_fused_add_rmsnorm_fp8, 3: hprms_fused_add_rmsnorm_out, 4:
- * hprms_reduce_add_rmsnorm), written to *config (tier 3 when only the
+ * hprms_reduce_add_rmsnorm, 5 / 6: hprms_fused_add_rmsnorm_mx with
+ * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1), written to *config (tier 3 when only the
  * general kernel fits hidden).  Pure function of its arguments; touches no
  * device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);

@@ -37,6 +37,15 @@
  * fused op to a with the output written to `out`.  It has no counterpart in
  * the reference; with P = 1 it is the fused op.
  *
+ * The MX forms (hprms_oracle_fused_add_rmsnorm_mx) quantise the 16-bit
+ * output y in blocks of 32 consecutive elements of a row, as the OCP
+ * Microscaling Formats (MX) v1.0 specification defines it: scale exponent
+ * s = floor(log2(max |y| over the block)) - emax (emax = 8 for E4M3 elements,
+ * 2 for E2M1), clamped to [-127, 127] and stored as E8M0 (s + 127; 0xFF when
+ * the block holds a NaN or an infinity); elements = y / 2^s rounded to nearest
+ * even in the element format, saturated to its largest normal (448 / 6).  E2M1
+ * codes pack two to a byte, the even element in the low nibble.
+ *
  * Parity pins (tests/test_oracle.py): golden vectors made by the reference's
  * own formula in torch (tests/golden/), the live torch formula, a binary64
  * brute force, closed forms (constant rows, power-of-two scaling), numpy's
@@ -388,6 +397,141 @@ int hprms_oracle_reduce_add_rmsnorm(uint16_t* out, const uint16_t* const* parts,
   }
   (void)threads;
   return 0;
+}
+
+/* ---- OCP MX block formats ------------------------------------------------ */
+
+/* E2M1 magnitudes by code: 0, 0.5, 1, 1.5, 2, 3, 4, 6. */
+static const float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+
+/* binary32 -> E2M1 code (sign in bit 3): the nearest magnitude, ties to the
+ * even code, saturating at 6; NaN gives a zero code with NaN's sign bit (the
+ * block's scale marks it NaN). */
+uint8_t hprms_oracle_f32_to_e2m1(float f) {
+  uint8_t sign = (f2u(f) >> 31) ? 8u : 0u;
+  float a = fabsf(f);
+  if (a != a) return sign;
+  if (a >= 6.0f) return (uint8_t)(sign | 7);  /* saturation, infinity included */
+  int best = 0;
+  float bd = INFINITY;
+  for (int c = 0; c < 8; ++c) {
+    float d = fabsf(a - kE2M1[c]);
+    if (d < bd || (d == bd && (c & 1) == 0)) {
+      bd = d;
+      best = c;
+    }
+  }
+  return (uint8_t)(sign | best);
+}
+
+float hprms_oracle_e2m1_to_f32(uint8_t c) {
+  float v = kE2M1[c & 7];
+  return (c & 8) ? -v : v;
+}
+
+/* planted mistakes of the MX step (tests only; 0 = the algorithm) */
+enum {
+  XMUT_CEIL_SCALE = 1,   /* ceil(log2 amax) instead of floor */
+  XMUT_EMAX_PLUS_1 = 2,  /* emax one too large */
+  XMUT_TRUNCATE = 3,     /* elements truncated instead of rounded */
+  XMUT_NIBBLES = 4       /* E2M1: odd element in the low nibble */
+};
+
+/* E8M0 scale exponent of a block from its largest magnitude; returns 128 for
+ * NaN / infinity (encoded 0xFF). */
+static int mx_scale_exp(float amax, int emax, int mutation) {
+  if (amax != amax || isinf(amax)) return 128;
+  if (amax == 0.0f) return -127;
+  int e;
+  float m = frexpf(amax, &e);           /* amax = m * 2^e, m in [0.5, 1) */
+  int fl = e - 1;                       /* floor(log2(amax)) */
+  if (mutation == XMUT_CEIL_SCALE && m != 0.5f) fl = e;
+  int s = fl - (mutation == XMUT_EMAX_PLUS_1 ? emax + 1 : emax);
+  if (s < -127) s = -127;
+  if (s > 127) s = 127;
+  return s;
+}
+
+/* The MX step on rows of 16-bit values y: scales[b] (E8M0) and q for each
+ * block of 32.  elem 0 = MXFP8 (one E4M3 byte per element), elem 1 = MXFP4
+ * (two E2M1 codes per byte, the even element in the low nibble). */
+static void mx_quantize_row(const uint16_t* y, int64_t hidden, int elem, int dtype, uint8_t* qr, uint8_t* sr,
+                            int mutation) {
+  const int emax = elem == 0 ? 8 : 2;
+  for (int64_t b = 0; b < hidden / 32; ++b) {
+    float amax = 0.0f;
+    int nan = 0;
+    for (int j = 0; j < 32; ++j) {
+      float v = fabsf(to_f32(y[b * 32 + j], dtype));
+      if (v != v) nan = 1;
+      else if (v > amax) amax = v;
+    }
+    int s = mx_scale_exp(nan ? NAN : amax, emax, mutation);
+    sr[b] = (uint8_t)(s == 128 ? 0xFF : s + 127);
+    for (int j = 0; j < 32; ++j) {
+      /* a NaN block keeps its values unscaled; the 0xFF scale marks it */
+      float v = s == 128 ? to_f32(y[b * 32 + j], dtype) : ldexpf(to_f32(y[b * 32 + j], dtype), -s);
+      int64_t col = b * 32 + j;
+      if (elem == 0) {
+        if (mutation == XMUT_TRUNCATE) v = truncf(v * 8.0f) / 8.0f;
+        v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
+        qr[col] = hprms_oracle_f32_to_e4m3(v);
+      } else {
+        if (mutation == XMUT_TRUNCATE) v = (v < 0 ? -1.0f : 1.0f) * floorf(fabsf(v) * 2.0f) / 2.0f;
+        uint8_t c = hprms_oracle_f32_to_e2m1(v);
+        int hi = (int)(col & 1) ^ (mutation == XMUT_NIBBLES);
+        uint8_t* dst = &qr[col / 2];
+        if (hi) *dst = (uint8_t)((*dst & 0x0F) | (c << 4));
+        else *dst = (uint8_t)((*dst & 0xF0) | c);
+      }
+    }
+  }
+}
+
+/* The MX step alone, on [rows, hidden] 16-bit values (contiguous rows). */
+int hprms_oracle_mx_quantize(uint8_t* q, uint8_t* scales, const uint16_t* y, int64_t rows, int64_t hidden,
+                             int elem, int dtype, int mutation) {
+  if (rows < 0 || hidden < 32 || hidden % 32 || (elem != 0 && elem != 1)) return -22;
+  if (dtype != ORACLE_BF16 && dtype != ORACLE_FP16) return -22;
+  const int64_t qw = elem == 0 ? hidden : hidden / 2;
+  for (int64_t i = 0; i < rows; ++i)
+    mx_quantize_row(y + i * hidden, hidden, elem, dtype, q + i * qw, scales + i * (hidden / 32), mutation);
+  return 0;
+}
+
+/* Fused op with an OCP MX output (the step above applied to the fused op's
+ * 16-bit output).  q has q_row_stride bytes per row, scales
+ * scale_row_stride bytes per row (hidden / 32 used).  The residual is updated
+ * in place; input is only read.  hidden % 32 == 0. */
+int hprms_oracle_fused_add_rmsnorm_mx(uint8_t* q, uint8_t* scales, const uint16_t* input,
+                                      const uint16_t* weight, uint16_t* residual, int64_t rows,
+                                      int64_t hidden, int64_t q_row_stride, int64_t scale_row_stride,
+                                      int64_t input_row_stride, int64_t residual_row_stride, int elem,
+                                      int dtype, double eps, int threads, int mutation) {
+  if (!check_rows(rows, hidden, input_row_stride, residual_row_stride)) return -22;
+  if ((dtype != ORACLE_BF16 && dtype != ORACLE_FP16) || (elem != 0 && elem != 1) || hidden % 32) return -22;
+  if (q_row_stride < (elem == 0 ? hidden : hidden / 2) || scale_row_stride < hidden / 32) return -22;
+  if (rows == 0) return 0;
+  if (!q || !scales || !input || !weight || !residual) return -22;
+  float epsf = (float)eps;
+#ifdef _OPENMP
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+  for (int64_t i = 0; i < rows; ++i) {
+    uint16_t* y = (uint16_t*)malloc((size_t)hidden * sizeof(uint16_t));
+    if (!y) continue;
+    memcpy(y, input + i * input_row_stride, (size_t)hidden * sizeof(uint16_t));
+    fused_row(y, weight, residual + i * residual_row_stride, hidden, dtype, epsf, MUT_NONE);
+    mx_quantize_row(y, hidden, elem, dtype, q + i * q_row_stride, scales + i * scale_row_stride, mutation);
+    free(y);
+  }
+  (void)threads;
+  return 0;
+}
+
+void hprms_oracle_e2m1_from_f32(const float* src, uint8_t* dst, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dst[i] = hprms_oracle_f32_to_e2m1(src[i]);
 }
 
 void hprms_oracle_e4m3_from_f32(const float* src, uint8_t* dst, int64_t n) {

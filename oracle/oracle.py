@@ -36,6 +36,15 @@ REDUCE_MUTATIONS = {
     "reversed": 3,
 }
 
+# planted mistakes of the MX quantisation step (fused_add_rmsnorm_mx)
+MX_MUTATIONS = {
+    "ceil_scale": 1,
+    "emax_plus_1": 2,
+    "truncate": 3,
+    "nibbles_swapped": 4,
+}
+MXFP8, MXFP4 = 0, 1
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhprms_oracle.so")
 _lib = None
@@ -70,6 +79,12 @@ def lib():
         L.hprms_oracle_fused_add_rmsnorm_fp8.argtypes = [_u8p, _f32p, _u16p, _u16p, _u16p, _i64, _i64, _i64,
                                                          _i64, _i64, ctypes.c_int, ctypes.c_double, ctypes.c_int]
         L.hprms_oracle_e4m3_from_f32.argtypes = [_f32p, _u8p, _i64]
+        L.hprms_oracle_fused_add_rmsnorm_mx.argtypes = [_u8p, _u8p, _u16p, _u16p, _u16p, _i64, _i64, _i64, _i64,
+                                                        _i64, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_double,
+                                                        ctypes.c_int, ctypes.c_int]
+        L.hprms_oracle_e2m1_from_f32.argtypes = [_f32p, _u8p, _i64]
+        L.hprms_oracle_mx_quantize.argtypes = [_u8p, _u8p, _u16p, _i64, _i64, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int]
         L.hprms_oracle_reduce_add_rmsnorm.argtypes = [_u16p, ctypes.POINTER(_u16p), ctypes.c_int, _u16p, _u16p,
                                                       _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
                                                       ctypes.c_double, ctypes.c_int, ctypes.c_int]
@@ -226,3 +241,48 @@ def e4m3_ulp_distance(a, b):
     d = np.abs(ordered(a) - ordered(b))
     d = np.where(na & nb, 0, d)
     return np.where(na ^ nb, 1 << 20, d)
+
+
+def fused_add_rmsnorm_mx(x, w, r, eps, dtype, elem, threads=1, mutation=0):
+    """OCP MX form: returns (q uint8 [rows, H] (MXFP8) or [rows, H/2] (MXFP4,
+    two E2M1 codes per byte, the even element in the low nibble), scales uint8
+    [rows, H/32] (E8M0), new residual); x is not modified."""
+    xc = np.ascontiguousarray(x)
+    rows, hidden, sx = _rows(xc)
+    ro = np.array(r, dtype=np.uint16, copy=True, order="C")
+    qw = hidden if elem == MXFP8 else hidden // 2
+    q = np.zeros((rows, qw), dtype=np.uint8)
+    sc = np.zeros((rows, max(1, hidden // 32)), dtype=np.uint8)
+    if isinstance(mutation, str):
+        mutation = MX_MUTATIONS[mutation]
+    _u8 = ctypes.POINTER(ctypes.c_uint8)
+    rc = lib().hprms_oracle_fused_add_rmsnorm_mx(q.ctypes.data_as(_u8), sc.ctypes.data_as(_u8), _p16(xc),
+                                                 _p16(np.ascontiguousarray(w)), _p16(ro), rows, hidden, qw,
+                                                 sc.shape[1], sx, hidden, elem, dtype, float(eps), threads, mutation)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+    return q, sc, ro
+
+
+def e2m1_from_f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint8)
+    lib().hprms_oracle_e2m1_from_f32(a.ctypes.data_as(_f32p), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
+                                     a.size)
+    return out
+
+
+def mx_quantize(y, dtype, elem, mutation=0):
+    """The MX step alone on [rows, H] 16-bit patterns: returns (q, scales)."""
+    yc = np.ascontiguousarray(y, dtype=np.uint16)
+    rows, hidden = yc.shape
+    q = np.zeros((rows, hidden if elem == MXFP8 else hidden // 2), dtype=np.uint8)
+    sc = np.zeros((rows, hidden // 32), dtype=np.uint8)
+    if isinstance(mutation, str):
+        mutation = MX_MUTATIONS[mutation]
+    _u8 = ctypes.POINTER(ctypes.c_uint8)
+    rc = lib().hprms_oracle_mx_quantize(q.ctypes.data_as(_u8), sc.ctypes.data_as(_u8), _p16(yc), rows, hidden, elem,
+                                        dtype, mutation)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments ({rc})")
+    return q, sc

@@ -41,6 +41,10 @@ int main(void) {
   EXPECT(hprms_reduce_add_rmsnorm(x, parts, HPRMS_MAX_PARTS + 1, w, r, 4, 64, 64, 64, 64, HPRMS_DTYPE_BF16, 1e-6,
                                   NULL) == HPRMS_E_INVALID);
   EXPECT(strstr(hprms_last_error(), "nparts") != NULL);
+  EXPECT(hprms_fused_add_rmsnorm_mx(x, r, x, w, r, 4, 4096, 2048, 128, 4096, 4096, 7, HPRMS_DTYPE_BF16, 1e-6, NULL) ==
+         HPRMS_E_INVALID);
+  EXPECT(hprms_fused_add_rmsnorm_mx(NULL, NULL, NULL, NULL, NULL, 0, 4096, 2048, 128, 4096, 4096, HPRMS_MX_FP4_E2M1,
+                                    HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
 
   /* zero rows: validated, no launch, null pointers accepted */
   EXPECT(hprms_fused_add_rmsnorm(NULL, NULL, NULL, 0, 4096, 4096, 4096, HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
@@ -50,7 +54,7 @@ int main(void) {
                                   NULL) == HPRMS_OK);
 
   /* the table: every mode has a vector-tier kernel covering H = 4096 */
-  for (mode = 0; mode <= 4; ++mode) {
+  for (mode = 0; mode <= 6; ++mode) {
     int n;
     EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, mode, &c) == HPRMS_OK);
     EXPECT(c.tier == 1 || c.tier == 2);
@@ -58,7 +62,7 @@ int main(void) {
     n = hprms_kernel_configs(HPRMS_DTYPE_BF16, mode, NULL, 0);
     EXPECT(n > 0);
   }
-  EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, 5, &c) == HPRMS_E_INVALID);
+  EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, 7, &c) == HPRMS_E_INVALID);
   EXPECT(hprms_select_config(4096, 4097, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 3);
 
   if (failures) return 1;

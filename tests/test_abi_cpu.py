@@ -126,6 +126,11 @@ def test_table_covers_every_hidden_with_a_built_kernel():
             assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
             rc = L.hprms_reduce_add_rmsnorm(0, None, 2, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
             assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
+            for fmt, qw in ((abi.MX_FP8_E4M3, hidden), (abi.MX_FP4_E2M1, hidden // 2)):
+                rc = L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, hidden, qw, hidden // 32, hidden, hidden, fmt,
+                                                  dtype, 1e-6, None)
+                want = abi.HPRMS_OK if hidden % 32 == 0 else abi.HPRMS_E_INVALID
+                assert rc == want, (hidden, fmt, abi.last_error())
             # the FP8 table's choice also exists as a fused (mode 0) kernel, so the
             # 16-bit op can be run with the same lane mapping
             c8 = abi.select_config(rows, hidden, dtype, 2)
@@ -149,7 +154,7 @@ def test_config_entry_rejects_unbuilt_and_misfit_configs():
 
 def test_every_built_config_is_well_formed():
     for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
-        for mode in range(5):
+        for mode in range(7):
             cfgs = abi.kernel_configs(dtype, mode)
             assert cfgs
             for c in cfgs:
@@ -230,3 +235,24 @@ def test_plain_c_caller_compiles_links_and_runs(tmp_path):
     assert p.returncode == 0, p.stderr[-2000:]
     p = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert p.returncode == 0 and "ok" in p.stdout, p.stdout + p.stderr
+
+
+def test_mx_entry_rejects_bad_arguments():
+    L = abi.lib()
+    ok = dict(out=0x4000, sc=0x5000, x=0x1000, w=0x2000, r=0x3000, h=4096, so=2048, ss=128, fmt=abi.MX_FP4_E2M1)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.hprms_fused_add_rmsnorm_mx(a["out"], a["sc"], a["x"], a["w"], a["r"], 4, a["h"], a["so"], a["ss"],
+                                            a["h"], a["h"], a["fmt"], 0, 1e-6, None)
+    assert call(fmt=2) == abi.HPRMS_E_INVALID and "format" in abi.last_error()
+    assert call(h=4104, so=4104, ss=200) == abi.HPRMS_E_INVALID and "32" in abi.last_error()
+    assert call(so=1024) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
+    assert call(fmt=abi.MX_FP8_E4M3) == abi.HPRMS_E_INVALID          # MXFP8 rows are hidden bytes wide
+    assert call(ss=64) == abi.HPRMS_E_INVALID and "scale row stride" in abi.last_error()
+    assert call(sc=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
+    assert call(out=0x4002) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
+    assert call(x=0x1008) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
+    for mode in (abi.MODE_MXFP8, abi.MODE_MXFP4):
+        c = abi.select_config(4096, 4096, abi.DTYPE_BF16, mode)
+        assert c.tier in (1, 2) and c.lanes_per_row % 4 == 0

@@ -158,3 +158,27 @@ def test_reduce_meta_checks():
         ops.reduce_add_rms_norm(t(4, 256), [t(4, 256), t(4, 256, dtype=torch.float16)], w, r, 1e-6)
     with pytest.raises(RuntimeError, match="one row stride"):
         ops.reduce_add_rms_norm(t(4, 256), [t(4, 256), t(4, 512)[:, :256]], w, r, 1e-6)
+
+
+def test_mx_op_schema_and_meta_checks():
+    s = str(torch.ops.hp_rms_norm.rms_norm_mx_quant.default._schema)
+    assert s == ("hp_rms_norm::rms_norm_mx_quant(Tensor(a!) out, Tensor(b!) scales, Tensor input, Tensor weight, "
+                 "Tensor(c!) residual, int format, float eps) -> ()")
+    x, w, r = t(4, 256), t(256), t(4, 256)
+    q4, sc = ops.fused_add_rms_norm_mxfp4(x, r, w, 1e-6)
+    assert q4.shape == (4, 128) and q4.dtype == torch.float4_e2m1fn_x2
+    assert sc.shape == (4, 8) and sc.dtype == torch.float8_e8m0fnu
+    q8, sc = ops.fused_add_rms_norm_mxfp8(x, r, w, 1e-6)
+    assert q8.shape == (4, 256) and q8.dtype == torch.float8_e4m3fn
+    u8 = lambda *sh: torch.empty(*sh, dtype=torch.uint8, device=M)   # noqa: E731
+    assert ops.hp_rms_norm_mx(u8(4, 128), u8(4, 8), x, w, r, 1e-6, ops.MXFP4) is None
+    with pytest.raises(RuntimeError, match="32"):
+        ops.hp_rms_norm_mx(u8(4, 120), u8(4, 7), t(4, 240), t(240), t(4, 240), 1e-6, ops.MXFP4)
+    with pytest.raises(RuntimeError, match="hidden / 2"):
+        ops.hp_rms_norm_mx(u8(4, 256), u8(4, 8), x, w, r, 1e-6, ops.MXFP4)
+    with pytest.raises(RuntimeError, match="hidden / 32"):
+        ops.hp_rms_norm_mx(u8(4, 128), u8(4, 4), x, w, r, 1e-6, ops.MXFP4)
+    with pytest.raises(RuntimeError, match="format"):
+        ops.hp_rms_norm_mx(u8(4, 128), u8(4, 8), x, w, r, 1e-6, 3)
+    with pytest.raises(RuntimeError, match="float8_e4m3fn or uint8"):
+        ops.hp_rms_norm_mx(t(4, 256), u8(4, 8), x, w, r, 1e-6, ops.MXFP8)
