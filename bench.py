@@ -416,6 +416,26 @@ def run_extra(torch, ops, args):
         del sets, qs
         torch.cuda.empty_cache()
     out["fp8_output_bf16"] = fp8
+    # OCP MX outputs (MXFP8 / MXFP4): reads x, r; writes r, the elements and one scale byte per 32
+    mx = []
+    for fmt, name in ((ops.MXFP8, "mxfp8"), (ops.MXFP4, "mxfp4")):
+        for h in (4096, 8192, 16384, 32768):
+            n = cold_sets(B, h)
+            sets = [make_set(torch, B, h, torch.bfloat16, 7500 + i, "cuda:0") for i in range(n)]
+            w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+            qs = [torch.empty(B, h if fmt == ops.MXFP8 else h // 2, dtype=torch.uint8, device="cuda:0")
+                  for _ in range(n)]
+            sc = torch.empty(B, h // 32, dtype=torch.uint8, device="cuda:0")
+
+            def call(i, sets=sets, qs=qs, sc=sc, w=w, fmt=fmt):
+                ops.hp_rms_norm_mx(qs[i], sc, sets[i][0], w, sets[i][1], EPS, fmt)
+            us = time_rotating(torch, call, n, steps, args.warmup)
+            nbytes = 6 * B * h + (B * h if fmt == ops.MXFP8 else B * h // 2) + B * h // 32 + 2 * h
+            mx.append({"format": name, "rows": B, "hidden": h, "us_per_call": round(us, 2),
+                       "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_call": nbytes})
+            del sets, qs
+            torch.cuda.empty_cache()
+    out["mx_output_bf16"] = mx
     # out-of-place fused op (input and residual only read): the same 4 rows of bytes per row
     oop = []
     for h in (4096, 8192, 16384, 32768):

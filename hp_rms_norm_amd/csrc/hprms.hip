@@ -66,6 +66,11 @@ struct FusedEntry {
   X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
   X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
 
+// entries of the plain-RMSNorm table that the fused table does not use
+#define HPRMS_PLAIN_SHAPES(X, DT, MODE)                                                        \
+  X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31) \
+  X(DT, MODE, 512, 8, 0, 512, 7)
+
 // entries of the FP8-output table that the other tables do not use
 #define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
 
@@ -89,6 +94,8 @@ const FusedEntry kFused[] = {
     HPRMS_TUNING_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 2)
     HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
@@ -99,12 +106,8 @@ const FusedEntry kFused[] = {
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 4)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 5)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 5)
-    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 5)
-    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 5)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 6)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 6)
-    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 6)
-    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 6)
 };
 
 const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
@@ -136,7 +139,6 @@ bool latency_config(int64_t rows, int64_t nvec, hprms_config* c) {
 // The FP8 output adds a second row reduction (the absolute maximum) and a
 // barrier; above 4K elements it prefers more, smaller workgroups per CU, and
 // at 32K the LDS tier (measured 5.8% faster than 1024 lanes x 4 in registers).
-// The MX outputs (per-block maxima, no second barrier) start from the same rows.
 bool fp8_config(int64_t nvec, hprms_config* c) {
   struct Row { int64_t min_nvec, max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row fp8[] = {{513, 1024, 512, 2, 0, 512, 7},
@@ -151,10 +153,54 @@ bool fp8_config(int64_t nvec, hprms_config* c) {
   return false;
 }
 
+// The MX outputs (per-block maxima: a DPP quad step, no second barrier)
+// measured best with the register tier at 32K (1024 x 4: 4.5% / 9.5% faster
+// than the FP8 table's LDS tier for MXFP8 / MXFP4), and MXFP4 with shorter
+// rows per lane at 4K and 16K.
+bool mx_config(int mode, int64_t nvec, hprms_config* c) {
+  struct Row { int64_t min_nvec, max_nvec; int lpr, vpl, ldsv, block, flags; };
+  static const Row mx8[] = {{385, 512, 256, 2, 0, 256, 7},
+                            {513, 1024, 512, 2, 0, 512, 7},
+                            {1537, 2048, 1024, 2, 0, 1024, 31},
+                            {3073, 4096, 1024, 4, 0, 1024, 31}};
+  static const Row mx4[] = {{385, 512, 256, 2, 0, 256, 7},
+                            {513, 1024, 512, 2, 0, 512, 7},
+                            {1537, 2048, 512, 4, 0, 512, 7},
+                            {3073, 4096, 1024, 4, 0, 1024, 31}};
+  for (const Row& r : (mode == 5 ? mx8 : mx4)) {
+    if (nvec >= r.min_nvec && nvec <= r.max_nvec) {
+      *c = hprms_config{1, r.lpr, r.vpl, r.ldsv, r.block, 0, r.flags};
+      return true;
+    }
+  }
+  return false;
+}
+
+// Plain RMSNorm moves half the bytes of the fused op per row and has no
+// residual phase; measured against the fused table it prefers one wave per row
+// at 2K < H <= 4K (10-14% faster, no barrier), 512 lanes up to 8K and at
+// 12K-16K (2-3%), and 512 lanes x 8 vectors at 24K-32K (4-8%).
+bool plain_config(int64_t nvec, hprms_config* c) {
+  struct Row { int64_t min_nvec, max_nvec; int lpr, vpl, block, flags; };
+  static const Row plain[] = {{257, 512, 64, 8, 256, 3},
+                              {513, 1024, 512, 2, 512, 31},
+                              {1537, 2048, 512, 4, 512, 31},
+                              {3073, 4096, 512, 8, 512, 7}};
+  for (const Row& r : plain) {
+    if (nvec >= r.min_nvec && nvec <= r.max_nvec) {
+      *c = hprms_config{1, r.lpr, r.vpl, 0, r.block, 0, r.flags};
+      return true;
+    }
+  }
+  return false;
+}
+
 void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   const int64_t nvec = hidden / 8;
   if (latency_config(rows, nvec, c)) return;
-  if ((mode == 2 || mode == 5 || mode == 6) && fp8_config(nvec, c)) return;
+  if (mode == 1 && plain_config(nvec, c)) return;
+  if (mode == 2 && fp8_config(nvec, c)) return;
+  if ((mode == 5 || mode == 6) && mx_config(mode, nvec, c)) return;
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row table[] = {

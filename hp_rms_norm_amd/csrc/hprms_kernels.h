@@ -269,8 +269,10 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
         const bool bad = e32 == 255u;
         const float mul = bad ? 1.0f : __uint_as_float((uint32_t)(127 - sexp) << 23);
         const bool ok = row_ok && vec_ok[k];
-        store1<SAUX>((uint8_t)(bad ? 0xFFu : (uint32_t)(sexp + 127)), xsrs,
-                     ok && xsoff != kOOB ? xsoff + (uint32_t)(k * (LPR / 4)) : kOOB);
+        // a wave writes 16 consecutive scale bytes: default cache policy, so
+        // that L2 merges the pieces of a line before it goes to memory
+        store1<0>((uint8_t)(bad ? 0xFFu : (uint32_t)(sexp + 127)), xsrs,
+                  ok && xsoff != kOOB ? xsoff + (uint32_t)(k * (LPR / 4)) : kOOB);
         if constexpr (MODE == 5) {
           u32x2 q;
 #pragma unroll
