@@ -154,20 +154,16 @@ bool fp8_config(int64_t nvec, hprms_config* c) {
 }
 
 // The MX outputs (per-block maxima: a DPP quad step, no second barrier)
-// measured best with the register tier at 32K (1024 x 4: 4.5% / 9.5% faster
-// than the FP8 table's LDS tier for MXFP8 / MXFP4), and MXFP4 with shorter
-// rows per lane at 4K and 16K.
-bool mx_config(int mode, int64_t nvec, hprms_config* c) {
+// measured best with the register tier at 32K (1024 x 4: 4.5% / 5% faster
+// than the FP8 table's LDS tier for MXFP8 / MXFP4) and with 256 lanes x 2 at
+// 3K < H <= 4K.
+bool mx_config(int64_t nvec, hprms_config* c) {
   struct Row { int64_t min_nvec, max_nvec; int lpr, vpl, ldsv, block, flags; };
-  static const Row mx8[] = {{385, 512, 256, 2, 0, 256, 7},
-                            {513, 1024, 512, 2, 0, 512, 7},
-                            {1537, 2048, 1024, 2, 0, 1024, 31},
-                            {3073, 4096, 1024, 4, 0, 1024, 31}};
-  static const Row mx4[] = {{385, 512, 256, 2, 0, 256, 7},
-                            {513, 1024, 512, 2, 0, 512, 7},
-                            {1537, 2048, 512, 4, 0, 512, 7},
-                            {3073, 4096, 1024, 4, 0, 1024, 31}};
-  for (const Row& r : (mode == 5 ? mx8 : mx4)) {
+  static const Row mx[] = {{385, 512, 256, 2, 0, 256, 7},
+                           {513, 1024, 512, 2, 0, 512, 7},
+                           {1537, 2048, 1024, 2, 0, 1024, 31},
+                           {3073, 4096, 1024, 4, 0, 1024, 31}};
+  for (const Row& r : mx) {
     if (nvec >= r.min_nvec && nvec <= r.max_nvec) {
       *c = hprms_config{1, r.lpr, r.vpl, r.ldsv, r.block, 0, r.flags};
       return true;
@@ -200,7 +196,7 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   if (latency_config(rows, nvec, c)) return;
   if (mode == 1 && plain_config(nvec, c)) return;
   if (mode == 2 && fp8_config(nvec, c)) return;
-  if ((mode == 5 || mode == 6) && mx_config(mode, nvec, c)) return;
+  if ((mode == 5 || mode == 6) && mx_config(nvec, c)) return;
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row table[] = {

@@ -109,14 +109,13 @@ __device__ __forceinline__ void store1(uint8_t v, __amdgpu_buffer_rsrc_t r, uint
 }
 
 // ---- OCP MX (E2M1 elements) ----------------------------------------------------------
-// binary32 -> E2M1 code (sign in bit 3): round to nearest, ties to the even
-// code, by the midpoints of the value table 0 .5 1 1.5 2 3 4 6; saturates at 6
-// (infinity included); NaN gives a zero code with NaN's sign bit.
-__device__ __forceinline__ uint32_t e2m1_code(float v) {
-  const float a = __builtin_fabsf(v);
-  const uint32_t c = (uint32_t)(a > 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a > 1.25f) +
-                     (uint32_t)(a >= 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a >= 3.5f) + (uint32_t)(a > 5.0f);
-  return c | ((__float_as_uint(v) >> 28) & 8u);
+// Two binary32 values to two E2M1 codes in byte SEL of w, the first value in
+// the low nibble (gfx950 v_cvt_scalef32_pk_fp4_f32 with scale 1.0: round to
+// nearest even, saturating at +-6; NaN gives code 7 with NaN's sign).  The
+// other bytes of w are kept.
+template <int SEL>
+__device__ __forceinline__ uint32_t cvt_e2m1x2(uint32_t w, float a, float b) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, 1.0f, SEL);
 }
 
 // ---- reductions ---------------------------------------------------------------

@@ -45,8 +45,9 @@
 // reduction -- each with the scale 2^s, s = floor(log2 max|y|) - emax (8 for
 // E4M3, 2 for E2M1) clamped to [-127, 127], written as one E8M0 byte, and
 // elements y / 2^s rounded to nearest even and saturated (E4M3 bytes; E2M1
-// codes two per byte, the even element in the low nibble).  A block holding
-// NaN or infinity gets the scale byte 0xFF and unscaled elements.  The
+// codes two per byte, the even element in the low nibble; both conversions
+// are gfx950 instructions).  A block holding NaN or infinity gets the scale
+// byte 0xFF and unscaled elements.  The
 // residual is updated in place and `input` is only read, as in MODE 2.
 #pragma once
 
@@ -284,9 +285,10 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
           store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
         } else {
           uint32_t q = 0;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            q |= (e2m1_code(F::lo(y[j]) * mul) | (e2m1_code(F::hi(y[j]) * mul) << 4)) << (8 * j);
+          q = cvt_e2m1x2<0>(q, F::lo(y[0]) * mul, F::hi(y[0]) * mul);
+          q = cvt_e2m1x2<1>(q, F::lo(y[1]) * mul, F::hi(y[1]) * mul);
+          q = cvt_e2m1x2<2>(q, F::lo(y[2]) * mul, F::hi(y[2]) * mul);
+          q = cvt_e2m1x2<3>(q, F::lo(y[3]) * mul, F::hi(y[3]) * mul);
           store4<SAUX>(q, ors, ok ? ooff + k * (LPR * 4u) : kOOB);
         }
       }

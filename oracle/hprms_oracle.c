@@ -405,12 +405,13 @@ int hprms_oracle_reduce_add_rmsnorm(uint16_t* out, const uint16_t* const* parts,
 static const float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
 
 /* binary32 -> E2M1 code (sign in bit 3): the nearest magnitude, ties to the
- * even code, saturating at 6; NaN gives a zero code with NaN's sign bit (the
- * block's scale marks it NaN). */
+ * even code, saturating at 6.  E2M1 has no NaN (an MX block marks NaN in its
+ * scale); NaN is given the largest code with NaN's sign, as the gfx950
+ * conversion instruction gives it. */
 uint8_t hprms_oracle_f32_to_e2m1(float f) {
   uint8_t sign = (f2u(f) >> 31) ? 8u : 0u;
   float a = fabsf(f);
-  if (a != a) return sign;
+  if (a != a) return (uint8_t)(sign | 7);
   if (a >= 6.0f) return (uint8_t)(sign | 7);  /* saturation, infinity included */
   int best = 0;
   float bd = INFINITY;

@@ -42,7 +42,7 @@ def e2m1_by_thresholds(v):
     a = np.abs(v)
     code = ((a > 0.25).astype(np.int32) + (a >= 0.75) + (a > 1.25) + (a >= 1.75) + (a > 2.5) + (a >= 3.5)
             + (a > 5.0))
-    code = np.where(np.isnan(a), 0, code)
+    code = np.where(np.isnan(a), 7, code)    # no NaN code: the largest, with NaN's sign
     return (np.signbit(v).astype(np.uint8) << 3) | code.astype(np.uint8)
 
 
