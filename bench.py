@@ -385,6 +385,36 @@ def run_extra(torch, ops, args):
     dec = [(b, h, torch.bfloat16, "outliers") for b in (1, 8, 32, 128, 512) for h in (4096, 8192)]
     us = time_shapes(torch, ops.hp_rms_norm, dec, steps, args.warmup)
     out["decode_bf16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2)} for (b, h, _, _), u in zip(dec, us)]
+    # the same decode shapes replayed from a HIP graph (64 calls per replay over 8 buffer sets):
+    # the per-call time a serving loop that captures its step sees, without Python's launch cost
+    graph = []
+    for (b, h, dt, dist) in dec:
+        bufs = make_bufs(torch, [(b, h, dt, dist)], lambda r, hh: 8)
+        sets, w = bufs[0]
+        s_ = torch.cuda.Stream()
+        s_.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s_):
+            for x, r in sets:
+                ops.hp_rms_norm(x, w, r, EPS)
+        torch.cuda.current_stream().wait_stream(s_)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(64):
+                x, r = sets[i % 8]
+                ops.hp_rms_norm(x, w, r, EPS)
+        for _ in range(3):
+            g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph.append({"rows": b, "hidden": h, "us_per_call": round(e0.elapsed_time(e1) * 1e3 / 640, 2)})
+        del g, bufs, sets
+    torch.cuda.empty_cache()
+    out["decode_bf16_hip_graph"] = graph
     # fp16 non-power-of-two hidden
     f16 = [(B, 5120, torch.float16, "bench"), (B, 7168, torch.float16, "bench")]
     us = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
