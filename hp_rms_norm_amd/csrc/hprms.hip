@@ -337,6 +337,8 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   int64_t smax = p.x_stride > p.out_stride ? p.x_stride : p.out_stride;
   if (has_res(p.mode) && p.res_stride > smax) smax = p.res_stride;
   if (p.mode == 3 && p.res_out_stride > smax) smax = p.res_out_stride;
+  // the MX scale rows have their own buffer resource (byte stride)
+  if (is_mx(p.mode) && (rpb - 1) * p.mx_scale_stride + p.hidden / 32 >= (int64_t)kOOB) return false;
   if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
     return false;
   return true;
@@ -389,9 +391,9 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   }
   if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
     return fail(HPRMS_E_INVALID,
-                "MX output needs 16-byte aligned input, residual and weight, row strides %% 8 == 0, and the "
-                "output %s", p.mode == 5 ? "8-byte aligned with a row stride % 8 == 0" :
-                "4-byte aligned with a row stride % 4 == 0");
+                "MX output needs 16-byte aligned input, residual and weight, row strides %% 8 == 0, the "
+                "output %s, and a row group's rows (strides times rows per workgroup) within 2 GiB",
+                p.mode == 5 ? "8-byte aligned with a row stride % 8 == 0" : "4-byte aligned with a row stride % 4 == 0");
   if (c.tier != 3 && !vec_fits(p, c)) {
     if (forced && forced->tier != 0)
       return fail(HPRMS_E_INVALID,

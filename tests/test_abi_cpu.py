@@ -253,6 +253,13 @@ def test_mx_entry_rejects_bad_arguments():
     assert call(sc=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
     assert call(out=0x4002) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
     assert call(x=0x1008) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
+    # a scale row stride whose row group would not fit one buffer resource is refused, not truncated
+    # (H = 256 maps 8 rows to a workgroup)
+    assert L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, 256, 128, 1 << 29, 256, 256, abi.MX_FP4_E2M1, 0, 1e-6,
+                                        None) == abi.HPRMS_E_INVALID
+    assert "2 GiB" in abi.last_error()
+    assert L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, 256, 128, 1 << 20, 256, 256, abi.MX_FP4_E2M1, 0, 1e-6,
+                                        None) == abi.HPRMS_OK
     for mode in (abi.MODE_MXFP8, abi.MODE_MXFP4):
         c = abi.select_config(4096, 4096, abi.DTYPE_BF16, mode)
         assert c.tier in (1, 2) and c.lanes_per_row % 4 == 0
