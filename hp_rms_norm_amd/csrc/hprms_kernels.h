@@ -30,8 +30,8 @@
 // MODE 0 is the fused op (in place on input and residual); MODE 1 is the
 // plain RMSNorm (reads `input`, writes `out`, no residual stream); MODE 2 is
 // the fused op with an FP8 output: the 16-bit output y is quantised per row
-// (scale = max(amax|y| / 448, FLT_MIN) to scale[row], q = e4m3fn(clamp(y /
-// scale)) to q), the residual is updated in place and `input` is only read.
+// (scale = max(amax|y| / 448, FLT_MIN) to scale[row], q = e4m3fn(clamp(y *
+// (1 / scale))) to q), the residual is updated in place and `input` is only read.
 // The row maximum is a second DPP/LDS reduction over the 16-bit magnitudes
 // (sign-magnitude bit patterns order like their values, NaN above inf).
 // MODE 3 is the fused op out of place: input and residual are only read, the
@@ -56,9 +56,9 @@
 namespace hprms {
 
 struct FusedArgs {
-  const uint16_t* x;     // input rows (MODE 0: also the output)
-  uint16_t* out;         // output rows (MODE 0: == x)
-  uint16_t* res;         // residual rows (MODE 0 only)
+  const uint16_t* x;     // input rows (MODE 0: also the output; MODE 4: part 0)
+  uint16_t* out;         // 16-bit output rows (MODES 1, 3, 4; MODE 0: == x)
+  uint16_t* res;         // residual rows (every mode but 1)
   const uint16_t* w;     // weight [hidden]
   int64_t rows;
   int64_t ngroups;       // ceil(rows / RPB)
@@ -69,9 +69,9 @@ struct FusedArgs {
   int32_t nvec;          // hidden / 8
   float hidden_f;
   float eps;
-  uint8_t* q;            // MODE 2: FP8 output rows
+  uint8_t* q;            // MODES 2, 5, 6: quantised output rows
   float* scale;          // MODE 2: per-row scales
-  int64_t q_stride;      // MODE 2: bytes between FP8 rows
+  int64_t q_stride;      // MODES 2, 5, 6: bytes between quantised rows
   uint16_t* res_out;     // MODE 3: residual output rows
   int64_t res_out_stride;
   int32_t nparts;        // MODE 4: number of partial rows summed (x is part 0)
