@@ -223,8 +223,8 @@ def main():
                          "(the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--profile-config", default="",
                     help="with --profile: force lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags")
-    ap.add_argument("--profile-op", default="fused", choices=("fused", "fp8"),
-                    help="with --profile: the 16-bit fused op or its FP8-output form")
+    ap.add_argument("--profile-op", default="fused", choices=("fused", "fp8", "plain", "mxfp8", "mxfp4"),
+                    help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, or plain RMSNorm")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the op has no cross-GPU step (rows are independent), and this "
@@ -353,6 +353,21 @@ def profile_driver(torch, abi, op, args):
 
         def op(x, w, r, eps):  # noqa: F811  (FP8 output; the input row is only read)
             hp_rms_norm_amd.hp_rms_norm_fp8(q, sc, x, w, r, eps)
+    if args.profile_op == "plain":
+        import hp_rms_norm_amd
+        o = torch.empty(B, hidden, dtype=torch.bfloat16, device="cuda:0")
+
+        def op(x, w, r, eps):  # noqa: F811  (plain RMSNorm of the input row; r unused)
+            hp_rms_norm_amd.rms_norm(o, x, w, eps)
+    if args.profile_op in ("mxfp8", "mxfp4"):
+        import hp_rms_norm_amd
+        fmt = hp_rms_norm_amd.MXFP8 if args.profile_op == "mxfp8" else hp_rms_norm_amd.MXFP4
+        q = torch.empty(B, hidden if fmt == hp_rms_norm_amd.MXFP8 else hidden // 2, dtype=torch.uint8,
+                        device="cuda:0")
+        sc = torch.empty(B, hidden // 32, dtype=torch.uint8, device="cuda:0")
+
+        def op(x, w, r, eps):  # noqa: F811  (MX output; the input row is only read)
+            hp_rms_norm_amd.hp_rms_norm_mx(q, sc, x, w, r, eps, fmt)
     us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup)[0]
     n = 1 << 29
     src = torch.empty(n, dtype=torch.bfloat16, device="cuda:0").normal_()
