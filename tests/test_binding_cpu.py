@@ -3,6 +3,7 @@ reference's shape checks and messages (hp_rms_norm/csrc/cuda/hp_rms_norm.cu:12-2
 activation_kernels.cu:11-15) exercised through the Meta kernels, and no CPU
 fallback (CPU tensors are refused by the dispatcher)."""
 import inspect
+import os
 
 import pytest
 import torch
@@ -182,3 +183,18 @@ def test_mx_op_schema_and_meta_checks():
         ops.hp_rms_norm_mx(u8(4, 128), u8(4, 8), x, w, r, 1e-6, 3)
     with pytest.raises(RuntimeError, match="float8_e4m3fn or uint8"):
         ops.hp_rms_norm_mx(t(4, 256), u8(4, 8), x, w, r, 1e-6, ops.MXFP8)
+
+
+def test_missing_native_library_is_an_import_error(tmp_path):
+    """The package has no fallback: a copy of it without its built libraries
+    refuses to import, naming the build command."""
+    import shutil
+    import subprocess
+    import sys
+    pkg = tmp_path / "hp_rms_norm_amd"
+    src = os.path.dirname(os.path.abspath(hp_rms_norm_amd.__file__))
+    shutil.copytree(src, pkg, ignore=shutil.ignore_patterns("*.so", "__pycache__", "csrc"))
+    code = "import hp_rms_norm_amd"
+    p = subprocess.run([sys.executable, "-c", code], cwd=tmp_path, capture_output=True, text=True, timeout=300)
+    assert p.returncode != 0
+    assert "ImportError" in p.stderr and "not built" in p.stderr and "hp_rms_norm_amd.build" in p.stderr
