@@ -137,11 +137,12 @@ bool latency_config(int64_t rows, int64_t nvec, hprms_config* c) {
 }
 
 // The FP8 output adds a second row reduction (the absolute maximum) and a
-// barrier; above 4K elements it prefers more, smaller workgroups per CU, and
+// barrier; from 3K elements it prefers more, smaller workgroups per CU, and
 // at 32K the LDS tier (measured 5.8% faster than 1024 lanes x 4 in registers).
 bool fp8_config(int64_t nvec, hprms_config* c) {
   struct Row { int64_t min_nvec, max_nvec; int lpr, vpl, ldsv, block, flags; };
-  static const Row fp8[] = {{513, 1024, 512, 2, 0, 512, 7},
+  static const Row fp8[] = {{385, 512, 256, 2, 0, 256, 7},
+                            {513, 1024, 512, 2, 0, 512, 7},
                             {1537, 2048, 1024, 2, 0, 1024, 31},
                             {3073, 4096, 512, 8, 4, 512, 31}};
   for (const Row& r : fp8) {
