@@ -260,6 +260,35 @@ def test_torch_compile_functionalises_the_in_place_op(abi):
     assert torch.equal(got_r.view(torch.int16), want_r.view(torch.int16))
 
 
+def test_torch_compile_with_the_other_ops(abi):
+    """The out-of-place, plain, FP8 / MX and partial-sum ops through
+    torch.compile (aot_eager, fullgraph): their alias annotations and Meta
+    kernels let functionalisation see every write; bit-for-bit equal to eager."""
+    import hp_rms_norm_amd as h
+
+    def f(x, w, r, p1):
+        out, res = h.fused_add_rms_norm(x, r, w, 1e-6)
+        plain = torch.empty_like(x)
+        h.rms_norm(plain, x, w, 1e-6)
+        r8 = r.clone()
+        q8, s8 = h.fused_add_rms_norm_fp8(x, r8, w, 1e-6)
+        r4 = r.clone()
+        q4, s4 = h.fused_add_rms_norm_mxfp4(x, r4, w, 1e-6)
+        rp, o2 = r.clone(), torch.empty_like(x)
+        h.reduce_add_rms_norm(o2, [x, p1], w, rp, 1e-6)
+        return (out, res, plain, q8.view(torch.uint8), s8, r8, q4.view(torch.uint8), s4.view(torch.uint8), r4,
+                o2, rp)
+
+    x, r, w = (t.to(DEV) for t in make_inputs(96, 2048, torch.bfloat16, 22))
+    p1 = torch.randn(96, 2048, device=DEV).to(torch.bfloat16)
+    want = f(x, w, r, p1)
+    got = torch.compile(f, backend="aot_eager", fullgraph=True)(x, w, r, p1)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert a.dtype == b.dtype and a.shape == b.shape, i
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), f"output {i} differs"
+
+
 # ---- streams and graphs ------------------------------------------------------------------
 def test_runs_on_current_stream(abi):
     import hp_rms_norm_amd
