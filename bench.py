@@ -158,7 +158,7 @@ def time_shapes(torch, op, shapes, calls, warmup):
     return out
 
 
-def cpu_baselines(torch, budget_s=12.0):
+def cpu_baselines(torch, budget_s=20.0):
     """The CPU oracle (kind "port") and the torch eager formula, on the box's
     host cores, over a bounded sample: rows of (4096, H) for H in the sweep,
     taken as a fixed number of rows per H so each leg stays within budget."""
@@ -200,7 +200,7 @@ def cpu_baselines(torch, budget_s=12.0):
     for name, fn in (("oracle", oracle_pass), ("torch", torch_pass)):
         sum(fn())  # warm-up pass
         reps, t_start = [], time.perf_counter()
-        while len(reps) < 3 or (time.perf_counter() - t_start < budget_s / 2 and len(reps) < 50):
+        while len(reps) < 3 or (time.perf_counter() - t_start < budget_s / 2 and len(reps) < 2000):
             reps.append(sum(fn()))
         med = statistics.median(reps)
         out[name] = {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s",
