@@ -1,8 +1,8 @@
 """MI355X (gfx950) fused residual-add + RMSNorm.
 
 Importing the package registers ``torch.ops.hp_rms_norm.*`` from the in-tree
-native library ``libhprms_torch.so`` (built by ``python -m
-hp_rms_norm_amd.build``), which calls the HIP kernels of ``libhprms.so``
+native library ``libhprms_torch.so`` (built by ``python
+hp_rms_norm_amd/build.py``), which calls the HIP kernels of ``libhprms.so``
 through their C ABI.  Mirrors the reference package's loader
 (hp_rms_norm/__init__.py:1-3): ``import torch``, load the native library,
 re-export the ops.  There is no CPU implementation: a missing library is an
@@ -21,7 +21,7 @@ def _load():
     if not os.path.exists(TORCH_LIB) or not os.path.exists(KERNEL_LIB):
         raise ImportError(
             f"hp_rms_norm_amd: native libraries not built ({TORCH_LIB}); "
-            "run `python -m hp_rms_norm_amd.build`")
+            "run `python hp_rms_norm_amd/build.py`")
     if not hasattr(torch.ops.hp_rms_norm, "rms_norm"):
         torch.ops.load_library(TORCH_LIB)
     return TORCH_LIB

@@ -68,7 +68,7 @@ def lib():
         except ImportError:
             pass
         if not os.path.exists(KERNEL_LIB):
-            raise ImportError(f"{KERNEL_LIB} not built: run `python -m hp_rms_norm_amd.build`")
+            raise ImportError(f"{KERNEL_LIB} not built: run `python hp_rms_norm_amd/build.py`")
         L = ctypes.CDLL(KERNEL_LIB)
         vp, i64, ci, cd = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double
         L.hprms_fused_add_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]

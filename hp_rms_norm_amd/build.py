@@ -4,8 +4,10 @@
     libhprms_torch.so  the torch operator registration on top of it (g++)
 
 Both land next to this file, so they travel with the source tree.  Run
-``python -m hp_rms_norm_amd.build`` (or ``__graft_entry__.build()``).
-No GPU is needed: hipcc cross-compiles for gfx950.
+``python hp_rms_norm_amd/build.py [all|kernels|torch|oracle]`` (or
+``__graft_entry__.build()``) -- as a script, not with ``-m``: importing it
+through the package would run the package's __init__, which needs the
+libraries this builds.  No GPU is needed: hipcc cross-compiles for gfx950.
 """
 import os
 import shutil

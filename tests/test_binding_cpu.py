@@ -197,4 +197,4 @@ def test_missing_native_library_is_an_import_error(tmp_path):
     code = "import hp_rms_norm_amd"
     p = subprocess.run([sys.executable, "-c", code], cwd=tmp_path, capture_output=True, text=True, timeout=300)
     assert p.returncode != 0
-    assert "ImportError" in p.stderr and "not built" in p.stderr and "hp_rms_norm_amd.build" in p.stderr
+    assert "ImportError" in p.stderr and "not built" in p.stderr and "hp_rms_norm_amd/build.py" in p.stderr
