@@ -135,6 +135,14 @@ def test_hidden_not_multiple_of_8(abi, hidden, dtype):
     check_case(abi, 37, hidden, dtype, seed=hidden)
 
 
+@pytest.mark.parametrize("rows,hidden", [(9, 100000), (2, 1 << 24)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_hidden_beyond_the_vector_tiers(abi, rows, hidden, dtype):
+    """H > 65536 takes the general kernel, up to the documented maximum 2^24."""
+    print("large hidden", rows, hidden, dtype, flush=True)
+    check_case(abi, rows, hidden, dtype, seed=rows)
+
+
 def test_general_tier_forced(abi):
     from hp_rms_norm_amd.abi import Config
     cfg = Config(3, 256, 0, 0, 256, 0, 0)
