@@ -20,7 +20,9 @@ roofline   = the kernel instantiation with the largest share of the step
 cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
                   on the host cores, on a bounded sample of the same shapes.
 cpu_torch_eager = the reference test's torch formula on the CPU, same sample.
-extra      = the other BASELINE configs (decode, fp16, streamer), µs/call.
+extra      = the other BASELINE configs (decode, fp16, streamer) and the other
+             operators (FP8 / MX outputs, out-of-place, plain RMSNorm, the
+             general tier, partial sums), µs/call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 """
@@ -513,6 +515,22 @@ def run_extra(torch, ops, args):
         del sets, outs
         torch.cuda.empty_cache()
     out["plain_rmsnorm_bf16"] = plain
+    # the general tier: odd widths, and a row start 2 bytes off 16-byte alignment
+    gen = []
+    for h, off in ((999, 0), (2049, 0), (4097, 0), (8191, 0), (16384, 1)):
+        n = cold_sets(B, h)
+        bases = [make_set(torch, B, h + 8, torch.bfloat16, 9500 + i, "cuda:0") for i in range(n)]
+        sets = [(x[:, off:off + h], r[:, off:off + h]) for x, r in bases]
+        w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+
+        def call(i, sets=sets, w=w):
+            ops.hp_rms_norm(sets[i][0], w, sets[i][1], EPS)
+        us = time_rotating(torch, call, n, steps, args.warmup)
+        gen.append({"rows": B, "hidden": h, "row_start_offset_bytes": 2 * off, "us_per_call": round(us, 2),
+                    "gbs": round(fused_bytes(B, h) / (us * 1e-6) / 1e9, 1)})
+        del bases, sets
+        torch.cuda.empty_cache()
+    out["general_tier_bf16"] = gen
     # partial sums + fused op: P parts read, residual read and written, output written
     red = []
     h = 8192

@@ -13,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
@@ -30,15 +31,29 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def _run(cmd):
-    print("+", " ".join(cmd), flush=True)
-    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(line for line in p.stdout.splitlines()
+def _report(cmd, p_returncode, text):
+    out = "\n".join(line for line in text.splitlines()
                     if "packed-fp32-ops' is not a recognized feature" not in line)
     if out.strip():
         print(out, flush=True)
-    if p.returncode != 0:
-        raise RuntimeError(f"build step failed ({p.returncode}): {' '.join(cmd)}")
+    if p_returncode != 0:
+        raise RuntimeError(f"build step failed ({p_returncode}): {' '.join(cmd)}")
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    _report(cmd, p.returncode, p.stdout)
+
+
+def _run_parallel(cmds):
+    """Runs the commands at once (each compiles one translation unit)."""
+    for cmd in cmds:
+        print("+", " ".join(cmd), flush=True)
+    procs = [subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True) for cmd in cmds]
+    outs = [p.communicate()[0] for p in procs]
+    for cmd, p, text in zip(cmds, procs, outs):
+        _report(cmd, p.returncode, text)
 
 
 def _atomic(dst, build_fn):
@@ -48,10 +63,15 @@ def _atomic(dst, build_fn):
 
 
 def build_kernels():
+    """Compiles every translation unit of csrc/ at once into a scratch
+    directory, then links libhprms.so."""
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, "hprms.hip")]
-    _atomic(KERNEL_LIB, lambda out: _run(
-        [hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", out]))
+    srcs = [os.path.join(CSRC, name) for name in ("hprms.hip", "hprms_general.hip")]
+    with tempfile.TemporaryDirectory(prefix="hprms_build_") as tmp:
+        objs = [os.path.join(tmp, os.path.basename(src) + ".o") for src in srcs]
+        _run_parallel([[hipcc, *HIP_FLAGS, "-c", f"-I{INCLUDE}", f"-I{CSRC}", src, "-o", obj]
+                       for src, obj in zip(srcs, objs)])
+        _atomic(KERNEL_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", *objs, "-o", out]))
 
 
 def build_torch_binding():

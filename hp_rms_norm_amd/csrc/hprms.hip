@@ -345,7 +345,9 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   return true;
 }
 
-template <int DT>
+// The general tier (hprms_general.hip): rows up to 16K elements stay in
+// registers (one read and one write per element); longer rows take the
+// two-pass kernel, which re-reads the residual row it has just written.
 int launch_general(const Problem& p, hipStream_t stream) {
   GeneralArgs a = {};
   a.x = (const uint16_t*)p.x;
@@ -367,13 +369,7 @@ int launch_general(const Problem& p, hipStream_t stream) {
   a.scale = p.scale;
   a.q_stride = p.mode == 2 ? p.out_stride : 0;
   const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
-  switch (p.mode) {
-    case 0: fused_general_kernel<DT, 0><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
-    case 1: fused_general_kernel<DT, 1><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
-    case 2: fused_general_kernel<DT, 2><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
-    case 3: fused_general_kernel<DT, 3><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
-    default: fused_general_kernel<DT, 4><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a); break;
-  }
+  launch_general_kernels(a, p.dtype, p.mode, grid, stream);
   return check_launch("general rmsnorm kernel");
 }
 
@@ -404,8 +400,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   }
   if (c.tier == 3) {
     if (p.rows == 0) return HPRMS_OK;
-    return p.dtype == HPRMS_DTYPE_BF16 ? launch_general<HPRMS_DTYPE_BF16>(p, stream)
-                                       : launch_general<HPRMS_DTYPE_FP16>(p, stream);
+    return launch_general(p, stream);
   }
 
   const FusedEntry* e = find_fused(p.dtype, p.mode, c);

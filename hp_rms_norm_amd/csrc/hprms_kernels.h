@@ -446,6 +446,121 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
   }
 }
 
+// General kernel, register-resident form: any alignment and row strides,
+// hidden <= BLOCK * E (the host picks E so that at most one element slot per
+// thread lies wholly past the row).  One workgroup per row (grid-stride);
+// thread t owns elements t, t + BLOCK, ..., t + (E-1) * BLOCK (each wave
+// instruction moves 128 contiguous bytes), issues all its loads first and
+// keeps the row in registers, so the row is read once and written once, as in
+// the vector tiers.  Accesses are 2-byte buffer loads and stores through
+// resources sized to the row: elements past its end read as 0 and their
+// stores are dropped by the hardware range check, so the code is straight-line
+// (a branch per slot would make the wait counters conservative and serialise
+// the stores).  Same modes 0-4 and arithmetic as fused_general_kernel.
+template <int DT, int MODE, int BLOCK, int E>
+__global__ __launch_bounds__(BLOCK) void fused_general_reg_kernel(GeneralArgs a) {
+  static_assert(MODE >= 0 && MODE <= 4 && BLOCK % 64 == 0, "mode / block");
+  using F = Fmt<DT>;
+  constexpr int NW = BLOCK / 64;
+  __shared__ float red[2][NW];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const uint32_t rowbytes = (uint32_t)a.hidden * 2u;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, rowbytes);
+  int buf = 0;
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row * a.x_stride, rowbytes);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(a.out + row * a.out_stride, rowbytes);
+    __amdgpu_buffer_rsrc_t rrs = xrs, srs = xrs;
+    if constexpr (MODE != 1) {
+      rrs = make_rsrc(a.res + row * a.res_stride, rowbytes);
+      srs = MODE == 3 ? make_rsrc(a.res_out + row * a.res_out_stride, rowbytes) : rrs;
+    }
+    // one 32-bit register per element: 16-bit arrays would be packed in
+    // pairs, and the packing waits for each load
+    uint32_t xv[E], rv[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      const uint32_t off = (uint32_t)(tid + k * BLOCK) * 2u;
+      xv[k] = __builtin_amdgcn_raw_buffer_load_b16(xrs, off, 0, 0);
+      if constexpr (MODE != 1) rv[k] = __builtin_amdgcn_raw_buffer_load_b16(rrs, off, 0, 0);
+    }
+    float acc[MODE == 4 ? E : 1];
+    if constexpr (MODE == 4) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) acc[k] = F::one((uint16_t)xv[k]);
+#pragma unroll
+      for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+        if (g >= a.nparts) break;
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row * a.x_stride, rowbytes);
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+          acc[k] += F::one(__builtin_amdgcn_raw_buffer_load_b16(prs, (uint32_t)(tid + k * BLOCK) * 2u, 0, 0));
+      }
+    }
+    float sv[E];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if constexpr (MODE != 1) {
+        const float xj = MODE == 4 ? F::one(F::pack1(acc[MODE == 4 ? k : 0])) : F::one((uint16_t)xv[k]);
+        const uint16_t s = F::pack1(xj + F::one((uint16_t)rv[k]));
+        __builtin_amdgcn_raw_buffer_store_b16(s, srs, (uint32_t)(tid + k * BLOCK) * 2u, 0, 0);
+        sv[k] = F::one(s);
+      } else {
+        sv[k] = F::one((uint16_t)xv[k]);
+      }
+      ss = __builtin_fmaf(sv[k], sv[k], ss);   // elements past the row are 0
+    }
+    float tot = group_sum<64>(ss);
+    if ((tid & 63) == 0) red[buf][wave] = tot;
+    __syncthreads();
+    tot = red[buf][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) tot += red[buf][w];
+    const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
+    // every weight load before the first output store: a load after a store
+    // could not be moved above it (the compiler cannot rule out aliasing)
+#pragma unroll
+    for (int k = 0; k < E; ++k) rv[k] = __builtin_amdgcn_raw_buffer_load_b16(wrs, (uint32_t)(tid + k * BLOCK) * 2u, 0, 0);
+    if constexpr (MODE != 2) {
+#pragma unroll
+      for (int k = 0; k < E; ++k)
+        __builtin_amdgcn_raw_buffer_store_b16(F::pack1((sv[k] * inv) * F::one((uint16_t)rv[k])), ors,
+                                              (uint32_t)(tid + k * BLOCK) * 2u, 0, 0);
+    } else {
+      uint32_t m = 0;
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        xv[k] = F::pack1((sv[k] * inv) * F::one((uint16_t)rv[k]));  // the 16-bit output (0 past the row)
+        m = __builtin_elementwise_max(m, xv[k] & 0x7fffu);
+      }
+      uint32_t mx = group_max_u32<64>(m);
+      buf ^= 1;
+      if ((tid & 63) == 0) red[buf][wave] = __builtin_bit_cast(float, mx);
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < NW; ++w) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w]));
+      float sc = F::one((uint16_t)mx) / 448.0f;
+      if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+      const float isc = 1.0f / sc;
+      if (tid == 0) a.scale[row] = sc;
+      const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q + row * a.q_stride, (uint32_t)a.hidden);
+#pragma unroll
+      for (int k = 0; k < E; ++k)
+        __builtin_amdgcn_raw_buffer_store_b8(
+            (uint8_t)(pack_e4m3x4(clamp_e4m3(F::one((uint16_t)xv[k]) * isc), 0.0f, 0.0f, 0.0f) & 0xffu), qrs,
+            (uint32_t)(tid + k * BLOCK), 0, 0);
+    }
+    buf ^= 1;
+  }
+}
+
+// Launches the general tier for `dtype` (HPRMS_DTYPE_*) and mode 0-4 on
+// `stream`: the register-resident kernel up to hidden = 16384, the two-pass
+// kernel above (hprms_general.hip).  Launch errors are left for the caller.
+void launch_general_kernels(const GeneralArgs& a, int dtype, int mode, int64_t grid, hipStream_t stream);
+
 // ---- streamer ------------------------------------------------------------------
 struct StreamArgs {
   uint16_t* out;

@@ -96,7 +96,8 @@ def test_out_of_place_torch_ops_and_aliases(abi):
     assert_output_close(bits(o2), want_out2, torch.bfloat16)
 
 
-@pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24), (4096, 3)])
+@pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24), (4096, 3), (6143, 1), (11001, 5), (16383, 1),
+                                        (20001, 2)])
 def test_out_of_place_strided_and_general_tier(abi, hidden, pad):
     dtype = torch.float16
     rows = 37
@@ -170,7 +171,7 @@ def test_reduce_torch_op_out_is_a_part(abi):
     assert_output_close(bits(pds[0]), want_out, torch.bfloat16)
 
 
-@pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24)])
+@pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24), (7167, 1), (12289, 7), (16383, 1), (20001, 2)])
 def test_reduce_strided_and_general_tier(abi, hidden, pad):
     dtype = torch.bfloat16
     rows = 29

@@ -129,10 +129,39 @@ def test_persistent_grid(abi):
 
 
 # ---- general kernel: tails, misalignment, row strides ---------------------------------
-@pytest.mark.parametrize("hidden", [1, 7, 13, 100, 1000, 4097, 40000])
+# odd widths on both sides of the register-resident general kernel's block sizes (64
+# threads up to 1024, 256 up to 8K, 1024 up to 16K) and of the two-pass kernel above 16K
+@pytest.mark.parametrize("hidden", [1, 7, 13, 100, 255, 257, 1023, 1025, 4095, 4097, 16383, 16385, 40000])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_hidden_not_multiple_of_8(abi, hidden, dtype):
     check_case(abi, 37, hidden, dtype, seed=hidden)
+
+
+# The register-resident general kernel's dispatch (hprms_general.hip): block size and
+# the element-slot counts E it is instantiated for, per width range.
+GENERAL_TIERS = ((64, 0, 1024, (1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16)),
+                 (256, 1024, 8192, (5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 28, 32)),
+                 (1024, 8192, 16384, (10, 12, 14, 16)))
+
+
+def general_widths():
+    """Odd widths at both ends of every (block, E) shape: the smallest width
+    that needs E slots per thread and the largest that E slots hold."""
+    out = []
+    for block, lo, hi, slots in GENERAL_TIERS:
+        prev = lo
+        for e in slots:
+            top = min(e * block, hi)
+            out += [(prev + 1, block, e), (top - 1, block, e)]
+            prev = top
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_general_every_slot_count(abi, dtype):
+    for hidden, block, e in general_widths():
+        print("general slots", hidden, block, e, dtype, flush=True)
+        check_case(abi, 23, hidden, dtype, seed=hidden + 1)
 
 
 @pytest.mark.parametrize("rows,hidden", [(9, 100000), (2, 1 << 24)])
@@ -415,6 +444,21 @@ def test_plain_rmsnorm_every_table_row(abi, dtype):
         hp_rms_norm_amd.rms_norm(out, xd, wd, 1e-6)
         torch.cuda.synchronize()
         assert_output_close(bits(out), want, dtype, f"plain 513x{hidden} {dtype}")
+
+
+@pytest.mark.parametrize("hidden", [13, 1001, 4095, 16383, 20001])
+def test_plain_rmsnorm_general_tier(abi, hidden):
+    """Odd widths take the general kernels (register-resident up to 16K, two
+    passes above)."""
+    import hp_rms_norm_amd
+    for dtype in (torch.bfloat16, torch.float16):
+        x, _, w = make_inputs(21, hidden, dtype, hidden)
+        want = oracle.rmsnorm(bits(x), bits(w), 1e-6, DT[dtype], threads=min(16, oracle.max_threads()))
+        xd, wd = x.to(DEV), w.to(DEV)
+        out = torch.empty_like(xd)
+        hp_rms_norm_amd.rms_norm(out, xd, wd, 1e-6)
+        torch.cuda.synchronize()
+        assert_output_close(bits(out), want, dtype, f"plain general 21x{hidden} {dtype}")
 
 
 def test_functional_form(abi):
