@@ -13,16 +13,17 @@ value      = algorithmic bytes of a step / time of a step (GB/s), where a
 per_shape  = per-H microseconds per call and GB/s: back-to-back calls over
              rotating buffer sets spanning >= 1 GiB (so every call is cold in
              the Infinity Cache), one HIP event pair around them on the
-             stream the kernels run on.  Each timed region starts behind a
-             short spin kernel so the host's launch rate is not measured.
+             stream the kernels run on; the median and p10/p90 over 7 such
+             blocks.  Each timed region starts behind a short spin kernel so
+             the host's launch rate is not measured.
 roofline   = the kernel instantiation with the largest share of the step
              time, against MI355X's 8 TB/s HBM peak.
 cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
                   on the host cores, on a bounded sample of the same shapes.
 cpu_torch_eager = the reference test's torch formula on the CPU, same sample.
 extra      = the other BASELINE configs (decode, fp16, streamer) and the other
-             operators (FP8 / MX outputs, out-of-place, plain RMSNorm, the
-             general tier, partial sums), µs/call.
+             operators (FP8 / MX outputs, out-of-place, plain RMSNorm, rows
+             off the 128-byte grid, partial sums), µs/call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 """
@@ -131,9 +132,18 @@ def cold_sets(rows, hidden, elem=2, floor=2, span=1 << 30):
     return max(floor, min(256, -(-span // (2 * rows * hidden * elem))))
 
 
-def time_shapes(torch, op, shapes, calls, warmup):
-    """Per shape: `calls` back-to-back calls over rotating buffer sets spanning
-    >= 1 GiB, one HIP event pair around them.  Returns µs per call."""
+def spread(samples):
+    """(median, p10, p90) of a list of timings."""
+    if len(samples) == 1:
+        return samples[0], samples[0], samples[0]
+    q = statistics.quantiles(samples, n=10, method="inclusive")
+    return statistics.median(samples), q[0], q[8]
+
+
+def time_shapes(torch, op, shapes, calls, warmup, trials=7):
+    """Per shape: `trials` timed blocks, each of `calls` back-to-back calls
+    over rotating buffer sets spanning >= 1 GiB with one HIP event pair around
+    it.  Returns (median, p10, p90) over the trials of µs per call."""
     out = []
     for shape in shapes:
         rows, hidden = shape[0], shape[1]
@@ -144,17 +154,22 @@ def time_shapes(torch, op, shapes, calls, warmup):
             x, r = sets[it % n]
             op(x, w, r, EPS)
         stream = torch.cuda.current_stream()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ncalls = max(calls, n)
-        torch.cuda.synchronize()
-        prefill(torch, 10)
-        t0.record(stream)
-        for it in range(ncalls):
-            x, r = sets[(warmup + it) % n]
-            op(x, w, r, EPS)
-        t1.record(stream)
-        torch.cuda.synchronize()
-        out.append(t0.elapsed_time(t1) * 1e3 / ncalls)
+        samples = []
+        base = warmup
+        for _ in range(trials):
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            prefill(torch, 10)
+            t0.record(stream)
+            for it in range(ncalls):
+                x, r = sets[(base + it) % n]
+                op(x, w, r, EPS)
+            t1.record(stream)
+            torch.cuda.synchronize()
+            base += ncalls
+            samples.append(t0.elapsed_time(t1) * 1e3 / ncalls)
+        out.append(spread(samples))
         del bufs, sets
         torch.cuda.empty_cache()
     return out
@@ -255,9 +270,10 @@ def main():
     per_us = time_shapes(torch, op, shapes, args.steps, args.warmup)
 
     per_shape, by_kernel = [], {}
-    for (rows, h, _, _), us in zip(shapes, per_us):
+    for (rows, h, _, _), (us, p10, p90) in zip(shapes, per_us):
         key = kernel_key(abi, rows, h, 0)
         per_shape.append({"rows": rows, "hidden": h, "us_per_call": round(us, 2),
+                          "us_p10": round(p10, 2), "us_p90": round(p90, 2),
                           "gbs": round(fused_bytes(rows, h) / (us * 1e-6) / 1e9, 1),
                           "kernel": {"lanes_per_row": key[1], "vec_per_lane": key[2],
                                      "lds_vec_per_lane": key[3], "block": key[4], "flags": key[6]}})
@@ -370,7 +386,7 @@ def profile_driver(torch, abi, op, args):
 
         def op(x, w, r, eps):  # noqa: F811  (MX output; the input row is only read)
             hp_rms_norm_amd.hp_rms_norm_mx(q, sc, x, w, r, eps, fmt)
-    us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup)[0]
+    us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup, trials=1)[0][0]
     n = 1 << 29
     src = torch.empty(n, dtype=torch.bfloat16, device="cuda:0").normal_()
     dst = torch.empty_like(src)
@@ -401,7 +417,8 @@ def run_extra(torch, ops, args):
     # decode shapes with 1% outliers x50
     dec = [(b, h, torch.bfloat16, "outliers") for b in (1, 8, 32, 128, 512) for h in (4096, 8192)]
     us = time_shapes(torch, ops.hp_rms_norm, dec, steps, args.warmup)
-    out["decode_bf16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2)} for (b, h, _, _), u in zip(dec, us)]
+    out["decode_bf16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2), "us_p10": round(p10, 2),
+                           "us_p90": round(p90, 2)} for (b, h, _, _), (u, p10, p90) in zip(dec, us)]
     # the same decode shapes replayed from a HIP graph (64 calls per replay over 8 buffer sets):
     # the per-call time a serving loop that captures its step sees, without Python's launch cost
     graph = []
@@ -435,8 +452,9 @@ def run_extra(torch, ops, args):
     # fp16 non-power-of-two hidden
     f16 = [(B, 5120, torch.float16, "bench"), (B, 7168, torch.float16, "bench")]
     us = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
-    out["fp16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2),
-                    "gbs": round(fused_bytes(b, h) / (u * 1e-6) / 1e9, 1)} for (b, h, _, _), u in zip(f16, us)]
+    out["fp16"] = [{"rows": b, "hidden": h, "us_per_call": round(u, 2), "us_p10": round(p10, 2),
+                    "us_p90": round(p90, 2), "gbs": round(fused_bytes(b, h) / (u * 1e-6) / 1e9, 1)}
+                   for (b, h, _, _), (u, p10, p90) in zip(f16, us)]
     # fused add+RMSNorm with FP8 output (reads x, r, w; writes r and H bytes + a scale per row)
     fp8 = []
     for h in (4096, 8192, 16384, 32768):
@@ -515,22 +533,25 @@ def run_extra(torch, ops, args):
         del sets, outs
         torch.cuda.empty_cache()
     out["plain_rmsnorm_bf16"] = plain
-    # the general tier: odd widths, and a row start 2 bytes off 16-byte alignment
-    gen = []
-    for h, off in ((999, 0), (2049, 0), (4097, 0), (8191, 0), (16384, 1)):
-        n = cold_sets(B, h)
-        bases = [make_set(torch, B, h + 8, torch.bfloat16, 9500 + i, "cuda:0") for i in range(n)]
+    # rows off the 128-byte grid: odd widths (the tail variants), row starts 2 bytes off 16-byte
+    # alignment, and 16-byte aligned rows with a stride of hidden + 8 (the unaligned variants)
+    una = []
+    for h, off, pad in ((999, 0, 0), (2049, 0, 0), (4097, 0, 0), (8191, 0, 0), (16391, 0, 0), (32775, 0, 0),
+                        (4096, 1, 8), (16384, 1, 8), (32768, 1, 8), (16384, 0, 8), (32768, 0, 8)):
+        stride = h + off + pad
+        n = cold_sets(B, stride)
+        bases = [make_set(torch, B, stride, torch.bfloat16, 9500 + i, "cuda:0") for i in range(n)]
         sets = [(x[:, off:off + h], r[:, off:off + h]) for x, r in bases]
         w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
 
         def call(i, sets=sets, w=w):
             ops.hp_rms_norm(sets[i][0], w, sets[i][1], EPS)
         us = time_rotating(torch, call, n, steps, args.warmup)
-        gen.append({"rows": B, "hidden": h, "row_start_offset_bytes": 2 * off, "us_per_call": round(us, 2),
-                    "gbs": round(fused_bytes(B, h) / (us * 1e-6) / 1e9, 1)})
+        una.append({"rows": B, "hidden": h, "row_start_offset_bytes": 2 * off, "row_stride": stride,
+                    "us_per_call": round(us, 2), "gbs": round(fused_bytes(B, h) / (us * 1e-6) / 1e9, 1)})
         del bases, sets
         torch.cuda.empty_cache()
-    out["general_tier_bf16"] = gen
+    out["unaligned_rows_bf16"] = una
     # partial sums + fused op: P parts read, residual read and written, output written
     red = []
     h = 8192

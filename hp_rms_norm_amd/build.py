@@ -66,7 +66,8 @@ def build_kernels():
     """Compiles every translation unit of csrc/ at once into a scratch
     directory, then links libhprms.so."""
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, name) for name in ("hprms.hip", "hprms_general.hip")]
+    srcs = [os.path.join(CSRC, name)
+            for name in ("hprms.hip", "hprms_unaligned.hip", "hprms_tail.hip", "hprms_general.hip")]
     with tempfile.TemporaryDirectory(prefix="hprms_build_") as tmp:
         objs = [os.path.join(tmp, os.path.basename(src) + ".o") for src in srcs]
         _run_parallel([[hipcc, *HIP_FLAGS, "-c", f"-I{INCLUDE}", f"-I{CSRC}", src, "-o", obj]

@@ -16,6 +16,7 @@
 
 #include "hp_rms_norm_amd.h"
 #include "hprms_kernels.h"
+#include "hprms_registry.h"
 
 namespace hprms {
 namespace {
@@ -37,54 +38,11 @@ int check_launch(const char* what) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
-// ---- fused kernel registry -------------------------------------------------------
-typedef void (*fused_fn)(FusedArgs);
-
-struct FusedEntry {
-  int dtype, mode, lpr, vpl, ldsv, block, flags;
-  fused_fn fn;
-};
-
-// flags: bits 0-1 = non-temporal loads / stores, bit 2 = weight loaded late,
-// bits 3-4 = sc1 policy bit on the row loads / stores
-#define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
-  {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
-   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 27, ((FLAGS) >> 2) & 1>},
-
-// (lanes per row, vectors per lane, of which in LDS, block, flags).  flags 3 =
-// nt on the row loads and stores, 7 = the same with the weight loaded late,
-// 27 / 31 = nt plus sc1 on loads and stores (without / with the late weight).
-// The table's entries (bandwidth rows, then the latency rows for few rows):
-#define HPRMS_TABLE_SHAPES(X, DT, MODE)                                                        \
-  X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
-  X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 3, 0, 256, 7)   \
-  X(DT, MODE, 128, 4, 0, 256, 3) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
-  X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27)                            \
-  X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)                           \
-  X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
-  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
-  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
-
-// entries of the plain-RMSNorm table that the fused table does not use
-#define HPRMS_PLAIN_SHAPES(X, DT, MODE)                                                        \
-  X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31) \
-  X(DT, MODE, 512, 8, 0, 512, 7)
-
-// entries of the FP8-output table that the other tables do not use
-#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
-
-// alternatives of the fused op that the tests run and the sweep compares against
-#define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
-  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
-  X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
-
-// extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
-#define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
-  X(DT, MODE, 64, 2, 0, 256, 11) X(DT, MODE, 128, 4, 0, 256, 27) X(DT, MODE, 256, 4, 0, 256, 27) \
-  X(DT, MODE, 512, 4, 0, 512, 3) X(DT, MODE, 1024, 4, 0, 1024, 7) X(DT, MODE, 512, 4, 0, 512, 27) \
-  X(DT, MODE, 256, 16, 8, 256, 31) X(DT, MODE, 128, 4, 0, 256, 0) X(DT, MODE, 1024, 4, 2, 1024, 31) \
-  X(DT, MODE, 256, 6, 3, 256, 31) X(DT, MODE, 256, 8, 4, 256, 3)
+bool aligned2(const void* p) { return ((uintptr_t)p & 1u) == 0; }
+// every row starts on a 128-byte boundary (a cache line)
+bool rows_aligned128(const void* base, int64_t stride_bytes) {
+  return ((uintptr_t)base & 127u) == 0 && stride_bytes % 128 == 0;
+}
 
 const FusedEntry kFused[] = {
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
@@ -110,11 +68,24 @@ const FusedEntry kFused[] = {
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 6)
 };
 
+bool entry_is(const FusedEntry& e, int dtype, int mode, const hprms_config& c) {
+  return e.dtype == dtype && e.mode == mode && e.lpr == c.lanes_per_row && e.vpl == c.vec_per_lane &&
+         e.ldsv == c.lds_vec_per_lane && e.block == c.block_threads && e.flags == c.flags;
+}
+
+// the three registries: the aligned kernels, the unaligned and the tail variants
+struct Registry {
+  const FusedEntry* entries;
+  int count;
+};
+const Registry kRegistries[] = {{kFused, (int)(sizeof(kFused) / sizeof(kFused[0]))},
+                                {kFusedUnaligned, kFusedUnalignedCount},
+                                {kFusedTail, kFusedTailCount}};
+
 const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
-  for (const FusedEntry& e : kFused)
-    if (e.dtype == dtype && e.mode == mode && e.lpr == c.lanes_per_row && e.vpl == c.vec_per_lane &&
-        e.ldsv == c.lds_vec_per_lane && e.block == c.block_threads && e.flags == c.flags)
-      return &e;
+  for (const Registry& r : kRegistries)
+    for (int i = 0; i < r.count; ++i)
+      if (entry_is(r.entries[i], dtype, mode, c)) return &r.entries[i];
   return nullptr;
 }
 
@@ -315,24 +286,37 @@ int check_problem(const Problem& p) {
   return HPRMS_OK;
 }
 
-// Can the vector tiers take this problem with configuration c?
+// Can the vector tiers take this problem with configuration c?  The
+// unaligned variants (flags bit 5) take rows at any 2-byte boundary, and with
+// the tail (bit 6) any hidden >= 8; the others need 16-byte aligned rows.
+// Without the tail, hidden % 8 == 0.
 bool vec_fits(const Problem& p, const hprms_config& c) {
-  if (p.hidden % 8 != 0) return false;
-  if (!aligned16(p.x) || !aligned16(p.w)) return false;
-  if (p.x_stride % 8 != 0) return false;
-  if (has_res(p.mode) && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
-  if (p.mode == 2 || p.mode == 5) {
-    if (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0) return false;
-  } else if (p.mode == 6) {
-    if (((uintptr_t)p.out & 3u) != 0 || p.out_stride % 4 != 0) return false;
-  } else if (has_out(p.mode) && (!aligned16(p.out) || p.out_stride % 8 != 0)) {
-    return false;
+  if ((c.flags & 64) ? p.hidden < 8 : p.hidden % 8 != 0) return false;  // the tail overlaps a whole vector
+  if (c.flags & 32) {
+    if (!aligned2(p.x) || !aligned2(p.w)) return false;
+    if (has_res(p.mode) && !aligned2(p.res)) return false;
+    if ((p.mode == 1 || p.mode == 3 || p.mode == 4) && !aligned2(p.out)) return false;
+    if (p.mode == 3 && !aligned2(p.res_out)) return false;
+    if (p.mode == 4 && p.parts)  // null only with rows == 0 (a configuration check)
+      for (int g = 0; g < p.nparts; ++g)
+        if (!aligned2(p.parts[g])) return false;
+  } else {
+    if (!aligned16(p.x) || !aligned16(p.w)) return false;
+    if (p.x_stride % 8 != 0) return false;
+    if (has_res(p.mode) && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
+    if (p.mode == 2 || p.mode == 5) {
+      if (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0) return false;
+    } else if (p.mode == 6) {
+      if (((uintptr_t)p.out & 3u) != 0 || p.out_stride % 4 != 0) return false;
+    } else if (has_out(p.mode) && (!aligned16(p.out) || p.out_stride % 8 != 0)) {
+      return false;
+    }
+    if (p.mode == 3 && (!aligned16(p.res_out) || p.res_out_stride % 8 != 0)) return false;
+    if (p.mode == 4 && p.parts)
+      for (int g = 0; g < p.nparts; ++g)
+        if (!aligned16(p.parts[g])) return false;
   }
-  if (p.mode == 3 && (!aligned16(p.res_out) || p.res_out_stride % 8 != 0)) return false;
-  if (p.mode == 4 && p.parts)  // null only with rows == 0 (a configuration check)
-    for (int g = 0; g < p.nparts; ++g)
-      if (!aligned16(p.parts[g])) return false;
-  if ((int64_t)c.lanes_per_row * c.vec_per_lane * 8 < p.hidden) return false;
+  if ((int64_t)c.lanes_per_row * c.vec_per_lane < p.hidden / 8) return false;  // whole vectors
   // every buffer resource of a row group spans < 2^31 bytes
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   int64_t smax = p.x_stride > p.out_stride ? p.x_stride : p.out_stride;
@@ -343,6 +327,29 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
     return false;
   return true;
+}
+
+// Which problems the table sends to the unaligned variant of its shape: rows
+// (of any stream) or the weight off the 128-byte grid, or hidden % 8 != 0.
+// Rows on the grid keep the measured table entry, sc1 bits included.
+bool needs_unaligned(const Problem& p) {
+  if (p.hidden % 8 != 0 || ((uintptr_t)p.w & 127u) != 0) return true;
+  if (!rows_aligned128(p.x, p.x_stride * 2)) return true;
+  if (has_res(p.mode) && !rows_aligned128(p.res, p.res_stride * 2)) return true;
+  if (has_out(p.mode)) {
+    const bool bytes = p.mode == 2 || is_mx(p.mode);  // quantised rows: byte strides
+    if (!rows_aligned128(p.out, bytes ? p.out_stride : p.out_stride * 2)) return true;
+  }
+  if (p.mode == 3 && !rows_aligned128(p.res_out, p.res_out_stride * 2)) return true;
+  if (p.mode == 4 && p.parts)
+    for (int g = 0; g < p.nparts; ++g)
+      if (!rows_aligned128(p.parts[g], p.x_stride * 2)) return true;
+  return false;
+}
+
+// the variant of a table entry for rows needs_unaligned() reports
+int unaligned_flags(int flags, int64_t hidden) {
+  return hidden % 8 != 0 ? HPRMS_TAIL_FLAGS(flags) : HPRMS_UNALIGNED_FLAGS(flags);
 }
 
 // The general tier (hprms_general.hip): rows up to 16K elements stay in
@@ -385,12 +392,12 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
     c = *forced;
   } else {
     table_config(p.rows, p.hidden, p.mode, &c);
+    if (c.tier != 3 && needs_unaligned(p)) c.flags = unaligned_flags(c.flags, p.hidden);
   }
   if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
     return fail(HPRMS_E_INVALID,
-                "MX output needs 16-byte aligned input, residual and weight, row strides %% 8 == 0, the "
-                "output %s, and a row group's rows (strides times rows per workgroup) within 2 GiB",
-                p.mode == 5 ? "8-byte aligned with a row stride % 8 == 0" : "4-byte aligned with a row stride % 4 == 0");
+                "MX output needs 2-byte aligned input, residual and weight and a row group's rows "
+                "(strides times rows per workgroup) within 2 GiB");
   if (c.tier != 3 && !vec_fits(p, c)) {
     if (forced && forced->tier != 0)
       return fail(HPRMS_E_INVALID,
@@ -546,7 +553,12 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms
   if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
   table_config(rows, hidden, mode, config);
-  if (hidden % 8 != 0) config->tier = 3;
+  if (hidden % 8 != 0) {
+    if (config->tier != 3 && hidden >= 8 && mode <= 4)
+      config->flags = unaligned_flags(config->flags, hidden);
+    else
+      config->tier = 3;
+  }
   return HPRMS_OK;
 }
 
@@ -577,11 +589,15 @@ int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
   if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
   if (capacity < 0 || (capacity > 0 && !out)) return fail(HPRMS_E_INVALID, "bad output array");
   int n = 0;
-  for (const FusedEntry& e : kFused) {
-    if (e.dtype != dtype || e.mode != mode) continue;
-    if (n < capacity)
-      out[n] = hprms_config{e.ldsv > 0 ? 2 : 1, e.lpr, e.vpl, e.ldsv, e.block, 0, e.flags};
-    ++n;
+  for (const Registry& r : kRegistries) {
+    for (int i = 0; i < r.count; ++i) {
+      const FusedEntry& e = r.entries[i];
+      if (e.dtype != dtype || e.mode != mode) continue;
+      const hprms_config c{e.ldsv > 0 ? 2 : 1, e.lpr, e.vpl, e.ldsv, e.block, 0, e.flags};
+      if (find_fused(dtype, mode, c) != &e) continue;  // listed once: the lookup's first match
+      if (n < capacity) out[n] = c;
+      ++n;
+    }
   }
   return n;
 }

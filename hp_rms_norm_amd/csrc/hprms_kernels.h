@@ -23,7 +23,16 @@
 // FLAGS bit 0 marks the row loads non-temporal, bit 1 the stores: the rows
 // are touched once, so they should not displace the weight from the caches.
 // Bits 3 and 4 add the sc1 (device-scope) policy bit to the loads and to the
-// stores respectively.  The residual is stored as soon as it is formed:
+// stores respectively.  Bit 5 marks the variants for rows that are not
+// 128-byte aligned (the host sends them there; the kernel code is the same and
+// correct for rows at any 2-byte boundary: 16-byte accesses at unaligned
+// addresses are legal on gfx9-family GPUs under the ROCm runtime, which runs
+// them in unaligned mode, and hipcc relies on the same for ordinary code).
+// Bit 6 adds TAIL, for hidden % 8 != 0: the lane holding
+// the last whole vector (nvec - 1) also loads the 16 bytes that end at the
+// row's end, counts only their last hidden % 8 elements in the sum of squares,
+// and stores all 8 -- the first 8 - hidden % 8 equal what that same lane
+// stores for vector nvec - 1, and all of a lane's loads precede its stores.  The residual is stored as soon as it is formed:
 // deferring it to the output phase (one write burst per workgroup) measured
 // up to 5% slower.
 //
@@ -94,6 +103,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   constexpr bool RES = MODE != 1;                                  // residual stream read
   constexpr bool MX = MODE == 5 || MODE == 6;                      // OCP MX output
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
+  constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // hidden % 8 trailing elements
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
@@ -111,6 +121,22 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   bool vec_ok[VPL];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < a.nvec;
+
+  // TAIL: byte offsets of the row's last 16 bytes (16-bit rows: tdelta; FP8
+  // rows: tqdelta) relative to the owning lane's first vector offset; the host
+  // guarantees nvec >= 1
+  int tcount = 0;
+  bool tlane = false;
+  uint32_t tdelta = 0, tqdelta = 0, twoff = kOOB;
+  if constexpr (TAIL) {
+    tcount = a.hidden - a.nvec * 8;
+    const int vt = a.nvec - 1;
+    const uint32_t kt = (uint32_t)(vt / LPR);
+    tlane = tcount > 0 && lane == (vt & (LPR - 1));
+    tdelta = kt * CH + 2u * (uint32_t)tcount;
+    tqdelta = kt * (LPR * 8u) + (uint32_t)tcount;
+    twoff = tlane ? (uint32_t)(a.hidden - 8) * 2u : kOOB;
+  }
 
   int buf = 0;
   for (int64_t g = blockIdx.x; g < a.ngroups; g += gridDim.x) {
@@ -166,15 +192,22 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
       xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
       if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
     }
+    const bool tok = tlane && row_ok;
+    u32x4 txv = {}, trv = {}, twv = {};
+    if constexpr (TAIL) {
+      txv = load16<LAUX>(xrs, tok ? xoff + tdelta : kOOB);
+      if constexpr (RES) trv = load16<LAUX>(rrs, tok ? roff + tdelta : kOOB);
+    }
     if constexpr (!WLATE) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
+      if constexpr (TAIL) twv = load16<0>(wrs, twoff);
     }
 
     if constexpr (MODE == 4) {
       // x := rne(sum of the parts), accumulated in fp32 in part order; the
       // unrolled loop keeps every parts[] index a constant
-      float acc[VPL][8];
+      float acc[VPL][8], tacc[8];
 #pragma unroll
       for (int k = 0; k < VPL; ++k)
 #pragma unroll
@@ -183,12 +216,18 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
           acc[k][2 * j + 1] = F::hi(xv[k][j]);
         }
 #pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tacc[2 * j] = F::lo(txv[j]);
+        tacc[2 * j + 1] = F::hi(txv[j]);
+      }
+#pragma unroll
       for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
         if (g >= a.nparts) break;
         const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * a.x_stride, xbytes);
-        u32x4 pv[VPL];
+        u32x4 pv[VPL], tpv = {};
 #pragma unroll
         for (int k = 0; k < VPL; ++k) pv[k] = load16<LAUX>(prs, (row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
+        if constexpr (TAIL) tpv = load16<LAUX>(prs, tok ? xoff + tdelta : kOOB);
 #pragma unroll
         for (int k = 0; k < VPL; ++k)
 #pragma unroll
@@ -196,11 +235,22 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
             acc[k][2 * j] += F::lo(pv[k][j]);
             acc[k][2 * j + 1] += F::hi(pv[k][j]);
           }
+        if constexpr (TAIL) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            tacc[2 * j] += F::lo(tpv[j]);
+            tacc[2 * j + 1] += F::hi(tpv[j]);
+          }
+        }
       }
 #pragma unroll
       for (int k = 0; k < VPL; ++k)
 #pragma unroll
         for (int j = 0; j < 4; ++j) xv[k][j] = F::pack(acc[k][2 * j], acc[k][2 * j + 1]);
+      if constexpr (TAIL) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) txv[j] = F::pack(tacc[2 * j], tacc[2 * j + 1]);
+      }
     }
 
     float ss0 = 0.0f, ss1 = 0.0f;
@@ -231,10 +281,28 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
       if (k < VREG) sv[k < VREG ? k : 0] = s;
       else spill[(k - VREG) * BLOCK + tid] = s;
     }
+    u32x4 tsv = {};
+    if constexpr (TAIL) {
+      // element e of the tail vector is row element hidden - 8 + e; only
+      // e >= 8 - tcount are not already counted (a select, so that a masked
+      // infinity adds 0 and not NaN)
+      const int first = 8 - tcount;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t p = RES ? F::pack(F::lo(txv[j]) + F::lo(trv[j]), F::hi(txv[j]) + F::hi(trv[j])) : txv[j];
+        tsv[j] = p;
+        const float b0 = 2 * j >= first ? F::lo(p) : 0.0f;
+        const float b1 = 2 * j + 1 >= first ? F::hi(p) : 0.0f;
+        ss0 = __builtin_fmaf(b0, b0, ss0);
+        ss1 = __builtin_fmaf(b1, b1, ss1);
+      }
+      if constexpr (RES) store16<SAUX>(tsv, srs, tok ? soff + tdelta : kOOB);
+    }
 
     if constexpr (WLATE) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
+      if constexpr (TAIL) twv = load16<0>(wrs, twoff);
     }
 
     float tot = group_sum<GW>(ss0 + ss1);
@@ -303,6 +371,13 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
         const bool ok = row_ok && vec_ok[k];
         store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
       }
+      if constexpr (TAIL) {
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = F::pack((F::lo(tsv[j]) * inv) * F::lo(twv[j]), (F::hi(tsv[j]) * inv) * F::hi(twv[j]));
+        store16<SAUX>(o, ors, tok ? ooff + tdelta : kOOB);
+      }
     } else {
       // y in 16-bit form, kept in the registers x came in; the row maximum of
       // |y| over the valid vectors, as packed 16-bit magnitudes
@@ -319,6 +394,20 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
             const uint32_t mag = xv[k][j] & 0x7fff7fffu;
             const uint32_t lo = mag & 0xffffu, hi = mag >> 16;
             m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(lo, hi));
+          }
+        }
+      }
+      if constexpr (TAIL) {
+        // the tail's first 8 - tcount elements repeat ones already counted:
+        // harmless for a maximum
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          txv[j] = F::pack((F::lo(tsv[j]) * inv) * F::lo(twv[j]), (F::hi(tsv[j]) * inv) * F::hi(twv[j]));
+        if (tok) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t mag = txv[j] & 0x7fff7fffu;
+            m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(mag & 0xffffu, mag >> 16));
           }
         }
       }
@@ -347,6 +436,16 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
         }
         const bool ok = row_ok && vec_ok[k];
         store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
+      }
+      if constexpr (TAIL) {
+        u32x2 q;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t y0 = txv[2 * h], y1 = txv[2 * h + 1];
+          q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * isc), clamp_e4m3(F::hi(y0) * isc),
+                             clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
+        }
+        store8<SAUX>(q, ors, tok ? ooff + tqdelta : kOOB);
       }
     }
   }

@@ -1,0 +1,81 @@
+// hprms_registry.h - the instantiated vector-tier kernels of the fused
+// add + RMSNorm family: (dtype, mode, shape, flags) -> kernel.  Shared by
+// hprms.hip (the 128-byte-aligned kernels and the dispatch),
+// hprms_unaligned.hip and hprms_tail.hip (the variants for every other row
+// layout), which the build compiles in parallel.
+#pragma once
+
+#include "hprms_kernels.h"
+
+namespace hprms {
+
+typedef void (*fused_fn)(FusedArgs);
+
+struct FusedEntry {
+  int dtype, mode, lpr, vpl, ldsv, block, flags;
+  fused_fn fn;
+};
+
+// flags: bits 0-1 = non-temporal loads / stores, bit 2 = weight loaded late,
+// bits 3-4 = sc1 policy bit on the row loads / stores, bit 5 = the variant for
+// rows that are not 128-byte aligned (any 2-byte boundary), bit 6 = with the
+// tail vector for hidden % 8 != 0 (with bit 5)
+#define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
+  {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
+   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 123, ((FLAGS) >> 2) & 1>},
+
+// The unaligned variants of a shape: the same lanes, vectors and weight
+// timing, no sc1 bits (partial cache lines written with sc1 measured 13-24%
+// slower at 16K-32K), bit 5 set; and the same with the tail (bit 6), which
+// costs about 30 VGPRs and so is kept apart from the rows that need no tail.
+#define HPRMS_UNALIGNED_FLAGS(FLAGS) ((((FLAGS) & ~24) | 32))
+#define HPRMS_TAIL_FLAGS(FLAGS) ((((FLAGS) & ~24) | 96))
+#define HPRMS_UNALIGNED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, HPRMS_UNALIGNED_FLAGS(FLAGS))
+#define HPRMS_TAIL_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, HPRMS_TAIL_FLAGS(FLAGS))
+
+// (lanes per row, vectors per lane, of which in LDS, block, flags).  flags 3 =
+// nt on the row loads and stores, 7 = the same with the weight loaded late,
+// 27 / 31 = nt plus sc1 on loads and stores (without / with the late weight).
+// The table's entries (bandwidth rows, then the latency rows for few rows):
+#define HPRMS_TABLE_SHAPES(X, DT, MODE)                                                        \
+  X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
+  X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 3, 0, 256, 7)   \
+  X(DT, MODE, 128, 4, 0, 256, 3) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
+  X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27)                            \
+  X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)                           \
+  X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
+  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
+
+// entries of the plain-RMSNorm table that the fused table does not use
+#define HPRMS_PLAIN_SHAPES(X, DT, MODE)                                                        \
+  X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31) \
+  X(DT, MODE, 512, 8, 0, 512, 7)
+
+// entries of the FP8-output table that the other tables do not use
+#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
+
+// alternatives of the fused op that the tests run and the sweep compares against
+#define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
+  X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
+  X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
+
+// extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
+#define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
+  X(DT, MODE, 64, 2, 0, 256, 11) X(DT, MODE, 128, 4, 0, 256, 27) X(DT, MODE, 256, 4, 0, 256, 27) \
+  X(DT, MODE, 512, 4, 0, 512, 3) X(DT, MODE, 1024, 4, 0, 1024, 7) X(DT, MODE, 512, 4, 0, 512, 27) \
+  X(DT, MODE, 256, 16, 8, 256, 31) X(DT, MODE, 128, 4, 0, 256, 0) X(DT, MODE, 1024, 4, 2, 1024, 31) \
+  X(DT, MODE, 256, 6, 3, 256, 31) X(DT, MODE, 256, 8, 4, 256, 3)
+
+// The unaligned variants (hprms_unaligned.hip) and the tail variants
+// (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every
+// entry the tables can choose, with HPRMS_UNALIGNED_FLAGS / HPRMS_TAIL_FLAGS
+// applied.
+extern const FusedEntry kFusedUnaligned[];
+extern const int kFusedUnalignedCount;
+extern const FusedEntry kFusedTail[];
+extern const int kFusedTailCount;
+
+}  // namespace hprms

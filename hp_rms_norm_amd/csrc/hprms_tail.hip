@@ -1,0 +1,31 @@
+// hprms_tail.hip - the vector-tier kernels for hidden % 8 != 0 (hidden >= 8):
+// the unaligned variants of hprms_unaligned.hip plus the tail vector, the
+// 16 bytes that end at the row's end, handled by the lane that holds the last
+// whole vector.  Modes 0-4 only: the MX outputs need hidden % 32 == 0.
+#include <hip/hip_runtime.h>
+
+#include "hp_rms_norm_amd.h"
+#include "hprms_registry.h"
+
+namespace hprms {
+
+const FusedEntry kFusedTail[] = {
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 0)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 2)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 2)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 3)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 3)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 4)
+    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 4)
+    HPRMS_PLAIN_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_PLAIN_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_FP8_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 2)
+    HPRMS_FP8_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 2)
+};
+
+const int kFusedTailCount = (int)(sizeof(kFusedTail) / sizeof(kFusedTail[0]));
+
+}  // namespace hprms

@@ -1,0 +1,44 @@
+// hprms_unaligned.hip - the vector-tier kernels for rows that do not start on
+// 128-byte boundaries (rows at any 2-byte boundary: 16-byte accesses at
+// unaligned addresses), hidden % 8 == 0.  One variant of every shape the
+// dispatch tables choose, with the same lanes, vectors and weight timing and
+// without the sc1 policy bit: with rows off the 128-byte grid, each wave's
+// 1 KiB chunk shares its first and last cache line with the next chunk, and
+// such partial lines written with sc1 measured 13-24% slower at 16K-32K (4096
+// rows, row stride hidden + 8).  Kept in its own translation unit so that the
+// build compiles it in parallel with hprms.hip; hprms_tail.hip holds the same
+// shapes with the tail vector for hidden % 8 != 0.
+#include <hip/hip_runtime.h>
+
+#include "hp_rms_norm_amd.h"
+#include "hprms_registry.h"
+
+namespace hprms {
+
+const FusedEntry kFusedUnaligned[] = {
+    // modes 0-6: the bandwidth and latency rows of the fused table
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 0)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 2)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 2)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 3)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 3)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 4)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 4)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 5)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 5)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 6)
+    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 6)
+    // the rows only the plain-RMSNorm and FP8-output tables use (some plain
+    // rows map onto a fused-table variant: the lookup takes the first match)
+    HPRMS_PLAIN_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 1)
+    HPRMS_PLAIN_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_FP8_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 2)
+    HPRMS_FP8_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 2)
+};
+
+const int kFusedUnalignedCount = (int)(sizeof(kFusedUnaligned) / sizeof(kFusedUnaligned[0]));
+
+}  // namespace hprms

@@ -61,9 +61,12 @@ typedef enum {
  * size_t tokens, int hidden_dim, double eps, cudaStream_t)`
  * (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618); the two row strides are new
  * (the reference assumes contiguous rows).  rows == 0 is a no-op.
- * hidden may be any value in [1, 2^24]; the fast tiers need hidden % 8 == 0,
- * row strides % 8 == 0 and 16-byte aligned pointers, other shapes take a
- * slower general kernel with the same results.
+ * hidden may be any value in [1, 2^24] and rows may start at any 2-byte
+ * boundary.  The vector tiers take every hidden in [8, 65543]: rows off the
+ * 128-byte grid run a variant without the sc1 cache-policy bit, and hidden %
+ * 8 != 0 adds a tail vector (flags bits 5 and 6 of hprms_config); other
+ * shapes take a slower general kernel.  The results are the same in every
+ * case: residual bit-exact, output within 1 ulp of the reference formula.
  */
 int hprms_fused_add_rmsnorm(void* input, const void* weight, void* residual,
                             int64_t rows, int64_t hidden,
@@ -105,8 +108,7 @@ int hprms_rmsnorm(void* out, const void* in, const void* weight,
  * (in bytes).  A row containing NaN gets a NaN scale and NaN outputs.  No
  * counterpart in the reference: it is the fused op followed by the
  * quantisation step that feeds an FP8 GEMM, with one write of H bytes
- * instead of 2H.  Fast tiers additionally need out 8-byte aligned and
- * out_row_stride % 8 == 0.
+ * instead of 2H.  `out` may start at any byte.
  */
 int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, const void* weight,
                                 void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
@@ -164,9 +166,9 @@ int hprms_reduce_add_rmsnorm(void* out, const void* const* parts, int nparts, co
  * `format` is HPRMS_MX_FP8_E4M3 (out: hidden bytes per row) or
  * HPRMS_MX_FP4_E2M1 (out: hidden / 2 bytes per row); `scales` holds hidden / 32
  * bytes per row; both row strides are in bytes.  `input` is only read.  Needs
- * hidden % 32 == 0, 16-byte aligned input, residual and weight with row
- * strides % 8 == 0, and `out` 8-byte (E4M3) or 4-byte (E2M1) aligned with a
- * row stride that is a multiple of that; there is no general-tier fallback.
+ * hidden % 32 == 0 and 2-byte aligned input, residual and weight (`out` and
+ * `scales` may start at any byte); there is no general-tier fallback, so a
+ * row group (rows per workgroup times the row strides) must span < 2 GiB.
  * No counterpart in the reference.
  */
 int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const void* weight,
@@ -191,7 +193,9 @@ typedef struct {
   int32_t grid_blocks;      /* 0 = one workgroup per row group; >0 = persistent grid of this many */
   int32_t flags;            /* bit 0: non-temporal row loads; bit 1: non-temporal stores;
                                bit 2: weight loaded after the residual is stored;
-                               bit 3 / bit 4: sc1 cache-policy bit on the row loads / stores */
+                               bit 3 / bit 4: sc1 cache-policy bit on the row loads / stores;
+                               bit 5: variant for rows off the 128-byte grid (any 2-byte
+                               boundary), bit 6 (with bit 5): tail vector, hidden % 8 != 0 */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
@@ -205,7 +209,9 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * hprms_fused_add_rmsnorm_fp8, 3: hprms_fused_add_rmsnorm_out, 4:
  * hprms_reduce_add_rmsnorm, 5 / 6: hprms_fused_add_rmsnorm_mx with
  * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1), written to *config (tier 3 when only the
- * general kernel fits hidden).  Pure function of its arguments; touches no
+ * general kernel fits hidden; with hidden % 8 != 0 the tail variant).  For
+ * rows on the 128-byte grid: rows off it run the same shape with flags
+ * (flags & ~24) | 32.  Pure function of its arguments; touches no
  * device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 

@@ -98,46 +98,75 @@ def test_errors_are_thread_local():
     assert "dtype" in abi.last_error()
 
 
+def variant_flags(flags, hidden):
+    """The flags of the kernel the dispatch runs for rows off the 128-byte grid
+    (hprms.hip, needs_unaligned / unaligned_flags): no sc1 bits, bit 5, and
+    bit 6 (the tail vector) when hidden % 8 != 0."""
+    return (flags & ~24) | (96 if hidden % 8 else 32)
+
+
+def entry_points_find_kernels(L, hidden, dtype, base):
+    """Every entry point with rows = 0 validates and looks its kernel up without
+    launching; `base` 0 gives 128-byte aligned rows, 2 rows at a 2-byte boundary
+    (the unaligned and tail variants)."""
+    x, w, r, o, ro = base, base, base, base, base
+    h = hidden
+    assert L.hprms_fused_add_rmsnorm(x, w, r, 0, h, h, h, dtype, 1e-6, None) == abi.HPRMS_OK, abi.last_error()
+    assert L.hprms_rmsnorm(o, x, w, 0, h, h, h, dtype, 1e-6, None) == abi.HPRMS_OK, abi.last_error()
+    rc = L.hprms_fused_add_rmsnorm_fp8(o, 0, x, w, r, 0, h, h, h, h, dtype, 1e-6, None)
+    assert rc == abi.HPRMS_OK, (h, abi.last_error())
+    rc = L.hprms_fused_add_rmsnorm_out(o, ro, x, w, r, 0, h, h, h, h, h, dtype, 1e-6, None)
+    assert rc == abi.HPRMS_OK, (h, abi.last_error())
+    rc = L.hprms_reduce_add_rmsnorm(o, None, 2, w, r, 0, h, h, h, h, dtype, 1e-6, None)
+    assert rc == abi.HPRMS_OK, (h, abi.last_error())
+    for fmt, qw in ((abi.MX_FP8_E4M3, h), (abi.MX_FP4_E2M1, h // 2)):
+        rc = L.hprms_fused_add_rmsnorm_mx(o, 0, x, w, r, 0, h, qw, h // 32, h, h, fmt, dtype, 1e-6, None)
+        want = abi.HPRMS_OK if h % 32 == 0 else abi.HPRMS_E_INVALID
+        assert rc == want, (h, fmt, abi.last_error())
+
+
 def test_table_covers_every_hidden_with_a_built_kernel():
     """Every hidden size maps either to a built vector-tier kernel that covers
-    it, or to the general kernel; checked through the config entry point with
-    rows = 0 (validates and looks the kernel up, launches nothing)."""
+    it, or (hidden < 8 or > 65543) to the general kernel; every table entry has
+    its unaligned and tail variants built; checked through the entry points
+    with rows = 0 (they validate and look the kernel up, and launch nothing)."""
     L = abi.lib()
+    built = {(dt, m): {c.as_tuple() for c in abi.kernel_configs(dt, m)}
+             for dt in (abi.DTYPE_BF16, abi.DTYPE_FP16) for m in range(7)}
     for dtype, rows in ((abi.DTYPE_BF16, 4096), (abi.DTYPE_FP16, 4096), (abi.DTYPE_BF16, 1), (abi.DTYPE_FP16, 256)):
-        for hidden in list(range(8, 70000, 8)) + [1, 3, 1001, 4097]:
+        for hidden in list(range(8, 70000, 8)) + [1, 3, 7, 9, 15, 1001, 4097, 65535, 65537, 65543, 65545]:
             c = abi.select_config(rows, hidden, dtype)
-            if hidden % 8:
+            if hidden < 8 or hidden // 8 > 8192:   # the table's last row holds 8192 whole vectors
                 assert c.tier == 3
                 continue
-            if c.tier == 3:
-                assert hidden > 65536
-                continue
-            assert c.lanes_per_row * c.vec_per_lane * 8 >= hidden
+            assert c.tier in (1, 2)
+            assert (c.flags & 96) == (96 if hidden % 8 else 0)
+            assert c.lanes_per_row * c.vec_per_lane >= hidden // 8
             assert c.block_threads % c.lanes_per_row == 0
-            rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
-                                                  ctypes.byref(c), None)
-            assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
-            rc = L.hprms_rmsnorm(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6, None)
-            assert rc == abi.HPRMS_OK
-            rc = L.hprms_fused_add_rmsnorm_fp8(0, 0, 0, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
-            assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
-            rc = L.hprms_fused_add_rmsnorm_out(0, 0, 0, 0, 0, 0, hidden, hidden, hidden, hidden, hidden, dtype,
-                                               1e-6, None)
-            assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
-            rc = L.hprms_reduce_add_rmsnorm(0, None, 2, 0, 0, 0, hidden, hidden, hidden, hidden, dtype, 1e-6, None)
-            assert rc == abi.HPRMS_OK, (hidden, abi.last_error())
-            for fmt, qw in ((abi.MX_FP8_E4M3, hidden), (abi.MX_FP4_E2M1, hidden // 2)):
-                rc = L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, hidden, qw, hidden // 32, hidden, hidden, fmt,
-                                                  dtype, 1e-6, None)
-                want = abi.HPRMS_OK if hidden % 32 == 0 else abi.HPRMS_E_INVALID
-                assert rc == want, (hidden, fmt, abi.last_error())
-            # the FP8 table's choice also exists as a fused (mode 0) kernel, so the
-            # 16-bit op can be run with the same lane mapping
-            c8 = abi.select_config(rows, hidden, dtype, 2)
-            assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
-            rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
-                                                  ctypes.byref(c8), None)
-            assert rc == abi.HPRMS_OK, (hidden, c8.as_tuple(), abi.last_error())
+            for mode in range(7):
+                if mode >= 5 and hidden % 32:
+                    continue
+                cm = abi.select_config(rows, hidden, dtype, mode)
+                t = cm.as_tuple()
+                assert t in built[(dtype, mode)], (hidden, mode, t)
+                assert t[:6] + (variant_flags(cm.flags, hidden),) in built[(dtype, mode)], (hidden, mode, t)
+                if mode <= 4 and hidden % 8 == 0:    # a tail variant of the same entry
+                    assert t[:6] + (variant_flags(cm.flags, 9),) in built[(dtype, mode)], (hidden, mode, t)
+            if hidden % 8 == 0 and hidden % 32 and hidden > 1024 and hidden not in (4104, 16392, 65528):
+                continue   # the lookups are exercised at every size class below and at the odd sizes
+            entry_points_find_kernels(L, hidden, dtype, 0)
+            entry_points_find_kernels(L, hidden, dtype, 2)
+            if hidden % 8 == 0:
+                rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
+                                                      ctypes.byref(c), None)
+                assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
+                # the FP8 table's choice also exists as a fused (mode 0) kernel, so the
+                # 16-bit op can be run with the same lane mapping
+                c8 = abi.select_config(rows, hidden, dtype, 2)
+                assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
+                rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
+                                                      ctypes.byref(c8), None)
+                assert rc == abi.HPRMS_OK, (hidden, c8.as_tuple(), abi.last_error())
 
 
 def test_config_entry_rejects_unbuilt_and_misfit_configs():
@@ -243,16 +272,17 @@ def test_mx_entry_rejects_bad_arguments():
 
     def call(**kw):
         a = dict(ok, **kw)
-        return L.hprms_fused_add_rmsnorm_mx(a["out"], a["sc"], a["x"], a["w"], a["r"], 4, a["h"], a["so"], a["ss"],
-                                            a["h"], a["h"], a["fmt"], 0, 1e-6, None)
+        return L.hprms_fused_add_rmsnorm_mx(a["out"], a["sc"], a["x"], a["w"], a["r"], a.get("rows", 4), a["h"],
+                                            a["so"], a["ss"], a["h"], a["h"], a["fmt"], 0, 1e-6, None)
     assert call(fmt=2) == abi.HPRMS_E_INVALID and "format" in abi.last_error()
     assert call(h=4104, so=4104, ss=200) == abi.HPRMS_E_INVALID and "32" in abi.last_error()
     assert call(so=1024) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
     assert call(fmt=abi.MX_FP8_E4M3) == abi.HPRMS_E_INVALID          # MXFP8 rows are hidden bytes wide
     assert call(ss=64) == abi.HPRMS_E_INVALID and "scale row stride" in abi.last_error()
     assert call(sc=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
-    assert call(out=0x4002) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
-    assert call(x=0x1008) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
+    # outputs and rows off the 16-byte grid take the unaligned variants; odd addresses are refused
+    assert call(out=0x4002, rows=0) == abi.HPRMS_OK and call(x=0x1008, rows=0) == abi.HPRMS_OK
+    assert call(x=0x1001) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
     # a scale row stride whose row group would not fit one buffer resource is refused, not truncated
     # (H = 256 maps 8 rows to a workgroup)
     assert L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, 256, 128, 1 << 29, 256, 256, abi.MX_FP4_E2M1, 0, 1e-6,

@@ -159,9 +159,13 @@ def general_widths():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_general_every_slot_count(abi, dtype):
+    """The general tier forced (the table sends these widths to the vector
+    tiers' tail variants)."""
+    from hp_rms_norm_amd.abi import Config
+    general = Config(3, 256, 0, 0, 256, 0, 0)
     for hidden, block, e in general_widths():
         print("general slots", hidden, block, e, dtype, flush=True)
-        check_case(abi, 23, hidden, dtype, seed=hidden + 1)
+        check_case(abi, 23, hidden, dtype, seed=hidden + 1, config=general)
 
 
 @pytest.mark.parametrize("rows,hidden", [(9, 100000), (2, 1 << 24)])

@@ -1,0 +1,307 @@
+"""GPU parity of the vector tiers' variants for rows off the 128-byte grid.
+
+The dispatch (hprms.hip, needs_unaligned) sends rows that do not all start on
+a 128-byte boundary to the unaligned variant of the table's shape (flags bit
+5: rows at any 2-byte boundary, no sc1 bits) and hidden % 8 != 0 to the tail
+variant (bit 6: the lane holding the last whole vector also handles the 16
+bytes that end at the row's end).  Both keep the shape's lane mapping and
+arithmetic, so:
+  * with hidden % 8 == 0, every mode on misaligned, padded views gives the
+    same bits as the same call on contiguous aligned copies (the table's
+    kernel), and writes nothing outside the views;
+  * every mode is within the usual bar of the oracle (residual bit-exact,
+    16-bit output within 1 ulp, FP8 within 1 e4m3 ulp);
+  * the tail is exercised at both ends of every table row, at every tail
+    length 1-7, on the latency rows and next to the general kernel's limits.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, assert_output_close, assert_residual_exact, bits, make_inputs, oracle_fused
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+EPS = 1e-6
+# whole vectors (8 elements) held by each row of the fused table (hprms.hip, table_config)
+TABLE_NVEC = [16, 32, 64, 128, 256, 384, 512, 1024, 1536, 1920, 2048, 3072, 4096, 8192]
+
+
+@pytest.fixture(scope="module")
+def abi():
+    assert torch.cuda.is_available(), "the gpu tests need a HIP device"
+    import hp_rms_norm_amd  # noqa: F401  (fails loudly if unbuilt)
+    from hp_rms_norm_amd import abi as a
+    a.lib()
+    return a
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+class View:
+    """A [rows, hidden] view at element offset `off` of a [rows, off + hidden +
+    pad] device buffer filled with `fill`; the buffer is kept to check that
+    nothing outside the view is written."""
+
+    def __init__(self, t, off, pad, fill=0x5A5A):
+        rows, hidden = t.shape
+        self.buf = torch.full((rows, off + hidden + pad), 0, dtype=torch.int16, device=DEV)
+        self.buf.fill_(fill - 65536 if fill > 32767 else fill)
+        self.buf = self.buf.view(t.dtype)
+        self.view = self.buf[:, off:off + hidden]
+        self.view.copy_(t.to(DEV))
+        self.off, self.hidden = off, hidden
+        self.outside = self._outside()
+
+    def _outside(self):
+        b = self.buf.view(torch.int16).cpu()
+        return torch.cat([b[:, :self.off], b[:, self.off + self.hidden:]], 1).clone()
+
+    @property
+    def ptr(self):
+        return self.view.data_ptr()
+
+    @property
+    def stride(self):
+        return self.buf.shape[1]
+
+    def check_outside(self, what):
+        assert torch.equal(self._outside(), self.outside), f"{what}: wrote outside the view"
+
+
+class ByteView:
+    """The same for byte rows (quantised outputs, MX scales)."""
+
+    def __init__(self, rows, width, off, pad):
+        self.buf = torch.full((rows, off + width + pad), 0xA5, dtype=torch.uint8, device=DEV)
+        self.view = self.buf[:, off:off + width]
+        self.off, self.width = off, width
+
+    @property
+    def ptr(self):
+        return self.view.data_ptr()
+
+    @property
+    def stride(self):
+        return self.buf.shape[1]
+
+    def check_outside(self, what):
+        b = self.buf.cpu()
+        assert bool((b[:, :self.off] == 0xA5).all()) and bool((b[:, self.off + self.width:] == 0xA5).all()), \
+            f"{what}: wrote outside the view"
+
+
+def u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16)
+
+
+# ---- mode 0: the fused op in place ----------------------------------------------------------
+def fused(abi, x, r, w, off=0, pad=0, woff=0, config=None):
+    xv, rv, wv = View(x, off, pad), View(r, off + 3 if off else 0, pad), View(w[None], woff, 0)
+    abi.fused_add_rmsnorm(xv.ptr, wv.ptr, rv.ptr, x.shape[0], x.shape[1], xv.stride, rv.stride, DT[x.dtype], EPS,
+                          _stream(), config)
+    torch.cuda.synchronize()
+    xv.check_outside("input")
+    rv.check_outside("residual")
+    return u16(xv.view), u16(rv.view)
+
+
+def widths_at_both_ends(tail):
+    """Per table row: its smallest and largest width (with a tail of 1 and 7
+    elements when `tail`, else whole vectors)."""
+    out, lo = [], 0
+    for hi in TABLE_NVEC:
+        out += [8 * (lo + 1) + 1, 8 * hi + 7] if tail else [8 * (lo + 1), 8 * hi]
+        lo = hi
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_misaligned_rows_equal_the_aligned_kernel_every_table_row(abi, dtype):
+    """Rows at a 2-byte offset with a row stride of hidden + 3 (and the weight
+    off by one element), and rows 16-byte aligned off the 128-byte grid (stride
+    hidden + 8): the same bits as contiguous aligned tensors, and the oracle's."""
+    for hidden in widths_at_both_ends(tail=False):
+        for rows in (67, 3):
+            x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + rows)
+            print("misaligned rows", rows, hidden, dtype, flush=True)
+            want_out, want_res = fused(abi, x, r, w)
+            for off, pad, woff in ((1, 2, 1), (8, 0, 0)):
+                got_out, got_res = fused(abi, x, r, w, off, pad, woff)
+                tag = f"{rows}x{hidden} {dtype} off {off} pad {pad}"
+                assert torch.equal(got_res, want_res), "residual differs from the aligned kernel " + tag
+                assert torch.equal(got_out, want_out), "output differs from the aligned kernel " + tag
+            o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+            assert_residual_exact(want_res.numpy().view(np.uint16), o_res, dtype)
+            assert_output_close(want_out.numpy().view(np.uint16), o_out, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_tail_at_both_ends_of_every_table_row(abi, dtype):
+    for hidden in widths_at_both_ends(tail=True):
+        c = abi.select_config(67, hidden, DT[dtype])
+        assert (c.flags & 96) == 96, (hidden, c.as_tuple())
+        x, r, w = make_inputs(67, hidden, dtype, seed=hidden)
+        print("tail", hidden, dtype, c.as_tuple(), flush=True)
+        got_out, got_res = fused(abi, x, r, w)
+        o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+        tag = f"67x{hidden} {dtype}"
+        assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, "residual " + tag)
+        assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, "output " + tag)
+        # the same rows at a 2-byte offset and padded: the same bits
+        m_out, m_res = fused(abi, x, r, w, off=1, pad=5, woff=1)
+        assert torch.equal(m_res, got_res) and torch.equal(m_out, got_out), "misaligned tail rows " + tag
+
+
+def test_every_tail_length_on_bandwidth_and_latency_rows(abi):
+    """hidden = 4096 + t, t = 1..7 (the tail overlaps the last whole vector by
+    8 - t elements), on the bandwidth table (300 rows) and the latency table
+    (5 rows); outliers, so that every element's square matters."""
+    for t in range(1, 8):
+        for rows in (300, 5):
+            hidden = 4096 + t
+            for dtype in (torch.bfloat16, torch.float16):
+                x, r, w = make_inputs(rows, hidden, dtype, seed=t + rows, dist="outliers")
+                print("tail length", t, rows, dtype, flush=True)
+                got_out, got_res = fused(abi, x, r, w)
+                o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+                tag = f"{rows}x{hidden} {dtype}"
+                assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, "residual " + tag)
+                assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, "output " + tag)
+
+
+def test_tail_limits_and_special_values(abi):
+    """The smallest widths with a tail (9 ... 15: the tail vector overlaps the
+    only whole vector), the largest the vector tiers take (65543), and a tail
+    element that is infinite or NaN (a masked duplicate must not turn an
+    infinite sum of squares into NaN)."""
+    dtype = torch.bfloat16
+    for hidden in (9, 10, 15, 17, 65543):
+        x, r, w = make_inputs(7, hidden, dtype, seed=hidden)
+        print("tail limit", hidden, flush=True)
+        got_out, got_res = fused(abi, x, r, w)
+        o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+        assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, f"residual {hidden}")
+        assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, f"output {hidden}")
+    hidden = 1003   # 125 whole vectors + 3: elements 995 ... 1002 form the tail vector
+    x, r, w = make_inputs(6, hidden, dtype, seed=5)
+    r[:] = 0
+    x[0, 1002] = float("inf")      # new element of the tail
+    x[1, 996] = float("inf")       # in the overlap: counted once, by its whole vector
+    x[2, 1001] = float("nan")
+    x[3, 995] = float("-inf")
+    print("tail special values", flush=True)
+    got_out, got_res = fused(abi, x, r, w)
+    o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+    assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, "residual special")
+    assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, "output special")
+
+
+# ---- modes 1-4 -------------------------------------------------------------------------
+OTHER_WIDTHS = [8, 1000, 1001, 4096, 4103, 12288, 16384, 16391, 32768, 32775, 65536]
+
+
+@pytest.mark.parametrize("hidden", OTHER_WIDTHS)
+def test_plain_fp8_out_and_reduce_on_misaligned_rows(abi, hidden):
+    dtype, rows = torch.float16, 37
+    x, r, w = make_inputs(rows, hidden, dtype, seed=hidden)
+    print("modes 1-4 misaligned", hidden, flush=True)
+    wv = View(w[None], 1, 0)
+    tag = f"{rows}x{hidden}"
+
+    # plain RMSNorm: input at a 2-byte offset, output 16-byte aligned off the 128-byte grid
+    xv, ov = View(x, 1, 4), View(torch.zeros_like(x), 8, 3)
+    abi.rmsnorm(ov.ptr, xv.ptr, wv.ptr, rows, hidden, ov.stride, xv.stride, DT[dtype], EPS, _stream())
+    xa, oa = x.to(DEV), torch.empty(rows, hidden, dtype=dtype, device=DEV)
+    abi.rmsnorm(oa.data_ptr(), xa.data_ptr(), w.to(DEV).data_ptr(), rows, hidden, hidden, hidden, DT[dtype], EPS,
+                _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("plain output")
+    if hidden % 8 == 0:
+        assert torch.equal(u16(ov.view), u16(oa)), "plain " + tag
+    want = oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=min(16, oracle.max_threads()))
+    assert_output_close(bits(ov.view), want, dtype, "plain " + tag)
+
+    # FP8 output at an odd byte offset
+    xv, rv = View(x, 1, 2), View(r, 3, 0)
+    qv = ByteView(rows, hidden, 3, 5)
+    sc = torch.empty(rows, dtype=torch.float32, device=DEV)
+    abi.fused_add_rmsnorm_fp8(qv.ptr, sc.data_ptr(), xv.ptr, wv.ptr, rv.ptr, rows, hidden, qv.stride, xv.stride,
+                              rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    qv.check_outside("fp8 output")
+    xv.check_outside("fp8 input")
+    assert torch.equal(u16(xv.view), u16(x)), "fp8: input modified " + tag
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8(bits(x), bits(w), bits(r), EPS, DT[dtype],
+                                                 threads=min(16, oracle.max_threads()))
+    assert_residual_exact(bits(rv.view), ores, dtype, "fp8 residual " + tag)
+    assert oracle.e4m3_ulp_distance(qv.view.contiguous().cpu().numpy(), oq).max() <= 1, "fp8 " + tag
+    np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7)
+
+    # out of place: every stream at its own offset
+    xv, rv = View(x, 1, 2), View(r, 2, 1)
+    ov, rov = View(torch.zeros_like(x), 3, 0), View(torch.zeros_like(x), 5, 2)
+    abi.fused_add_rmsnorm_out(ov.ptr, rov.ptr, xv.ptr, rv.ptr, wv.ptr, rows, hidden, ov.stride, rov.stride,
+                              xv.stride, rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("out")
+    rov.check_outside("residual_out")
+    assert torch.equal(u16(xv.view), u16(x)) and torch.equal(u16(rv.view), u16(r)), "out: inputs modified " + tag
+    o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+    assert_residual_exact(bits(rov.view), o_res, dtype, "out residual " + tag)
+    assert_output_close(bits(ov.view), o_out, dtype, "out output " + tag)
+
+    # partial sums: three parts sharing one row stride at different offsets
+    g = torch.Generator().manual_seed(hidden)
+    parts = [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(3)]
+    stride = hidden + 7
+    pbuf = torch.zeros(3, rows, stride + 4, dtype=dtype, device=DEV)
+    pviews = [pbuf[i, :, 1 + i:1 + i + hidden] for i in range(3)]
+    for pvw, p in zip(pviews, parts):
+        pvw.copy_(p.to(DEV))
+    rv, ov = View(r, 1, 0), View(torch.zeros_like(x), 2, 1)
+    abi.reduce_add_rmsnorm(ov.ptr, [p.data_ptr() for p in pviews], wv.ptr, rv.ptr, rows, hidden, ov.stride,
+                           pbuf.shape[2], rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("reduce output")
+    o_out, o_res = oracle.reduce_add_rmsnorm([bits(p) for p in parts], bits(w), bits(r), EPS, DT[dtype],
+                                             threads=min(16, oracle.max_threads()))
+    assert_residual_exact(bits(rv.view), o_res, dtype, "reduce residual " + tag)
+    assert_output_close(bits(ov.view), o_out, dtype, "reduce output " + tag)
+
+
+# ---- modes 5, 6: the MX outputs --------------------------------------------------------
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+def test_mx_on_misaligned_rows_equals_the_aligned_kernel(abi, fmt):
+    """Input and residual at 2-byte offsets, the elements and the scales at odd
+    byte offsets: the same bytes as the aligned call, nothing written outside."""
+    f = abi.MX_FP8_E4M3 if fmt == "mxfp8" else abi.MX_FP4_E2M1
+    dtype = torch.bfloat16
+    for hidden in (256, 2048, 4096, 16384, 32768):
+        for rows in (67, 3):
+            x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + rows)
+            qw = hidden if fmt == "mxfp8" else hidden // 2
+            print("mx misaligned", fmt, rows, hidden, flush=True)
+            # aligned reference call
+            xa, ra, wa = x.to(DEV), r.to(DEV), w.to(DEV)
+            qa = torch.empty(rows, qw, dtype=torch.uint8, device=DEV)
+            sa = torch.empty(rows, hidden // 32, dtype=torch.uint8, device=DEV)
+            abi.fused_add_rmsnorm_mx(qa.data_ptr(), sa.data_ptr(), xa.data_ptr(), wa.data_ptr(), ra.data_ptr(), rows,
+                                     hidden, qw, hidden // 32, hidden, hidden, f, DT[dtype], EPS, _stream())
+            xv, rv, wv = View(x, 1, 2), View(r, 5, 0), View(w[None], 1, 0)
+            qv, sv = ByteView(rows, qw, 3, 2), ByteView(rows, hidden // 32, 1, 3)
+            abi.fused_add_rmsnorm_mx(qv.ptr, sv.ptr, xv.ptr, wv.ptr, rv.ptr, rows, hidden, qv.stride, sv.stride,
+                                     xv.stride, rv.stride, f, DT[dtype], EPS, _stream())
+            torch.cuda.synchronize()
+            tag = f"{fmt} {rows}x{hidden}"
+            qv.check_outside("mx elements " + tag)
+            sv.check_outside("mx scales " + tag)
+            xv.check_outside("mx input " + tag)
+            rv.check_outside("mx residual " + tag)
+            assert torch.equal(u16(rv.view), u16(ra)), "residual " + tag
+            assert torch.equal(sv.view.cpu(), sa.cpu()), "scales " + tag
+            assert torch.equal(qv.view.cpu(), qa.cpu()), "elements " + tag
+            assert torch.equal(u16(xv.view), u16(x)), "input modified " + tag
