@@ -466,8 +466,13 @@ int launch_stream(const StreamArgs& base, bool flat, hipStream_t stream) {
       return fail(HPRMS_E_RANGE, "streamer: %lld elements exceed the grid limit", (long long)(a.rows * a.hidden));
     stream_chunk_kernel<DT, OP, kUnroll, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(a);
   } else {
-    const int64_t grid = a.rows < kMaxGrid ? a.rows : kMaxGrid;
-    stream_rows_kernel<DT, OP><<<dim3((unsigned)grid), dim3(256), 0, stream>>>(a);
+    // strided or misaligned rows: 4 KiB chunks of a row per workgroup
+    constexpr int kBlock = 256;
+    a.nvec = a.hidden / 8;
+    const int64_t chunks = a.nvec > 0 ? (a.nvec + kBlock - 1) / kBlock : 1;
+    const int64_t units = a.rows * chunks;
+    const int64_t grid = units < kMaxGrid ? units : kMaxGrid;
+    stream_rows_kernel<DT, OP, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(a);
   }
   return check_launch("streamer kernel");
 }
@@ -572,6 +577,8 @@ int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int6
   if (hidden < 1) return fail(HPRMS_E_INVALID, "hidden must be >= 1 (got %lld)", (long long)hidden);
   if (out_row_stride < hidden || in_row_stride < hidden)
     return fail(HPRMS_E_INVALID, "row strides must be >= hidden");
+  if (hidden >= (int64_t(1) << 30))  // a row's buffer resource spans 2 * hidden < 2^31 bytes
+    return fail(HPRMS_E_RANGE, "hidden %lld exceeds the streamer's row limit 2^30 - 1", (long long)hidden);
   if (rows == 0) return HPRMS_OK;
   if (!out || !in) return fail(HPRMS_E_INVALID, "null tensor pointer");
   StreamArgs a{(uint16_t*)out, (const uint16_t*)in, rows, hidden, out_row_stride, in_row_stride, 0};

@@ -1,7 +1,8 @@
 // hprms_kernels.h - the gfx950 kernels of libhprms.so.
 //
-// Fused residual-add + RMSNorm, "vector" tiers (hidden % 8 == 0, 16-byte
-// aligned rows).  A row of H elements is nvec = H/8 16-byte vectors.  A
+// Fused residual-add + RMSNorm, "vector" tiers (hidden >= 8; rows at any
+// 2-byte boundary, see FLAGS bits 5 and 6 below).  A row of H elements is
+// nvec = H/8 whole 16-byte vectors (plus a tail when H % 8 != 0).  A
 // workgroup of BLOCK lanes works on RPB = BLOCK/LPR rows at a time, LPR lanes
 // per row; lane l of a row owns vectors l, l+LPR, ..., l+(VPL-1)*LPR, so every
 // load instruction of a wave covers 1 KiB of contiguous bytes.  The row is
@@ -28,13 +29,14 @@
 // correct for rows at any 2-byte boundary: 16-byte accesses at unaligned
 // addresses are legal on gfx9-family GPUs under the ROCm runtime, which runs
 // them in unaligned mode, and hipcc relies on the same for ordinary code).
-// Bit 6 adds TAIL, for hidden % 8 != 0: the lane holding
-// the last whole vector (nvec - 1) also loads the 16 bytes that end at the
-// row's end, counts only their last hidden % 8 elements in the sum of squares,
-// and stores all 8 -- the first 8 - hidden % 8 equal what that same lane
-// stores for vector nvec - 1, and all of a lane's loads precede its stores.  The residual is stored as soon as it is formed:
-// deferring it to the output phase (one write burst per workgroup) measured
-// up to 5% slower.
+// Bit 6 adds TAIL, for hidden % 8 != 0: the lane holding the last whole
+// vector (nvec - 1) also loads the 16 bytes that end at the row's end, counts
+// only their last hidden % 8 elements in the sum of squares, and stores all 8
+// -- the first 8 - hidden % 8 equal what that same lane stores for vector
+// nvec - 1, and all of a lane's loads precede its stores.
+//
+// The residual is stored as soon as it is formed: deferring it to the output
+// phase (one write burst per workgroup) measured up to 5% slower.
 //
 // MODE 0 is the fused op (in place on input and residual); MODE 1 is the
 // plain RMSNorm (reads `input`, writes `out`, no residual stream); MODE 2 is
@@ -724,13 +726,46 @@ __global__ __launch_bounds__(BLOCK) void stream_chunk_kernel(StreamArgs a) {
   }
 }
 
-// General streamer: any strides and alignment; one workgroup per row.
-template <int DT, int OP>
-__global__ __launch_bounds__(256) void stream_rows_kernel(StreamArgs a) {
-  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
-    const uint16_t* in = a.in + row * a.in_stride;
-    uint16_t* out = a.out + row * a.out_stride;
-    for (int64_t j = threadIdx.x; j < a.hidden; j += 256) out[j] = stream_op1<DT, OP>(in[j]);
+// Row streamer: any row strides, rows at any 2-byte boundary.  Work unit u =
+// (row, chunk): BLOCK lanes, one 16-byte vector each (4 KiB per workgroup, as
+// the flat kernel), accesses through buffer resources sized to the row
+// (unaligned 16-byte accesses are legal here, see fused_vec_kernel), so the
+// range check drops everything past the row's whole vectors (a.nvec per
+// row).  hidden % 8 != 0: the lane holding the last whole vector also moves
+// the 16 bytes that end at the row's end; they overlap that vector, whose
+// elements it writes again with the same values (both ops are idempotent, so
+// this holds in place too).  hidden < 8: the first hidden lanes move one
+// element each.
+template <int DT, int OP, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void stream_rows_kernel(StreamArgs a) {
+  const int64_t chunks = a.nvec > 0 ? (a.nvec + BLOCK - 1) / BLOCK : 1;
+  const uint32_t rowbytes = (uint32_t)a.hidden * 2u;
+  const int tcount = (int)(a.hidden - a.nvec * 8);
+  for (int64_t u = blockIdx.x; u < a.rows * chunks; u += gridDim.x) {
+    const int64_t row = u / chunks;
+    const int64_t v = (u - row * chunks) * BLOCK + threadIdx.x;
+    const __amdgpu_buffer_rsrc_t irs = make_rsrc(a.in + row * a.in_stride, rowbytes);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(a.out + row * a.out_stride, rowbytes);
+    if (a.nvec == 0) {  // hidden < 8
+      const uint32_t off = (uint32_t)threadIdx.x * 2u;
+      __builtin_amdgcn_raw_buffer_store_b16(stream_op1<DT, OP>(__builtin_amdgcn_raw_buffer_load_b16(irs, off, 0, 0)),
+                                            ors, off, 0, 0);
+      continue;
+    }
+    const bool ok = v < a.nvec;
+    const bool tail = tcount > 0 && v == a.nvec - 1;
+    const uint32_t off = ok ? (uint32_t)v * 16u : kOOB;
+    const uint32_t toff = tail ? rowbytes - 16u : kOOB;
+    const u32x4 x = load16<kAuxNT>(irs, off);
+    const u32x4 t = load16<kAuxNT>(irs, toff);
+    u32x4 o, ot;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[j] = stream_op2<DT, OP>(x[j]);
+      ot[j] = stream_op2<DT, OP>(t[j]);
+    }
+    store16<kAuxNT>(o, ors, off);
+    store16<kAuxNT>(ot, ors, toff);
   }
 }
 

@@ -80,6 +80,10 @@ def test_streamer_and_plain_reject_bad_arguments():
     assert "op" in abi.last_error()
     assert L.hprms_streamer(0x1000, 0x2000, 4, 64, 32, 64, 0, 0, None) == abi.HPRMS_E_INVALID
     assert L.hprms_streamer(0, 0, 0, 64, 64, 64, 0, 0, None) == abi.HPRMS_OK
+    # a row's buffer resource spans 2 * hidden bytes, below 2^31
+    assert L.hprms_streamer(0, 0, 0, 1 << 30, 1 << 30, 1 << 30, 0, 0, None) == abi.HPRMS_E_RANGE
+    assert "2^30" in abi.last_error()
+    assert L.hprms_streamer(0, 0, 0, (1 << 30) - 1, 1 << 30, 1 << 30, 0, 0, None) == abi.HPRMS_OK
     assert L.hprms_rmsnorm(0x1000, 0x2000, 0, 4, 64, 64, 64, 0, 1e-6, None) == abi.HPRMS_E_INVALID
     assert L.hprms_rmsnorm(0x1000, 0x2000, 0x3000, 4, 64, 63, 64, 0, 1e-6, None) == abi.HPRMS_E_INVALID
 

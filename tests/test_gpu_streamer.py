@@ -77,19 +77,34 @@ def test_streamer_vs_oracle(ops, rows, hidden, dtype):
     torch.testing.assert_close(out, torch.relu(xd), rtol=0, atol=0, equal_nan=True)
 
 
-@pytest.mark.parametrize("offset,pad", [(0, 8), (1, 3), (1, 0)])
-def test_streamer_strided_and_misaligned(ops, offset, pad):
-    rows, hidden, dtype = 31, 1000, torch.bfloat16
-    x = _rand(rows, hidden, dtype, 5)
-    bi = torch.zeros(rows, hidden + pad + offset, dtype=dtype, device=DEV)
-    bo = torch.zeros_like(bi)
-    xi = bi[:, offset:offset + hidden]
-    xo = bo[:, offset:offset + hidden]
-    xi.copy_(x.to(DEV))
-    ops.relu_max0(xo, xi)
-    torch.cuda.synchronize()
-    assert np.array_equal(bits(xo), oracle.streamer(bits(x), DT[dtype], oracle.RELU))
-    assert torch.count_nonzero(bo[:, :offset]) == 0 and torch.count_nonzero(bo[:, offset + hidden:]) == 0
+# the row kernel (strided or misaligned rows): H < 8 (one element per lane), odd widths (the
+# tail vector), one 4 KiB chunk exactly (2048) and one vector past it, several chunks
+STRIDED_WIDTHS = [1, 7, 8, 9, 1000, 1001, 2048, 2049, 2056, 14337, 40000]
+
+
+@pytest.mark.parametrize("hidden", STRIDED_WIDTHS)
+def test_streamer_strided_and_misaligned(ops, hidden):
+    for dtype in (torch.bfloat16, torch.float16):
+        for offset, pad in ((0, 8), (1, 3), (1, 0), (3, 5)):
+            rows = 31
+            x = _rand(rows, hidden, dtype, hidden + offset)
+            for name, fn, op in (("copy", ops.relu, oracle.COPY), ("relu", ops.relu_max0, oracle.RELU)):
+                print("streamer rows", hidden, dtype, offset, pad, name, flush=True)
+                bi = torch.zeros(rows, hidden + pad + offset, dtype=dtype, device=DEV)
+                bo = torch.zeros_like(bi)
+                xi = bi[:, offset:offset + hidden]
+                xo = bo[:, offset + 1:offset + 1 + hidden] if pad else bo[:, offset:offset + hidden]
+                xi.copy_(x.to(DEV))
+                fn(xo, xi)
+                torch.cuda.synchronize()
+                want = oracle.streamer(bits(x), DT[dtype], op)
+                assert np.array_equal(bits(xo), want), (hidden, offset, pad, name)
+                lo = offset + 1 if pad else offset
+                assert torch.count_nonzero(bo[:, :lo]) == 0 and torch.count_nonzero(bo[:, lo + hidden:]) == 0
+                # in place on the strided view
+                fn(xi, xi)
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(xi), want), ("in place", hidden, offset, pad, name)
 
 
 def test_streamer_in_place(ops):
