@@ -207,51 +207,70 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     }
 
     if constexpr (MODE == 4) {
-      // x := rne(sum of the parts), accumulated in fp32 in part order; the
-      // unrolled loop keeps every parts[] index a constant
-      float acc[VPL][8], tacc[8];
+      // x := rne(sum of the parts), accumulated in fp32 in part order and
+      // rounded once, for groups of at most 2 vector slots at a time when a
+      // lane holds more than 4 (8 slots would need 64 fp32 accumulators per
+      // lane: past the VGPR budget of the wide shapes); the tail goes with the
+      // last group.  The unrolled loops keep every parts[] and slot index a
+      // constant.
+      constexpr int G = VPL <= 4 ? VPL : 2;
 #pragma unroll
-      for (int k = 0; k < VPL; ++k)
+      for (int k0 = 0; k0 < VPL; k0 += G) {
+        const bool with_tail = TAIL && k0 + G >= VPL;
+        float acc[G][8], tacc[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[k][2 * j] = F::lo(xv[k][j]);
-          acc[k][2 * j + 1] = F::hi(xv[k][j]);
-        }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        tacc[2 * j] = F::lo(txv[j]);
-        tacc[2 * j + 1] = F::hi(txv[j]);
-      }
-#pragma unroll
-      for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
-        if (g >= a.nparts) break;
-        const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * a.x_stride, xbytes);
-        u32x4 pv[VPL], tpv = {};
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) pv[k] = load16<LAUX>(prs, (row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
-        if constexpr (TAIL) tpv = load16<LAUX>(prs, tok ? xoff + tdelta : kOOB);
-#pragma unroll
-        for (int k = 0; k < VPL; ++k)
+        for (int i = 0; i < G; ++i) {
+          const int k = k0 + i < VPL ? k0 + i : 0;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            acc[k][2 * j] += F::lo(pv[k][j]);
-            acc[k][2 * j + 1] += F::hi(pv[k][j]);
-          }
-        if constexpr (TAIL) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            tacc[2 * j] += F::lo(tpv[j]);
-            tacc[2 * j + 1] += F::hi(tpv[j]);
+            acc[i][2 * j] = F::lo(xv[k][j]);
+            acc[i][2 * j + 1] = F::hi(xv[k][j]);
           }
         }
-      }
+        if (with_tail) {
 #pragma unroll
-      for (int k = 0; k < VPL; ++k)
+          for (int j = 0; j < 4; ++j) {
+            tacc[2 * j] = F::lo(txv[j]);
+            tacc[2 * j + 1] = F::hi(txv[j]);
+          }
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[k][j] = F::pack(acc[k][2 * j], acc[k][2 * j + 1]);
-      if constexpr (TAIL) {
+        for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+          if (g >= a.nparts) break;
+          const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * a.x_stride, xbytes);
+          u32x4 pv[G], tpv = {};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) txv[j] = F::pack(tacc[2 * j], tacc[2 * j + 1]);
+          for (int i = 0; i < G; ++i) {
+            const int k = k0 + i < VPL ? k0 + i : 0;
+            pv[i] = load16<LAUX>(prs, (k0 + i < VPL && row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
+          }
+          if (with_tail) tpv = load16<LAUX>(prs, tok ? xoff + tdelta : kOOB);
+#pragma unroll
+          for (int i = 0; i < G; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              acc[i][2 * j] += F::lo(pv[i][j]);
+              acc[i][2 * j + 1] += F::hi(pv[i][j]);
+            }
+          if (with_tail) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              tacc[2 * j] += F::lo(tpv[j]);
+              tacc[2 * j + 1] += F::hi(tpv[j]);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          if (k0 + i < VPL) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[k0 + i < VPL ? k0 + i : 0][j] = F::pack(acc[i][2 * j], acc[i][2 * j + 1]);
+          }
+        }
+        if (with_tail) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) txv[j] = F::pack(tacc[2 * j], tacc[2 * j + 1]);
+        }
       }
     }
 
