@@ -451,9 +451,9 @@ def test_plain_rmsnorm_every_table_row(abi, dtype):
 
 
 @pytest.mark.parametrize("hidden", [13, 1001, 4095, 16383, 20001])
-def test_plain_rmsnorm_general_tier(abi, hidden):
-    """Odd widths take the general kernels (register-resident up to 16K, two
-    passes above)."""
+def test_plain_rmsnorm_odd_widths(abi, hidden):
+    """Odd widths take the vector tiers' tail variants (the general tier for
+    every mode is tested in test_gpu_unaligned.py)."""
     import hp_rms_norm_amd
     for dtype in (torch.bfloat16, torch.float16):
         x, _, w = make_inputs(21, hidden, dtype, hidden)

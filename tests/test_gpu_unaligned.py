@@ -305,3 +305,87 @@ def test_mx_on_misaligned_rows_equals_the_aligned_kernel(abi, fmt):
             assert torch.equal(sv.view.cpu(), sa.cpu()), "scales " + tag
             assert torch.equal(qv.view.cpu(), qa.cpu()), "elements " + tag
             assert torch.equal(u16(xv.view), u16(x)), "input modified " + tag
+
+
+# ---- the general tier in every mode -------------------------------------------------------
+def strided_rows(t, stride):
+    """A [rows, hidden] device view with the given row stride over a flat buffer
+    of (rows - 1) * stride + hidden elements (no storage between the rows)."""
+    rows, hidden = t.shape
+    flat = torch.zeros((rows - 1) * stride + hidden, dtype=t.dtype, device=DEV)
+    v = flat.as_strided((rows, hidden), (stride, 1))
+    v.copy_(t.to(DEV))
+    return v
+
+
+# hidden < 8 (the general register kernel), > 65543 (the two-pass kernel), and 101 with a
+# row stride of 2^27 elements: its table shape puts 16 rows in a workgroup, whose buffer
+# resources would span 4 GiB, so the vector shapes are refused and the register kernel takes
+# the call.  1001 with a stride of 2^28 stays on the vector tier: with 2 rows the latency
+# table gives one row per workgroup, so huge strides fit its resources.
+GENERAL_CASES = [(7, 5, 7), (70001, 3, 70001), (101, 2, 1 << 27), (1001, 2, 1 << 28)]
+
+
+@pytest.mark.parametrize("hidden,rows,stride", GENERAL_CASES)
+def test_general_tier_every_mode(abi, hidden, rows, stride):
+    dtype = torch.bfloat16
+    x, r, w = make_inputs(rows, hidden, dtype, seed=hidden)
+    wd = w.to(DEV)
+    tag = f"{rows}x{hidden} stride {stride}"
+    print("general tier", tag, flush=True)
+    threads = min(16, oracle.max_threads())
+    o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+
+    # mode 0, in place
+    xd, rd = strided_rows(x, stride), strided_rows(r, stride)
+    abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden, stride, stride, DT[dtype], EPS,
+                          _stream())
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rd), o_res, dtype, "fused residual " + tag)
+    assert_output_close(bits(xd), o_out, dtype, "fused output " + tag)
+    del xd, rd
+
+    # mode 1, plain RMSNorm
+    xd, od = strided_rows(x, stride), strided_rows(torch.zeros_like(x), stride)
+    abi.rmsnorm(od.data_ptr(), xd.data_ptr(), wd.data_ptr(), rows, hidden, stride, stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    assert_output_close(bits(od), oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=threads), dtype,
+                        "plain " + tag)
+    del xd, od
+
+    # mode 2, FP8 output (rows of `stride` bytes)
+    xd, rd = strided_rows(x, stride), strided_rows(r, stride)
+    qflat = torch.zeros((rows - 1) * stride + hidden, dtype=torch.uint8, device=DEV)
+    q = qflat.as_strided((rows, hidden), (stride, 1))
+    sc = torch.empty(rows, dtype=torch.float32, device=DEV)
+    abi.fused_add_rmsnorm_fp8(q.data_ptr(), sc.data_ptr(), xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden,
+                              stride, stride, stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8(bits(x), bits(w), bits(r), EPS, DT[dtype], threads=threads)
+    assert_residual_exact(bits(rd), ores, dtype, "fp8 residual " + tag)
+    assert oracle.e4m3_ulp_distance(q.contiguous().cpu().numpy(), oq).max() <= 1, "fp8 " + tag
+    np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7)
+    del xd, rd, qflat, q
+
+    # mode 3, out of place
+    xd, rd = strided_rows(x, stride), strided_rows(r, stride)
+    od, rod = strided_rows(torch.zeros_like(x), stride), strided_rows(torch.zeros_like(x), stride)
+    abi.fused_add_rmsnorm_out(od.data_ptr(), rod.data_ptr(), xd.data_ptr(), rd.data_ptr(), wd.data_ptr(), rows,
+                              hidden, stride, stride, stride, stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rod), o_res, dtype, "out residual " + tag)
+    assert_output_close(bits(od), o_out, dtype, "out output " + tag)
+    del xd, rd, od, rod
+
+    # mode 4, three partial sums
+    g = torch.Generator().manual_seed(hidden + 1)
+    parts = [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(3)]
+    pds = [strided_rows(p, stride) for p in parts]
+    rd, od = strided_rows(r, stride), strided_rows(torch.zeros_like(x), stride)
+    abi.reduce_add_rmsnorm(od.data_ptr(), [p.data_ptr() for p in pds], wd.data_ptr(), rd.data_ptr(), rows, hidden,
+                           stride, stride, stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    p_out, p_res = oracle.reduce_add_rmsnorm([bits(p) for p in parts], bits(w), bits(r), EPS, DT[dtype],
+                                             threads=threads)
+    assert_residual_exact(bits(rd), p_res, dtype, "reduce residual " + tag)
+    assert_output_close(bits(od), p_out, dtype, "reduce output " + tag)
