@@ -134,7 +134,7 @@ bool mx_config(int64_t nvec, hprms_config* c) {
   static const Row mx[] = {{385, 512, 256, 2, 0, 256, 7},
                            {513, 1024, 512, 2, 0, 512, 7},
                            {1537, 2048, 1024, 2, 0, 1024, 31},
-                           {3073, 4096, 1024, 4, 0, 1024, 31}};
+                           {3073, 4096, 1024, 4, 0, 1024, 159}};
   for (const Row& r : mx) {
     if (nvec >= r.min_nvec && nvec <= r.max_nvec) {
       *c = hprms_config{1, r.lpr, r.vpl, r.ldsv, r.block, 0, r.flags};
@@ -175,16 +175,16 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
       {16, 16, 1, 0, 256, 3},        // H <= 128:   16 rows per workgroup
       {32, 32, 1, 0, 256, 3},        // H <= 256
       {64, 64, 1, 0, 256, 3},        // H <= 512:   one row per wave
-      {128, 32, 4, 0, 256, 3},       // H <= 1024:  two rows per wave
-      {256, 64, 4, 0, 256, 7},       // H <= 2048
+      {128, 32, 4, 0, 256, 131},     // H <= 1024:  two rows per wave
+      {256, 64, 4, 0, 256, 135},     // H <= 2048
       {384, 128, 3, 0, 256, 7},      // H <= 3072:  two waves per row
-      {512, 128, 4, 0, 256, 3},      // H <= 4096
+      {512, 128, 4, 0, 256, 131},    // H <= 4096
       {1024, 256, 4, 0, 256, 3},     // H <= 8192:  one row per 4-wave workgroup
       {1536, 512, 3, 0, 512, 31},    // H <= 12288
       {1920, 1024, 2, 0, 1024, 31},  // H <= 15360
       {2048, 256, 8, 4, 256, 27},    // H <= 16384: LDS tier, half the row in LDS
-      {3072, 1024, 3, 0, 1024, 31},  // H <= 24576
-      {4096, 1024, 4, 0, 1024, 31},  // H <= 32768
+      {3072, 1024, 3, 0, 1024, 159}, // H <= 24576
+      {4096, 1024, 4, 0, 1024, 159}, // H <= 32768
       {8192, 1024, 8, 4, 1024, 31},  // H <= 65536: LDS tier
   };
   for (const Row& r : table) {

@@ -33,7 +33,9 @@
 // vector (nvec - 1) also loads the 16 bytes that end at the row's end, counts
 // only their last hidden % 8 elements in the sum of squares, and stores all 8
 // -- the first 8 - hidden % 8 equal what that same lane stores for vector
-// nvec - 1, and all of a lane's loads precede its stores.
+// nvec - 1, and all of a lane's loads precede its stores.  Bit 7 issues all
+// of a lane's residual loads before its input loads (otherwise the two
+// streams alternate per vector); which is faster depends on the shape.
 //
 // The residual is stored as soon as it is formed: deferring it to the output
 // phase (one write burst per workgroup) measured up to 5% slower.
@@ -106,6 +108,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   constexpr bool MX = MODE == 5 || MODE == 6;                      // OCP MX output
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
   constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // hidden % 8 trailing elements
+  constexpr bool RFIRST = (FLAGS & 128) != 0 && RES;               // residual loads issued first
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
@@ -188,11 +191,22 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     }
 
     u32x4 xv[VPL], rv[VPL], wv[VPL];
+    if constexpr (RFIRST) {
+      // all of the residual's vectors, then all of the input's (the
+      // scheduling barriers keep the two groups apart)
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const bool ok = row_ok && vec_ok[k];
-      xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
-      if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+      for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + k * CH : kOOB);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const bool ok = row_ok && vec_ok[k];
+        xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
+        if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+      }
     }
     const bool tok = tlane && row_ok;
     u32x4 txv = {}, trv = {}, twv = {};

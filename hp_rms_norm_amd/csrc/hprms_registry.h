@@ -19,10 +19,10 @@ struct FusedEntry {
 // flags: bits 0-1 = non-temporal loads / stores, bit 2 = weight loaded late,
 // bits 3-4 = sc1 policy bit on the row loads / stores, bit 5 = the variant for
 // rows that are not 128-byte aligned (any 2-byte boundary), bit 6 = with the
-// tail vector for hidden % 8 != 0 (with bit 5)
+// tail vector for hidden % 8 != 0 (with bit 5), bit 7 = residual loads first
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
-   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 123, ((FLAGS) >> 2) & 1>},
+   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 251, ((FLAGS) >> 2) & 1>},
 
 // The unaligned variants of a shape: the same lanes, vectors and weight
 // timing, no sc1 bits (partial cache lines written with sc1 measured 13-24%
@@ -37,14 +37,15 @@ struct FusedEntry {
 
 // (lanes per row, vectors per lane, of which in LDS, block, flags).  flags 3 =
 // nt on the row loads and stores, 7 = the same with the weight loaded late,
-// 27 / 31 = nt plus sc1 on loads and stores (without / with the late weight).
+// 27 / 31 = nt plus sc1 on loads and stores (without / with the late weight);
+// +128 = the residual's loads issued before the input's.
 // The table's entries (bandwidth rows, then the latency rows for few rows):
 #define HPRMS_TABLE_SHAPES(X, DT, MODE)                                                        \
   X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
-  X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 3, 0, 256, 7)   \
-  X(DT, MODE, 128, 4, 0, 256, 3) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
+  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) \
+  X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
   X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27)                            \
-  X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)                           \
+  X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 4, 0, 1024, 159)                         \
   X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
   X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 256, 2, 0, 256, 7)    \
   X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
@@ -58,9 +59,12 @@ struct FusedEntry {
 #define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
 
 // alternatives of the fused op that the tests run and the sweep compares against
+// (the last five: the table's shapes with the two streams' loads alternating)
 #define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
   X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
-  X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)
+  X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)                           \
+  X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 4, 0, 256, 3)   \
+  X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)
 
 // extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \

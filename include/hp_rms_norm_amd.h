@@ -195,7 +195,8 @@ typedef struct {
                                bit 2: weight loaded after the residual is stored;
                                bit 3 / bit 4: sc1 cache-policy bit on the row loads / stores;
                                bit 5: variant for rows off the 128-byte grid (any 2-byte
-                               boundary), bit 6 (with bit 5): tail vector, hidden % 8 != 0 */
+                               boundary), bit 6 (with bit 5): tail vector, hidden % 8 != 0;
+                               bit 7: a lane's residual loads issued before its input loads */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
