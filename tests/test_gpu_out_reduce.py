@@ -154,8 +154,14 @@ def test_reduce_every_table_row(abi, dtype, nparts):
             assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
             assert_output_close(bits(od), want_out, dtype, "out " + tag)
             if nparts == 1:
-                ip_out, ip_res = in_place(parts[0], r, w, 1e-6)
-                assert np.array_equal(bits(od), ip_out), "P=1 differs from the in-place op " + tag
+                # the in-place op with the reduce form's shape (the same fp32 summation order)
+                cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_REDUCE)
+                xd, rd2 = parts[0].to(DEV), r.to(DEV)
+                abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd2.data_ptr(), rows, hidden, hidden, hidden,
+                                      DT[dtype], 1e-6, _stream(), cfg)
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(od), bits(xd)), "P=1 differs from the in-place op " + tag
+                assert np.array_equal(bits(rd), bits(rd2)), "P=1 residual differs from the in-place op " + tag
 
 
 def test_reduce_torch_op_out_is_a_part(abi):
@@ -203,7 +209,10 @@ def test_reduce_full_size_identities(abi):
     rows, hidden = 4096, 8192
     x, r, w = (t.to(DEV) for t in make_inputs(rows, hidden, torch.bfloat16, seed=21))
     want_x, want_r = x.clone(), r.clone()
-    hp_rms_norm_amd.hp_rms_norm(want_x, w, want_r, 1e-6)
+    # the in-place op with the reduce form's shape (the same fp32 summation order)
+    cfg = abi.select_config(rows, hidden, abi.DTYPE_BF16, abi.MODE_REDUCE)
+    abi.fused_add_rmsnorm(want_x.data_ptr(), w.data_ptr(), want_r.data_ptr(), rows, hidden, hidden, hidden,
+                          abi.DTYPE_BF16, 1e-6, _stream(), cfg)
     zeros = torch.zeros_like(x)
     for parts in ([x, zeros, zeros, zeros], [x * 0.5, x * 0.5]):
         rd = r.clone()
