@@ -82,10 +82,12 @@ const Registry kRegistries[] = {{kFused, (int)(sizeof(kFused) / sizeof(kFused[0]
                                 {kFusedUnaligned, kFusedUnalignedCount},
                                 {kFusedTail, kFusedTailCount}};
 
+// Each registry holds one kind of variant, told apart by flags bits 5 and 6,
+// so a lookup scans only the registry the configuration belongs to.
 const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
-  for (const Registry& r : kRegistries)
-    for (int i = 0; i < r.count; ++i)
-      if (entry_is(r.entries[i], dtype, mode, c)) return &r.entries[i];
+  const Registry& r = kRegistries[(c.flags & 64) ? 2 : (c.flags & 32) ? 1 : 0];
+  for (int i = 0; i < r.count; ++i)
+    if (entry_is(r.entries[i], dtype, mode, c)) return &r.entries[i];
   return nullptr;
 }
 
