@@ -182,6 +182,8 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   if (mode == 2 && fp8_config(nvec, c)) return;
   if ((mode == 5 || mode == 6) && mx_config(nvec, c)) return;
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
+  // flags: 3 = non-temporal row loads and stores, +4 = weight loaded late,
+  // +24 = sc1 on loads and stores, +128 = residual loads before input loads
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row table[] = {
       {16, 16, 1, 0, 256, 3},        // H <= 128:   16 rows per workgroup
