@@ -103,8 +103,9 @@ def test_fp8_every_table_entry(ops):
             run_case(ops, rows, hidden, torch.bfloat16, seed=hidden + rows)
 
 
+# odd widths: the tail variants from 8 up, the general tier below
 @pytest.mark.parametrize("hidden", [1, 13, 255, 700, 1001, 2049, 4097, 7167, 9999, 13313, 16383, 16385])
-def test_fp8_general_kernel(ops, hidden):
+def test_fp8_odd_widths(ops, hidden):
     run_case(ops, 37, hidden, torch.bfloat16, seed=hidden)
     run_case(ops, 5, hidden, torch.float16, seed=hidden + 1)
 

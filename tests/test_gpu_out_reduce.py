@@ -98,7 +98,7 @@ def test_out_of_place_torch_ops_and_aliases(abi):
 
 @pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24), (4096, 3), (6143, 1), (11001, 5), (16383, 1),
                                         (20001, 2)])
-def test_out_of_place_strided_and_general_tier(abi, hidden, pad):
+def test_out_of_place_strided_and_odd_widths(abi, hidden, pad):
     dtype = torch.float16
     rows = 37
     x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + pad)
@@ -178,7 +178,7 @@ def test_reduce_torch_op_out_is_a_part(abi):
 
 
 @pytest.mark.parametrize("hidden,pad", [(1001, 3), (4096, 24), (7167, 1), (12289, 7), (16383, 1), (20001, 2)])
-def test_reduce_strided_and_general_tier(abi, hidden, pad):
+def test_reduce_strided_and_odd_widths(abi, hidden, pad):
     dtype = torch.bfloat16
     rows = 29
     parts = make_parts(3, rows, hidden, dtype, seed=hidden)

@@ -128,9 +128,9 @@ def test_persistent_grid(abi):
         check_case(abi, 1000, 4096, torch.bfloat16, seed=grid, config=cfg)
 
 
-# ---- general kernel: tails, misalignment, row strides ---------------------------------
-# odd widths on both sides of the register-resident general kernel's block sizes (64
-# threads up to 1024, 256 up to 8K, 1024 up to 16K) and of the two-pass kernel above 16K
+# ---- odd widths, misalignment, row strides, the general tier --------------------------
+# odd widths (the vector tiers' tail variants from 8 up, the general tier below 8 and above
+# 65543) on both sides of the table's rows and of the general kernels' block sizes
 @pytest.mark.parametrize("hidden", [1, 7, 13, 100, 255, 257, 1023, 1025, 4095, 4097, 16383, 16385, 40000])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_hidden_not_multiple_of_8(abi, hidden, dtype):
