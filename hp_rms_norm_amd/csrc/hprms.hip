@@ -361,9 +361,45 @@ bool needs_unaligned(const Problem& p) {
   return false;
 }
 
+// Where a stream's rows start relative to its vector boundaries (16 bytes; 8
+// bytes for the FP8 output's byte rows): row r starts (base + r * step) mod 8
+// elements past one.
+struct Phase {
+  uint32_t base, step;
+  bool operator==(const Phase& o) const { return base == o.base && step == o.step; }
+};
+Phase phase16(const void* p, int64_t stride) { return {(uint32_t)(((uintptr_t)p >> 1) & 7u), (uint32_t)(stride & 7)}; }
+Phase phase8(const void* p, int64_t stride) { return {(uint32_t)((uintptr_t)p & 7u), (uint32_t)(stride & 7)}; }
+
+// Shifted rows (the tail variant's FusedArgs::shift_*): modes 0-4 from 513
+// whole vectors up shift each row so that the streams the kernel writes are
+// accessed aligned, when they all share one phase ({0, 0} otherwise: no
+// shift).  Measured on MI355X (4096 rows, bf16, rows 2 bytes off alignment or
+// hidden % 8 != 0): aligning every stream is 8-19% faster than 16-byte
+// accesses at unaligned addresses from H = 4104 to 64K, and 5-18% slower at
+// 1K-4K, where a row's set-up weighs more; aligning the reads at the cost of
+// the writes measured 3-22% slower (plain, out of place, FP8 output), so the
+// written streams decide.
+constexpr int64_t kShiftMinVec = 513;
+
+Phase shift_phase(const Problem& p) {
+  const Phase none = {0, 0};
+  if (p.mode > 4 || p.hidden / 8 < kShiftMinVec) return none;
+  Phase w[2];
+  switch (p.mode) {
+    case 0: w[0] = phase16(p.x, p.x_stride); w[1] = phase16(p.res, p.res_stride); break;
+    case 1: w[0] = w[1] = phase16(p.out, p.out_stride); break;
+    case 2: w[0] = phase16(p.res, p.res_stride); w[1] = phase8(p.out, p.out_stride); break;
+    case 3: w[0] = phase16(p.out, p.out_stride); w[1] = phase16(p.res_out, p.res_out_stride); break;
+    default: w[0] = phase16(p.out, p.out_stride); w[1] = phase16(p.res, p.res_stride); break;
+  }
+  return w[0] == w[1] ? w[0] : none;
+}
+
 // the variant of a table entry for rows needs_unaligned() reports
-int unaligned_flags(int flags, int64_t hidden) {
-  return hidden % 8 != 0 ? HPRMS_TAIL_FLAGS(flags) : HPRMS_UNALIGNED_FLAGS(flags);
+int unaligned_flags(const Problem& p, int flags) {
+  return p.hidden % 8 != 0 || !(shift_phase(p) == Phase{0, 0}) ? HPRMS_TAIL_FLAGS(flags)
+                                                               : HPRMS_UNALIGNED_FLAGS(flags);
 }
 
 // The general tier (hprms_general.hip): rows up to 16K elements stay in
@@ -406,7 +442,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
     c = *forced;
   } else {
     table_config(p.rows, p.hidden, p.mode, &c);
-    if (c.tier != 3 && needs_unaligned(p)) c.flags = unaligned_flags(c.flags, p.hidden);
+    if (c.tier != 3 && needs_unaligned(p)) c.flags = unaligned_flags(p, c.flags);
   }
   if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
     return fail(HPRMS_E_INVALID,
@@ -454,6 +490,11 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   a.res_stride = p.res_stride;
   a.hidden = (int32_t)p.hidden;
   a.nvec = (int32_t)(p.hidden / 8);
+  if (c.flags & 64) {
+    const Phase ph = shift_phase(p);
+    a.shift_base = ph.base;
+    a.shift_step = ph.step;
+  }
   a.hidden_f = (float)p.hidden;
   a.eps = (float)p.eps;
 
@@ -574,7 +615,7 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms
   table_config(rows, hidden, mode, config);
   if (hidden % 8 != 0) {
     if (config->tier != 3 && hidden >= 8 && mode <= 4)
-      config->flags = unaligned_flags(config->flags, hidden);
+      config->flags = HPRMS_TAIL_FLAGS(config->flags);
     else
       config->tier = 3;
   }

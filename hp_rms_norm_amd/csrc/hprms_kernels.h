@@ -29,11 +29,18 @@
 // correct for rows at any 2-byte boundary: 16-byte accesses at unaligned
 // addresses are legal on gfx9-family GPUs under the ROCm runtime, which runs
 // them in unaligned mode, and hipcc relies on the same for ordinary code).
-// Bit 6 adds TAIL, for hidden % 8 != 0: the lane holding the last whole
-// vector (nvec - 1) also loads the 16 bytes that end at the row's end, counts
-// only their last hidden % 8 elements in the sum of squares, and stores all 8
-// -- the first 8 - hidden % 8 equal what that same lane stores for vector
-// nvec - 1, and all of a lane's loads precede its stores.  Bit 7 issues all
+// Bit 6 selects the tail variant (TAIL), for widths that are not a multiple
+// of 8 (hidden >= 8) and for shifted rows (hidden >= 16).  Row r is shifted by
+// delta = (shift_base + r * shift_step) mod 8 elements (both 0: no shift): the
+// lanes' "body" vectors start at element 8j - delta (j >= 1 when delta > 0),
+// so a stream whose row r starts delta elements past a vector boundary (16
+// bytes; 8 bytes for the FP8 output) is accessed aligned; the elements before the first body
+// vector come from a head vector (the row's first 16 bytes, lane 0) and those
+// after the last from a tail vector (the row's last 16 bytes, the lane holding
+// the last body vector, or lane 1 when that is lane 0).  An edge vector counts
+// only its elements no body vector holds, and stores all 8: the others equal
+// what their body vector stores, from a lane of the same wave, and a wave
+// issues all its loads before its stores.  Bit 7 issues all
 // of a lane's residual loads before its input loads (otherwise the two
 // streams alternate per vector); which is faster depends on the shape.
 //
@@ -80,6 +87,8 @@ struct FusedArgs {
   int64_t res_stride;
   int32_t hidden;
   int32_t nvec;          // hidden / 8
+  uint32_t shift_base;   // tail variant: row r is shifted by (shift_base + r * shift_step) mod 8 elements
+  uint32_t shift_step;
   float hidden_f;
   float eps;
   uint8_t* q;            // MODES 2, 5, 6: quantised output rows
@@ -107,7 +116,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
   constexpr bool RES = MODE != 1;                                  // residual stream read
   constexpr bool MX = MODE == 5 || MODE == 6;                      // OCP MX output
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
-  constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // hidden % 8 trailing elements
+  constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // shifted rows, head and tail vectors
   // residual loads issued first (not for the partial-sum form, where it measured 0.1-1.8% slower)
   constexpr bool RFIRST = (FLAGS & 128) != 0 && RES && MODE != 4;
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
@@ -128,22 +137,6 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
 #pragma unroll
   for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < a.nvec;
 
-  // TAIL: byte offsets of the row's last 16 bytes (16-bit rows: tdelta; FP8
-  // rows: tqdelta) relative to the owning lane's first vector offset; the host
-  // guarantees nvec >= 1
-  int tcount = 0;
-  bool tlane = false;
-  uint32_t tdelta = 0, tqdelta = 0, twoff = kOOB;
-  if constexpr (TAIL) {
-    tcount = a.hidden - a.nvec * 8;
-    const int vt = a.nvec - 1;
-    const uint32_t kt = (uint32_t)(vt / LPR);
-    tlane = tcount > 0 && lane == (vt & (LPR - 1));
-    tdelta = kt * CH + 2u * (uint32_t)tcount;
-    tqdelta = kt * (LPR * 8u) + (uint32_t)tcount;
-    twoff = tlane ? (uint32_t)(a.hidden - 8) * 2u : kOOB;
-  }
-
   int buf = 0;
   for (int64_t g = blockIdx.x; g < a.ngroups; g += gridDim.x) {
     const int64_t row0 = g * RPB;
@@ -153,7 +146,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
 
     const uint32_t xbytes = (uint32_t)(((int64_t)(nrows - 1) * a.x_stride + a.hidden) * 2);
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row0 * a.x_stride, xbytes);
-    const uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + (uint32_t)lane * 16u;
+    uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + (uint32_t)lane * 16u;
 
     // rrs/roff: residual loads; srs/soff: residual stores; ors/ooff: output
     __amdgpu_buffer_rsrc_t rrs = xrs, srs = xrs, ors = xrs;
@@ -191,6 +184,50 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
     }
 
+    // TAIL: this row's shift and the lane's edge vector (head or tail); the
+    // e*off offsets address the edge vector in each stream, kOOB elsewhere
+    uint32_t wshift = 0, exoff = kOOB, eroff = kOOB, esoff = kOOB, eooff = kOOB, ewoff = kOOB;
+    int elo = 0, ehi = 0;
+    bool eok = false;
+    if constexpr (TAIL) {
+      const int delta = (int)((a.shift_base + (uint32_t)(row0 + rib) * a.shift_step) & 7u);
+      const int j0 = delta > 0 ? 1 : 0;
+      const int jend = (a.hidden + delta) >> 3;
+      const int nb = jend - j0;  // body vectors of this row (>= 1: hidden >= 8, and >= 16 when shifted)
+      const int t = a.hidden + delta - 8 * jend;  // elements after the last body vector
+      const uint32_t xrow = xoff - (uint32_t)lane * 16u;
+      const uint32_t rrow = roff - (uint32_t)lane * 16u, srow = soff - (uint32_t)lane * 16u;
+      const uint32_t orow = ooff - (uint32_t)lane * (MODE == 2 ? 8u : 16u);
+      wshift = 16u * (uint32_t)j0 - 2u * (uint32_t)delta;
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < nb;
+      xoff += wshift;
+      if constexpr (RES) {
+        roff += wshift;
+        soff += wshift;
+      }
+      ooff += MODE == 2 ? (uint32_t)(8 * j0 - delta) : wshift;
+      int tl = (nb - 1) & (LPR - 1);
+      if (delta > 0 && tl == 0) tl = 1;
+      uint32_t eb = 0, eq = 0;
+      if (delta > 0 && lane == 0) {
+        eok = row_ok; elo = 0; ehi = 8 - delta;
+      } else if (t > 0 && lane == tl) {
+        eok = row_ok; elo = 8 - t; ehi = 8;
+        eb = 2u * (uint32_t)a.hidden - 16u;
+        eq = (uint32_t)a.hidden - 8u;
+      }
+      if (eok) {
+        exoff = xrow + eb;
+        if constexpr (RES) {
+          eroff = rrow + eb;
+          esoff = srow + eb;
+        }
+        eooff = orow + (MODE == 2 ? eq : eb);
+        ewoff = eb;
+      }
+    }
+
     u32x4 xv[VPL], rv[VPL], wv[VPL];
     if constexpr (RFIRST) {
       // all of the residual's vectors, then all of the input's (the
@@ -209,16 +246,15 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
         if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
       }
     }
-    const bool tok = tlane && row_ok;
     u32x4 txv = {}, trv = {}, twv = {};
     if constexpr (TAIL) {
-      txv = load16<LAUX>(xrs, tok ? xoff + tdelta : kOOB);
-      if constexpr (RES) trv = load16<LAUX>(rrs, tok ? roff + tdelta : kOOB);
+      txv = load16<LAUX>(xrs, exoff);
+      if constexpr (RES) trv = load16<LAUX>(rrs, eroff);
     }
     if constexpr (!WLATE) {
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
-      if constexpr (TAIL) twv = load16<0>(wrs, twoff);
+      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u + wshift);
+      if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
     }
 
     if constexpr (MODE == 4) {
@@ -259,7 +295,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
             const int k = k0 + i < VPL ? k0 + i : 0;
             pv[i] = load16<LAUX>(prs, (k0 + i < VPL && row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
           }
-          if (with_tail) tpv = load16<LAUX>(prs, tok ? xoff + tdelta : kOOB);
+          if (with_tail) tpv = load16<LAUX>(prs, exoff);
 #pragma unroll
           for (int i = 0; i < G; ++i)
 #pragma unroll
@@ -319,26 +355,24 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
     }
     u32x4 tsv = {};
     if constexpr (TAIL) {
-      // element e of the tail vector is row element hidden - 8 + e; only
-      // e >= 8 - tcount are not already counted (a select, so that a masked
-      // infinity adds 0 and not NaN)
-      const int first = 8 - tcount;
+      // only the edge vector's elements elo <= e < ehi are not held by a body
+      // vector (a select, so that a masked infinity adds 0 and not NaN)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t p = RES ? F::pack(F::lo(txv[j]) + F::lo(trv[j]), F::hi(txv[j]) + F::hi(trv[j])) : txv[j];
         tsv[j] = p;
-        const float b0 = 2 * j >= first ? F::lo(p) : 0.0f;
-        const float b1 = 2 * j + 1 >= first ? F::hi(p) : 0.0f;
+        const float b0 = (2 * j >= elo && 2 * j < ehi) ? F::lo(p) : 0.0f;
+        const float b1 = (2 * j + 1 >= elo && 2 * j + 1 < ehi) ? F::hi(p) : 0.0f;
         ss0 = __builtin_fmaf(b0, b0, ss0);
         ss1 = __builtin_fmaf(b1, b1, ss1);
       }
-      if constexpr (RES) store16<SAUX>(tsv, srs, tok ? soff + tdelta : kOOB);
+      if constexpr (RES) store16<SAUX>(tsv, srs, esoff);
     }
 
     if constexpr (WLATE) {
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u);
-      if constexpr (TAIL) twv = load16<0>(wrs, twoff);
+      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u + wshift);
+      if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
     }
 
     float tot = group_sum<GW>(ss0 + ss1);
@@ -412,7 +446,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           o[j] = F::pack((F::lo(tsv[j]) * inv) * F::lo(twv[j]), (F::hi(tsv[j]) * inv) * F::hi(twv[j]));
-        store16<SAUX>(o, ors, tok ? ooff + tdelta : kOOB);
+        store16<SAUX>(o, ors, eooff);
       }
     } else {
       // y in 16-bit form, kept in the registers x came in; the row maximum of
@@ -434,12 +468,12 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
         }
       }
       if constexpr (TAIL) {
-        // the tail's first 8 - tcount elements repeat ones already counted:
-        // harmless for a maximum
+        // the edge vector's elements outside [elo, ehi) repeat ones already
+        // counted: harmless for a maximum
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           txv[j] = F::pack((F::lo(tsv[j]) * inv) * F::lo(twv[j]), (F::hi(tsv[j]) * inv) * F::hi(twv[j]));
-        if (tok) {
+        if (eok) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const uint32_t mag = txv[j] & 0x7fff7fffu;
@@ -481,7 +515,7 @@ __global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
           q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * isc), clamp_e4m3(F::hi(y0) * isc),
                              clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
         }
-        store8<SAUX>(q, ors, tok ? ooff + tqdelta : kOOB);
+        store8<SAUX>(q, ors, eooff);
       }
     }
   }

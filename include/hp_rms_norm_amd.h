@@ -195,7 +195,9 @@ typedef struct {
                                bit 2: weight loaded after the residual is stored;
                                bit 3 / bit 4: sc1 cache-policy bit on the row loads / stores;
                                bit 5: variant for rows off the 128-byte grid (any 2-byte
-                               boundary), bit 6 (with bit 5): tail vector, hidden % 8 != 0;
+                               boundary), bit 6 (with bit 5): head and tail vectors, for
+                               hidden % 8 != 0 and (from hidden 4104 up, modes 0-4) rows
+                               shifted to the written streams' 16-byte phase;
                                bit 7: a lane's residual loads issued before its input loads */
 } hprms_config;
 

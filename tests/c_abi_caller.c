@@ -63,8 +63,9 @@ int main(void) {
     EXPECT(n > 0);
   }
   EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, 7, &c) == HPRMS_E_INVALID);
-  /* hidden % 8 != 0: the same shape with the tail vector (flags bit 6); below 8 elements, the general kernel */
+  /* hidden % 8 != 0: the same shape with a tail vector (flags bit 6); below 8 elements, the general kernel */
   EXPECT(hprms_select_config(4096, 4097, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 1 && (c.flags & 96) == 96);
+  EXPECT(hprms_select_config(4096, 15, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 1 && (c.flags & 96) == 96);
   EXPECT(hprms_select_config(4096, 7, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 3);
 
   if (failures) return 1;

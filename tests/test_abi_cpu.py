@@ -104,8 +104,9 @@ def test_errors_are_thread_local():
 
 def variant_flags(flags, hidden):
     """The flags of the kernel the dispatch runs for rows off the 128-byte grid
-    (hprms.hip, needs_unaligned / unaligned_flags): no sc1 bits, bit 5, and
-    bit 6 (the tail vector) when hidden % 8 != 0."""
+    (hprms.hip, needs_unaligned / unaligned_flags): no sc1 bits, and bit 6 (the
+    tail variant) when hidden % 8 != 0, else bit 5 (bit 6 also for input rows
+    off 16-byte boundaries from 513 whole vectors up: the shifted rows)."""
     return (flags & ~24) | (96 if hidden % 8 else 32)
 
 

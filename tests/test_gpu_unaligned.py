@@ -1,18 +1,23 @@
 """GPU parity of the vector tiers' variants for rows off the 128-byte grid.
 
-The dispatch (hprms.hip, needs_unaligned) sends rows that do not all start on
-a 128-byte boundary to the unaligned variant of the table's shape (flags bit
-5: rows at any 2-byte boundary, no sc1 bits) and hidden % 8 != 0 to the tail
-variant (bit 6: the lane holding the last whole vector also handles the 16
-bytes that end at the row's end).  Both keep the shape's lane mapping and
-arithmetic, so:
-  * with hidden % 8 == 0, every mode on misaligned, padded views gives the
-    same bits as the same call on contiguous aligned copies (the table's
-    kernel), and writes nothing outside the views;
-  * every mode is within the usual bar of the oracle (residual bit-exact,
-    16-bit output within 1 ulp, FP8 within 1 e4m3 ulp);
-  * the tail is exercised at both ends of every table row, at every tail
-    length 1-7, on the latency rows and next to the general kernel's limits.
+The dispatch (hprms.hip, needs_unaligned / shift_rows) sends rows that do not
+all start on a 128-byte boundary to a variant of the table's shape:
+  * hidden % 8 == 0: the unaligned variant (flags bit 5: rows at any 2-byte
+    boundary, no sc1 bits), which keeps the shape's lane mapping and
+    arithmetic, so it gives the same bits as the table's kernel on contiguous
+    aligned copies;
+  * hidden % 8 != 0: the tail variant (bit 6), whose lane holding the last
+    whole vector also handles the 16 bytes that end at the row's end;
+  * from 513 whole vectors up, modes 0-4 with input rows off 16-byte
+    boundaries: the tail variant with shifted rows, which starts each row's
+    body vectors at the input's first 16-byte boundary and adds a head vector
+    for the elements before them; its sum of squares runs in another order,
+    so its output is held to the oracle's bar and its residual to the same
+    bits.
+Every mode is within the usual bar of the oracle (residual bit-exact, 16-bit
+output within 1 ulp, FP8 within 1 e4m3 ulp) and writes nothing outside the
+views; the edge vectors are exercised at both ends of every table row, at
+every tail length 1-7, on the latency rows and next to the limits.
 """
 import numpy as np
 import pytest
@@ -121,22 +126,26 @@ def widths_at_both_ends(tail):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_misaligned_rows_equal_the_aligned_kernel_every_table_row(abi, dtype):
-    """Rows at a 2-byte offset with a row stride of hidden + 3 (and the weight
-    off by one element), and rows 16-byte aligned off the 128-byte grid (stride
-    hidden + 8): the same bits as contiguous aligned tensors, and the oracle's."""
+    """Rows 16-byte aligned off the 128-byte grid (stride hidden + 8): the same
+    bits as contiguous aligned tensors.  Rows at a 2-byte offset with a row
+    stride of hidden + 3 (and the weight off by one element): the same residual
+    bits and the oracle's bar for the output."""
     for hidden in widths_at_both_ends(tail=False):
         for rows in (67, 3):
             x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + rows)
             print("misaligned rows", rows, hidden, dtype, flush=True)
             want_out, want_res = fused(abi, x, r, w)
+            o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+            assert_residual_exact(want_res.numpy().view(np.uint16), o_res, dtype)
+            assert_output_close(want_out.numpy().view(np.uint16), o_out, dtype)
             for off, pad, woff in ((1, 2, 1), (8, 0, 0)):
                 got_out, got_res = fused(abi, x, r, w, off, pad, woff)
                 tag = f"{rows}x{hidden} {dtype} off {off} pad {pad}"
                 assert torch.equal(got_res, want_res), "residual differs from the aligned kernel " + tag
-                assert torch.equal(got_out, want_out), "output differs from the aligned kernel " + tag
-            o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
-            assert_residual_exact(want_res.numpy().view(np.uint16), o_res, dtype)
-            assert_output_close(want_out.numpy().view(np.uint16), o_out, dtype)
+                if off % 8 == 0:
+                    assert torch.equal(got_out, want_out), "output differs from the aligned kernel " + tag
+                else:
+                    assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, "output " + tag)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
@@ -151,18 +160,21 @@ def test_tail_at_both_ends_of_every_table_row(abi, dtype):
         tag = f"67x{hidden} {dtype}"
         assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, "residual " + tag)
         assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, "output " + tag)
-        # the same rows at a 2-byte offset and padded: the same bits
+        # the same rows at a 2-byte offset and padded (above 512 whole vectors each row is
+        # shifted to its own 16-byte boundary)
         m_out, m_res = fused(abi, x, r, w, off=1, pad=5, woff=1)
-        assert torch.equal(m_res, got_res) and torch.equal(m_out, got_out), "misaligned tail rows " + tag
+        assert torch.equal(m_res, got_res), "misaligned tail rows, residual " + tag
+        assert_output_close(m_out.numpy().view(np.uint16), o_out, dtype, "misaligned tail rows, output " + tag)
 
 
 def test_every_tail_length_on_bandwidth_and_latency_rows(abi):
-    """hidden = 4096 + t, t = 1..7 (the tail overlaps the last whole vector by
-    8 - t elements), on the bandwidth table (300 rows) and the latency table
-    (5 rows); outliers, so that every element's square matters."""
+    """hidden = 4096 + t and 8192 + t, t = 1..7 (the tail overlaps the last
+    whole vector by 8 - t elements; at 8192 + t rows are shifted and start at
+    2t-byte steps, so the head and tail vectors take every length), on the
+    bandwidth table (300 rows) and the latency table (5 rows); outliers, so
+    that every element's square matters."""
     for t in range(1, 8):
-        for rows in (300, 5):
-            hidden = 4096 + t
+        for rows, hidden in ((300, 4096 + t), (5, 4096 + t), (300, 8192 + t), (5, 8192 + t)):
             for dtype in (torch.bfloat16, torch.float16):
                 x, r, w = make_inputs(rows, hidden, dtype, seed=t + rows, dist="outliers")
                 print("tail length", t, rows, dtype, flush=True)
@@ -175,29 +187,40 @@ def test_every_tail_length_on_bandwidth_and_latency_rows(abi):
 
 def test_tail_limits_and_special_values(abi):
     """The smallest widths with a tail (9 ... 15: the tail vector overlaps the
-    only whole vector), the largest the vector tiers take (65543), and a tail
-    element that is infinite or NaN (a masked duplicate must not turn an
-    infinite sum of squares into NaN)."""
+    only whole vector), the smallest with shifted rows (4104, 4105), the
+    largest the vector tiers take (65543), and edge elements that are infinite
+    or NaN (a masked duplicate must not turn an infinite sum of squares into
+    NaN), on contiguous rows and at a 2-byte offset."""
     dtype = torch.bfloat16
-    for hidden in (9, 10, 15, 17, 65543):
+    for hidden in (9, 10, 15, 16, 17, 4103, 4104, 4105, 65543):
         x, r, w = make_inputs(7, hidden, dtype, seed=hidden)
         print("tail limit", hidden, flush=True)
         got_out, got_res = fused(abi, x, r, w)
         o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
         assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, f"residual {hidden}")
         assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, f"output {hidden}")
-    hidden = 1003   # 125 whole vectors + 3: elements 995 ... 1002 form the tail vector
-    x, r, w = make_inputs(6, hidden, dtype, seed=5)
+        m_out, m_res = fused(abi, x, r, w, off=1, pad=2, woff=1)
+        assert_residual_exact(m_res.numpy().view(np.uint16), o_res, dtype, f"residual {hidden} off 1")
+        assert_output_close(m_out.numpy().view(np.uint16), o_out, dtype, f"output {hidden} off 1")
+    # 8195 elements (shifted rows): the tail vector is elements 8187 ... 8194; rows at
+    # 16390-byte steps start 0, 3, 6, 1, 4, 7, 2, 5 elements past a 16-byte boundary, so
+    # the head vector covers 0 ... 7 and its own elements are the first 8 - shift
+    hidden = 8195
+    x, r, w = make_inputs(8, hidden, dtype, seed=5)
     r[:] = 0
-    x[0, 1002] = float("inf")      # new element of the tail
-    x[1, 996] = float("inf")       # in the overlap: counted once, by its whole vector
-    x[2, 1001] = float("nan")
-    x[3, 995] = float("-inf")
-    print("tail special values", flush=True)
-    got_out, got_res = fused(abi, x, r, w)
+    x[0, 8194] = float("inf")      # element of the tail only
+    x[1, 8188] = float("inf")      # in the tail's overlap: counted once, by its body vector
+    x[2, 8193] = float("nan")
+    x[3, 8187] = float("-inf")
+    x[4, 0] = float("inf")         # element of the head only
+    x[5, 7] = float("-inf")        # in the head's overlap
+    x[6, 5] = float("nan")
+    print("edge special values", flush=True)
     o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
-    assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, "residual special")
-    assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, "output special")
+    for off, pad in ((0, 0), (1, 2)):
+        got_out, got_res = fused(abi, x, r, w, off=off, pad=pad)
+        assert_residual_exact(got_res.numpy().view(np.uint16), o_res, dtype, f"residual special off {off}")
+        assert_output_close(got_out.numpy().view(np.uint16), o_out, dtype, f"output special off {off}")
 
 
 # ---- modes 1-4 -------------------------------------------------------------------------
@@ -220,8 +243,6 @@ def test_plain_fp8_out_and_reduce_on_misaligned_rows(abi, hidden):
                 _stream())
     torch.cuda.synchronize()
     ov.check_outside("plain output")
-    if hidden % 8 == 0:
-        assert torch.equal(u16(ov.view), u16(oa)), "plain " + tag
     want = oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=min(16, oracle.max_threads()))
     assert_output_close(bits(ov.view), want, dtype, "plain " + tag)
 
@@ -269,6 +290,83 @@ def test_plain_fp8_out_and_reduce_on_misaligned_rows(abi, hidden):
     ov.check_outside("reduce output")
     o_out, o_res = oracle.reduce_add_rmsnorm([bits(p) for p in parts], bits(w), bits(r), EPS, DT[dtype],
                                              threads=min(16, oracle.max_threads()))
+    assert_residual_exact(bits(rv.view), o_res, dtype, "reduce residual " + tag)
+    assert_output_close(bits(ov.view), o_out, dtype, "reduce output " + tag)
+
+
+# ---- shifted rows: the written streams share one phase ----------------------------------
+SHIFT_WIDTHS = [4104, 4105, 8195, 16384, 32773]
+
+
+@pytest.mark.parametrize("hidden", SHIFT_WIDTHS)
+def test_shifted_rows_every_mode(abi, hidden):
+    """From 513 whole vectors up, rows whose written streams share one phase
+    (element offsets 1-7; row strides not a multiple of 8, so each row has its
+    own shift) are shifted to it: modes 0-4 against the oracle, with the read
+    streams at other phases, and nothing written outside the views."""
+    dtype, rows = torch.bfloat16, 21
+    x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + 7)
+    tag = f"{rows}x{hidden}"
+    print("shifted rows", tag, flush=True)
+    th = min(16, oracle.max_threads())
+    o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+    wv = View(w[None], 1, 0)
+
+    # the fused op: input and residual at one phase
+    xv, rv = View(x, 3, 2), View(r, 3, 2)
+    abi.fused_add_rmsnorm(xv.ptr, wv.ptr, rv.ptr, rows, hidden, xv.stride, rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    xv.check_outside("input")
+    rv.check_outside("residual")
+    assert_residual_exact(bits(rv.view), o_res, dtype, "fused residual " + tag)
+    assert_output_close(bits(xv.view), o_out, dtype, "fused output " + tag)
+
+    # plain RMSNorm: the output decides
+    xv, ov = View(x, 2, 1), View(torch.zeros_like(x), 5, 3)
+    abi.rmsnorm(ov.ptr, xv.ptr, wv.ptr, rows, hidden, ov.stride, xv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("plain output")
+    want = oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=th)
+    assert_output_close(bits(ov.view), want, dtype, "plain " + tag)
+
+    # FP8 output: the residual's element phase equals the byte rows' phase
+    xv, rv, qv = View(x, 6, 0), View(r, 1, 2), ByteView(rows, hidden, 1, 2)
+    sc = torch.empty(rows, dtype=torch.float32, device=DEV)
+    abi.fused_add_rmsnorm_fp8(qv.ptr, sc.data_ptr(), xv.ptr, wv.ptr, rv.ptr, rows, hidden, qv.stride, xv.stride,
+                              rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    qv.check_outside("fp8 output")
+    rv.check_outside("fp8 residual")
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8(bits(x), bits(w), bits(r), EPS, DT[dtype], threads=th)
+    assert_residual_exact(bits(rv.view), ores, dtype, "fp8 residual " + tag)
+    assert oracle.e4m3_ulp_distance(qv.view.contiguous().cpu().numpy(), oq).max() <= 1, "fp8 " + tag
+    np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7)
+
+    # out of place: both outputs at one phase
+    xv, rv = View(x, 0, 3), View(r, 2, 0)
+    ov, rov = View(torch.zeros_like(x), 7, 1), View(torch.zeros_like(x), 7, 1)
+    abi.fused_add_rmsnorm_out(ov.ptr, rov.ptr, xv.ptr, rv.ptr, wv.ptr, rows, hidden, ov.stride, rov.stride,
+                              xv.stride, rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("out")
+    rov.check_outside("residual_out")
+    assert_residual_exact(bits(rov.view), o_res, dtype, "out residual " + tag)
+    assert_output_close(bits(ov.view), o_out, dtype, "out output " + tag)
+
+    # partial sums: the output and the residual at one phase, the parts elsewhere
+    g = torch.Generator().manual_seed(hidden)
+    parts = [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(3)]
+    pbuf = torch.zeros(3, rows, hidden + 11, dtype=dtype, device=DEV)
+    pviews = [pbuf[i, :, 1 + i:1 + i + hidden] for i in range(3)]
+    for pvw, p in zip(pviews, parts):
+        pvw.copy_(p.to(DEV))
+    rv, ov = View(r, 4, 6), View(torch.zeros_like(x), 4, 6)
+    abi.reduce_add_rmsnorm(ov.ptr, [p.data_ptr() for p in pviews], wv.ptr, rv.ptr, rows, hidden, ov.stride,
+                           pbuf.shape[2], rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("reduce output")
+    rv.check_outside("reduce residual")
+    o_out, o_res = oracle.reduce_add_rmsnorm([bits(p) for p in parts], bits(w), bits(r), EPS, DT[dtype], threads=th)
     assert_residual_exact(bits(rv.view), o_res, dtype, "reduce residual " + tag)
     assert_output_close(bits(ov.view), o_out, dtype, "reduce output " + tag)
 
