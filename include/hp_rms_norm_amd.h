@@ -214,8 +214,11 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1), written to *config (tier 3 when only the
  * general kernel fits hidden; with hidden % 8 != 0 the tail variant).  For
  * rows on the 128-byte grid: rows off it run the same shape with flags
- * (flags & ~24) | 32.  Pure function of its arguments; touches no
- * device. */
+ * (flags & ~24) | 32, or | 96 (the tail variant) for hidden % 8 != 0 and, in
+ * modes 0-4 from hidden 4104 up, for rows off 16-byte alignment when every
+ * tensor the call writes is off by the same amount in each row (the kernel
+ * then shifts its vectors to align them).  Pure function of its arguments;
+ * touches no device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
