@@ -299,14 +299,16 @@ SHIFT_WIDTHS = [4104, 4105, 8195, 16384, 32773]
 
 
 @pytest.mark.parametrize("hidden", SHIFT_WIDTHS)
-def test_shifted_rows_every_mode(abi, hidden):
+@pytest.mark.parametrize("dtype,rows,nparts", [(torch.bfloat16, 21, 3), (torch.float16, 300, 8)],
+                         ids=["bf16-latency-table", "fp16-bandwidth-table"])
+def test_shifted_rows_every_mode(abi, hidden, dtype, rows, nparts):
     """From 513 whole vectors up, rows whose written streams share one phase
     (element offsets 1-7; row strides not a multiple of 8, so each row has its
     own shift) are shifted to it: modes 0-4 against the oracle, with the read
-    streams at other phases, and nothing written outside the views."""
-    dtype, rows = torch.bfloat16, 21
+    streams at other phases, and nothing written outside the views; on the
+    latency table's shapes (few rows) and the bandwidth table's."""
     x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + 7)
-    tag = f"{rows}x{hidden}"
+    tag = f"{rows}x{hidden} {dtype}"
     print("shifted rows", tag, flush=True)
     th = min(16, oracle.max_threads())
     o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
@@ -355,9 +357,9 @@ def test_shifted_rows_every_mode(abi, hidden):
 
     # partial sums: the output and the residual at one phase, the parts elsewhere
     g = torch.Generator().manual_seed(hidden)
-    parts = [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(3)]
-    pbuf = torch.zeros(3, rows, hidden + 11, dtype=dtype, device=DEV)
-    pviews = [pbuf[i, :, 1 + i:1 + i + hidden] for i in range(3)]
+    parts = [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(nparts)]
+    pbuf = torch.zeros(nparts, rows, hidden + 11, dtype=dtype, device=DEV)
+    pviews = [pbuf[i, :, 1 + i:1 + i + hidden] for i in range(nparts)]
     for pvw, p in zip(pviews, parts):
         pvw.copy_(p.to(DEV))
     rv, ov = View(r, 4, 6), View(torch.zeros_like(x), 4, 6)
