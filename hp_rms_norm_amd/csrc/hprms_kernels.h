@@ -2,7 +2,8 @@
 //
 // Fused residual-add + RMSNorm, "vector" tiers (hidden >= 8; rows at any
 // 2-byte boundary, see FLAGS bits 5 and 6 below).  A row of H elements is
-// nvec = H/8 whole 16-byte vectors (plus a tail when H % 8 != 0).  A
+// nvec = H/8 whole 16-byte vectors (plus a tail when H % 8 != 0, and a head
+// when the tail variant shifts the row).  A
 // workgroup of BLOCK lanes works on RPB = BLOCK/LPR rows at a time, LPR lanes
 // per row; lane l of a row owns vectors l, l+LPR, ..., l+(VPL-1)*LPR, so every
 // load instruction of a wave covers 1 KiB of contiguous bytes.  The row is
