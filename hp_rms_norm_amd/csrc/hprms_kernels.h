@@ -88,8 +88,6 @@ struct FusedArgs {
   int64_t res_stride;
   int32_t hidden;
   int32_t nvec;          // hidden / 8
-  uint32_t shift_base;   // tail variant: row r is shifted by (shift_base + r * shift_step) mod 8 elements
-  uint32_t shift_step;
   float hidden_f;
   float eps;
   uint8_t* q;            // MODES 2, 5, 6: quantised output rows
@@ -101,6 +99,8 @@ struct FusedArgs {
   const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
   uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes, hidden / 32 per row
   int64_t mx_scale_stride;  // bytes between scale rows
+  uint32_t shift_base;   // tail variant: row r is shifted by (shift_base + r * shift_step) mod 8 elements
+  uint32_t shift_step;
 };
 
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
