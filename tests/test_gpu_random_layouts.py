@@ -3,9 +3,10 @@
 Each case draws a dtype, a width (1 ... 70000, weighted towards the table's
 boundaries and odd values), a row count, and for every stream its own element
 offset into a wider buffer and its own row padding; so the streams of one call
-can start at different 2-byte boundaries with different strides, and the
-dispatch picks among the aligned kernels, their unaligned and tail variants and
-the general tier.  Bar as everywhere: residual bit-exact, 16-bit output within
+can start at different 2-byte boundaries with different strides (every third
+case puts all streams at one offset and padding, which the shifted rows need),
+and the dispatch picks among the aligned kernels, their unaligned and tail
+variants and the general tier.  Bar as everywhere: residual bit-exact, 16-bit output within
 1 ulp, FP8 within one step, MX scales and elements bit-exact against the
 oracle's MX step of the same kernel family's 16-bit output.  The cases are
 fixed by the seed, so a failure names a reproducible layout.
@@ -72,6 +73,10 @@ def cases(n, seed):
         dtype = rng.choice([torch.bfloat16, torch.float16])
         offs = [rng.choice([0, 0, 1, 3, 8, 13]) for _ in range(6)]
         pads = [rng.choice([0, 0, 1, 5, 8, 64]) for _ in range(6)]
+        if i % 3 == 2:
+            # every stream at one offset and padding: the written streams share one phase,
+            # so from 4104 elements up the rows are shifted
+            offs, pads = [offs[0]] * 6, [pads[0]] * 6
         out.append((i, hidden, rows, dtype, offs, pads))
     return out
 
