@@ -21,7 +21,7 @@ roofline   = the kernel instantiation with the largest share of the step
 cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
                   on the host cores, on a bounded sample of the same shapes.
 cpu_torch_eager = the reference test's torch formula on the CPU, same sample.
-extra      = the other BASELINE configs (decode, fp16, streamer) and the other
+extra      = BASELINE.json's other configs (decode, fp16, streamer) and the other
              operators (FP8 / MX outputs, out-of-place, plain RMSNorm, rows
              off the 128-byte grid, partial sums), µs/call.
 
@@ -411,7 +411,7 @@ def load_traffic(key):
 
 
 def run_extra(torch, ops, args):
-    """The other BASELINE configs, µs/call (median over timed calls)."""
+    """BASELINE.json's other configs, µs/call (median over timed calls)."""
     out = {}
     steps = max(10, args.steps)
     # configs[3]: decode shapes with 1% outliers x50

@@ -72,7 +72,7 @@ def test_golden_fused_through_torch_op(abi, golden):
         assert_output_close(bits(x), c["out"], dtype, name + " output")
 
 
-# ---- the BASELINE configurations --------------------------------------------------
+# ---- BASELINE.json's configurations --------------------------------------------------
 C1 = [(4096, 4096, torch.bfloat16, "bench")]
 C2 = [(4096, h, torch.bfloat16, "bench") for h in range(1024, 12288 + 1, 1024)]
 C3 = [(4096, h, torch.bfloat16, "bench") for h in (13312, 14336, 16384, 20480, 24576, 28672, 32768)]
