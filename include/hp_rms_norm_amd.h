@@ -63,10 +63,13 @@ typedef enum {
  * (the reference assumes contiguous rows).  rows == 0 is a no-op.
  * hidden may be any value in [1, 2^24] and rows may start at any 2-byte
  * boundary.  The vector tiers take every hidden in [8, 65543]: rows off the
- * 128-byte grid run a variant without the sc1 cache-policy bit, and hidden %
- * 8 != 0 adds a tail vector (flags bits 5 and 6 of hprms_config); other
- * shapes take a slower general kernel.  The results are the same in every
- * case: residual bit-exact, output within 1 ulp of the reference formula.
+ * 128-byte grid run a variant without the sc1 cache-policy bit, hidden % 8
+ * != 0 adds a tail vector, and from hidden 4104 up rows off 16-byte
+ * alignment are shifted so that input and residual are accessed aligned
+ * when both are off by the same amount (flags bits 5 and 6 of
+ * hprms_config); other shapes take a slower general kernel.  The results
+ * meet the same bar in every case: residual bit-exact, output within 1 ulp
+ * of the reference formula.
  */
 int hprms_fused_add_rmsnorm(void* input, const void* weight, void* residual,
                             int64_t rows, int64_t hidden,
