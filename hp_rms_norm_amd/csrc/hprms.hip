@@ -371,29 +371,62 @@ struct Phase {
 Phase phase16(const void* p, int64_t stride) { return {(uint32_t)(((uintptr_t)p >> 1) & 7u), (uint32_t)(stride & 7)}; }
 Phase phase8(const void* p, int64_t stride) { return {(uint32_t)((uintptr_t)p & 7u), (uint32_t)(stride & 7)}; }
 
-// Shifted rows (the tail variant's FusedArgs::shift_*): modes 0-4 from 513
-// whole vectors up shift each row so that the streams the kernel writes are
-// accessed aligned, when they all share one phase ({0, 0} otherwise: no
-// shift).  Measured on MI355X (4096 rows, bf16, rows 2 bytes off alignment or
-// hidden % 8 != 0): aligning every stream is 8-19% faster than 16-byte
-// accesses at unaligned addresses from H = 4104 to 64K, and 5-18% slower at
-// 1K-4K, where a row's set-up weighs more; aligning the reads at the cost of
-// the writes measured 3-22% slower (plain, out of place, FP8 output), so the
-// written streams decide.
+// Shifted rows (the tail variant's FusedArgs::shift_*), modes 0-4 from 513
+// whole vectors up, when no stream of the call (the weight aside: it stays in
+// L2) has all its rows on 16-byte boundaries.  The rows are shifted to the
+// phase of the first written stream (input / residual in place, the output
+// otherwise), which aligns every stream that shares it.  Measured on MI355X
+// (4096 rows, bf16, 8K-32K, against the unaligned and unshifted tail
+// variants): with every stream off alignment, 6-20% faster in modes 0, 3
+// and 4 whether or not the streams share a phase (the least at 16K), and
+// 3-34% faster for contiguous rows of odd widths in every mode; shifting an aligned stream off its
+// boundaries instead costs 9-39%, so one aligned stream rules the shift out.
+// Plain RMSNorm with input and output at different phases shifts only from
+// 16K up (up to 5% slower below, 3-10% faster at 24K-32K).  The FP8 output
+// shifts only rows of odd widths whose streams share one phase (14-34%
+// faster): its byte rows misaligned cost 15-25% at 16K, and for whole-vector
+// widths its unaligned variant was as fast or faster.
 constexpr int64_t kShiftMinVec = 513;
 
 Phase shift_phase(const Problem& p) {
   const Phase none = {0, 0};
   if (p.mode > 4 || p.hidden / 8 < kShiftMinVec) return none;
-  Phase w[2];
+  Phase s[4 + HPRMS_MAX_PARTS];
+  int n = 0;
   switch (p.mode) {
-    case 0: w[0] = phase16(p.x, p.x_stride); w[1] = phase16(p.res, p.res_stride); break;
-    case 1: w[0] = w[1] = phase16(p.out, p.out_stride); break;
-    case 2: w[0] = phase16(p.res, p.res_stride); w[1] = phase8(p.out, p.out_stride); break;
-    case 3: w[0] = phase16(p.out, p.out_stride); w[1] = phase16(p.res_out, p.res_out_stride); break;
-    default: w[0] = phase16(p.out, p.out_stride); w[1] = phase16(p.res, p.res_stride); break;
+    case 0:
+      s[n++] = phase16(p.x, p.x_stride);
+      s[n++] = phase16(p.res, p.res_stride);
+      break;
+    case 1:
+      s[n++] = phase16(p.out, p.out_stride);
+      s[n++] = phase16(p.x, p.x_stride);
+      break;
+    case 2:
+      s[n++] = phase16(p.res, p.res_stride);
+      s[n++] = phase8(p.out, p.out_stride);
+      s[n++] = phase16(p.x, p.x_stride);
+      break;
+    case 3:
+      s[n++] = phase16(p.out, p.out_stride);
+      s[n++] = phase16(p.res_out, p.res_out_stride);
+      s[n++] = phase16(p.x, p.x_stride);
+      s[n++] = phase16(p.res, p.res_stride);
+      break;
+    default:
+      s[n++] = phase16(p.out, p.out_stride);
+      s[n++] = phase16(p.res, p.res_stride);
+      for (int g = 0; g < p.nparts && p.parts; ++g) s[n++] = phase16(p.parts[g], p.x_stride);
+      break;
   }
-  return w[0] == w[1] ? w[0] : none;
+  bool shared = true;
+  for (int i = 0; i < n; ++i) {
+    if (s[i] == none) return none;
+    if (!(s[i] == s[0])) shared = false;
+  }
+  if (p.mode == 2) return shared && p.hidden % 8 != 0 ? s[0] : none;
+  if (p.mode == 1 && !shared && p.hidden < 16384) return none;
+  return s[0];
 }
 
 // the variant of a table entry for rows needs_unaligned() reports

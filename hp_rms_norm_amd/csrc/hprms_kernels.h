@@ -103,8 +103,17 @@ struct FusedArgs {
   uint32_t shift_step;
 };
 
+// Waves per SIMD the compiler must leave room for: the tail variant of the
+// 1024-lane shapes with up to 2 vectors per lane is held to 64 VGPRs, so two
+// workgroups share a CU as they do without the tail (the FP8 form needed 66:
+// held to 64 it runs 19-23% faster at 13K-16K).  At 3 vectors per lane the
+// same limit spills and measured 3-7% slower.
+template <int FLAGS, int BLOCK, int VPL>
+constexpr int kMinWavesPerEU = ((FLAGS & 64) != 0 && BLOCK == 1024 && VPL <= 2) ? 8 : 1;
+
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
-__global__ __launch_bounds__(BLOCK) void fused_vec_kernel(FusedArgs a) {
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<FLAGS, BLOCK, VPL>)))
+void fused_vec_kernel(FusedArgs a) {
   static_assert(LPR >= 16 && (LPR & (LPR - 1)) == 0 && BLOCK % LPR == 0 && BLOCK % 64 == 0, "shape");
   static_assert(LDSV >= 0 && LDSV <= VPL, "LDS share");
   using F = Fmt<DT>;

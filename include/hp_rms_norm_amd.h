@@ -64,10 +64,10 @@ typedef enum {
  * hidden may be any value in [1, 2^24] and rows may start at any 2-byte
  * boundary.  The vector tiers take every hidden in [8, 65543]: rows off the
  * 128-byte grid run a variant without the sc1 cache-policy bit, hidden % 8
- * != 0 adds a tail vector, and from hidden 4104 up rows off 16-byte
- * alignment are shifted so that input and residual are accessed aligned
- * when both are off by the same amount (flags bits 5 and 6 of
- * hprms_config); other shapes take a slower general kernel.  The results
+ * != 0 adds a tail vector, and from hidden 4104 up, when neither input nor
+ * residual has its rows on 16-byte boundaries, the rows are shifted so that
+ * the input is accessed aligned (flags bits 5 and 6 of hprms_config); other
+ * shapes take a slower general kernel.  The results
  * meet the same bar in every case: residual bit-exact, output within 1 ulp
  * of the reference formula.
  */
@@ -200,7 +200,7 @@ typedef struct {
                                bit 5: variant for rows off the 128-byte grid (any 2-byte
                                boundary), bit 6 (with bit 5): head and tail vectors, for
                                hidden % 8 != 0 and (from hidden 4104 up, modes 0-4) rows
-                               shifted to the written streams' 16-byte phase;
+                               shifted to the first written tensor's 16-byte phase;
                                bit 7: a lane's residual loads issued before its input loads */
 } hprms_config;
 
@@ -218,10 +218,12 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * general kernel fits hidden; with hidden % 8 != 0 the tail variant).  For
  * rows on the 128-byte grid: rows off it run the same shape with flags
  * (flags & ~24) | 32, or | 96 (the tail variant) for hidden % 8 != 0 and, in
- * modes 0-4 from hidden 4104 up, for rows off 16-byte alignment when every
- * tensor the call writes is off by the same amount in each row (the kernel
- * then shifts its vectors to align them).  Pure function of its arguments;
- * touches no device. */
+ * modes 0-4 from hidden 4104 up, for calls none of whose tensors (the weight
+ * aside) has its rows on 16-byte boundaries (the kernel then shifts its
+ * vectors to align the first written tensor; plain RMSNorm with input and
+ * output off by different amounts from hidden 16384 up, the FP8 output only
+ * for odd hidden with every tensor off by the same amount).  Pure function of
+ * its arguments; touches no device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 
 /* Lists the vector-tier configurations built into the library for (dtype,

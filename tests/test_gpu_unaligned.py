@@ -8,12 +8,12 @@ all start on a 128-byte boundary to a variant of the table's shape:
     aligned copies;
   * hidden % 8 != 0: the tail variant (bit 6), whose lane holding the last
     whole vector also handles the 16 bytes that end at the row's end;
-  * from 513 whole vectors up, modes 0-4 with input rows off 16-byte
-    boundaries: the tail variant with shifted rows, which starts each row's
-    body vectors at the input's first 16-byte boundary and adds a head vector
-    for the elements before them; its sum of squares runs in another order,
-    so its output is held to the oracle's bar and its residual to the same
-    bits.
+  * from 513 whole vectors up, modes 0-4 whose streams (the weight aside)
+    are all off 16-byte alignment: the tail variant with shifted rows, which
+    starts each row's body vectors at the first written stream's first
+    16-byte boundary and adds a head vector for the elements before them; its
+    sum of squares runs in another order, so its output is held to the
+    oracle's bar and its residual to the same bits.
 Every mode is within the usual bar of the oracle (residual bit-exact, 16-bit
 output within 1 ulp, FP8 within 1 e4m3 ulp) and writes nothing outside the
 views; the edge vectors are exercised at both ends of every table row, at
@@ -302,11 +302,13 @@ SHIFT_WIDTHS = [4104, 4105, 8195, 16384, 32773]
 @pytest.mark.parametrize("dtype,rows,nparts", [(torch.bfloat16, 21, 3), (torch.float16, 300, 8)],
                          ids=["bf16-latency-table", "fp16-bandwidth-table"])
 def test_shifted_rows_every_mode(abi, hidden, dtype, rows, nparts):
-    """From 513 whole vectors up, rows whose written streams share one phase
-    (element offsets 1-7; row strides not a multiple of 8, so each row has its
-    own shift) are shifted to it: modes 0-4 against the oracle, with the read
-    streams at other phases, and nothing written outside the views; on the
-    latency table's shapes (few rows) and the bandwidth table's."""
+    """From 513 whole vectors up, rows of calls whose streams are all off
+    16-byte alignment (element offsets 1-7; row strides not a multiple of 8,
+    so each row has its own shift) are shifted to the first written stream's
+    phase: modes 0-4 against the oracle, with the written streams at one phase
+    and the read streams at others (the FP8 output: every stream at one
+    phase), and nothing written outside the views; on the latency table's
+    shapes (few rows) and the bandwidth table's."""
     x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + 7)
     tag = f"{rows}x{hidden} {dtype}"
     print("shifted rows", tag, flush=True)
@@ -331,8 +333,8 @@ def test_shifted_rows_every_mode(abi, hidden, dtype, rows, nparts):
     want = oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=th)
     assert_output_close(bits(ov.view), want, dtype, "plain " + tag)
 
-    # FP8 output: the residual's element phase equals the byte rows' phase
-    xv, rv, qv = View(x, 6, 0), View(r, 1, 2), ByteView(rows, hidden, 1, 2)
+    # FP8 output: the input's and the residual's element phase equals the byte rows' phase
+    xv, rv, qv = View(x, 1, 2), View(r, 1, 2), ByteView(rows, hidden, 1, 2)
     sc = torch.empty(rows, dtype=torch.float32, device=DEV)
     abi.fused_add_rmsnorm_fp8(qv.ptr, sc.data_ptr(), xv.ptr, wv.ptr, rv.ptr, rows, hidden, qv.stride, xv.stride,
                               rv.stride, DT[dtype], EPS, _stream())
@@ -345,7 +347,7 @@ def test_shifted_rows_every_mode(abi, hidden, dtype, rows, nparts):
     np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7)
 
     # out of place: both outputs at one phase
-    xv, rv = View(x, 0, 3), View(r, 2, 0)
+    xv, rv = View(x, 2, 3), View(r, 2, 0)
     ov, rov = View(torch.zeros_like(x), 7, 1), View(torch.zeros_like(x), 7, 1)
     abi.fused_add_rmsnorm_out(ov.ptr, rov.ptr, xv.ptr, rv.ptr, wv.ptr, rows, hidden, ov.stride, rov.stride,
                               xv.stride, rv.stride, DT[dtype], EPS, _stream())
@@ -359,7 +361,7 @@ def test_shifted_rows_every_mode(abi, hidden, dtype, rows, nparts):
     g = torch.Generator().manual_seed(hidden)
     parts = [torch.randn((rows, hidden), generator=g).to(dtype) for _ in range(nparts)]
     pbuf = torch.zeros(nparts, rows, hidden + 11, dtype=dtype, device=DEV)
-    pviews = [pbuf[i, :, 1 + i:1 + i + hidden] for i in range(nparts)]
+    pviews = [pbuf[i, :, 1 + i % 7:1 + i % 7 + hidden] for i in range(nparts)]
     for pvw, p in zip(pviews, parts):
         pvw.copy_(p.to(DEV))
     rv, ov = View(r, 4, 6), View(torch.zeros_like(x), 4, 6)
