@@ -240,8 +240,10 @@ def main():
                          "(the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--profile-config", default="",
                     help="with --profile: force lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags")
-    ap.add_argument("--profile-op", default="fused", choices=("fused", "fp8", "plain", "mxfp8", "mxfp4"),
-                    help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, or plain RMSNorm")
+    ap.add_argument("--profile-op", default="fused",
+                    choices=("fused", "fp8", "plain", "mxfp8", "mxfp4", "copy", "relu"),
+                    help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, plain RMSNorm, "
+                         "or the streamer (the reference's relu = copy, and the true ReLU)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the op has no cross-GPU step (rows are independent), and this "
@@ -386,6 +388,12 @@ def profile_driver(torch, abi, op, args):
 
         def op(x, w, r, eps):  # noqa: F811  (MX output; the input row is only read)
             hp_rms_norm_amd.hp_rms_norm_mx(q, sc, x, w, r, eps, fmt)
+    if args.profile_op in ("copy", "relu"):
+        import hp_rms_norm_amd
+        stream_fn = hp_rms_norm_amd.relu if args.profile_op == "copy" else hp_rms_norm_amd.relu_max0
+
+        def op(x, w, r, eps):  # noqa: F811  (streamer: reads x, writes r; w and eps unused)
+            stream_fn(r, x)
     us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup, trials=1)[0][0]
     n = 1 << 29
     src = torch.empty(n, dtype=torch.bfloat16, device="cuda:0").normal_()
