@@ -23,7 +23,9 @@ cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
 cpu_torch_eager = the reference test's torch formula on the CPU, same sample.
 extra      = BASELINE.json's other configs (decode, fp16, streamer) and the other
              operators (FP8 / MX outputs, out-of-place, plain RMSNorm, rows
-             off the 128-byte grid, partial sums), µs/call.
+             off the 128-byte grid, partial sums), µs/call; and a copy moving
+             the fused op's bytes at six of the widths, with the fused op's
+             time as a fraction of it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 """
@@ -306,6 +308,11 @@ def main():
     extra = {}
     if not args.no_extra:
         extra = run_extra(torch, hp_rms_norm_amd, args)
+        fused_us = {p["hidden"]: p["us_per_call"] for p in per_shape}
+        for c in extra.get("copy_same_bytes_bf16", []):
+            if c["hidden"] in fused_us:
+                c["fused_us_per_call"] = fused_us[c["hidden"]]
+                c["fused_over_copy"] = round(fused_us[c["hidden"]] / c["us_per_call"], 3)
 
     cpu = None
     torch_cpu = None
@@ -630,6 +637,24 @@ def run_extra(torch, ops, args):
     out["vendor_stack_bandwidth"] = ceil
     del a, b
     torch.cuda.empty_cache()
+    # a copy that moves the fused op's bytes at (B, H): the streamer over (B, 2H), one read
+    # and one write of 2·B·H elements; the time any one kernel launch needs to stream that
+    # many bytes on this stack (main() sets the fused op's time beside it)
+    same = []
+    for h in (1024, 2048, 4096, 8192, 16384, 32768):
+        n = cold_sets(B, 2 * h)
+        srcs = [torch.randn(B, 2 * h, device="cuda:0").to(torch.bfloat16) for _ in range(n)]
+        dsts = [torch.empty_like(t) for t in srcs]
+
+        def call(i, srcs=srcs, dsts=dsts):
+            ops.relu(dsts[i], srcs[i])
+        us = statistics.median(time_rotating(torch, call, n, steps, args.warmup) for _ in range(3))
+        nbytes = 4 * B * h * 2
+        same.append({"hidden": h, "copy_shape": [B, 2 * h], "copy_bytes": nbytes, "us_per_call": round(us, 2),
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        del srcs, dsts
+        torch.cuda.empty_cache()
+    out["copy_same_bytes_bf16"] = same
     # the reference's published harness is not in its repository; for comparison
     # with those numbers, the same shapes with one buffer set reused every call
     # (working sets up to 256 MB then sit in the Infinity Cache)
