@@ -56,17 +56,18 @@ struct FusedEntry {
   X(DT, MODE, 512, 8, 0, 512, 7)
 
 // entries of the FP8-output table that the other tables do not use
-#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 31)
+#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 159)
 
 // alternatives of the fused op that the tests run and the sweep compares against
-// (then five of the table's shapes with the two streams' loads alternating, and
-// the two smallest latency rows with the weight loaded late)
+// (then five of the table's shapes with the two streams' loads alternating, the
+// two smallest latency rows with the weight loaded late, and the FP8 table's
+// 32K row, so that the 16-bit op runs with each FP8 row's lane mapping)
 #define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
   X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
   X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)                           \
   X(DT, MODE, 32, 4, 0, 256, 3) X(DT, MODE, 64, 4, 0, 256, 7) X(DT, MODE, 128, 4, 0, 256, 3)   \
   X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)                         \
-  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7)
+  X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 512, 8, 4, 512, 159)
 
 // extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
