@@ -200,8 +200,8 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
       {512, 128, 4, 0, 256, 131},    // H <= 4096
       {1024, 512, 2, 0, 512, 7},     // H <= 8192:  one row per 8-wave workgroup
       {1536, 512, 3, 0, 512, 31},    // H <= 12288
-      {1920, 1024, 2, 0, 1024, 31},  // H <= 15360
-      {2048, 256, 8, 4, 256, 27},    // H <= 16384: LDS tier, half the row in LDS
+      {2047, 1024, 2, 0, 1024, 31},  // H <= 16376
+      {2048, 256, 8, 4, 256, 27},    // H = 16384: LDS tier, half the row in LDS
       {3072, 1024, 3, 0, 1024, 159}, // H <= 24576
       {4096, 1024, 4, 0, 1024, 159}, // H <= 32768
       {8192, 1024, 8, 4, 1024, 31},  // H <= 65536: LDS tier

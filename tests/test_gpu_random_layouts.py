@@ -23,7 +23,7 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 EPS = 1e-6
-TABLE_EDGES = [128, 256, 512, 1024, 2048, 3072, 4096, 8192, 12288, 15360, 16384, 24576, 32768, 65536]
+TABLE_EDGES = [128, 256, 512, 1024, 2048, 3072, 4096, 8192, 12288, 16376, 16384, 24576, 32768, 65536]
 
 
 @pytest.fixture(scope="module")
