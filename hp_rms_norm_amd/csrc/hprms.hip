@@ -92,20 +92,37 @@ const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
 }
 
 // ---- the gfx950 table -------------------------------------------------------------
-// Chosen from (rows, hidden) by measurement on MI355X.  With few rows (at most
-// one per CU) the kernel is latency-bound: one row per workgroup and at most
-// two vectors per lane shortens each wave's serial work.  Up to 2048 elements
-// the weight is loaded together with the row: a one- or two-wave row then
-// waits for one memory round trip instead of two (H = 1024: 2.4-4.5% faster
-// for the fused, out-of-place and MX forms, 1-256 rows, hot and cold; H = 2048:
-// up to 1.2%).  From 4096 up, loading it after the row's sum measured as fast
-// or faster.  Otherwise the bandwidth table below applies.
-bool latency_config(int64_t rows, int64_t nvec, hprms_config* c) {
-  if (rows > 256 || nvec <= 64 || nvec > 2048) return false;
+// Chosen from (rows, hidden) by measurement on MI355X.  With few rows the
+// kernel is latency-bound: one row per workgroup and at most two vectors per
+// lane shortens each wave's serial work.  Up to 2048 elements the weight is
+// loaded together with the row: a one- or two-wave row then waits for one
+// memory round trip instead of two (H = 1024: 2.4-4.5% faster for the fused,
+// out-of-place and MX forms, 1-256 rows, hot and cold; H = 2048: up to 1.2%).
+// From 4096 up, loading it after the row's sum measured as fast or faster.
+//
+// These rows stay ahead of the bandwidth table well past one row per CU, by
+// how much depending on the mode, so the largest row count that still takes
+// them is set per mode (two builds of the library timed side by side, 8
+// interleaved trials, 320-1536 rows, hot and cold): the fused op gains 2-29% up to 768-1024 rows at
+// H <= 4096 and 37-62% with its rows cache-resident at 8K-16K up to 384
+// (within 2% cold); plain RMSNorm 8-36% at H <= 1024 and 2K-4K, the FP8 and MX
+// outputs 2-23%.  The out-of-place and partial-sum forms were faster at some
+// row counts and up to 15% slower at others, so they keep one row per CU.
+// Otherwise the bandwidth table below applies.
+bool latency_config(int64_t rows, int64_t nvec, int mode, hprms_config* c) {
+  if (nvec <= 64 || nvec > 2048) return false;
   struct Row { int64_t max_nvec; int lpr, vpl; };
   static const Row lat[] = {{128, 64, 2}, {256, 128, 2}, {512, 256, 2}, {1024, 512, 2}, {2048, 512, 4}};
-  for (const Row& r : lat) {
+  // most rows that take each latency row: fused; plain; FP8 and MX; out of place and partial sums
+  static const int16_t max_rows[4][5] = {{1024, 768, 768, 256, 384},
+                                         {1024, 256, 768, 256, 256},
+                                         {1024, 768, 768, 256, 256},
+                                         {256, 256, 256, 256, 256}};
+  const int cls = mode == 0 ? 0 : mode == 1 ? 1 : (mode == 2 || mode == 5 || mode == 6) ? 2 : 3;
+  for (int i = 0; i < 5; ++i) {
+    const Row& r = lat[i];
     if (nvec <= r.max_nvec) {
+      if (rows > max_rows[cls][i]) return false;
       *c = hprms_config{1, r.lpr, r.vpl, 0, r.lpr, 0, nvec <= 256 ? 3 : 7};
       return true;
     }
@@ -181,7 +198,7 @@ bool reduce_config(int64_t nvec, hprms_config* c) {
 
 void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   const int64_t nvec = hidden / 8;
-  if (latency_config(rows, nvec, c)) return;
+  if (latency_config(rows, nvec, mode, c)) return;
   if (mode == 1 && plain_config(nvec, c)) return;
   if (mode == 4 && reduce_config(nvec, c)) return;
   if (mode == 2 && fp8_config(nvec, c)) return;

@@ -85,7 +85,7 @@ HIDDENS = [32, 96, 256, 512, 1024, 2016, 3072, 4096, 8192, 12288, 13312, 16384, 
 @pytest.mark.parametrize("fmt", sorted(FMT))
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_mx_every_table_row(ops, dtype, fmt):
-    for rows in (513, 64):
+    for rows in (1100, 64):
         for hidden in HIDDENS:
             print("mx", fmt, rows, hidden, dtype, flush=True)
             run_case(ops, rows, hidden, dtype, FMT[fmt], seed=rows + hidden)

@@ -441,13 +441,13 @@ def test_plain_rmsnorm_every_table_row(abi, dtype):
     import hp_rms_norm_amd
     for hidden in (128, 256, 512, 1000, 2048, 3064, 4096, 6144, 8192, 12288, 16376, 24576, 28672, 32768, 65536):
         print("plain", hidden, dtype, flush=True)
-        x, _, w = make_inputs(513, hidden, dtype, hidden + 1)
+        x, _, w = make_inputs(1100, hidden, dtype, hidden + 1)
         want = oracle.rmsnorm(bits(x), bits(w), 1e-6, DT[dtype], threads=min(16, oracle.max_threads()))
         xd, wd = x.to(DEV), w.to(DEV)
         out = torch.empty_like(xd)
         hp_rms_norm_amd.rms_norm(out, xd, wd, 1e-6)
         torch.cuda.synchronize()
-        assert_output_close(bits(out), want, dtype, f"plain 513x{hidden} {dtype}")
+        assert_output_close(bits(out), want, dtype, f"plain 1100x{hidden} {dtype}")
 
 
 @pytest.mark.parametrize("hidden", [13, 1001, 4095, 16383, 20001])

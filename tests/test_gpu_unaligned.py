@@ -171,10 +171,10 @@ def test_every_tail_length_on_bandwidth_and_latency_rows(abi):
     """hidden = 4096 + t and 8192 + t, t = 1..7 (the tail overlaps the last
     whole vector by 8 - t elements; at 8192 + t rows are shifted and start at
     2t-byte steps, so the head and tail vectors take every length), on the
-    bandwidth table (300 rows) and the latency table (5 rows); outliers, so
+    bandwidth table (1100 rows) and the latency table (5 rows); outliers, so
     that every element's square matters."""
     for t in range(1, 8):
-        for rows, hidden in ((300, 4096 + t), (5, 4096 + t), (300, 8192 + t), (5, 8192 + t)):
+        for rows, hidden in ((1100, 4096 + t), (5, 4096 + t), (1100, 8192 + t), (5, 8192 + t)):
             for dtype in (torch.bfloat16, torch.float16):
                 x, r, w = make_inputs(rows, hidden, dtype, seed=t + rows, dist="outliers")
                 print("tail length", t, rows, dtype, flush=True)
