@@ -28,6 +28,7 @@ extra      = BASELINE.json's other configs (decode, fp16, streamer) and the othe
              time as a fraction of it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+       python bench.py --sweep STEP [--sweep-max H]   (per-H table sweep, one JSON line per H)
 """
 import argparse
 import json
@@ -240,6 +241,10 @@ def main():
     ap.add_argument("--profile", type=int, default=0, metavar="H",
                     help="profiling driver: only run (4096, H) bf16 calls, then a 1 GiB device copy "
                          "(the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--sweep", type=int, default=0, metavar="STEP",
+                    help="only time the fused op at (4096, H) for every H = STEP, 2*STEP, ... <= --sweep-max "
+                         "(cold, like per_shape), one JSON line per H, with the kernel it runs")
+    ap.add_argument("--sweep-max", type=int, default=32768)
     ap.add_argument("--profile-config", default="",
                     help="with --profile: force lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags")
     ap.add_argument("--profile-op", default="fused",
@@ -264,6 +269,8 @@ def main():
     op = hp_rms_norm_amd.hp_rms_norm
     if args.profile:
         return profile_driver(torch, abi, op, args)
+    if args.sweep:
+        return sweep(torch, abi, op, args)
 
     shapes = [(B, h, torch.bfloat16, "bench") for h in H_SWEEP]
     log(f"bench: timing {len(shapes)} shapes x {args.steps} steps (warmup {args.warmup})")
@@ -409,6 +416,29 @@ def profile_driver(torch, abi, op, args):
         dst.copy_(src)
     torch.cuda.synchronize()
     log(f"profile: (4096, {hidden}) {us:.2f} us/call; then {args.steps} copies of {2 * n} bytes")
+
+
+def sweep(torch, abi, op, args):
+    """Every H = STEP, 2*STEP, ... at 4096 rows: µs/call (median of 3 timed
+    blocks over rotating buffer sets spanning >= 1 GiB) and GB/s, with the
+    kernel the table chooses, one JSON line per H.  The buffers are views of
+    one pool, so the sweep allocates once."""
+    per_max = B * args.sweep_max
+    pool = torch.empty(max(2 * per_max, (1 << 30) // 2 * 2), dtype=torch.bfloat16, device="cuda:0").normal_()
+    w_all = make_weight(torch, args.sweep_max, torch.bfloat16, 0, "cuda:0")
+    for h in range(args.sweep, args.sweep_max + 1, args.sweep):
+        per = B * h
+        n = max(2, min(cold_sets(B, h), pool.numel() // (2 * per)))
+        sets = [(pool[2 * i * per:(2 * i + 1) * per].view(B, h), pool[(2 * i + 1) * per:(2 * i + 2) * per].view(B, h))
+                for i in range(n)]
+        w = w_all[:h]
+        us = statistics.median(time_rotating(torch, lambda i: op(sets[i][0], w, sets[i][1], EPS), n, args.steps,
+                                             args.warmup) for _ in range(3))
+        key = kernel_key(abi, B, h, 0)
+        print(json.dumps({"rows": B, "hidden": h, "us_per_call": round(us, 2),
+                          "gbs": round(fused_bytes(B, h) / (us * 1e-6) / 1e9, 1),
+                          "kernel": {"lanes_per_row": key[1], "vec_per_lane": key[2], "lds_vec_per_lane": key[3],
+                                     "block": key[4], "flags": key[6]}}), flush=True)
 
 
 def load_traffic(key):
