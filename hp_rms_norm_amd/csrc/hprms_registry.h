@@ -48,7 +48,7 @@ struct FusedEntry {
   X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 4, 0, 1024, 159)                         \
   X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
   X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)    \
-  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7) X(DT, MODE, 256, 3, 0, 256, 7)
 
 // entries of the plain-RMSNorm table that the fused table does not use
 #define HPRMS_PLAIN_SHAPES(X, DT, MODE)                                                        \

@@ -97,7 +97,8 @@ def test_fp8_baseline_shapes(ops, rows, hidden, dtype):
 def test_fp8_every_table_entry(ops):
     """H at every breakpoint of the table (and one below), with 1100 rows (the
     bandwidth rows) and 7 rows (the latency rows)."""
-    for hidden in (128, 256, 512, 1024, 2048, 3072, 4096, 8192, 12288, 16384, 24576, 32768, 65536, 520, 4088):
+    for hidden in (128, 256, 512, 1024, 1032, 2048, 3072, 4096, 4104, 5120, 8192, 12288, 16384, 24576, 32768, 65536,
+                   520, 4088):
         for rows in (1100, 7):
             print("fp8 table", rows, hidden, flush=True)
             run_case(ops, rows, hidden, torch.bfloat16, seed=hidden + rows)

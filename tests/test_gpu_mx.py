@@ -79,7 +79,8 @@ def run_case(ops, rows, hidden, dtype, elem, seed, dist="bench", eps=1e-6, w=Non
 
 
 # every row of the table, each with a ragged width below it (hidden % 32 == 0)
-HIDDENS = [32, 96, 256, 512, 1024, 2016, 3072, 4096, 8192, 12288, 13312, 16384, 24576, 32768, 65536]
+HIDDENS = [32, 96, 256, 512, 1024, 1056, 2016, 3072, 4096, 4128, 5120, 8192, 12288, 13312, 16384, 24576, 32768,
+           65536]
 
 
 @pytest.mark.parametrize("fmt", sorted(FMT))

@@ -439,7 +439,8 @@ def test_plain_rmsnorm_every_table_row(abi, dtype):
     """Enough rows for the bandwidth table (its plain-RMSNorm rows included),
     every row of it with a ragged width, against the oracle."""
     import hp_rms_norm_amd
-    for hidden in (128, 256, 512, 1000, 2048, 3064, 4096, 6144, 8192, 12288, 16376, 24576, 28672, 32768, 65536):
+    for hidden in (128, 256, 512, 1000, 2048, 3064, 4096, 4104, 5120, 6144, 8192, 12288, 16376, 24576, 28672, 32768,
+                   65536):
         print("plain", hidden, dtype, flush=True)
         x, _, w = make_inputs(1100, hidden, dtype, hidden + 1)
         want = oracle.rmsnorm(bits(x), bits(w), 1e-6, DT[dtype], threads=min(16, oracle.max_threads()))
