@@ -222,8 +222,11 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * aside) has its rows on 16-byte boundaries (the kernel then shifts its
  * vectors to align the first written tensor; plain RMSNorm with input and
  * output off by different amounts from hidden 16384 up, the FP8 output only
- * for odd hidden with every tensor off by the same amount).  Pure function of
- * its arguments; touches no device. */
+ * for odd hidden with every tensor off by the same amount).  Calls of modes
+ * 0, 2, 4, 5 and 6 with rows * hidden <= 2^24 also run the shape with flags
+ * (flags & ~24) | 32 when the reported flags carry the sc1 bits (8, 16): the
+ * same kernel without them.  Pure function of its arguments; touches no
+ * device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
