@@ -298,3 +298,20 @@ def test_mx_entry_rejects_bad_arguments():
     for mode in (abi.MODE_MXFP8, abi.MODE_MXFP4):
         c = abi.select_config(4096, 4096, abi.DTYPE_BF16, mode)
         assert c.tier in (1, 2) and c.lanes_per_row % 4 == 0
+
+
+def test_latency_rows_end_at_the_per_mode_limits():
+    """The latency rows take calls up to a per-mode, per-width row count; the
+    next row count takes the bandwidth table (the same choice as 4096 rows)."""
+    fp8_mx = {1024: 1024, 2048: 768, 4096: 768, 8192: 256, 16384: 256}
+    limits = {abi.MODE_FUSED: {1024: 1024, 2048: 768, 4096: 768, 8192: 256, 16384: 384},
+              abi.MODE_PLAIN: {1024: 1024, 2048: 256, 4096: 768, 8192: 256, 16384: 256},
+              abi.MODE_FP8: fp8_mx, abi.MODE_MXFP8: fp8_mx, abi.MODE_MXFP4: fp8_mx,
+              abi.MODE_OUT: {h: 256 for h in fp8_mx}, abi.MODE_REDUCE: {h: 256 for h in fp8_mx}}
+    for mode, by_hidden in limits.items():
+        for hidden, limit in by_hidden.items():
+            for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+                lat = abi.select_config(1, hidden, dtype, mode).as_tuple()
+                assert abi.select_config(limit, hidden, dtype, mode).as_tuple() == lat, (mode, hidden)
+                past = abi.select_config(limit + 1, hidden, dtype, mode).as_tuple()
+                assert past == abi.select_config(4096, hidden, dtype, mode).as_tuple(), (mode, hidden)

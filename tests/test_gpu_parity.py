@@ -497,3 +497,33 @@ def test_errors_on_device_tensors(abi):
     xt = torch.zeros(256, 4, dtype=torch.bfloat16, device=DEV).t()   # [4, 256], inner stride 4
     with pytest.raises(RuntimeError, match=r"input.stride\(-1\) == 1"):
         hp_rms_norm_amd.hp_rms_norm(xt, w, x.clone(), 1e-6)
+
+
+# ---- the per-mode end of the latency rows; small in-place calls without sc1 ------------
+@pytest.mark.parametrize("hidden,limit", [(1024, 1024), (2048, 768), (4096, 768), (12288, 384)])
+def test_fused_on_both_sides_of_the_latency_row_limit(abi, hidden, limit):
+    """The fused op's latency rows end at a per-width row count: the last row
+    count that takes them and the first that does not, through the torch op,
+    against the oracle."""
+    lat = abi.select_config(1, hidden, abi.DTYPE_BF16).as_tuple()
+    for rows in (limit, limit + 1):
+        assert (abi.select_config(rows, hidden, abi.DTYPE_BF16).as_tuple() == lat) == (rows == limit)
+        check_case(abi, rows, hidden, torch.bfloat16, seed=rows, via="torch")
+
+
+@pytest.mark.parametrize("rows,hidden", [(512, 12288), (1024, 16384), (1536, 9216), (320, 32768)])
+def test_small_in_place_calls_without_sc1_give_the_table_kernels_bits(abi, rows, hidden):
+    """Calls with rows * hidden <= 2^24 run the table's shape without the sc1
+    bits; the bits equal those of the table's kernel (forced, sc1 included),
+    and the oracle's bar holds."""
+    c = abi.select_config(rows, hidden, abi.DTYPE_BF16)
+    assert rows * hidden <= 1 << 24 and c.flags & 24, c.as_tuple()
+    x, r, w = make_inputs(rows, hidden, torch.bfloat16, seed=hidden + rows)
+    outs = []
+    for config in (None, c):
+        xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+        run_abi(abi, xd, wd, rd, 1e-6, config)
+        torch.cuda.synchronize()
+        outs.append((bits(xd), bits(rd)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    check_case(abi, rows, hidden, torch.bfloat16, seed=hidden + rows)
