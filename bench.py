@@ -18,9 +18,11 @@ per_shape  = per-H microseconds per call and GB/s: back-to-back calls over
              the host's launch rate is not measured.
 roofline   = the kernel instantiation with the largest share of the step
              time, against MI355X's 8 TB/s HBM peak.
-cpu_baseline    = the CPU oracle (a scalar C restatement, OpenMP over rows)
-                  on the host cores, on a bounded sample of the same shapes.
-cpu_torch_eager = the reference test's torch formula on the CPU, same sample.
+cpu_baseline = the reference's CPU path: its test's torch formula
+               (x + r; torch.rms_norm) in eager mode on the host's usable
+               cores, on the whole workload; core count and CPU model stated.
+cpu_oracle   = the CPU oracle (a scalar C restatement, OpenMP over rows) on a
+               bounded sample of the same shapes.
 extra      = BASELINE.json's other configs (decode, fp16, streamer) and the other
              operators (FP8 / MX outputs, out-of-place, plain RMSNorm, rows
              off the 128-byte grid, partial sums), µs/call; and a copy moving
@@ -31,6 +33,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extr
        python bench.py --sweep STEP [--sweep-max H]   (per-H table sweep, one JSON line per H)
 """
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -178,16 +181,79 @@ def time_shapes(torch, op, shapes, calls, warmup, trials=7):
     return out
 
 
-def cpu_baselines(torch, budget_s=20.0):
-    """The CPU oracle (kind "port") and the torch eager formula, on the box's
-    host cores, over a bounded sample: rows of (4096, H) for H in the sweep,
-    taken as a fixed number of rows per H so each leg stays within budget."""
+def usable_cpus():
+    """CPUs this process may run on: its affinity set, capped by a cgroup v2
+    CPU quota when one is set (a box may show more cores than it grants)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_torch_baseline(torch, shapes=None, reps=3):
+    """The reference's CPU path: its test's formula (test/test_hp_rms_norm.py:6-19),
+    ``s = x + r; torch.rms_norm(s, (H,), weight=w, eps=eps)``, in torch eager
+    mode on the host's usable cores, on the benchmark's own shapes (bf16,
+    4096 rows, every H of the sweep) and distributions.  Per shape: 1 warm-up
+    call, then the median of `reps` timed calls (time.perf_counter)."""
+    threads = usable_cpus()
+    torch.set_num_threads(threads)
+    shapes = shapes or [(B, h) for h in H_SWEEP]
+    per, total_s, total_bytes = [], 0.0, 0
+    for i, (rows, h) in enumerate(shapes):
+        g = torch.Generator().manual_seed(i)
+        x = torch.randn((rows, h), generator=g).to(torch.bfloat16)
+        r = torch.randn((rows, h), generator=g).to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn((h,), generator=g)).to(torch.bfloat16)
+
+        def call():
+            s_ = x + r
+            return torch.rms_norm(s_, (h,), weight=w, eps=EPS)
+        call()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            call()
+            ts.append(time.perf_counter() - t0)
+        med = statistics.median(ts)
+        per.append({"rows": rows, "hidden": h, "ms_per_call": round(med * 1e3, 2),
+                    "gbs": round(fused_bytes(rows, h) / med / 1e9, 2)})
+        total_s += med
+        total_bytes += fused_bytes(rows, h)
+        del x, r, w
+    return {"value": round(total_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "what": "the reference test's torch formula (test/test_hp_rms_norm.py:6-19), torch eager on the CPU",
+            "sample": (f"the full benchmark workload: bf16 ({B}, H) for the {len(shapes)} H of the sweep, "
+                       f"{total_bytes / 1e9:.2f} GB algorithmic; per shape 1 warm-up + median of {reps} calls"),
+            "torch_threads": torch.get_num_threads(), "os_cpu_count": os.cpu_count(),
+            "cpu_model": cpu_model(), "per_shape": per}
+
+
+def cpu_oracle_baseline(torch, budget_s=10.0):
+    """The CPU oracle (a scalar C restatement, OpenMP over rows) on the same
+    cores, on a bounded sample: 256 rows of (4096, H) for every H of the sweep."""
     import numpy as np
 
     from oracle import oracle
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    threads = usable_cpus()
     sample_rows = 256
     shapes = [(sample_rows, h) for h in H_SWEEP]
     g = torch.Generator().manual_seed(0)
@@ -202,33 +268,24 @@ def cpu_baselines(torch, budget_s=20.0):
     def bitsnp(t):
         return t.contiguous().view(torch.int16).numpy().view(np.uint16)
 
-    def oracle_pass():
+    def one_pass():
+        t = 0.0
         for x, r, w in data:
             xo, ro = bitsnp(x).copy(), bitsnp(r).copy()
             t0 = time.perf_counter()
             oracle.fused_add_rmsnorm_(xo, bitsnp(w), ro, EPS, oracle.BF16, threads=threads)
-            yield time.perf_counter() - t0
+            t += time.perf_counter() - t0
+        return t
 
-    def torch_pass():
-        for x, r, w in data:
-            t0 = time.perf_counter()
-            s = x + r
-            torch.rms_norm(s, (x.shape[-1],), weight=w, eps=EPS)
-            yield time.perf_counter() - t0
-
-    out = {}
-    for name, fn in (("oracle", oracle_pass), ("torch", torch_pass)):
-        sum(fn())  # warm-up pass
-        reps, t_start = [], time.perf_counter()
-        while len(reps) < 3 or (time.perf_counter() - t_start < budget_s / 2 and len(reps) < 2000):
-            reps.append(sum(fn()))
-        med = statistics.median(reps)
-        out[name] = {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s",
-                     "us_per_4096_row_call": round(med / len(shapes) * (B / sample_rows) * 1e6, 1),
-                     "reps": len(reps), "seconds_per_pass": round(med, 4)}
-    sample = (f"{sample_rows} rows x each H in the 1024..32768 sweep (bf16, {len(shapes)} shapes, "
-              f"{sample_bytes / 1e6:.0f} MB algorithmic per pass), median of repeated passes")
-    return out, threads, sample
+    one_pass()
+    reps, t_start = [], time.perf_counter()
+    while len(reps) < 3 or (time.perf_counter() - t_start < budget_s and len(reps) < 200):
+        reps.append(one_pass())
+    med = statistics.median(reps)
+    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "what": "the CPU oracle (oracle/hprms_oracle.c, OpenMP over rows)",
+            "sample": (f"{sample_rows} rows x each H of the sweep (bf16, {len(shapes)} shapes, "
+                       f"{sample_bytes / 1e6:.0f} MB algorithmic per pass), median of {len(reps)} passes")}
 
 
 def main():
@@ -247,6 +304,11 @@ def main():
     ap.add_argument("--sweep-max", type=int, default=32768)
     ap.add_argument("--profile-config", default="",
                     help="with --profile: force lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags")
+    ap.add_argument("--ceiling", default="", metavar="H,H,...",
+                    help="only the ceiling leg: the fused op beside the skeleton, copy, read, write and empty "
+                         "kernels of the bench library at (4096, H), one JSON line")
+    ap.add_argument("--timeline-dump", default="", metavar="DIR",
+                    help="with --ceiling: also save each H's raw per-workgroup timeline as DIR/timeline_H.npy")
     ap.add_argument("--profile-op", default="fused",
                     choices=("fused", "fp8", "plain", "mxfp8", "mxfp4", "copy", "relu"),
                     help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, plain RMSNorm, "
@@ -271,6 +333,12 @@ def main():
         return profile_driver(torch, abi, op, args)
     if args.sweep:
         return sweep(torch, abi, op, args)
+    if args.ceiling:
+        hs = [int(v) for v in args.ceiling.split(",")]
+        rows = ceiling(torch, abi, hp_rms_norm_amd, hs, max(args.steps, 10), args.warmup,
+                       dump=args.timeline_dump or None)
+        print(json.dumps({"ceiling_bf16": rows}), flush=True)
+        return
 
     shapes = [(B, h, torch.bfloat16, "bench") for h in H_SWEEP]
     log(f"bench: timing {len(shapes)} shapes x {args.steps} steps (warmup {args.warmup})")
@@ -322,15 +390,12 @@ def main():
                 c["fused_over_copy"] = round(fused_us[c["hidden"]] / c["us_per_call"], 3)
 
     cpu = None
-    torch_cpu = None
+    cpu_oracle = None
     if not args.no_cpu:
-        log("bench: CPU baselines")
-        res, threads, sample = cpu_baselines(torch)
-        cpu = {"value": res["oracle"]["value"], "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": sample, "us_per_4096_row_call": res["oracle"]["us_per_4096_row_call"]}
-        torch_cpu = {"value": res["torch"]["value"], "unit": "GB/s", "cores": threads,
-                     "sample": sample, "us_per_4096_row_call": res["torch"]["us_per_4096_row_call"],
-                     "formula": "x + r; torch.rms_norm(s, (H,), weight=w, eps=eps) on CPU (test/test_hp_rms_norm.py:6-19)"}
+        log("bench: CPU baseline (torch eager formula)")
+        cpu = cpu_torch_baseline(torch)
+        log("bench: CPU oracle")
+        cpu_oracle = cpu_oracle_baseline(torch)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -346,7 +411,7 @@ def main():
         "per_shape": per_shape,
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "cpu_torch_eager": torch_cpu,
+        "cpu_oracle": cpu_oracle,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
@@ -439,6 +504,118 @@ def sweep(torch, abi, op, args):
                           "gbs": round(fused_bytes(B, h) / (us * 1e-6) / 1e9, 1),
                           "kernel": {"lanes_per_row": key[1], "vec_per_lane": key[2], "lds_vec_per_lane": key[3],
                                      "block": key[4], "flags": key[6]}}), flush=True)
+
+
+SKEL_FLAG_MASK = 1 | 2 | 8 | 16 | 128   # the cache-policy and load-order bits the skeleton kernels take
+
+
+def timeline_summary(tl, events_us):
+    """Per-workgroup {start, end} realtime ticks (10 ns) of one launch ->
+    when the workgroups started and ended relative to the first start."""
+    import numpy as np
+    t = np.asarray(tl, dtype=np.int64)
+    t0 = t[:, 0].min()
+    start = (t[:, 0] - t0) * 0.01
+    end = (t[:, 1] - t0) * 0.01
+    dur = end - start
+    q = lambda a, p: round(float(np.percentile(a, p)), 2)  # noqa: E731
+    xcc = t[:, 3] & 0xF
+    per_xcd_end = [round(float(end[xcc == i].max()), 2) for i in range(8) if (xcc == i).any()]
+    return {"workgroups": int(t.shape[0]), "events_us": round(events_us, 2),
+            "span_us": round(float(end.max()), 2),
+            "outside_span_us": round(events_us - float(end.max()), 2),
+            "start_us_p50_p90_max": [q(start, 50), q(start, 90), q(start, 100)],
+            "end_us_min_p10_p50_p90": [q(end, 0), q(end, 10), q(end, 50), q(end, 90)],
+            "wg_us_p10_p50_p90": [q(dur, 10), q(dur, 50), q(dur, 90)],
+            "last_end_per_xcd_us": per_xcd_end,
+            "wgs_per_xcd": [int((xcc == i).sum()) for i in range(8)]}
+
+
+def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
+    """The fused op beside kernels that move its bytes without its arithmetic
+    (hprms_ceiling.hip, bench library), at (4096, H) bf16, cold (rotating
+    buffer sets spanning >= 1 GiB), interleaved over `trials` rounds, median
+    µs per call:
+      fused     the product op (the table's kernel)
+      skeleton  the op's data movement with the table row's shape and cache
+                policy, no fp32 arithmetic, no weight
+      copy      one read and one write stream of the op's 4*B*H*2 bytes
+      read      the op's two read streams only (2*B*H*2 bytes)
+      write     the op's two write streams only (2*B*H*2 bytes)
+      empty     the table row's grid of empty workgroups
+    and one timeline launch of the table's kernel (per-workgroup start/end)."""
+    import numpy as np
+    bench = abi.BENCH
+    BL = bench.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+    out = []
+    for h in hs:
+        n = cold_sets(B, h)
+        bufs = [torch.empty((2, B, h), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
+        w = make_weight(torch, h, torch.bfloat16, 0, "cuda:0")
+        cfg = abi.select_config(B, h, abi.DTYPE_BF16)
+        rpb = cfg.block_threads // cfg.lanes_per_row
+        grid = (B + rpb - 1) // rpb
+        nb = B * h * 2   # bytes of one [B, H] tensor
+        sflags = cfg.flags & SKEL_FLAG_MASK
+
+        def chk(rc, what):
+            if rc != 0:
+                raise RuntimeError(f"{what}: status {rc}")
+        kinds = {
+            "fused": lambda i: ops.hp_rms_norm(bufs[i][0], w, bufs[i][1], EPS),
+            "skeleton": lambda i: chk(BL.hprms_ceil_skeleton(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), B, h,
+                                                             cfg.lanes_per_row, cfg.vec_per_lane,
+                                                             cfg.block_threads, sflags, stream), "skeleton"),
+            "copy": lambda i: chk(BL.hprms_ceil_copy(bufs[(i + 1) % n].data_ptr(), bufs[i].data_ptr(), 2 * nb,
+                                                     stream), "copy"),
+            "read": lambda i: chk(BL.hprms_ceil_read(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nb,
+                                                     sink.data_ptr(), stream), "read"),
+            "write": lambda i: chk(BL.hprms_ceil_write(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nb, stream),
+                                   "write"),
+            "empty": lambda i: chk(BL.hprms_ceil_empty(grid, cfg.block_threads, stream), "empty"),
+        }
+        samples = {k: [] for k in kinds}
+        for t in range(trials):
+            for k, fn in (kinds.items() if t % 2 == 0 else reversed(list(kinds.items()))):
+                samples[k].append(time_rotating(torch, fn, n, steps, warmup))
+        us = {k: statistics.median(v) for k, v in samples.items()}
+        nbytes = {"fused": fused_bytes(B, h), "skeleton": 4 * nb, "copy": 4 * nb, "read": 2 * nb, "write": 2 * nb}
+        row = {"hidden": h, "rows": B,
+               "kernel": {"lanes_per_row": cfg.lanes_per_row, "vec_per_lane": cfg.vec_per_lane,
+                          "lds_vec_per_lane": cfg.lds_vec_per_lane, "block": cfg.block_threads,
+                          "flags": cfg.flags, "grid": grid, "skeleton_flags": sflags},
+               "us_per_call": {k: round(v, 2) for k, v in us.items()},
+               "gbs": {k: round(nbytes[k] / (us[k] * 1e-6) / 1e9, 1) for k in nbytes},
+               "fused_over_skeleton": round(us["fused"] / us["skeleton"], 3),
+               "fused_over_copy": round(us["fused"] / us["copy"], 3)}
+        # one timeline launch of the table's kernel on a cold buffer set
+        tcfg = abi.Config(*cfg.as_tuple())
+        tcfg.flags = cfg.flags | 512
+        tl = torch.zeros((grid, 4), dtype=torch.int64, device="cuda:0")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for k in range(n):  # leave set 0 the least recently used
+            kinds["fused"](k)
+        torch.cuda.synchronize()
+        prefill(torch, 5)
+        e0.record()
+        rc = BL.hprms_bench_fused_timeline(bufs[0][0].data_ptr(), w.data_ptr(), bufs[0][1].data_ptr(), B, h,
+                                           abi.DTYPE_BF16, EPS, ctypes.byref(tcfg), tl.data_ptr(), stream)
+        e1.record()
+        torch.cuda.synchronize()
+        if rc == 0:
+            tlh = tl.cpu().numpy()
+            row["timeline"] = timeline_summary(tlh, e0.elapsed_time(e1) * 1e3)
+            if dump:
+                np.save(os.path.join(dump, f"timeline_{h}.npy"), tlh)
+        else:
+            row["timeline"] = {"skipped": bench.last_error()}
+        log("ceiling", json.dumps(row))
+        out.append(row)
+        del bufs, tl
+        torch.cuda.empty_cache()
+    return out
 
 
 def load_traffic(key):
@@ -709,6 +886,9 @@ def run_extra(torch, ops, args):
         del bufs, x, r
         torch.cuda.empty_cache()
     out["same_buffers_every_call"] = hot
+    # the op beside kernels that move its bytes without its arithmetic (bench library)
+    from hp_rms_norm_amd import abi
+    out["ceiling_bf16"] = ceiling(torch, abi, ops, [4096, 8192, 16384, 32768], steps, args.warmup, trials=3)
     return out
 
 

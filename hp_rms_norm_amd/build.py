@@ -1,9 +1,13 @@
-"""In-tree build of the two native libraries of hp_rms_norm_amd.
+"""In-tree build of the native libraries of hp_rms_norm_amd.
 
     libhprms.so        the gfx950 kernels and their C ABI (hipcc)
-    libhprms_torch.so  the torch operator registration on top of it (g++)
+    _C.so              the extension module that registers torch.ops.hp_rms_norm.*
+                       on top of it (g++)
+    libhprms_bench.so  bench and test library, not part of the product: the same
+                       C ABI plus the kernel shapes only the tuning sweeps use and
+                       the ceiling kernels (hprms_ceiling.hip)
 
-Both land next to this file, so they travel with the source tree.  Run
+All land next to this file, so they travel with the source tree.  Run
 ``python hp_rms_norm_amd/build.py [all|kernels|torch|oracle]`` (or
 ``__graft_entry__.build()``) -- as a script, not with ``-m``: importing it
 through the package would run the package's __init__, which needs the
@@ -13,6 +17,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 import tempfile
 
 PKG = os.path.dirname(os.path.abspath(__file__))
@@ -22,7 +27,8 @@ INCLUDE = os.path.join(ROOT, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 KERNEL_LIB = os.path.join(PKG, "libhprms.so")
-TORCH_LIB = os.path.join(PKG, "libhprms_torch.so")
+TORCH_LIB = os.path.join(PKG, "_C.so")
+BENCH_LIB = os.path.join(PKG, "libhprms_bench.so")
 
 ARCH = "gfx950"
 # Packed fp32 VALU ops stay off: plain fp32 code is what the kernels need, and
@@ -64,15 +70,19 @@ def _atomic(dst, build_fn):
 
 def build_kernels():
     """Compiles every translation unit of csrc/ at once into a scratch
-    directory, then links libhprms.so."""
+    directory, then links libhprms.so and libhprms_bench.so.  The two share
+    the variant and general-tier objects; hprms.hip is compiled once per
+    library (HPRMS_BENCH_BUILD adds the bench-only shapes and entry point)."""
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, name)
-            for name in ("hprms.hip", "hprms_unaligned.hip", "hprms_tail.hip", "hprms_general.hip")]
+    units = [("hprms.hip", []), ("hprms_unaligned.hip", []), ("hprms_tail.hip", []), ("hprms_general.hip", []),
+             ("hprms.hip", ["-DHPRMS_BENCH_BUILD"]), ("hprms_ceiling.hip", [])]
     with tempfile.TemporaryDirectory(prefix="hprms_build_") as tmp:
-        objs = [os.path.join(tmp, os.path.basename(src) + ".o") for src in srcs]
-        _run_parallel([[hipcc, *HIP_FLAGS, "-c", f"-I{INCLUDE}", f"-I{CSRC}", src, "-o", obj]
-                       for src, obj in zip(srcs, objs)])
-        _atomic(KERNEL_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", *objs, "-o", out]))
+        objs = [os.path.join(tmp, f"{i}_{name}.o") for i, (name, _) in enumerate(units)]
+        _run_parallel([[hipcc, *HIP_FLAGS, *defs, "-c", f"-I{INCLUDE}", f"-I{CSRC}", os.path.join(CSRC, name),
+                        "-o", obj] for (name, defs), obj in zip(units, objs)])
+        product, shared, bench = objs[0], objs[1:4], objs[4:]
+        _atomic(KERNEL_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", product, *shared, "-o", out]))
+        _atomic(BENCH_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", *bench, *shared, "-o", out]))
 
 
 def build_torch_binding():
@@ -81,7 +91,8 @@ def build_torch_binding():
 
     cxx = shutil.which("g++") or "c++"
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    incs = [f"-I{p}" for p in cpp_extension.include_paths()] + [f"-I{INCLUDE}", f"-I{ROCM}/include"]
+    incs = [f"-I{p}" for p in cpp_extension.include_paths()] + [
+        f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}", f"-I{ROCM}/include"]
     tlib = cpp_extension.library_paths()[0]
     cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",

@@ -44,12 +44,19 @@ bool rows_aligned128(const void* base, int64_t stride_bytes) {
   return ((uintptr_t)base & 127u) == 0 && stride_bytes % 128 == 0;
 }
 
+// Every kernel a dispatch table can choose for rows on the 128-byte grid; the
+// bench library (HPRMS_BENCH_BUILD) adds the shapes only the tuning sweeps
+// and the ceiling measurements use.
 const FusedEntry kFused[] = {
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
+#ifdef HPRMS_BENCH_BUILD
     HPRMS_ALT_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_ALT_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
     HPRMS_TUNING_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_CANDIDATE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_TIMELINE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+#endif
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
     HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
@@ -270,6 +277,7 @@ struct Problem {
   const void* const* parts = nullptr;
   void* mx_scales = nullptr;   // modes 5, 6: E8M0 bytes
   int64_t mx_scale_stride = 0; // bytes
+  int64_t* timeline = nullptr; // configurations with flags bit 9 (bench library)
 };
 
 bool is_mx(int mode) { return mode == 5 || mode == 6; }
@@ -525,6 +533,8 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
     table_config(p.rows, p.hidden, p.mode, &c);
     if (c.tier != 3 && (needs_unaligned(p) || ((c.flags & 24) && skip_sc1(p)))) c.flags = unaligned_flags(p, c.flags);
   }
+  if ((c.flags & 512) && !p.timeline)
+    return fail(HPRMS_E_INVALID, "flags bit 9 (timeline) needs hprms_bench_fused_timeline and its buffer");
   if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
     return fail(HPRMS_E_INVALID,
                 "MX output needs 2-byte aligned input, residual and weight and a row group's rows "
@@ -578,11 +588,14 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   }
   a.hidden_f = (float)p.hidden;
   a.eps = (float)p.eps;
+  a.timeline = p.timeline;
 
   int64_t grid = a.ngroups;
   if (c.grid_blocks > 0 && c.grid_blocks < grid) grid = c.grid_blocks;
   if (grid > kMaxGrid) grid = kMaxGrid;
-  hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(c.block_threads), 0, stream, a);
+  // flags bit 11: 96 KiB of (unused) dynamic LDS, so one workgroup holds a CU
+  const unsigned lds = (c.flags & 2048) ? 96u * 1024u : 0u;
+  hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(c.block_threads), lds, stream, a);
   return check_launch("fused rmsnorm kernel");
 }
 
@@ -744,6 +757,21 @@ int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
   }
   return n;
 }
+
+#ifdef HPRMS_BENCH_BUILD
+// Bench library only: the in-place fused op on contiguous rows with a forced
+// configuration whose flags carry bit 9, recording per workgroup {start, end,
+// HW_ID, XCC_ID} (realtime clock ticks of 10 ns) into timeline[4 * workgroup
+// + i]; the caller sizes timeline for the launched grid.
+int hprms_bench_fused_timeline(void* input, const void* weight, void* residual, int64_t rows, int64_t hidden,
+                               int dtype, double eps, const hprms_config* config, int64_t* timeline,
+                               hipStream_t stream) {
+  if (!config) return fail(HPRMS_E_INVALID, "config is null");
+  Problem p{0, input, input, residual, weight, rows, hidden, hidden, hidden, hidden, dtype, eps, nullptr};
+  p.timeline = timeline;
+  return run(p, config, stream);
+}
+#endif
 
 const char* hprms_last_error(void) { return g_err; }
 

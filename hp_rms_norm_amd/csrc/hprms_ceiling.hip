@@ -1,0 +1,242 @@
+// hprms_ceiling.hip - measurement kernels of the bench library
+// libhprms_bench.so (never linked into libhprms.so).  They move the bytes of
+// the fused add + RMSNorm op in simpler ways, so that the op's time can be
+// set beside what the same hardware needs for the same traffic:
+//
+//   hprms_ceil_empty     a grid of empty workgroups of 256, 512 or 1024 lanes
+//                        (launch, dispatch and teardown of a kernel of that
+//                        grid, no memory traffic)
+//   hprms_ceil_read      read two tensors of n bytes (the op's two read streams)
+//   hprms_ceil_write     write two tensors of n bytes (the op's two write streams)
+//   hprms_ceil_copy      copy n bytes (one read and one write stream)
+//   hprms_ceil_skeleton  the op's own data movement in place on [rows, hidden]
+//                        x and r with the lane mapping of a table row: every
+//                        load first, r <- x + r stored as soon as it is formed,
+//                        a row-wide reduction (DPP inside the wave, LDS and one
+//                        barrier across waves), then x <- f(x, row value)
+//                        stored; no fp32 arithmetic and no weight.
+//
+// The flat kernels give each 256-lane workgroup one 16-byte vector per lane of
+// each stream (4 KiB), the shape the streamer measured fastest.  All
+// accesses are non-temporal unless a kernel's flags say otherwise.  Every entry
+// point returns HPRMS_OK or HPRMS_E_INVALID / HPRMS_E_LAUNCH, like the
+// product's C ABI.
+#include <hip/hip_runtime.h>
+
+#include "hp_rms_norm_amd.h"
+#include "hprms_device.h"
+
+namespace hprms {
+namespace {
+
+constexpr int kFlatBlock = 256;
+
+template <int BLOCK>
+__global__ __launch_bounds__(BLOCK) void ceil_empty_kernel() {}
+
+// Reads vector i of a and of b; the loaded bits feed a compare whose store
+// never happens for random data, so the loads cannot be dropped.
+__global__ __launch_bounds__(kFlatBlock) void ceil_read_kernel(const u32x4* a, const u32x4* b, int64_t nvec,
+                                                               uint32_t* sink) {
+  const int64_t i = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
+  if (i >= nvec) return;
+  const u32x4 u = __builtin_nontemporal_load(a + i);
+  const u32x4 v = __builtin_nontemporal_load(b + i);
+  const uint32_t t = (u[0] ^ v[0]) + (u[1] ^ v[1]) + (u[2] ^ v[2]) + (u[3] ^ v[3]);
+  if (t == 0x9e3779b9u) sink[0] = t;
+}
+
+__global__ __launch_bounds__(kFlatBlock) void ceil_write_kernel(u32x4* a, u32x4* b, int64_t nvec) {
+  const int64_t i = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
+  if (i >= nvec) return;
+  const uint32_t v = (uint32_t)i;
+  __builtin_nontemporal_store((u32x4){v, v, v, v}, a + i);
+  __builtin_nontemporal_store((u32x4){~v, ~v, ~v, ~v}, b + i);
+}
+
+__global__ __launch_bounds__(kFlatBlock) void ceil_copy_kernel(u32x4* dst, const u32x4* src, int64_t nvec) {
+  const int64_t i = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
+  if (i >= nvec) return;
+  __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+struct SkelArgs {
+  uint16_t* x;
+  uint16_t* r;
+  int64_t rows;
+  int32_t hidden;
+  int32_t nvec;
+};
+
+// The op's data movement with a table row's shape (LPR lanes per row, VPL
+// vectors per lane, BLOCK lanes per workgroup) and cache-policy flags (bits
+// 0, 1, 3, 4 and 7 as in fused_vec_kernel).  Contiguous rows, hidden % 8 == 0,
+// 16-byte aligned tensors.
+template <int LPR, int VPL, int BLOCK, int FLAGS>
+__global__ __launch_bounds__(BLOCK) void ceil_skeleton_kernel(SkelArgs a) {
+  constexpr int RPB = BLOCK / LPR;
+  constexpr int GW = LPR < 64 ? LPR : 64;
+  constexpr int WPR = LPR > 64 ? LPR / 64 : 1;
+  constexpr int NW = BLOCK / 64;
+  constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
+  constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
+  constexpr uint32_t CH = LPR * 16;
+  __shared__ float red[WPR > 1 ? NW : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (LPR - 1);
+  const int rib = tid / LPR;
+  const int64_t row0 = (int64_t)blockIdx.x * RPB;
+  const int64_t left = a.rows - row0;
+  const int nrows = left < RPB ? (int)left : RPB;
+  const bool row_ok = rib < nrows;
+  const uint32_t bytes = (uint32_t)((int64_t)nrows * a.hidden * 2);
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row0 * a.hidden, bytes);
+  const __amdgpu_buffer_rsrc_t rrs = make_rsrc(a.r + row0 * a.hidden, bytes);
+  const uint32_t off = (uint32_t)rib * (uint32_t)a.hidden * 2u + (uint32_t)lane * 16u;
+
+  u32x4 xv[VPL], rv[VPL];
+  uint32_t o[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) o[k] = (row_ok && (k * LPR + lane) < a.nvec) ? off + k * CH : kOOB;
+  if constexpr ((FLAGS & 128) != 0) {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, o[k]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, o[k]);
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      xv[k] = load16<LAUX>(xrs, o[k]);
+      rv[k] = load16<LAUX>(rrs, o[k]);
+    }
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    u32x4 s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s[j] = xv[k][j] + rv[k][j];
+      acc += s[j] & 0xffu;
+    }
+    rv[k] = s;
+    store16<SAUX>(s, rrs, o[k]);
+  }
+  float tot = group_sum<GW>((float)acc);
+  if constexpr (WPR > 1) {
+    const int wave = tid >> 6;
+    if ((tid & 63) == 0) red[wave] = tot;
+    __syncthreads();
+    const int w0 = (wave / WPR) * WPR;
+    tot = red[w0];
+#pragma unroll
+    for (int j = 1; j < WPR; ++j) tot += red[w0 + j];
+  }
+  const uint32_t t = __float_as_uint(tot);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    u32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = xv[k][j] ^ (rv[k][j] + t);
+    store16<SAUX>(v, xrs, o[k]);
+  }
+}
+
+typedef void (*skel_fn)(SkelArgs);
+struct SkelEntry {
+  int lpr, vpl, block, flags;
+  skel_fn fn;
+};
+
+#define HPRMS_SKEL(LPR, VPL, BLOCK, FLAGS) {LPR, VPL, BLOCK, FLAGS, &ceil_skeleton_kernel<LPR, VPL, BLOCK, FLAGS>},
+#define HPRMS_SKEL_FLAGS(LPR, VPL, BLOCK) \
+  HPRMS_SKEL(LPR, VPL, BLOCK, 3) HPRMS_SKEL(LPR, VPL, BLOCK, 27) HPRMS_SKEL(LPR, VPL, BLOCK, 131) \
+  HPRMS_SKEL(LPR, VPL, BLOCK, 155)
+
+// the lane shapes of the bandwidth table's rows and their neighbours
+const SkelEntry kSkel[] = {
+    HPRMS_SKEL_FLAGS(32, 4, 256) HPRMS_SKEL_FLAGS(64, 4, 256) HPRMS_SKEL_FLAGS(128, 3, 256)
+    HPRMS_SKEL_FLAGS(128, 4, 256) HPRMS_SKEL_FLAGS(256, 2, 256) HPRMS_SKEL_FLAGS(256, 4, 256)
+    HPRMS_SKEL_FLAGS(512, 2, 512) HPRMS_SKEL_FLAGS(512, 3, 512) HPRMS_SKEL_FLAGS(512, 4, 512)
+    HPRMS_SKEL_FLAGS(1024, 2, 1024) HPRMS_SKEL_FLAGS(256, 8, 256) HPRMS_SKEL_FLAGS(1024, 3, 1024)
+    HPRMS_SKEL_FLAGS(1024, 4, 1024)
+};
+
+int launched() { return hipGetLastError() == hipSuccess ? HPRMS_OK : HPRMS_E_LAUNCH; }
+
+int64_t flat_grid(int64_t nvec) { return (nvec + kFlatBlock - 1) / kFlatBlock; }
+
+bool flat_ok(const void* p, int64_t nbytes) {
+  return p && ((uintptr_t)p & 15u) == 0 && nbytes > 0 && nbytes % 16 == 0 && flat_grid(nbytes / 16) <= 0x7fffffff;
+}
+
+}  // namespace
+}  // namespace hprms
+
+using namespace hprms;
+
+extern "C" {
+
+// block: 256, 512 or 1024 lanes (the table's workgroup sizes)
+int hprms_ceil_empty(int64_t grid, int block, hipStream_t stream) {
+  if (grid < 1 || grid > 0x7fffffff) return HPRMS_E_INVALID;
+  const dim3 g((unsigned)grid);
+  if (block == 256)
+    ceil_empty_kernel<256><<<g, dim3(256), 0, stream>>>();
+  else if (block == 512)
+    ceil_empty_kernel<512><<<g, dim3(512), 0, stream>>>();
+  else if (block == 1024)
+    ceil_empty_kernel<1024><<<g, dim3(1024), 0, stream>>>();
+  else
+    return HPRMS_E_INVALID;
+  return launched();
+}
+
+int hprms_ceil_read(const void* a, const void* b, int64_t nbytes, void* sink, hipStream_t stream) {
+  if (!flat_ok(a, nbytes) || !flat_ok(b, nbytes) || !sink) return HPRMS_E_INVALID;
+  const int64_t nvec = nbytes / 16;
+  ceil_read_kernel<<<dim3((unsigned)flat_grid(nvec)), dim3(kFlatBlock), 0, stream>>>(
+      (const u32x4*)a, (const u32x4*)b, nvec, (uint32_t*)sink);
+  return launched();
+}
+
+int hprms_ceil_write(void* a, void* b, int64_t nbytes, hipStream_t stream) {
+  if (!flat_ok(a, nbytes) || !flat_ok(b, nbytes)) return HPRMS_E_INVALID;
+  const int64_t nvec = nbytes / 16;
+  ceil_write_kernel<<<dim3((unsigned)flat_grid(nvec)), dim3(kFlatBlock), 0, stream>>>((u32x4*)a, (u32x4*)b, nvec);
+  return launched();
+}
+
+int hprms_ceil_copy(void* dst, const void* src, int64_t nbytes, hipStream_t stream) {
+  if (!flat_ok(dst, nbytes) || !flat_ok(src, nbytes)) return HPRMS_E_INVALID;
+  const int64_t nvec = nbytes / 16;
+  ceil_copy_kernel<<<dim3((unsigned)flat_grid(nvec)), dim3(kFlatBlock), 0, stream>>>((u32x4*)dst,
+                                                                                   (const u32x4*)src, nvec);
+  return launched();
+}
+
+// x and r: contiguous [rows, hidden] 16-bit tensors, 16-byte aligned, hidden %
+// 8 == 0, lpr * vpl * 8 >= hidden and a row group within 2 GiB.  (lpr, vpl,
+// block, flags) must be one of kSkel's shapes.
+int hprms_ceil_skeleton(void* x, void* r, int64_t rows, int64_t hidden, int lpr, int vpl, int block, int flags,
+                        hipStream_t stream) {
+  if (!x || !r || ((uintptr_t)x & 15u) || ((uintptr_t)r & 15u) || rows < 1 || hidden < 8 || hidden % 8 != 0 ||
+      (int64_t)lpr * vpl * 8 < hidden)
+    return HPRMS_E_INVALID;
+  for (const SkelEntry& e : kSkel) {
+    if (e.lpr != lpr || e.vpl != vpl || e.block != block || e.flags != flags) continue;
+    const int64_t rpb = block / lpr;
+    if (rpb * hidden * 2 >= (int64_t)kOOB) return HPRMS_E_INVALID;
+    const int64_t grid = (rows + rpb - 1) / rpb;
+    if (grid > 0x7fffffff) return HPRMS_E_INVALID;
+    SkelArgs a{(uint16_t*)x, (uint16_t*)r, rows, (int32_t)hidden, (int32_t)(hidden / 8)};
+    hipLaunchKernelGGL(e.fn, dim3((unsigned)grid), dim3(block), 0, stream, a);
+    return launched();
+  }
+  return HPRMS_E_INVALID;
+}
+
+}  // extern "C"

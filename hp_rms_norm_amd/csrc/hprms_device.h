@@ -50,10 +50,20 @@ __device__ __forceinline__ void store16(u32x4 v, __amdgpu_buffer_rsrc_t r, uint3
 template <int DT>
 struct Fmt;
 
+// olo / ohi: the same unpacks as lo / hi, through a byte permute
+// (v_perm_b32).  The output phase of the kernels unpacks the row it holds with
+// them: sharing the square phase's unpacks, the compiler would keep two floats
+// per held 32-bit word live across the row reduction instead of the word.
 template <>
 struct Fmt<HPRMS_DTYPE_BF16> {
   __device__ static __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ static __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static __forceinline__ float olo(uint32_t w) {
+    return __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000c0cu));
+  }
+  __device__ static __forceinline__ float ohi(uint32_t w) {
+    return __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x03020c0cu));
+  }
   __device__ static __forceinline__ uint32_t pack(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
   }
@@ -68,6 +78,12 @@ struct Fmt<HPRMS_DTYPE_FP16> {
   }
   __device__ static __forceinline__ float hi(uint32_t w) {
     return (float)__builtin_bit_cast(f16x2, w)[1];
+  }
+  __device__ static __forceinline__ float olo(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, w, 0x0c0c0100u))[0];
+  }
+  __device__ static __forceinline__ float ohi(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, w, 0x0c0c0302u))[0];
   }
   __device__ static __forceinline__ uint32_t pack(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));

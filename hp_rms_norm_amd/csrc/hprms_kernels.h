@@ -101,15 +101,17 @@ struct FusedArgs {
   int64_t mx_scale_stride;  // bytes between scale rows
   uint32_t shift_base;   // tail variant: row r is shifted by (shift_base + r * shift_step) mod 8 elements
   uint32_t shift_step;
+  int64_t* timeline;     // FLAGS bit 9 only (bench library): 4 values per workgroup
 };
 
 // Waves per SIMD the compiler must leave room for: the tail variant of the
 // 1024-lane shapes with up to 2 vectors per lane is held to 64 VGPRs, so two
 // workgroups share a CU as they do without the tail (the FP8 form needed 66:
 // held to 64 it runs 19-23% faster at 13K-16K).  At 3 vectors per lane the
-// same limit spills and measured 3-7% slower.
+// same limit spills and measured 3-7% slower.  FLAGS bit 8 asks for 8 waves
+// per SIMD (64 VGPRs) on any shape.
 template <int FLAGS, int BLOCK, int VPL>
-constexpr int kMinWavesPerEU = ((FLAGS & 64) != 0 && BLOCK == 1024 && VPL <= 2) ? 8 : 1;
+constexpr int kMinWavesPerEU = ((FLAGS & 256) != 0 || ((FLAGS & 64) != 0 && BLOCK == 1024 && VPL <= 2)) ? 8 : 1;
 
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<FLAGS, BLOCK, VPL>)))
@@ -140,9 +142,19 @@ void fused_vec_kernel(FusedArgs a) {
   const int lane = tid & (LPR - 1);
   const int rib = tid / LPR;
   const int wave = tid >> 6;
+  // FLAGS bit 9 (bench library only): per workgroup, the realtime clock
+  // (100 MHz) at its start and after its last store has completed, and the
+  // hardware ids of the CU it ran on
+  constexpr bool TIMELINE = (FLAGS & 512) != 0;
+  const uint64_t t_start = TIMELINE ? __builtin_amdgcn_s_memrealtime() : 0;
 
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)a.hidden * 2u);
 
+  // slots past the row's vectors: their row accesses and (in the tail
+  // variant, whose shifted weight slot past the row could start inside the
+  // weight) their weight loads take the out-of-range offset; elsewhere such a
+  // weight slot starts at or past the weight's end and the range check
+  // returns zeros
   bool vec_ok[VPL];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < a.nvec;
@@ -263,7 +275,8 @@ void fused_vec_kernel(FusedArgs a) {
     }
     if constexpr (!WLATE) {
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u + wshift);
+      for (int k = 0; k < VPL; ++k)
+        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : (uint32_t)(k * LPR + lane) * 16u + wshift);
       if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
     }
 
@@ -381,7 +394,8 @@ void fused_vec_kernel(FusedArgs a) {
 
     if constexpr (WLATE) {
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) wv[k] = load16<0>(wrs, (uint32_t)(k * LPR + lane) * 16u + wshift);
+      for (int k = 0; k < VPL; ++k)
+        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : (uint32_t)(k * LPR + lane) * 16u + wshift);
       if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
     }
 
@@ -406,7 +420,7 @@ void fused_vec_kernel(FusedArgs a) {
         uint32_t m2 = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          y[j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+          y[j] = F::pack((F::olo(s[j]) * inv) * F::lo(wv[k][j]), (F::ohi(s[j]) * inv) * F::hi(wv[k][j]));
           const uint32_t mag = y[j] & 0x7fff7fffu;
           m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(mag & 0xffffu, mag >> 16));
         }
@@ -447,7 +461,7 @@ void fused_vec_kernel(FusedArgs a) {
         u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          o[j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+          o[j] = F::pack((F::olo(s[j]) * inv) * F::lo(wv[k][j]), (F::ohi(s[j]) * inv) * F::hi(wv[k][j]));
         const bool ok = row_ok && vec_ok[k];
         store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
       }
@@ -455,7 +469,7 @@ void fused_vec_kernel(FusedArgs a) {
         u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          o[j] = F::pack((F::lo(tsv[j]) * inv) * F::lo(twv[j]), (F::hi(tsv[j]) * inv) * F::hi(twv[j]));
+          o[j] = F::pack((F::olo(tsv[j]) * inv) * F::lo(twv[j]), (F::ohi(tsv[j]) * inv) * F::hi(twv[j]));
         store16<SAUX>(o, ors, eooff);
       }
     } else {
@@ -467,7 +481,7 @@ void fused_vec_kernel(FusedArgs a) {
         const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          xv[k][j] = F::pack((F::lo(s[j]) * inv) * F::lo(wv[k][j]), (F::hi(s[j]) * inv) * F::hi(wv[k][j]));
+          xv[k][j] = F::pack((F::olo(s[j]) * inv) * F::lo(wv[k][j]), (F::ohi(s[j]) * inv) * F::hi(wv[k][j]));
         if (row_ok && vec_ok[k]) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -482,7 +496,7 @@ void fused_vec_kernel(FusedArgs a) {
         // counted: harmless for a maximum
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          txv[j] = F::pack((F::lo(tsv[j]) * inv) * F::lo(twv[j]), (F::hi(tsv[j]) * inv) * F::hi(twv[j]));
+          txv[j] = F::pack((F::olo(tsv[j]) * inv) * F::lo(twv[j]), (F::ohi(tsv[j]) * inv) * F::hi(twv[j]));
         if (eok) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -527,6 +541,17 @@ void fused_vec_kernel(FusedArgs a) {
         }
         store8<SAUX>(q, ors, eooff);
       }
+    }
+  }
+  if constexpr (TIMELINE) {
+    __builtin_amdgcn_s_waitcnt(0);  // every load and store of this wave has completed
+    __syncthreads();
+    if (tid == 0) {
+      int64_t* t = a.timeline + 4 * (int64_t)blockIdx.x;
+      t[0] = (int64_t)t_start;
+      t[1] = (int64_t)__builtin_amdgcn_s_memrealtime();
+      t[2] = (int64_t)(uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID: wave, SIMD, CU, SH, SE
+      t[3] = (int64_t)(uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 20);  // XCC_ID
     }
   }
 }

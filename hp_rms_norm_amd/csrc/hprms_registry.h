@@ -19,10 +19,12 @@ struct FusedEntry {
 // flags: bits 0-1 = non-temporal loads / stores, bit 2 = weight loaded late,
 // bits 3-4 = sc1 policy bit on the row loads / stores, bit 5 = the variant for
 // rows that are not 128-byte aligned (any 2-byte boundary), bit 6 = with the
-// tail vector for hidden % 8 != 0 (with bit 5), bit 7 = residual loads first
+// tail vector for hidden % 8 != 0 (with bit 5), bit 7 = residual loads first,
+// bit 8 = held to 8 waves per SIMD, bit 9 = timeline instrumentation (bench
+// library only), bit 11 = one workgroup per CU (the launch reserves LDS)
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
-   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & 251, ((FLAGS) >> 2) & 1>},
+   &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
 
 // The unaligned variants of a shape: the same lanes, vectors and weight
 // timing, no sc1 bits (partial cache lines written with sc1 measured 13-24%
@@ -58,10 +60,14 @@ struct FusedEntry {
 // entries of the FP8-output table that the other tables do not use
 #define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 159)
 
-// alternatives of the fused op that the tests run and the sweep compares against
-// (then five of the table's shapes with the two streams' loads alternating, the
-// two smallest latency rows with the weight loaded late, and the FP8 table's
-// 32K row, so that the 16-bit op runs with each FP8 row's lane mapping)
+// The shapes below are built only into the bench library libhprms_bench.so
+// (hprms.hip compiled with HPRMS_BENCH_BUILD), never into libhprms.so: no
+// table row selects them.
+//
+// Alternatives of the fused op that the tuning sweeps compare against (five
+// of the table's shapes with the two streams' loads alternating, the two
+// smallest latency rows with the weight loaded late, and the FP8 table's 32K
+// row, so that the 16-bit op runs with each FP8 row's lane mapping).
 #define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
   X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
   X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)                           \
@@ -69,12 +75,31 @@ struct FusedEntry {
   X(DT, MODE, 1024, 3, 0, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 31)                         \
   X(DT, MODE, 64, 2, 0, 64, 7) X(DT, MODE, 128, 2, 0, 128, 7) X(DT, MODE, 512, 8, 4, 512, 159)
 
-// extra bf16 fused shapes kept for the tuning sweep (other cache policies, ...)
+// other cache policies and LDS splits of the fused op (bf16)
 #define HPRMS_TUNING_SHAPES(X, DT, MODE)                                                        \
   X(DT, MODE, 64, 2, 0, 256, 11) X(DT, MODE, 128, 4, 0, 256, 27) X(DT, MODE, 256, 4, 0, 256, 27) \
   X(DT, MODE, 512, 4, 0, 512, 3) X(DT, MODE, 1024, 4, 0, 1024, 7) X(DT, MODE, 512, 4, 0, 512, 27) \
   X(DT, MODE, 256, 16, 8, 256, 31) X(DT, MODE, 128, 4, 0, 256, 0) X(DT, MODE, 1024, 4, 2, 1024, 31) \
   X(DT, MODE, 256, 6, 3, 256, 31) X(DT, MODE, 256, 8, 4, 256, 3)
+
+// candidates of the table's rows (bf16): +256 = held to 8 waves per SIMD,
+// +2048 = one workgroup per CU (the launch reserves 96 KiB of LDS)
+#define HPRMS_CANDIDATE_SHAPES(X, DT, MODE)                                                          \
+  X(DT, MODE, 32, 4, 0, 256, 135) X(DT, MODE, 64, 4, 0, 256, 131) X(DT, MODE, 128, 2, 0, 256, 135)    \
+  X(DT, MODE, 128, 4, 0, 256, 135) X(DT, MODE, 128, 4, 0, 256, 159) X(DT, MODE, 128, 4, 0, 256, 391) \
+  X(DT, MODE, 256, 2, 0, 256, 131) X(DT, MODE, 256, 2, 0, 256, 135) X(DT, MODE, 256, 2, 0, 256, 155)  \
+  X(DT, MODE, 256, 2, 0, 256, 159) X(DT, MODE, 256, 4, 0, 256, 135) X(DT, MODE, 256, 4, 0, 256, 159)  \
+  X(DT, MODE, 512, 2, 0, 512, 135) X(DT, MODE, 512, 2, 0, 512, 159) X(DT, MODE, 256, 6, 0, 256, 159)  \
+  X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 512, 4, 0, 512, 159) X(DT, MODE, 1024, 2, 0, 1024, 159) \
+  X(DT, MODE, 1024, 2, 0, 1024, 2079) X(DT, MODE, 1024, 3, 0, 1024, 2207) X(DT, MODE, 1024, 4, 0, 1024, 2207) \
+  X(DT, MODE, 256, 8, 4, 256, 155) X(DT, MODE, 256, 12, 0, 256, 159) X(DT, MODE, 512, 6, 0, 512, 159)
+
+// the bandwidth table's rows with the timeline instrumentation (+512)
+#define HPRMS_TIMELINE_SHAPES(X, DT, MODE)                                                        \
+  X(DT, MODE, 32, 4, 0, 256, 643) X(DT, MODE, 64, 4, 0, 256, 647) X(DT, MODE, 128, 3, 0, 256, 519) \
+  X(DT, MODE, 128, 4, 0, 256, 643) X(DT, MODE, 512, 2, 0, 512, 519) X(DT, MODE, 512, 3, 0, 512, 543) \
+  X(DT, MODE, 1024, 2, 0, 1024, 543) X(DT, MODE, 256, 8, 4, 256, 539) X(DT, MODE, 1024, 3, 0, 1024, 671) \
+  X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 903) X(DT, MODE, 256, 2, 0, 256, 519)
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every

@@ -9,6 +9,12 @@
 // functionalisation and torch.compile see them.  Messages of the shape checks
 // are the reference's (hp_rms_norm/csrc/cuda/hp_rms_norm.cu:12-24,48 and
 // activation_kernels.cu:11-15,38).
+//
+// The library is the package's importable extension module `_C`, as the
+// reference's is (hp_rms_norm/__init__.py:2): importing it loads the library,
+// whose static initialisers at the end of this file register the operators.
+#include <Python.h>
+
 #include <ATen/MemoryOverlap.h>
 #include <ATen/core/Tensor.h>
 #include <c10/core/DeviceGuard.h>
@@ -185,6 +191,15 @@ Fp8Shape check_fp8(const at::Tensor& out, const at::Tensor& scale, const at::Ten
               "out, scale and input must be on the same device");
   int64_t orows = 0;
   rows_of(out, s.f.hidden, &orows, &s.out_stride);
+  if (s.f.rows > 0) {
+    // the FP8 rows and the scales are written while input and residual are
+    // read: no sharing between any two of them
+    at::assert_no_overlap(out, residual);
+    at::assert_no_overlap(out, input);
+    at::assert_no_overlap(scale, residual);
+    at::assert_no_overlap(scale, input);
+    at::assert_no_overlap(scale, out);
+  }
   return s;
 }
 
@@ -368,7 +383,9 @@ MxShape check_mx(const at::Tensor& out, const at::Tensor& scales, const at::Tens
   if (s.f.rows > 0) {
     at::assert_no_overlap(out, scales);
     at::assert_no_overlap(out, residual);
+    at::assert_no_overlap(out, input);
     at::assert_no_overlap(scales, residual);
+    at::assert_no_overlap(scales, input);
   }
   return s;
 }
@@ -391,6 +408,20 @@ void rms_norm_mx_meta(at::Tensor& out, at::Tensor& scales, const at::Tensor& inp
 }
 
 }  // namespace
+
+// Module init of `hp_rms_norm_amd._C`.  The operators live in torch's
+// registry, so the module itself carries only the C ABI version it was built
+// against.
+extern "C" PyObject* PyInit__C(void) {
+  static PyModuleDef def = {PyModuleDef_HEAD_INIT, "_C",
+                            "torch.ops.hp_rms_norm.* on the gfx950 kernels of libhprms.so", -1, nullptr};
+  PyObject* m = PyModule_Create(&def);
+  if (m && PyModule_AddIntConstant(m, "abi_version", hprms_abi_version()) != 0) {
+    Py_DECREF(m);
+    return nullptr;
+  }
+  return m;
+}
 
 TORCH_LIBRARY(hp_rms_norm, m) {
   m.def("rms_norm(Tensor(a!) input, Tensor weight, Tensor(b!) residual, float eps) -> ()");

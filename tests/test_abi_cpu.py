@@ -165,13 +165,13 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
                                                       ctypes.byref(c), None)
                 assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
-                # the FP8 table's choice also exists as a fused (mode 0) kernel, so the
-                # 16-bit op can be run with the same lane mapping
+                # the bench library also has the FP8 table's choice as a fused (mode 0)
+                # kernel, so the 16-bit op can be run with the same lane mapping
                 c8 = abi.select_config(rows, hidden, dtype, 2)
                 assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
-                rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
-                                                      ctypes.byref(c8), None)
-                assert rc == abi.HPRMS_OK, (hidden, c8.as_tuple(), abi.last_error())
+                rc = abi.BENCH.lib().hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype,
+                                                                    1e-6, ctypes.byref(c8), None)
+                assert rc == abi.HPRMS_OK, (hidden, c8.as_tuple(), abi.BENCH.last_error())
 
 
 def test_config_entry_rejects_unbuilt_and_misfit_configs():
@@ -315,3 +315,43 @@ def test_latency_rows_end_at_the_per_mode_limits():
                 assert abi.select_config(limit, hidden, dtype, mode).as_tuple() == lat, (mode, hidden)
                 past = abi.select_config(limit + 1, hidden, dtype, mode).as_tuple()
                 assert past == abi.select_config(4096, hidden, dtype, mode).as_tuple(), (mode, hidden)
+
+
+def test_bench_library_is_apart_from_the_product():
+    """libhprms_bench.so carries the same C ABI plus the tuning-only kernel
+    shapes and the ceiling / timeline entry points; libhprms.so exports none
+    of those and holds only shapes the dispatch tables can choose."""
+    bench = abi.BENCH.lib()
+    for n in declared_functions():
+        assert hasattr(bench, n), n
+    extra = ("hprms_bench_fused_timeline", "hprms_ceil_empty", "hprms_ceil_read", "hprms_ceil_write",
+             "hprms_ceil_copy", "hprms_ceil_skeleton")
+    for n in extra:
+        assert hasattr(bench, n), n
+        assert not hasattr(abi.lib(), n), f"{n} must not be in the product library"
+    for mode in range(7):
+        for dt in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+            prod = {c.as_tuple() for c in abi.kernel_configs(dt, mode)}
+            more = {c.as_tuple() for c in abi.BENCH.kernel_configs(dt, mode)}
+            assert prod <= more
+    tuning = {c.as_tuple() for c in abi.BENCH.kernel_configs(abi.DTYPE_BF16, 0)} - \
+        {c.as_tuple() for c in abi.kernel_configs(abi.DTYPE_BF16, 0)}
+    assert (1, 128, 4, 0, 256, 0, 391) in tuning and (1, 1024, 4, 0, 1024, 0, 671) in tuning
+
+
+def test_bench_entry_points_reject_bad_arguments():
+    L = abi.BENCH.lib()
+    assert L.hprms_ceil_empty(0, 256, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_ceil_empty(4, 128, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_ceil_copy(0x1000, 0x2008, 4096, None) == abi.HPRMS_E_INVALID   # misaligned source
+    assert L.hprms_ceil_read(0x1000, 0x2000, 4095, 0x3000, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_ceil_skeleton(0x1000, 0x2000, 4, 4096, 128, 3, 256, 3, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_ceil_skeleton(0x1000, 0x2000, 4, 4096, 128, 4, 256, 7, None) == abi.HPRMS_E_INVALID
+    c = abi.Config(1, 128, 4, 0, 256, 0, 643)
+    assert L.hprms_bench_fused_timeline(0x1000, 0x2000, 0x3000, 4, 4096, abi.DTYPE_BF16, 1e-6, ctypes.byref(c),
+                                        None, None) == abi.HPRMS_E_INVALID
+    # a timeline configuration through the ordinary forced-config entry has no buffer to write
+    assert abi.BENCH.lib().hprms_fused_add_rmsnorm_config(0x1000, 0x2000, 0x3000, 4, 4096, 4096, 4096,
+                                                          abi.DTYPE_BF16, 1e-6, ctypes.byref(c),
+                                                          None) == abi.HPRMS_E_INVALID
+    assert "timeline" in abi.BENCH.last_error()

@@ -34,6 +34,26 @@ def test_python_surface_matches_reference_ops():
     assert hp_rms_norm.ops.hp_rms_norm is ops.hp_rms_norm
 
 
+def test_reference_import_paths():
+    """Every import form of the reference package works on the alias
+    (hp_rms_norm/__init__.py:1-3, hp_rms_norm/ops.py:1-24): the ``ops``
+    submodule and ``_C``, the extension module whose import registers the ops."""
+    import importlib
+    import types
+
+    import hp_rms_norm
+    import hp_rms_norm.ops
+    from hp_rms_norm import _C
+    from hp_rms_norm.ops import hp_rms_norm as f, relu
+    c2 = importlib.import_module("hp_rms_norm._C")
+    assert f is ops.hp_rms_norm and relu is ops.relu
+    assert hp_rms_norm.ops.hp_rms_norm is ops.hp_rms_norm and hp_rms_norm.ops.relu is ops.relu
+    assert isinstance(_C, types.ModuleType) and c2 is _C and _C is hp_rms_norm_amd._C
+    assert os.path.samefile(_C.__file__, hp_rms_norm_amd.TORCH_LIB)
+    from hp_rms_norm_amd import abi
+    assert _C.abi_version == abi.lib().hprms_abi_version()
+
+
 def test_meta_accepts_valid_shapes():
     assert ops.hp_rms_norm(t(4, 4096), t(4096), t(4, 4096), 1e-6) is None
     assert ops.hp_rms_norm(t(2, 3, 128), t(128), t(2, 3, 128), 1e-6) is None
@@ -198,3 +218,38 @@ def test_missing_native_library_is_an_import_error(tmp_path):
     p = subprocess.run([sys.executable, "-c", code], cwd=tmp_path, capture_output=True, text=True, timeout=300)
     assert p.returncode != 0
     assert "ImportError" in p.stderr and "not built" in p.stderr and "hp_rms_norm_amd/build.py" in p.stderr
+
+
+def test_fp8_meta_rejects_overlapping_outputs():
+    """The FP8 rows and the scales are written while input and residual are
+    read: any overlap among them is refused."""
+    x, w, r = t(4, 256), t(256), t(4, 256)
+    qbuf = torch.empty(4 * 256 + 64, dtype=torch.uint8, device=M)
+    q = qbuf[:1024].view(torch.float8_e4m3fn).view(4, 256)
+    sc = torch.empty(4, 1, device=M)
+    assert ops.hp_rms_norm_fp8(q, sc, x, w, r, 1e-6) is None
+    rbuf = torch.empty(4 * 256 * 2, dtype=torch.uint8, device=M)
+    r_shared = rbuf.view(torch.bfloat16).view(4, 256)
+    xbuf = torch.empty(4 * 256 * 2, dtype=torch.uint8, device=M)
+    x_shared = xbuf.view(torch.bfloat16).view(4, 256)
+    cases = [
+        (rbuf[:1024].view(torch.float8_e4m3fn).view(4, 256), sc, x, r_shared),      # out on residual
+        (xbuf[:1024].view(torch.float8_e4m3fn).view(4, 256), sc, x_shared, r),      # out on input
+        (q, rbuf[:16].view(torch.float32).view(4, 1), x, r_shared),                  # scale on residual
+        (q, xbuf[:16].view(torch.float32).view(4, 1), x_shared, r),                  # scale on input
+        (q, qbuf[:16].view(torch.float32).view(4, 1), x, r),                         # scale on out
+    ]
+    for out, scale, inp, res in cases:
+        with pytest.raises(RuntimeError, match="written-to"):
+            ops.hp_rms_norm_fp8(out, scale, inp, w, res, 1e-6)
+
+
+def test_mx_meta_rejects_outputs_on_the_input():
+    w, r = t(256), t(4, 256)
+    xbuf = torch.empty(4 * 256 * 2, dtype=torch.uint8, device=M)
+    x_shared = xbuf.view(torch.bfloat16).view(4, 256)
+    u8 = lambda *sh: torch.empty(*sh, dtype=torch.uint8, device=M)   # noqa: E731
+    with pytest.raises(RuntimeError, match="written-to"):
+        ops.hp_rms_norm_mx(xbuf[:512].view(4, 128), u8(4, 8), x_shared, w, r, 1e-6, ops.MXFP4)
+    with pytest.raises(RuntimeError, match="written-to"):
+        ops.hp_rms_norm_mx(u8(4, 128), xbuf[:32].view(4, 8), x_shared, w, r, 1e-6, ops.MXFP4)

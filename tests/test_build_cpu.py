@@ -24,5 +24,6 @@ def test_build_from_a_clean_tree(tmp_path):
                        capture_output=True, text=True, timeout=1200)
     assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-3000:]
     assert "build: ok" in p.stdout
-    for lib in ("hp_rms_norm_amd/libhprms.so", "hp_rms_norm_amd/libhprms_torch.so", "oracle/libhprms_oracle.so"):
+    for lib in ("hp_rms_norm_amd/libhprms.so", "hp_rms_norm_amd/_C.so", "hp_rms_norm_amd/libhprms_bench.so",
+                "oracle/libhprms_oracle.so"):
         assert (tmp_path / lib).exists(), lib
