@@ -888,7 +888,7 @@ def run_extra(torch, ops, args):
     out["same_buffers_every_call"] = hot
     # the op beside kernels that move its bytes without its arithmetic (bench library)
     from hp_rms_norm_amd import abi
-    out["ceiling_bf16"] = ceiling(torch, abi, ops, [4096, 8192, 16384, 32768], steps, args.warmup, trials=3)
+    out["ceiling_bf16"] = ceiling(torch, abi, ops, [4096, 8192, 12288, 16384, 32768], steps, args.warmup, trials=3)
     return out
 
 

@@ -56,9 +56,12 @@ const FusedEntry kFused[] = {
     HPRMS_TUNING_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_CANDIDATE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_TIMELINE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_SHARED_UNPACK_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
 #endif
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
+    HPRMS_INPLACE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_INPLACE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
     HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
     HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
     HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
@@ -206,6 +209,16 @@ bool plain_config(int64_t nvec, hprms_config* c) {
   return false;
 }
 
+// The in-place op (mode 0) takes one row per 256-lane workgroup at 3K < H <=
+// 4K: 256 lanes x 2 vectors, 0.9-1.8% faster than 128 x 4 with two rows per
+// workgroup (interleaved cold trials at 4096 rows, five runs, H = 3584 and
+// 4096).  The out-of-place and partial-sum forms keep the shared row.
+bool inplace_config(int64_t nvec, hprms_config* c) {
+  if (nvec <= 384 || nvec > 512) return false;
+  *c = hprms_config{1, 256, 2, 0, 256, 0, 131};
+  return true;
+}
+
 // The partial-sum form reads P + 1 rows per output row; at 4K < H <= 8K it
 // measured 1.3-5.8% faster with 256 lanes x 4 than with the fused table's
 // 512 x 2 (which the fused and out-of-place forms prefer by 0.2-2.1%).
@@ -218,6 +231,7 @@ bool reduce_config(int64_t nvec, hprms_config* c) {
 void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   const int64_t nvec = hidden / 8;
   if (latency_config(rows, nvec, mode, c)) return;
+  if (mode == 0 && inplace_config(nvec, c)) return;
   if (mode == 1 && plain_config(nvec, c)) return;
   if (mode == 4 && reduce_config(nvec, c)) return;
   if (mode == 2 && fp8_config(nvec, c)) return;
@@ -225,6 +239,7 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   // flags: 3 = non-temporal row loads and stores, +4 = weight loaded late,
   // +24 = sc1 on loads and stores, +128 = residual loads before input loads
+  // (9K-12K: 0.4-0.6% faster with them, interleaved cold trials)
   struct Row { int64_t max_nvec; int lpr, vpl, ldsv, block, flags; };
   static const Row table[] = {
       {16, 16, 1, 0, 256, 3},        // H <= 128:   16 rows per workgroup
@@ -235,7 +250,7 @@ void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
       {384, 128, 3, 0, 256, 7},      // H <= 3072:  two waves per row
       {512, 128, 4, 0, 256, 131},    // H <= 4096
       {1024, 512, 2, 0, 512, 7},     // H <= 8192:  one row per 8-wave workgroup
-      {1536, 512, 3, 0, 512, 31},    // H <= 12288
+      {1536, 512, 3, 0, 512, 159},   // H <= 12288
       {2047, 1024, 2, 0, 1024, 31},  // H <= 16376
       {2048, 256, 8, 4, 256, 27},    // H = 16384: LDS tier, half the row in LDS
       {3072, 1024, 3, 0, 1024, 159}, // H <= 24576

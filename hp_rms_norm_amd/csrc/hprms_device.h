@@ -51,9 +51,8 @@ template <int DT>
 struct Fmt;
 
 // olo / ohi: the same unpacks as lo / hi, through a byte permute
-// (v_perm_b32).  The output phase of the kernels unpacks the row it holds with
-// them: sharing the square phase's unpacks, the compiler would keep two floats
-// per held 32-bit word live across the row reduction instead of the word.
+// (v_perm_b32), which the compiler does not merge with lo / hi (the bench
+// library's variant of the output phase, fused_vec_kernel FLAGS bit 12).
 template <>
 struct Fmt<HPRMS_DTYPE_BF16> {
   __device__ static __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }

@@ -134,6 +134,14 @@ void fused_vec_kernel(FusedArgs a) {
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
+  // The output phase's unpack of the held row.  With the square phase's lo /
+  // hi the compiler merges the two and keeps the row's unpacked floats live
+  // across the reduction (more VGPRs); FLAGS bit 12 (bench library) unpacks
+  // through a byte permute instead (Fmt::olo / ohi), which keeps packed words
+  // and lowers VGPRs and raises occupancy, but measured 0-3% slower (2.5-3.2%
+  // at 28K-32K, 2.9% at 16K): more rows in flight per CU do not stream faster.
+  auto olo = [](uint32_t w) { if constexpr ((FLAGS & 4096) != 0) return F::olo(w); else return F::lo(w); };
+  auto ohi = [](uint32_t w) { if constexpr ((FLAGS & 4096) != 0) return F::ohi(w); else return F::hi(w); };
 
   __shared__ float red[2][WPR > 1 ? NW : 1];
   __shared__ u32x4 spill[LDSV > 0 ? LDSV * BLOCK : 1];
@@ -420,7 +428,7 @@ void fused_vec_kernel(FusedArgs a) {
         uint32_t m2 = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          y[j] = F::pack((F::olo(s[j]) * inv) * F::lo(wv[k][j]), (F::ohi(s[j]) * inv) * F::hi(wv[k][j]));
+          y[j] = F::pack((olo(s[j]) * inv) * F::lo(wv[k][j]), (ohi(s[j]) * inv) * F::hi(wv[k][j]));
           const uint32_t mag = y[j] & 0x7fff7fffu;
           m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(mag & 0xffffu, mag >> 16));
         }
@@ -461,7 +469,7 @@ void fused_vec_kernel(FusedArgs a) {
         u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          o[j] = F::pack((F::olo(s[j]) * inv) * F::lo(wv[k][j]), (F::ohi(s[j]) * inv) * F::hi(wv[k][j]));
+          o[j] = F::pack((olo(s[j]) * inv) * F::lo(wv[k][j]), (ohi(s[j]) * inv) * F::hi(wv[k][j]));
         const bool ok = row_ok && vec_ok[k];
         store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
       }
@@ -469,7 +477,7 @@ void fused_vec_kernel(FusedArgs a) {
         u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          o[j] = F::pack((F::olo(tsv[j]) * inv) * F::lo(twv[j]), (F::ohi(tsv[j]) * inv) * F::hi(twv[j]));
+          o[j] = F::pack((olo(tsv[j]) * inv) * F::lo(twv[j]), (ohi(tsv[j]) * inv) * F::hi(twv[j]));
         store16<SAUX>(o, ors, eooff);
       }
     } else {
@@ -481,7 +489,7 @@ void fused_vec_kernel(FusedArgs a) {
         const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          xv[k][j] = F::pack((F::olo(s[j]) * inv) * F::lo(wv[k][j]), (F::ohi(s[j]) * inv) * F::hi(wv[k][j]));
+          xv[k][j] = F::pack((olo(s[j]) * inv) * F::lo(wv[k][j]), (ohi(s[j]) * inv) * F::hi(wv[k][j]));
         if (row_ok && vec_ok[k]) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -496,7 +504,7 @@ void fused_vec_kernel(FusedArgs a) {
         // counted: harmless for a maximum
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          txv[j] = F::pack((F::olo(tsv[j]) * inv) * F::lo(twv[j]), (F::ohi(tsv[j]) * inv) * F::hi(twv[j]));
+          txv[j] = F::pack((olo(tsv[j]) * inv) * F::lo(twv[j]), (ohi(tsv[j]) * inv) * F::hi(twv[j]));
         if (eok) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {

@@ -21,7 +21,8 @@ struct FusedEntry {
 // rows that are not 128-byte aligned (any 2-byte boundary), bit 6 = with the
 // tail vector for hidden % 8 != 0 (with bit 5), bit 7 = residual loads first,
 // bit 8 = held to 8 waves per SIMD, bit 9 = timeline instrumentation (bench
-// library only), bit 11 = one workgroup per CU (the launch reserves LDS)
+// library only), bit 11 = one workgroup per CU (the launch reserves LDS),
+// bit 12 = the output phase's separate unpack (bench library)
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
@@ -45,12 +46,15 @@ struct FusedEntry {
 #define HPRMS_TABLE_SHAPES(X, DT, MODE)                                                        \
   X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
   X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) \
-  X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 31) \
+  X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 159) \
   X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27)                            \
   X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 4, 0, 1024, 159)                         \
   X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
   X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)    \
   X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7) X(DT, MODE, 256, 3, 0, 256, 7)
+
+// entries of the in-place op's own rows (mode 0) that the shared table does not use
+#define HPRMS_INPLACE_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
 
 // entries of the plain-RMSNorm table that the fused table does not use
 #define HPRMS_PLAIN_SHAPES(X, DT, MODE)                                                        \
@@ -94,12 +98,19 @@ struct FusedEntry {
   X(DT, MODE, 1024, 2, 0, 1024, 2079) X(DT, MODE, 1024, 3, 0, 1024, 2207) X(DT, MODE, 1024, 4, 0, 1024, 2207) \
   X(DT, MODE, 256, 8, 4, 256, 155) X(DT, MODE, 256, 12, 0, 256, 159) X(DT, MODE, 512, 6, 0, 512, 159)
 
+// the bandwidth table's rows with the output phase's separate unpack (+4096)
+#define HPRMS_SHARED_UNPACK_SHAPES(X, DT, MODE)                                                        \
+  X(DT, MODE, 32, 4, 0, 256, 4227) X(DT, MODE, 64, 4, 0, 256, 4231) X(DT, MODE, 128, 3, 0, 256, 4103)   \
+  X(DT, MODE, 128, 4, 0, 256, 4227) X(DT, MODE, 512, 2, 0, 512, 4103) X(DT, MODE, 512, 3, 0, 512, 4127) \
+  X(DT, MODE, 1024, 2, 0, 1024, 4127) X(DT, MODE, 256, 8, 4, 256, 4123) X(DT, MODE, 1024, 3, 0, 1024, 4255) \
+  X(DT, MODE, 1024, 4, 0, 1024, 4255) X(DT, MODE, 256, 2, 0, 256, 4251) X(DT, MODE, 256, 8, 4, 256, 4251)
+
 // the bandwidth table's rows with the timeline instrumentation (+512)
 #define HPRMS_TIMELINE_SHAPES(X, DT, MODE)                                                        \
   X(DT, MODE, 32, 4, 0, 256, 643) X(DT, MODE, 64, 4, 0, 256, 647) X(DT, MODE, 128, 3, 0, 256, 519) \
-  X(DT, MODE, 128, 4, 0, 256, 643) X(DT, MODE, 512, 2, 0, 512, 519) X(DT, MODE, 512, 3, 0, 512, 543) \
+  X(DT, MODE, 256, 2, 0, 256, 643) X(DT, MODE, 512, 2, 0, 512, 519) X(DT, MODE, 512, 3, 0, 512, 671) \
   X(DT, MODE, 1024, 2, 0, 1024, 543) X(DT, MODE, 256, 8, 4, 256, 539) X(DT, MODE, 1024, 3, 0, 1024, 671) \
-  X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 903) X(DT, MODE, 256, 2, 0, 256, 519)
+  X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 643)
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every

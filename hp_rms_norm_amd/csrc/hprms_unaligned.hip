@@ -33,6 +33,8 @@ const FusedEntry kFusedUnaligned[] = {
     HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 6)
     // the rows only the plain-RMSNorm and FP8-output tables use (some plain
     // rows map onto a fused-table variant: the lookup takes the first match)
+    HPRMS_INPLACE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_INPLACE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 0)
     HPRMS_PLAIN_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 1)
     HPRMS_PLAIN_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 1)
     HPRMS_FP8_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 2)
