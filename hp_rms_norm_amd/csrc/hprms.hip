@@ -48,9 +48,13 @@ bool rows_aligned128(const void* base, int64_t stride_bytes) {
 // bench library (HPRMS_BENCH_BUILD) adds the shapes only the tuning sweeps
 // and the ceiling measurements use.
 const FusedEntry kFused[] = {
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
+    HPRMS_ALL_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_MX_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_MX_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16)
 #ifdef HPRMS_BENCH_BUILD
+    HPRMS_OTHER_MODE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_OTHER_MODE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
     HPRMS_ALT_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_ALT_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
     HPRMS_TUNING_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
@@ -58,24 +62,6 @@ const FusedEntry kFused[] = {
     HPRMS_TIMELINE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_SHARED_UNPACK_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
 #endif
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
-    HPRMS_INPLACE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_INPLACE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
-    HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_PLAIN_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 1)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 2)
-    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 2)
-    HPRMS_FP8_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 2)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 3)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 3)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 4)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 4)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 5)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 5)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 6)
-    HPRMS_TABLE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 6)
 };
 
 bool entry_is(const FusedEntry& e, int dtype, int mode, const hprms_config& c) {

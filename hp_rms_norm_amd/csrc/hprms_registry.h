@@ -42,27 +42,54 @@ struct FusedEntry {
 // nt on the row loads and stores, 7 = the same with the weight loaded late,
 // 27 / 31 = nt plus sc1 on loads and stores (without / with the late weight);
 // +128 = the residual's loads issued before the input's.
-// The table's entries (bandwidth rows, then the latency rows for few rows):
-#define HPRMS_TABLE_SHAPES(X, DT, MODE)                                                        \
-  X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)    \
-  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) \
-  X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 512, 3, 0, 512, 159) \
-  X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27)                            \
-  X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 4, 0, 1024, 159)                         \
-  X(DT, MODE, 1024, 8, 4, 1024, 31)                                                            \
-  X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)    \
-  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7) X(DT, MODE, 256, 3, 0, 256, 7)
+//
+// Per mode, exactly the shapes its dispatch table (hprms.hip) can choose:
+// the rows every mode shares, then each mode's own.  A CPU test enumerates the
+// tables and checks that these lists hold every reachable shape and no other.
+#define HPRMS_COMMON_SHAPES(X, DT, MODE)                                                         \
+  X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)      \
+  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 3, 0, 1024, 159) \
+  X(DT, MODE, 1024, 8, 4, 1024, 31)                                                              \
+  X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)      \
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
 
-// entries of the in-place op's own rows (mode 0) that the shared table does not use
-#define HPRMS_INPLACE_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
+// the fused op in place (mode 0) and its out-of-place (3) and partial-sum (4) forms
+#define HPRMS_FUSED_SHAPES(X, DT, MODE)                                                          \
+  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                               \
+  X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
+  X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 4, 0, 1024, 159)
+#define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
+#define HPRMS_MODE3_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
+#define HPRMS_MODE4_SHAPES(X, DT, MODE) \
+  HPRMS_MODE3_SHAPES(X, DT, MODE) X(DT, MODE, 256, 4, 0, 256, 3)
 
-// entries of the plain-RMSNorm table that the fused table does not use
-#define HPRMS_PLAIN_SHAPES(X, DT, MODE)                                                        \
-  X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31) \
-  X(DT, MODE, 512, 8, 0, 512, 7)
+// plain RMSNorm (mode 1)
+#define HPRMS_MODE1_SHAPES(X, DT, MODE)                                                           \
+  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                                \
+  X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 256, 3, 0, 256, 7)      \
+  X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31) X(DT, MODE, 512, 8, 0, 512, 7)
 
-// entries of the FP8-output table that the other tables do not use
-#define HPRMS_FP8_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 159)
+// the FP8 output (mode 2) and the OCP MX outputs (modes 5 and 6)
+#define HPRMS_QUANT_SHAPES(X, DT, MODE)                                                           \
+  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                                \
+  X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 256, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31)
+#define HPRMS_MODE2_SHAPES(X, DT, MODE) HPRMS_QUANT_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 159)
+#define HPRMS_MX_SHAPES(X, DT, MODE) HPRMS_QUANT_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 4, 0, 1024, 159)
+
+// Every mode's lists for one registry variant (ENTRY: HPRMS_FUSED_ENTRY and the
+// unaligned and tail entries below; the tail variant has no MX form).
+#define HPRMS_ALL_MODES(ENTRY, DT)                                                                \
+  HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2) \
+  HPRMS_MODE3_SHAPES(ENTRY, DT, 3) HPRMS_MODE4_SHAPES(ENTRY, DT, 4)
+#define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
+
+// Bench library: the shapes the other modes choose, as in-place (mode 0)
+// kernels, so a test can run the 16-bit op with another form's lane mapping
+// (and so the same fp32 reduction order) as that form's bit-level reference.
+#define HPRMS_OTHER_MODE_SHAPES(X, DT, MODE)                                                      \
+  X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 256, 3, 0, 256, 7)  \
+  X(DT, MODE, 512, 8, 4, 512, 159) X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 31)  \
+  X(DT, MODE, 512, 4, 0, 512, 31) X(DT, MODE, 512, 8, 0, 512, 7)
 
 // The shapes below are built only into the bench library libhprms_bench.so
 // (hprms.hip compiled with HPRMS_BENCH_BUILD), never into libhprms.so: no
@@ -70,8 +97,7 @@ struct FusedEntry {
 //
 // Alternatives of the fused op that the tuning sweeps compare against (five
 // of the table's shapes with the two streams' loads alternating, the two
-// smallest latency rows with the weight loaded late, and the FP8 table's 32K
-// row, so that the 16-bit op runs with each FP8 row's lane mapping).
+// smallest latency rows with the weight loaded late, and other lane shapes).
 #define HPRMS_ALT_SHAPES(X, DT, MODE)                                                          \
   X(DT, MODE, 64, 2, 0, 256, 3) X(DT, MODE, 256, 8, 0, 256, 27)                               \
   X(DT, MODE, 512, 8, 4, 512, 31) X(DT, MODE, 1024, 8, 0, 1024, 31)                           \

@@ -10,22 +10,8 @@
 namespace hprms {
 
 const FusedEntry kFusedTail[] = {
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 0)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 1)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 2)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 2)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 3)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 3)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 4)
-    HPRMS_TABLE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 4)
-    HPRMS_INPLACE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_INPLACE_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 0)
-    HPRMS_PLAIN_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_PLAIN_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 1)
-    HPRMS_FP8_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16, 2)
-    HPRMS_FP8_SHAPES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16, 2)
+    HPRMS_ALL_MODES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16)
 };
 
 const int kFusedTailCount = (int)(sizeof(kFusedTail) / sizeof(kFusedTail[0]));

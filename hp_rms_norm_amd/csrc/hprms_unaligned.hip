@@ -16,29 +16,10 @@
 namespace hprms {
 
 const FusedEntry kFusedUnaligned[] = {
-    // modes 0-6: the bandwidth and latency rows of the fused table
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 0)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 1)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 2)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 2)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 3)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 3)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 4)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 4)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 5)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 5)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 6)
-    HPRMS_TABLE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 6)
-    // the rows only the plain-RMSNorm and FP8-output tables use (some plain
-    // rows map onto a fused-table variant: the lookup takes the first match)
-    HPRMS_INPLACE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 0)
-    HPRMS_INPLACE_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 0)
-    HPRMS_PLAIN_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 1)
-    HPRMS_PLAIN_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 1)
-    HPRMS_FP8_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16, 2)
-    HPRMS_FP8_SHAPES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16, 2)
+    HPRMS_ALL_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_MX_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_MX_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16)
 };
 
 const int kFusedUnalignedCount = (int)(sizeof(kFusedUnaligned) / sizeof(kFusedUnaligned[0]));

@@ -355,3 +355,31 @@ def test_bench_entry_points_reject_bad_arguments():
                                                           abi.DTYPE_BF16, 1e-6, ctypes.byref(c),
                                                           None) == abi.HPRMS_E_INVALID
     assert "timeline" in abi.BENCH.last_error()
+
+
+def _reachable(dtype, mode):
+    """Every vector-tier kernel the dispatch tables can launch for (dtype,
+    mode): the table's choice at each width and at both sides of each latency
+    row's row-count limit, in its aligned, unaligned and (modes 0-4) tail
+    variants."""
+    out = set()
+    for rows in (1, 256, 257, 384, 385, 768, 769, 1024, 1025, 4096):
+        for nvec in range(1, 8193):
+            c = abi.select_config(rows, nvec * 8, dtype, mode)
+            if c.tier == 3:
+                continue
+            shape = (c.tier, c.lanes_per_row, c.vec_per_lane, c.lds_vec_per_lane, c.block_threads, 0)
+            out.add(shape + (c.flags,))
+            out.add(shape + ((c.flags & ~24) | 32,))
+            if mode <= 4:
+                out.add(shape + ((c.flags & ~24) | 96,))
+    return out
+
+
+def test_product_library_holds_exactly_the_reachable_kernels():
+    """libhprms.so instantiates the kernels its tables can choose and no
+    other (the tuning shapes live in the bench library)."""
+    for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+        for mode in range(7):
+            built = {c.as_tuple() for c in abi.kernel_configs(dtype, mode)}
+            assert built == _reachable(dtype, mode), (dtype, mode, sorted(built ^ _reachable(dtype, mode)))

@@ -56,8 +56,8 @@ def run_case(ops, rows, hidden, dtype, elem, seed, dist="bench", eps=1e-6, w=Non
     q, sc = fn(xd, rd, wd, eps)
     cfg = abi.select_config(rows, hidden, DT[dtype], 5 if elem == oracle.MXFP8 else 6)
     y, r16 = x.to(DEV), r.to(DEV)
-    abi.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype], eps,
-                          torch.cuda.current_stream().cuda_stream, cfg)
+    abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
+                                eps, torch.cuda.current_stream().cuda_stream, cfg)
     torch.cuda.synchronize()
     tag = f"{rows}x{hidden} {dtype} elem {elem} seed {seed} cfg {cfg.as_tuple()}"
     assert torch.equal(xd.cpu().view(torch.int16), x.view(torch.int16)), "input modified " + tag
@@ -161,8 +161,8 @@ def test_mx_dequantises_close_to_the_16_bit_output(ops):
     # y from the 16-bit op with the MX kernel's lane mapping (the same reduction order)
     cfg = abi.select_config(rows, hidden, abi.DTYPE_BF16, abi.MODE_MXFP4)
     y, r16 = x.clone(), r.clone()
-    abi.fused_add_rmsnorm(y.data_ptr(), w.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, abi.DTYPE_BF16,
-                          1e-6, torch.cuda.current_stream().cuda_stream, cfg)
+    abi.BENCH.fused_add_rmsnorm(y.data_ptr(), w.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, abi.DTYPE_BF16,
+                                1e-6, torch.cuda.current_stream().cuda_stream, cfg)
     q, sc = ops.fused_add_rms_norm_mxfp4(x, r, w, 1e-6)
     torch.cuda.synchronize()
     assert torch.equal(r.view(torch.int16), r16.view(torch.int16))

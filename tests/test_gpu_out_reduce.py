@@ -40,10 +40,11 @@ def _stride(t):
 
 
 def in_place(abi, x, r, w, eps, config):
-    """The in-place op forced to `config` (through the C ABI)."""
+    """The in-place op forced to `config` (through the C ABI of the bench
+    library, which also holds the other forms' shapes as in-place kernels)."""
     xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
-    abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), xd.shape[0], xd.shape[1], _stride(xd),
-                          _stride(rd), DT[xd.dtype], eps, _stream(), config)
+    abi.BENCH.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), xd.shape[0], xd.shape[1], _stride(xd),
+                                _stride(rd), DT[xd.dtype], eps, _stream(), config)
     torch.cuda.synchronize()
     return bits(xd), bits(rd)
 
@@ -162,8 +163,8 @@ def test_reduce_every_table_row(abi, dtype, nparts):
                 # the in-place op with the reduce form's shape (the same fp32 summation order)
                 cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_REDUCE)
                 xd, rd2 = parts[0].to(DEV), r.to(DEV)
-                abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd2.data_ptr(), rows, hidden, hidden, hidden,
-                                      DT[dtype], 1e-6, _stream(), cfg)
+                abi.BENCH.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd2.data_ptr(), rows, hidden, hidden, hidden,
+                                            DT[dtype], 1e-6, _stream(), cfg)
                 torch.cuda.synchronize()
                 assert np.array_equal(bits(od), bits(xd)), "P=1 differs from the in-place op " + tag
                 assert np.array_equal(bits(rd), bits(rd2)), "P=1 residual differs from the in-place op " + tag
@@ -216,8 +217,8 @@ def test_reduce_full_size_identities(abi):
     want_x, want_r = x.clone(), r.clone()
     # the in-place op with the reduce form's shape (the same fp32 summation order)
     cfg = abi.select_config(rows, hidden, abi.DTYPE_BF16, abi.MODE_REDUCE)
-    abi.fused_add_rmsnorm(want_x.data_ptr(), w.data_ptr(), want_r.data_ptr(), rows, hidden, hidden, hidden,
-                          abi.DTYPE_BF16, 1e-6, _stream(), cfg)
+    abi.BENCH.fused_add_rmsnorm(want_x.data_ptr(), w.data_ptr(), want_r.data_ptr(), rows, hidden, hidden, hidden,
+                                abi.DTYPE_BF16, 1e-6, _stream(), cfg)
     zeros = torch.zeros_like(x)
     for parts in ([x, zeros, zeros, zeros], [x * 0.5, x * 0.5]):
         rd = r.clone()

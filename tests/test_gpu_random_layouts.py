@@ -197,8 +197,8 @@ def test_random_layouts_mx(abi, case):
         # the 16-bit output of the same shape (in place, contiguous copies)
         cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_MXFP8 if fmt == abi.MX_FP8_E4M3 else abi.MODE_MXFP4)
         y, r16, wd = x.to(DEV), r.to(DEV), w.to(DEV)
-        abi.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype], EPS,
-                              _stream(), cfg)
+        abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
+                                    EPS, _stream(), cfg)
         torch.cuda.synchronize()
         assert np.array_equal(bits(rv), bits(r16)), "mx residual " + t
         wq, wsc = oracle.mx_quantize(bits(y).reshape(rows, hidden), DT[dtype], elem)
