@@ -543,6 +543,10 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
       read      the op's two read streams only (2*B*H*2 bytes)
       write     the op's two write streams only (2*B*H*2 bytes)
       empty     the table row's grid of empty workgroups
+      inplace_1stream / inplace_2stream / copy_2stream
+                the op's bytes as flat 4 KiB-per-workgroup streams: one tensor
+                rewritten in place, x and r rewritten in place, x and r
+                copied to two other tensors
     and one timeline launch of the table's kernel (per-workgroup start/end)."""
     import numpy as np
     bench = abi.BENCH
@@ -575,13 +579,22 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
             "write": lambda i: chk(BL.hprms_ceil_write(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nb, stream),
                                    "write"),
             "empty": lambda i: chk(BL.hprms_ceil_empty(grid, cfg.block_threads, stream), "empty"),
+            "inplace_1stream": lambda i: chk(BL.hprms_ceil_streams(0, bufs[i].data_ptr(), None, None, None, nb,
+                                                                   stream), "inplace_1stream"),
+            "inplace_2stream": lambda i: chk(BL.hprms_ceil_streams(1, bufs[i][0].data_ptr(), bufs[i][1].data_ptr(),
+                                                                   None, None, nb, stream), "inplace_2stream"),
+            "copy_2stream": lambda i: chk(BL.hprms_ceil_streams(2, bufs[i][0].data_ptr(), bufs[i][1].data_ptr(),
+                                                                bufs[(i + 1) % n][0].data_ptr(),
+                                                                bufs[(i + 1) % n][1].data_ptr(), nb, stream),
+                                          "copy_2stream"),
         }
         samples = {k: [] for k in kinds}
         for t in range(trials):
             for k, fn in (kinds.items() if t % 2 == 0 else reversed(list(kinds.items()))):
                 samples[k].append(time_rotating(torch, fn, n, steps, warmup))
         us = {k: statistics.median(v) for k, v in samples.items()}
-        nbytes = {"fused": fused_bytes(B, h), "skeleton": 4 * nb, "copy": 4 * nb, "read": 2 * nb, "write": 2 * nb}
+        nbytes = {"fused": fused_bytes(B, h), "skeleton": 4 * nb, "copy": 4 * nb, "read": 2 * nb, "write": 2 * nb,
+                  "inplace_1stream": 4 * nb, "inplace_2stream": 4 * nb, "copy_2stream": 4 * nb}
         row = {"hidden": h, "rows": B,
                "kernel": {"lanes_per_row": cfg.lanes_per_row, "vec_per_lane": cfg.vec_per_lane,
                           "lds_vec_per_lane": cfg.lds_vec_per_lane, "block": cfg.block_threads,

@@ -9,6 +9,7 @@
 //   hprms_ceil_read      read two tensors of n bytes (the op's two read streams)
 //   hprms_ceil_write     write two tensors of n bytes (the op's two write streams)
 //   hprms_ceil_copy      copy n bytes (one read and one write stream)
+//   hprms_ceil_streams   the op's bytes as flat in-place or copying streams
 //   hprms_ceil_skeleton  the op's own data movement in place on [rows, hidden]
 //                        x and r with the lane mapping of a table row: every
 //                        load first, r <- x + r stored as soon as it is formed,
@@ -58,6 +59,25 @@ __global__ __launch_bounds__(kFlatBlock) void ceil_copy_kernel(u32x4* dst, const
   const int64_t i = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
   if (i >= nvec) return;
   __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+// The op's bytes as flat streams of 4 KiB workgroups, to tell the number of
+// streams from updating in place: kind 0 rewrites a in place (one stream, read
+// then written), kind 1 rewrites a and b in place (two streams), kind 2 copies
+// a and b to c and d (two read and two write streams).
+template <int KIND>
+__global__ __launch_bounds__(kFlatBlock) void ceil_streams_kernel(u32x4* a, u32x4* b, u32x4* c, u32x4* d,
+                                                                  int64_t nvec) {
+  const int64_t i = (int64_t)blockIdx.x * kFlatBlock + threadIdx.x;
+  if (i >= nvec) return;
+  const u32x4 u = __builtin_nontemporal_load(a + i);
+  if constexpr (KIND == 0) {
+    __builtin_nontemporal_store(u + 1u, a + i);
+  } else {
+    const u32x4 v = __builtin_nontemporal_load(b + i);
+    __builtin_nontemporal_store(u + v, KIND == 1 ? a + i : c + i);
+    __builtin_nontemporal_store(u ^ v, KIND == 1 ? b + i : d + i);
+  }
 }
 
 struct SkelArgs {
@@ -215,6 +235,24 @@ int hprms_ceil_copy(void* dst, const void* src, int64_t nbytes, hipStream_t stre
   const int64_t nvec = nbytes / 16;
   ceil_copy_kernel<<<dim3((unsigned)flat_grid(nvec)), dim3(kFlatBlock), 0, stream>>>((u32x4*)dst,
                                                                                    (const u32x4*)src, nvec);
+  return launched();
+}
+
+// kind 0: a (2 * nbytes) rewritten in place; kind 1: a and b (nbytes each)
+// rewritten in place; kind 2: a and b copied to c and d (nbytes each).
+int hprms_ceil_streams(int kind, void* a, void* b, void* c, void* d, int64_t nbytes, hipStream_t stream) {
+  if (kind < 0 || kind > 2 || !flat_ok(a, kind == 0 ? 2 * nbytes : nbytes)) return HPRMS_E_INVALID;
+  if (kind >= 1 && !flat_ok(b, nbytes)) return HPRMS_E_INVALID;
+  if (kind == 2 && (!flat_ok(c, nbytes) || !flat_ok(d, nbytes))) return HPRMS_E_INVALID;
+  const int64_t nvec = (kind == 0 ? 2 * nbytes : nbytes) / 16;
+  const dim3 g((unsigned)flat_grid(nvec));
+  u32x4 *pa = (u32x4*)a, *pb = (u32x4*)b, *pc = (u32x4*)c, *pd = (u32x4*)d;
+  if (kind == 0)
+    ceil_streams_kernel<0><<<g, dim3(kFlatBlock), 0, stream>>>(pa, pb, pc, pd, nvec);
+  else if (kind == 1)
+    ceil_streams_kernel<1><<<g, dim3(kFlatBlock), 0, stream>>>(pa, pb, pc, pd, nvec);
+  else
+    ceil_streams_kernel<2><<<g, dim3(kFlatBlock), 0, stream>>>(pa, pb, pc, pd, nvec);
   return launched();
 }
 

@@ -120,3 +120,29 @@ def test_skeleton_moves_the_ops_bytes(abi, shape):
     assert np.array_equal(r.cpu().numpy().view(np.uint32), s)
     assert np.array_equal(x.cpu().numpy().view(np.uint32), x0 ^ (s + t[:, None]))
 
+
+
+def test_stream_pattern_kernels(abi):
+    """hprms_ceil_streams: kind 0 adds 1 to every 32-bit word of a in place;
+    kind 1 stores a + b to a and a ^ b to b; kind 2 stores them to c and d."""
+    L = abi.BENCH.lib()
+    s = _stream()
+    n = 1 << 20
+    g = torch.Generator(device=DEV).manual_seed(3)
+    a = torch.randint(0, 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device=DEV, generator=g)
+    b = torch.randint(0, 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device=DEV, generator=g)
+    a0, b0 = a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32)
+    c, d = torch.zeros_like(a), torch.zeros_like(a)
+    assert L.hprms_ceil_streams(2, a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), n, s) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy().view(np.uint32), a0 + b0)
+    assert np.array_equal(d.cpu().numpy().view(np.uint32), a0 ^ b0)
+    assert L.hprms_ceil_streams(1, a.data_ptr(), b.data_ptr(), None, None, n, s) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy().view(np.uint32), a0 + b0)
+    assert np.array_equal(b.cpu().numpy().view(np.uint32), a0 ^ b0)
+    ab = torch.cat([a, b])
+    ab0 = ab.cpu().numpy().view(np.uint32).copy()
+    assert L.hprms_ceil_streams(0, ab.data_ptr(), None, None, None, n, s) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(ab.cpu().numpy().view(np.uint32), ab0 + 1)
