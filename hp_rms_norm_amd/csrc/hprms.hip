@@ -195,10 +195,14 @@ bool plain_config(int64_t nvec, hprms_config* c) {
   return false;
 }
 
-// The in-place op (mode 0) takes one row per 256-lane workgroup at 3K < H <=
-// 4K: 256 lanes x 2 vectors, 0.9-1.8% faster than 128 x 4 with two rows per
-// workgroup (interleaved cold trials at 4096 rows, five runs, H = 3584 and
-// 4096).  The out-of-place and partial-sum forms keep the shared row.
+// The in-place op (mode 0) on rows on the 128-byte grid takes one row per
+// 256-lane workgroup at 3K < H <= 4K: 256 lanes x 2 vectors, 0.9-1.8% faster
+// than 128 x 4 with two rows per workgroup (interleaved cold trials at 4096
+// rows, five runs, H = 3584 and 4096).  Rows off the grid keep 128 x 4: with
+// one row per workgroup every cache line two neighbouring rows share is
+// written by two workgroups, and its variants measured 13-18% slower (4096
+// rows at H = 4097, and at H = 4096 with rows 2 bytes off).  The out-of-place
+// and partial-sum forms keep the shared row.
 bool inplace_config(int64_t nvec, hprms_config* c) {
   if (nvec <= 384 || nvec > 512) return false;
   *c = hprms_config{1, 256, 2, 0, 256, 0, 131};
@@ -214,10 +218,12 @@ bool reduce_config(int64_t nvec, hprms_config* c) {
   return true;
 }
 
-void table_config(int64_t rows, int64_t hidden, int mode, hprms_config* c) {
+// `grid`: every row of every stream starts on the 128-byte grid (only the
+// in-place op's rows depend on it).
+void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_config* c) {
   const int64_t nvec = hidden / 8;
   if (latency_config(rows, nvec, mode, c)) return;
-  if (mode == 0 && inplace_config(nvec, c)) return;
+  if (mode == 0 && grid && inplace_config(nvec, c)) return;
   if (mode == 1 && plain_config(nvec, c)) return;
   if (mode == 4 && reduce_config(nvec, c)) return;
   if (mode == 2 && fp8_config(nvec, c)) return;
@@ -531,8 +537,9 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   if (forced && forced->tier != 0) {
     c = *forced;
   } else {
-    table_config(p.rows, p.hidden, p.mode, &c);
-    if (c.tier != 3 && (needs_unaligned(p) || ((c.flags & 24) && skip_sc1(p)))) c.flags = unaligned_flags(p, c.flags);
+    const bool off_grid = needs_unaligned(p);
+    table_config(p.rows, p.hidden, p.mode, !off_grid, &c);
+    if (c.tier != 3 && (off_grid || ((c.flags & 24) && skip_sc1(p)))) c.flags = unaligned_flags(p, c.flags);
   }
   if ((c.flags & 512) && !p.timeline)
     return fail(HPRMS_E_INVALID, "flags bit 9 (timeline) needs hprms_bench_fused_timeline and its buffer");
@@ -707,7 +714,9 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
   if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
-  table_config(rows, hidden, mode, config);
+  // the choice for rows on the 128-byte grid; odd widths: the tail variant of
+  // the choice for rows off it
+  table_config(rows, hidden, mode, hidden % 8 == 0, config);
   if (hidden % 8 != 0) {
     if (config->tier != 3 && hidden >= 8 && mode <= 4)
       config->flags = HPRMS_TAIL_FLAGS(config->flags);

@@ -59,6 +59,8 @@ struct FusedEntry {
   X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
   X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 4, 0, 1024, 159)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
+// rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
+#define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
 #define HPRMS_MODE3_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
 #define HPRMS_MODE4_SHAPES(X, DT, MODE) \
   HPRMS_MODE3_SHAPES(X, DT, MODE) X(DT, MODE, 256, 4, 0, 256, 3)
@@ -76,11 +78,14 @@ struct FusedEntry {
 #define HPRMS_MODE2_SHAPES(X, DT, MODE) HPRMS_QUANT_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 159)
 #define HPRMS_MX_SHAPES(X, DT, MODE) HPRMS_QUANT_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 4, 0, 1024, 159)
 
-// Every mode's lists for one registry variant (ENTRY: HPRMS_FUSED_ENTRY and the
-// unaligned and tail entries below; the tail variant has no MX form).
-#define HPRMS_ALL_MODES(ENTRY, DT)                                                                \
-  HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2) \
-  HPRMS_MODE3_SHAPES(ENTRY, DT, 3) HPRMS_MODE4_SHAPES(ENTRY, DT, 4)
+// Every mode's lists for one registry: the kernels for rows on the 128-byte
+// grid (ENTRY = HPRMS_FUSED_ENTRY), and for rows off it (the unaligned and
+// tail entries below; the tail variant has no MX form).
+#define HPRMS_MODES_1_TO_4(ENTRY, DT)                                                             \
+  HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2) HPRMS_MODE3_SHAPES(ENTRY, DT, 3) \
+  HPRMS_MODE4_SHAPES(ENTRY, DT, 4)
+#define HPRMS_ALL_MODES(ENTRY, DT) HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
+#define HPRMS_ALL_MODES_OFFGRID(ENTRY, DT) HPRMS_MODE0_OFFGRID_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
 
 // Bench library: the shapes the other modes choose, as in-place (mode 0)

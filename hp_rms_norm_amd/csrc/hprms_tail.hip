@@ -10,8 +10,8 @@
 namespace hprms {
 
 const FusedEntry kFusedTail[] = {
-    HPRMS_ALL_MODES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16)
-    HPRMS_ALL_MODES(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_ALL_MODES_OFFGRID(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES_OFFGRID(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16)
 };
 
 const int kFusedTailCount = (int)(sizeof(kFusedTail) / sizeof(kFusedTail[0]));

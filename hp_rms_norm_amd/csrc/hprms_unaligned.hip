@@ -16,8 +16,8 @@
 namespace hprms {
 
 const FusedEntry kFusedUnaligned[] = {
-    HPRMS_ALL_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16)
-    HPRMS_ALL_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_ALL_MODES_OFFGRID(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES_OFFGRID(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16)
     HPRMS_MX_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_BF16)
     HPRMS_MX_MODES(HPRMS_UNALIGNED_ENTRY, HPRMS_DTYPE_FP16)
 };

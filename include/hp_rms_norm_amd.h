@@ -216,7 +216,9 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * hprms_reduce_add_rmsnorm, 5 / 6: hprms_fused_add_rmsnorm_mx with
  * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1), written to *config (tier 3 when only the
  * general kernel fits hidden; with hidden % 8 != 0 the tail variant).  For
- * rows on the 128-byte grid: rows off it run the same shape with flags
+ * rows on the 128-byte grid: rows off it run the same shape (mode 0 at
+ * 384 < hidden / 8 <= 512 excepted: 128 lanes x 4 vectors, flags 131, where
+ * rows on the grid take 256 x 2) with flags
  * (flags & ~24) | 32, or | 96 (the tail variant) for hidden % 8 != 0 and, in
  * modes 0-4 from hidden 4104 up, for calls none of whose tensors (the weight
  * aside) has its rows on 16-byte boundaries (the kernel then shifts its

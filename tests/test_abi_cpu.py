@@ -132,9 +132,10 @@ def entry_points_find_kernels(L, hidden, dtype, base):
 
 def test_table_covers_every_hidden_with_a_built_kernel():
     """Every hidden size maps either to a built vector-tier kernel that covers
-    it, or (hidden < 8 or > 65543) to the general kernel; every table entry has
-    its unaligned and tail variants built; checked through the entry points
-    with rows = 0 (they validate and look the kernel up, and launch nothing)."""
+    it, or (hidden < 8 or > 65543) to the general kernel; the choice for rows
+    off the 128-byte grid has its unaligned and tail variants built; checked
+    through the entry points with rows = 0 (they validate and look the kernel
+    up, and launch nothing)."""
     L = abi.lib()
     built = {(dt, m): {c.as_tuple() for c in abi.kernel_configs(dt, m)}
              for dt in (abi.DTYPE_BF16, abi.DTYPE_FP16) for m in range(7)}
@@ -154,9 +155,13 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 cm = abi.select_config(rows, hidden, dtype, mode)
                 t = cm.as_tuple()
                 assert t in built[(dtype, mode)], (hidden, mode, t)
-                assert t[:6] + (variant_flags(cm.flags, hidden),) in built[(dtype, mode)], (hidden, mode, t)
-                if mode <= 4 and hidden % 8 == 0:    # a tail variant of the same entry
-                    assert t[:6] + (variant_flags(cm.flags, 9),) in built[(dtype, mode)], (hidden, mode, t)
+                # the choice for rows off the grid (odd widths report it) in its
+                # unaligned and tail variants
+                off = abi.select_config(rows, hidden + (1 if hidden % 8 == 0 and mode <= 4 else 0), dtype,
+                                        mode).as_tuple()
+                assert off[:6] + ((off[6] & ~(24 | 64)) | 32,) in built[(dtype, mode)], (hidden, mode, off)
+                if mode <= 4:
+                    assert off[:6] + (variant_flags(off[6], 9),) in built[(dtype, mode)], (hidden, mode, off)
             if hidden % 8 == 0 and hidden % 32 and hidden > 1024 and hidden not in (4104, 16392, 65528):
                 continue   # the lookups are exercised at every size class below and at the odd sizes
             entry_points_find_kernels(L, hidden, dtype, 0)
@@ -359,9 +364,10 @@ def test_bench_entry_points_reject_bad_arguments():
 
 def _reachable(dtype, mode):
     """Every vector-tier kernel the dispatch tables can launch for (dtype,
-    mode): the table's choice at each width and at both sides of each latency
-    row's row-count limit, in its aligned, unaligned and (modes 0-4) tail
-    variants."""
+    mode): at each width and at both sides of each latency row's row-count
+    limit, the choice for rows on the 128-byte grid (aligned, and unaligned
+    when sc1 is dropped for small calls) and the choice for rows off it
+    (reported for odd widths) in its unaligned and (modes 0-4) tail variants."""
     out = set()
     for rows in (1, 256, 257, 384, 385, 768, 769, 1024, 1025, 4096):
         for nvec in range(1, 8193):
@@ -370,9 +376,15 @@ def _reachable(dtype, mode):
                 continue
             shape = (c.tier, c.lanes_per_row, c.vec_per_lane, c.lds_vec_per_lane, c.block_threads, 0)
             out.add(shape + (c.flags,))
-            out.add(shape + ((c.flags & ~24) | 32,))
+            if c.flags & 24:
+                out.add(shape + ((c.flags & ~24) | 32,))
             if mode <= 4:
-                out.add(shape + ((c.flags & ~24) | 96,))
+                t = abi.select_config(rows, nvec * 8 + 1, dtype, mode)   # off the grid: its tail variant
+                tshape = (t.tier, t.lanes_per_row, t.vec_per_lane, t.lds_vec_per_lane, t.block_threads, 0)
+                out.add(tshape + (t.flags,))
+                out.add(tshape + (t.flags & ~64,))
+            else:
+                out.add(shape + ((c.flags & ~24) | 32,))
     return out
 
 
