@@ -31,6 +31,8 @@ extra      = BASELINE.json's other configs (decode, fp16, streamer) and the othe
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
        python bench.py --sweep STEP [--sweep-max H]   (per-H table sweep, one JSON line per H)
+       python bench.py --ab 'H:lpr,vpl,ldsv,block,flags;...' ... [--hot]
+                      (forced bench-library configurations against the table's, one JSON line each)
 """
 import argparse
 import ctypes
@@ -309,6 +311,14 @@ def main():
                          "kernels of the bench library at (4096, H), one JSON line")
     ap.add_argument("--timeline-dump", default="", metavar="DIR",
                     help="with --ceiling: also save each H's raw per-workgroup timeline as DIR/timeline_H.npy")
+    ap.add_argument("--ab", nargs="+", default=None, metavar="H:CFG;CFG",
+                    help="only an A/B of the fused op at (4096, H) bf16: the table's configuration against "
+                         "forced bench-library ones (CFG = lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags)")
+    ap.add_argument("--hot", action="store_true",
+                    help="with --ab: one buffer set, the same every call (resident in the Infinity Cache)")
+    ap.add_argument("--ab-layout", default="0,0", metavar="OFF,PAD",
+                    help="with --ab: input and residual rows start OFF elements into rows of H + OFF + PAD "
+                         "elements (rows off the 128-byte grid take the configurations' off-grid variants)")
     ap.add_argument("--profile-op", default="fused",
                     choices=("fused", "fp8", "plain", "mxfp8", "mxfp4", "copy", "relu"),
                     help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, plain RMSNorm, "
@@ -333,6 +343,9 @@ def main():
         return profile_driver(torch, abi, op, args)
     if args.sweep:
         return sweep(torch, abi, op, args)
+    if args.ab:
+        off, pad = (int(v) for v in args.ab_layout.split(","))
+        return ab_trials(torch, abi, op, args.ab, args.hot, off, pad)
     if args.ceiling:
         hs = [int(v) for v in args.ceiling.split(",")]
         rows = ceiling(torch, abi, hp_rms_norm_amd, hs, max(args.steps, 10), args.warmup,
@@ -431,6 +444,61 @@ def time_rotating(torch, call, n, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / ncalls
+
+
+def ab_trials(torch, abi, op, specs, hot, off=0, pad=0, trials=7):
+    """A/B of the fused op at (4096, H) bf16: the table's configuration and
+    forced configurations of the bench library, timed in one process in
+    `trials` interleaved rounds (the order reversed every other round); each
+    timing is back-to-back calls between one HIP event pair, over buffer sets
+    spanning >= 1 GiB (cold) or over one set (hot: resident in the 256 MB
+    Infinity Cache after the first call).  Rows start `off` elements into rows
+    of H + off + pad elements.  One JSON line per configuration: the median µs
+    per call and its ratio to the table's."""
+    built = {c.as_tuple() for c in abi.BENCH.kernel_configs(abi.DTYPE_BF16, abi.MODE_FUSED)}
+    plan = []
+    for spec in specs:
+        h, _, cfgs = spec.partition(":")
+        h = int(h)
+        forced = []
+        for c in filter(None, cfgs.split(";")):
+            lpr, vpl, ldsv, block, flags = (int(v) for v in c.split(","))
+            cfg = abi.Config(2 if ldsv else 1, lpr, vpl, ldsv, block, 0, flags)
+            if cfg.as_tuple() not in built or lpr * vpl < h // 8:
+                raise SystemExit(f"--ab: {c} is not a bench-library configuration that covers H = {h}")
+            forced.append((c, cfg))
+        plan.append((h, forced))
+    stream = torch.cuda.current_stream().cuda_stream
+    for h, forced in plan:
+        stride = h + off + pad
+        n = 1 if hot else cold_sets(B, stride)
+        bufs = [torch.empty((2, B, stride), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
+        sets = [b[:, :, off:off + h] for b in bufs]
+        w = (1 + 0.1 * torch.randn(h, device="cuda:0")).to(torch.bfloat16)
+        base = abi.select_config(B, h, abi.DTYPE_BF16)
+
+        def table_call(i):
+            op(sets[i][0], w, sets[i][1], EPS)
+
+        def forced_call(cfg):
+            return lambda i: abi.BENCH.fused_add_rmsnorm(sets[i][0].data_ptr(), w.data_ptr(), sets[i][1].data_ptr(),
+                                                         B, h, stride, stride, abi.DTYPE_BF16, EPS, stream, cfg)
+        runs = [("table", table_call)] + [(c, forced_call(cfg)) for c, cfg in forced]
+        res = {k: [] for k, _ in runs}
+        for t in range(trials):
+            for k, call in (runs if t % 2 == 0 else runs[::-1]):
+                res[k].append(time_rotating(torch, call, n, max(40, 2 * n), 3))
+        tab = statistics.median(res["table"])
+        for k, v in res.items():
+            m = statistics.median(v)
+            cfg = "table " + ",".join(str(x) for x in (base.lanes_per_row, base.vec_per_lane, base.lds_vec_per_lane,
+                                                        base.block_threads, base.flags)) if k == "table" else k
+            print(json.dumps({"hidden": h, "rows": B, "row_offset": off, "row_stride": stride, "hot": hot,
+                              "cfg": cfg, "us": round(m, 2),
+                              "gbs": round(fused_bytes(B, h) / m / 1e3, 1), "vs_table": round(m / tab - 1, 4),
+                              "spread": round((max(v) - min(v)) / m, 4)}), flush=True)
+        del sets, bufs
+        torch.cuda.empty_cache()
 
 
 def profile_driver(torch, abi, op, args):

@@ -478,6 +478,38 @@ Phase shift_phase(const Problem& p) {
   return s[0];
 }
 
+// Rotated rows (FusedArgs::rot_*, the off-grid variants of modes 0, 1, 3, 4).  With
+// rows off the 128-byte grid, a wave's 1 KiB access to a row shares its first
+// and last cache line with the neighbouring accesses: such half-written lines
+// cost 7-11% against whole ones (a flat two-stream in-place probe at a 16-byte
+// offset, 256 MiB per tensor; 24-27% with sc1 stores), and the rows' own
+// measured 10-17% at 16K-32K.  The kernel rotates each row's lane mapping so
+// that every access starts on a cache line of one written stream: the stream
+// the shift aligns when rows are shifted, otherwise the first written stream
+// whose rows are 16-byte aligned but off the grid.  Returns that stream's
+// 128-byte phase {base, step} in bytes, or {0, 0} (no rotation).
+Phase rot_phase(const Problem& p) {
+  const Phase none = {0, 0};
+  if (p.mode == 2 || p.mode > 4) return none;
+  struct Stream { const void* ptr; int64_t stride; };
+  Stream w[2];
+  int n = 0;
+  switch (p.mode) {
+    case 0: w[n++] = {p.x, p.x_stride}; w[n++] = {p.res, p.res_stride}; break;
+    case 1: w[n++] = {p.out, p.out_stride}; break;
+    case 3: w[n++] = {p.out, p.out_stride}; w[n++] = {p.res_out, p.res_out_stride}; break;
+    default: w[n++] = {p.out, p.out_stride}; w[n++] = {p.res, p.res_stride}; break;
+  }
+  auto phase128 = [](const Stream& s) {
+    return Phase{(uint32_t)((uintptr_t)s.ptr & 127u), (uint32_t)((s.stride * 2) & 127)};
+  };
+  if (p.hidden % 8 != 0 || !(shift_phase(p) == none)) return phase128(w[0]);  // the shifted stream
+  for (int i = 0; i < n; ++i)
+    if (aligned16(w[i].ptr) && w[i].stride % 8 == 0 && !rows_aligned128(w[i].ptr, w[i].stride * 2))
+      return phase128(w[i]);
+  return none;
+}
+
 // the variant of a table entry for rows needs_unaligned() reports
 int unaligned_flags(const Problem& p, int flags) {
   return p.hidden % 8 != 0 || !(shift_phase(p) == Phase{0, 0}) ? HPRMS_TAIL_FLAGS(flags)
@@ -593,6 +625,11 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
     const Phase ph = shift_phase(p);
     a.shift_base = ph.base;
     a.shift_step = ph.step;
+  }
+  if (c.flags & 32) {
+    const Phase rot = rot_phase(p);
+    a.rot_base = rot.base;
+    a.rot_step = rot.step;
   }
   a.hidden_f = (float)p.hidden;
   a.eps = (float)p.eps;

@@ -29,6 +29,7 @@ constexpr int kRsrcWord3 = 0x00020000;
 constexpr uint32_t kOOB = 0x80000000u;
 // Cache-policy field of buffer instructions on gfx940+: sc0 = 1, nt
 // (streaming) = 2, sc1 = 16.
+constexpr int kAuxSC0 = 1;
 constexpr int kAuxNT = 2;
 constexpr int kAuxSC1 = 16;
 

@@ -25,11 +25,18 @@
 // FLAGS bit 0 marks the row loads non-temporal, bit 1 the stores: the rows
 // are touched once, so they should not displace the weight from the caches.
 // Bits 3 and 4 add the sc1 (device-scope) policy bit to the loads and to the
-// stores respectively.  Bit 5 marks the variants for rows that are not
-// 128-byte aligned (the host sends them there; the kernel code is the same and
-// correct for rows at any 2-byte boundary: 16-byte accesses at unaligned
-// addresses are legal on gfx9-family GPUs under the ROCm runtime, which runs
-// them in unaligned mode, and hipcc relies on the same for ordinary code).
+// stores respectively; bit 13 (bench library) adds sc0 to the stores.  Bit 5
+// marks the variants for rows that are not 128-byte aligned (the host sends
+// them there; the code is correct for rows at any 2-byte boundary: 16-byte
+// accesses at unaligned addresses are legal on gfx9-family GPUs under the ROCm
+// runtime, which runs them in unaligned mode, and hipcc relies on the same for
+// ordinary code).  In modes 0, 1, 3 and 4 these variants also rotate each
+// row's lane mapping: with the row's first body vector rp 16-byte steps past a
+// 128-byte boundary of the rotation stream (FusedArgs::rot_*; rp = 0 when that
+// phase is not a multiple of 16 bytes), slot k * LPR + lane holds body vector
+// k * LPR + lane - rp and the first rp slots the row's last rp vectors, so
+// every wave's 1 KiB access starts on a cache line and writes whole lines
+// (partial lines written by two accesses cost 7-11% on HBM).
 // Bit 6 selects the tail variant (TAIL), for widths that are not a multiple
 // of 8 (hidden >= 8) and for shifted rows (hidden >= 16).  Row r is shifted by
 // delta = (shift_base + r * shift_step) mod 8 elements (both 0: no shift): the
@@ -102,6 +109,10 @@ struct FusedArgs {
   uint32_t shift_base;   // tail variant: row r is shifted by (shift_base + r * shift_step) mod 8 elements
   uint32_t shift_step;
   int64_t* timeline;     // FLAGS bit 9 only (bench library): 4 values per workgroup
+  // FLAGS bit 5 (modes 0, 1, 3, 4): the rotation stream's row r starts (rot_base +
+  // r * rot_step) mod 128 bytes past a 128-byte boundary (both 0: no rotation)
+  uint32_t rot_base;
+  uint32_t rot_step;
 };
 
 // Waves per SIMD the compiler must leave room for: the tail variant of the
@@ -129,10 +140,15 @@ void fused_vec_kernel(FusedArgs a) {
   constexpr bool MX = MODE == 5 || MODE == 6;                      // OCP MX output
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
   constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // shifted rows, head and tail vectors
+  // rows off the 128-byte grid: each row's lane mapping rotated so that every
+  // wave's 1 KiB access starts on a cache line (FusedArgs::rot_*)
+  // (not the FP8 and MX outputs: the FP8 form's 1024 x 2 tail kernel,
+  // held to 64 VGPRs, would spill, and an MX block must stay one quad's)
+  constexpr bool ROT = (FLAGS & 32) != 0 && !MX && MODE != 2;
   // residual loads issued first (not for the partial-sum form, where it measured 0.1-1.8% slower)
   constexpr bool RFIRST = (FLAGS & 128) != 0 && RES && MODE != 4;
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
-  constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0);
+  constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0) | ((FLAGS & 8192) ? kAuxSC0 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
   // The output phase's unpack of the held row.  With the square phase's lo /
   // hi the compiler merges the two and keeps the row's unpacked floats live
@@ -174,9 +190,35 @@ void fused_vec_kernel(FusedArgs a) {
     const int nrows = left < RPB ? (int)left : RPB;
     const bool row_ok = rib < nrows;
 
+    // TAIL: this row's shift delta (elements), its first body vector j0 and
+    // its body vectors nb; without the tail every row is nvec whole vectors
+    int delta = 0, j0 = 0, nb = a.nvec, t = 0;
+    uint32_t wshift = 0;
+    if constexpr (TAIL) {
+      delta = (int)((a.shift_base + (uint32_t)(row0 + rib) * a.shift_step) & 7u);
+      j0 = delta > 0 ? 1 : 0;
+      const int jend = (a.hidden + delta) >> 3;
+      nb = jend - j0;  // >= 1: hidden >= 8, and >= 16 when shifted
+      t = a.hidden + delta - 8 * jend;  // elements after the last body vector
+      wshift = 16u * (uint32_t)j0 - 2u * (uint32_t)delta;
+    }
+    // ROT: the row's rotation rp, in vectors, from the 128-byte phase of its
+    // first body vector in the rotation stream (when that is a multiple of 16
+    // bytes); slot k * LPR + lane then holds body vector k * LPR + lane - rp,
+    // and the first rp slots (k = 0, lane < rp) the row's last rp vectors
+    int rp = 0;
+    if constexpr (ROT) {
+      const uint32_t ph = (a.rot_base + (uint32_t)(row0 + rib) * a.rot_step + wshift) & 127u;
+      if ((ph & 15u) == 0 && nb >= 8) rp = (int)(ph >> 4);
+    }
+    const uint32_t lofs = (uint32_t)(lane - rp) * 16u;        // lane * 16 without rotation
+    const uint32_t wrap = (ROT && lane < rp) ? (uint32_t)nb : 0u;  // vectors added to slot k = 0
+    // byte offset of slot k's vector past the lane's first (16-byte vectors)
+    auto vk = [&](int k) -> uint32_t { return (uint32_t)(k * CH) + (k == 0 ? wrap * 16u : 0u); };
+
     const uint32_t xbytes = (uint32_t)(((int64_t)(nrows - 1) * a.x_stride + a.hidden) * 2);
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row0 * a.x_stride, xbytes);
-    uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + (uint32_t)lane * 16u;
+    uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + lofs;
 
     // rrs/roff: residual loads; srs/soff: residual stores; ors/ooff: output
     __amdgpu_buffer_rsrc_t rrs = xrs, srs = xrs, ors = xrs;
@@ -184,14 +226,14 @@ void fused_vec_kernel(FusedArgs a) {
     if constexpr (RES) {
       const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_stride + a.hidden) * 2);
       rrs = make_rsrc(a.res + row0 * a.res_stride, rbytes);
-      roff = (uint32_t)rib * (uint32_t)a.res_stride * 2u + (uint32_t)lane * 16u;
+      roff = (uint32_t)rib * (uint32_t)a.res_stride * 2u + lofs;
       srs = rrs;
       soff = roff;
     }
     if constexpr (MODE == 3) {
       const uint32_t sbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_out_stride + a.hidden) * 2);
       srs = make_rsrc(a.res_out + row0 * a.res_out_stride, sbytes);
-      soff = (uint32_t)rib * (uint32_t)a.res_out_stride * 2u + (uint32_t)lane * 16u;
+      soff = (uint32_t)rib * (uint32_t)a.res_out_stride * 2u + lofs;
     }
     // MX: the scale bytes of the row group
     __amdgpu_buffer_rsrc_t xsrs = xrs;
@@ -200,7 +242,7 @@ void fused_vec_kernel(FusedArgs a) {
       constexpr uint32_t QB = MODE == 6 ? 4u : 8u;  // output bytes per 8-element vector
       const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + a.hidden * (int64_t)QB / 8);
       ors = make_rsrc(a.q + row0 * a.q_stride, qbytes);
-      ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)lane * QB;
+      ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)(lane - rp) * QB;
     }
     if constexpr (MX) {
       const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * a.mx_scale_stride + a.hidden / 32);
@@ -211,24 +253,18 @@ void fused_vec_kernel(FusedArgs a) {
     if constexpr (OUT16) {
       const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + a.hidden) * 2);
       ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
-      ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + (uint32_t)lane * 16u;
+      ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + lofs;
     }
 
-    // TAIL: this row's shift and the lane's edge vector (head or tail); the
-    // e*off offsets address the edge vector in each stream, kOOB elsewhere
-    uint32_t wshift = 0, exoff = kOOB, eroff = kOOB, esoff = kOOB, eooff = kOOB, ewoff = kOOB;
+    // TAIL: the lane's edge vector (head or tail); the e*off offsets address
+    // the edge vector in each stream, kOOB elsewhere
+    uint32_t exoff = kOOB, eroff = kOOB, esoff = kOOB, eooff = kOOB, ewoff = kOOB;
     int elo = 0, ehi = 0;
     bool eok = false;
     if constexpr (TAIL) {
-      const int delta = (int)((a.shift_base + (uint32_t)(row0 + rib) * a.shift_step) & 7u);
-      const int j0 = delta > 0 ? 1 : 0;
-      const int jend = (a.hidden + delta) >> 3;
-      const int nb = jend - j0;  // body vectors of this row (>= 1: hidden >= 8, and >= 16 when shifted)
-      const int t = a.hidden + delta - 8 * jend;  // elements after the last body vector
-      const uint32_t xrow = xoff - (uint32_t)lane * 16u;
-      const uint32_t rrow = roff - (uint32_t)lane * 16u, srow = soff - (uint32_t)lane * 16u;
-      const uint32_t orow = ooff - (uint32_t)lane * (MODE == 2 ? 8u : 16u);
-      wshift = 16u * (uint32_t)j0 - 2u * (uint32_t)delta;
+      const uint32_t xrow = xoff - lofs;
+      const uint32_t rrow = roff - lofs, srow = soff - lofs;
+      const uint32_t orow = ooff - (MODE == 2 ? (uint32_t)(lane - rp) * 8u : lofs);
 #pragma unroll
       for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < nb;
       xoff += wshift;
@@ -237,10 +273,14 @@ void fused_vec_kernel(FusedArgs a) {
         soff += wshift;
       }
       ooff += MODE == 2 ? (uint32_t)(8 * j0 - delta) : wshift;
-      int tl = (nb - 1) & (LPR - 1);
-      if (delta > 0 && tl == 0) tl = 1;
+      // the head goes to the lane holding body vector 0 (slot rp), the tail
+      // to the lane holding body vector nb - 1 (slot rp - 1, or nb - 1
+      // unrotated), or to the next lane when that is the head's
+      const int hl = rp;
+      int tl = rp > 0 ? rp - 1 : (nb - 1) & (LPR - 1);
+      if (delta > 0 && tl == hl) tl = hl + 1;
       uint32_t eb = 0, eq = 0;
-      if (delta > 0 && lane == 0) {
+      if (delta > 0 && lane == hl) {
         eok = row_ok; elo = 0; ehi = 8 - delta;
       } else if (t > 0 && lane == tl) {
         eok = row_ok; elo = 8 - t; ehi = 8;
@@ -263,17 +303,17 @@ void fused_vec_kernel(FusedArgs a) {
       // all of the residual's vectors, then all of the input's (the
       // scheduling barriers keep the two groups apart)
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + k * CH : kOOB);
+      for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
+      for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
       __builtin_amdgcn_sched_barrier(0);
     } else {
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         const bool ok = row_ok && vec_ok[k];
-        xv[k] = load16<LAUX>(xrs, ok ? xoff + k * CH : kOOB);
-        if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + k * CH : kOOB);
+        xv[k] = load16<LAUX>(xrs, ok ? xoff + vk(k) : kOOB);
+        if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + vk(k) : kOOB);
       }
     }
     u32x4 txv = {}, trv = {}, twv = {};
@@ -284,7 +324,7 @@ void fused_vec_kernel(FusedArgs a) {
     if constexpr (!WLATE) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k)
-        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : (uint32_t)(k * LPR + lane) * 16u + wshift);
+        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
       if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
     }
 
@@ -324,7 +364,7 @@ void fused_vec_kernel(FusedArgs a) {
 #pragma unroll
           for (int i = 0; i < G; ++i) {
             const int k = k0 + i < VPL ? k0 + i : 0;
-            pv[i] = load16<LAUX>(prs, (k0 + i < VPL && row_ok && vec_ok[k]) ? xoff + k * CH : kOOB);
+            pv[i] = load16<LAUX>(prs, (k0 + i < VPL && row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
           }
           if (with_tail) tpv = load16<LAUX>(prs, exoff);
 #pragma unroll
@@ -371,7 +411,7 @@ void fused_vec_kernel(FusedArgs a) {
           ss1 = __builtin_fmaf(b1, b1, ss1);
         }
         const bool ok = row_ok && vec_ok[k];
-        store16<SAUX>(s, srs, ok ? soff + k * CH : kOOB);
+        store16<SAUX>(s, srs, ok ? soff + vk(k) : kOOB);
       } else {
         s = xv[k];
 #pragma unroll
@@ -403,7 +443,7 @@ void fused_vec_kernel(FusedArgs a) {
     if constexpr (WLATE) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k)
-        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : (uint32_t)(k * LPR + lane) * 16u + wshift);
+        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
       if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
     }
 
@@ -471,7 +511,7 @@ void fused_vec_kernel(FusedArgs a) {
         for (int j = 0; j < 4; ++j)
           o[j] = F::pack((olo(s[j]) * inv) * F::lo(wv[k][j]), (ohi(s[j]) * inv) * F::hi(wv[k][j]));
         const bool ok = row_ok && vec_ok[k];
-        store16<SAUX>(o, ors, ok ? ooff + k * CH : kOOB);
+        store16<SAUX>(o, ors, ok ? ooff + vk(k) : kOOB);
       }
       if constexpr (TAIL) {
         u32x4 o;
@@ -537,7 +577,7 @@ void fused_vec_kernel(FusedArgs a) {
                              clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
         }
         const bool ok = row_ok && vec_ok[k];
-        store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
+        store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) + (k == 0 ? wrap * 8u : 0u) : kOOB);
       }
       if constexpr (TAIL) {
         u32x2 q;

@@ -22,15 +22,18 @@ struct FusedEntry {
 // tail vector for hidden % 8 != 0 (with bit 5), bit 7 = residual loads first,
 // bit 8 = held to 8 waves per SIMD, bit 9 = timeline instrumentation (bench
 // library only), bit 11 = one workgroup per CU (the launch reserves LDS),
-// bit 12 = the output phase's separate unpack (bench library)
+// bit 12 = the output phase's separate unpack (bench library), bit 13 = sc0 on
+// the stores (bench library)
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
 
 // The unaligned variants of a shape: the same lanes, vectors and weight
 // timing, no sc1 bits (partial cache lines written with sc1 measured 13-24%
-// slower at 16K-32K), bit 5 set; and the same with the tail (bit 6), which
-// costs about 30 VGPRs and so is kept apart from the rows that need no tail.
+// slower at 16K-32K), bit 5 set (which also rotates each row's lane mapping
+// onto the cache lines in modes 0, 1, 3 and 4); and the same with the tail
+// (bit 6), which costs about 30 VGPRs and so is kept apart from the rows that
+// need no tail.
 #define HPRMS_UNALIGNED_FLAGS(FLAGS) ((((FLAGS) & ~24) | 32))
 #define HPRMS_TAIL_FLAGS(FLAGS) ((((FLAGS) & ~24) | 96))
 #define HPRMS_UNALIGNED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
@@ -118,7 +121,9 @@ struct FusedEntry {
   X(DT, MODE, 256, 6, 3, 256, 31) X(DT, MODE, 256, 8, 4, 256, 3)
 
 // candidates of the table's rows (bf16): +256 = held to 8 waves per SIMD,
-// +2048 = one workgroup per CU (the launch reserves 96 KiB of LDS)
+// +2048 = one workgroup per CU (the launch reserves 96 KiB of LDS), other
+// cache policies of the 3K-12K rows (sc1 on the stores alone: +16; sc0 on the
+// stores: +8192; no nt on the loads, the stores or either)
 #define HPRMS_CANDIDATE_SHAPES(X, DT, MODE)                                                          \
   X(DT, MODE, 32, 4, 0, 256, 135) X(DT, MODE, 64, 4, 0, 256, 131) X(DT, MODE, 128, 2, 0, 256, 135)    \
   X(DT, MODE, 128, 4, 0, 256, 135) X(DT, MODE, 128, 4, 0, 256, 159) X(DT, MODE, 128, 4, 0, 256, 391) \
@@ -127,7 +132,14 @@ struct FusedEntry {
   X(DT, MODE, 512, 2, 0, 512, 135) X(DT, MODE, 512, 2, 0, 512, 159) X(DT, MODE, 256, 6, 0, 256, 159)  \
   X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 512, 4, 0, 512, 159) X(DT, MODE, 1024, 2, 0, 1024, 159) \
   X(DT, MODE, 1024, 2, 0, 1024, 2079) X(DT, MODE, 1024, 3, 0, 1024, 2207) X(DT, MODE, 1024, 4, 0, 1024, 2207) \
-  X(DT, MODE, 256, 8, 4, 256, 155) X(DT, MODE, 256, 12, 0, 256, 159) X(DT, MODE, 512, 6, 0, 512, 159)
+  X(DT, MODE, 256, 8, 4, 256, 155) X(DT, MODE, 256, 12, 0, 256, 159) X(DT, MODE, 512, 6, 0, 512, 159)         \
+  X(DT, MODE, 128, 3, 0, 256, 23) X(DT, MODE, 128, 3, 0, 256, 31) X(DT, MODE, 256, 2, 0, 256, 147)            \
+  X(DT, MODE, 512, 2, 0, 512, 23) X(DT, MODE, 512, 3, 0, 512, 143) X(DT, MODE, 512, 3, 0, 512, 135)           \
+  X(DT, MODE, 256, 2, 0, 256, 8323) X(DT, MODE, 512, 2, 0, 512, 8199) X(DT, MODE, 128, 3, 0, 256, 8199)        \
+  X(DT, MODE, 256, 2, 0, 256, 8339) X(DT, MODE, 512, 2, 0, 512, 8215)                                        \
+  X(DT, MODE, 256, 2, 0, 256, 128) X(DT, MODE, 256, 2, 0, 256, 129) X(DT, MODE, 256, 2, 0, 256, 130)           \
+  X(DT, MODE, 32, 4, 0, 256, 128) X(DT, MODE, 32, 4, 0, 256, 129) X(DT, MODE, 32, 4, 0, 256, 130)              \
+  X(DT, MODE, 512, 2, 0, 512, 4) X(DT, MODE, 512, 2, 0, 512, 5) X(DT, MODE, 512, 2, 0, 512, 6)
 
 // the bandwidth table's rows with the output phase's separate unpack (+4096)
 #define HPRMS_SHARED_UNPACK_SHAPES(X, DT, MODE)                                                        \

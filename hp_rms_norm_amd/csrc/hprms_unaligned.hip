@@ -3,9 +3,11 @@
 // unaligned addresses), hidden % 8 == 0.  One variant of every shape the
 // dispatch tables choose, with the same lanes, vectors and weight timing and
 // without the sc1 policy bit: with rows off the 128-byte grid, each wave's
-// 1 KiB chunk shares its first and last cache line with the next chunk, and
-// such partial lines written with sc1 measured 13-24% slower at 16K-32K (4096
-// rows, row stride hidden + 8).  Kept in its own translation unit so that the
+// 1 KiB chunk would share its first and last cache line with the next chunk,
+// and such partial lines written with sc1 measured 13-24% slower at 16K-32K
+// (4096 rows, row stride hidden + 8).  In modes 0, 1, 3 and 4 the variants
+// rotate each row's lane mapping so that the chunks start on cache lines
+// (FusedArgs::rot_*).  Kept in its own translation unit so that the
 // build compiles it in parallel with hprms.hip; hprms_tail.hip holds the same
 // shapes with the tail vector for hidden % 8 != 0.
 #include <hip/hip_runtime.h>

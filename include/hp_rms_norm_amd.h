@@ -63,11 +63,12 @@ typedef enum {
  * (the reference assumes contiguous rows).  rows == 0 is a no-op.
  * hidden may be any value in [1, 2^24] and rows may start at any 2-byte
  * boundary.  The vector tiers take every hidden in [8, 65543]: rows off the
- * 128-byte grid run a variant without the sc1 cache-policy bit, hidden % 8
- * != 0 adds a tail vector, and from hidden 4104 up, when neither input nor
- * residual has its rows on 16-byte boundaries, the rows are shifted so that
- * the input is accessed aligned (flags bits 5 and 6 of hprms_config); other
- * shapes take a slower general kernel.  The results
+ * 128-byte grid run a variant without the sc1 cache-policy bit that rotates
+ * each row's lane mapping onto the input's cache lines, hidden % 8 != 0 adds
+ * a tail vector, and from hidden 4104 up, when neither input nor residual has
+ * its rows on 16-byte boundaries, the rows are shifted so that the input is
+ * accessed aligned (flags bits 5 and 6 of hprms_config); other shapes take a
+ * slower general kernel.  The results
  * meet the same bar in every case: residual bit-exact, output within 1 ulp
  * of the reference formula.
  */
@@ -198,7 +199,9 @@ typedef struct {
                                bit 2: weight loaded after the residual is stored;
                                bit 3 / bit 4: sc1 cache-policy bit on the row loads / stores;
                                bit 5: variant for rows off the 128-byte grid (any 2-byte
-                               boundary), bit 6 (with bit 5): head and tail vectors, for
+                               boundary; in modes 0, 1, 3, 4 each row's lane mapping rotated
+                               so that every wave's access starts on a cache line of the
+                               first written tensor), bit 6 (with bit 5): head and tail vectors, for
                                hidden % 8 != 0 and (from hidden 4104 up, modes 0-4) rows
                                shifted to the first written tensor's 16-byte phase;
                                bit 7: a lane's residual loads issued before its input loads */

@@ -66,3 +66,16 @@ def assert_output_close(got_bits, want_bits, dtype, what="output"):
     wt = from_bits(want, dtype).float()
     torch.testing.assert_close(gt, wt, atol=ATOL, rtol=RTOL, equal_nan=True)
     return d
+
+
+def as_dispatched(abi, cfg, hidden):
+    """`cfg`, a table configuration, as the dispatch runs it on contiguous rows
+    of `hidden` elements: rows off the 128-byte grid (hidden * 2 % 128 != 0)
+    take its unaligned variant (flags bit 5 set, the sc1 bits cleared), which
+    rotates each row's lane mapping by the row's 128-byte phase, and so sums
+    the squares in another order than the table's kernel forced on them."""
+    if cfg.tier == 3 or hidden % 8 != 0 or (hidden * 2) % 128 == 0:
+        return cfg
+    c = abi.Config(*cfg.as_tuple())
+    c.flags = (c.flags & ~24) | 32
+    return c

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DT, assert_output_close, assert_residual_exact, bits, make_inputs, oracle_fused
+from helpers import DT, as_dispatched, assert_output_close, assert_residual_exact, bits, make_inputs, oracle_fused
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -72,8 +72,9 @@ def test_out_of_place_every_table_row(abi, dtype):
             assert_residual_exact(bits(rod), want_res, dtype, "residual_out " + tag)
             assert_output_close(bits(od), want_out, dtype, "out " + tag)
             # the in-place op run with the configuration the out-of-place form chose (the
-            # two forms' tables differ at some row counts) gives the same bits
-            c_out = abi.select_config(rows, hidden, DT[dtype], abi.MODE_OUT)
+            # two forms' tables differ at some row counts), in the variant the dispatch
+            # runs on these rows, gives the same bits
+            c_out = as_dispatched(abi, abi.select_config(rows, hidden, DT[dtype], abi.MODE_OUT), hidden)
             ip_out, ip_res = in_place(abi, x, r, w, 1e-6, c_out)
             assert np.array_equal(bits(od), ip_out), "differs from the in-place op " + tag
             assert np.array_equal(bits(rod), ip_res), "residual differs from the in-place op " + tag
@@ -160,8 +161,9 @@ def test_reduce_every_table_row(abi, dtype, nparts):
             assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
             assert_output_close(bits(od), want_out, dtype, "out " + tag)
             if nparts == 1:
-                # the in-place op with the reduce form's shape (the same fp32 summation order)
-                cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_REDUCE)
+                # the in-place op with the reduce form's shape and variant (the same fp32
+                # summation order)
+                cfg = as_dispatched(abi, abi.select_config(rows, hidden, DT[dtype], abi.MODE_REDUCE), hidden)
                 xd, rd2 = parts[0].to(DEV), r.to(DEV)
                 abi.BENCH.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd2.data_ptr(), rows, hidden, hidden, hidden,
                                             DT[dtype], 1e-6, _stream(), cfg)
