@@ -838,10 +838,12 @@ def run_extra(torch, ops, args):
     out["plain_rmsnorm_bf16"] = plain
     # rows off the 128-byte grid: odd widths (the tail variants; from 4104 elements shifted rows),
     # row starts 2 bytes off 16-byte alignment (shifted from 4104), and 16-byte aligned rows with
-    # a stride of hidden + 8 (the unaligned variants)
+    # a stride of hidden + 8 (the unaligned variants, rotated); beside them rows on the grid at
+    # strides of hidden + 64 and + 128 (the table's kernels at a pitch other than hidden)
     una = []
     for h, off, pad in ((999, 0, 0), (2049, 0, 0), (4097, 0, 0), (8191, 0, 0), (16391, 0, 0), (32775, 0, 0),
-                        (4096, 1, 8), (16384, 1, 8), (32768, 1, 8), (16384, 0, 8), (32768, 0, 8)):
+                        (4096, 1, 8), (16384, 1, 8), (32768, 1, 8), (16384, 0, 8), (32768, 0, 8),
+                        (16384, 0, 64), (32768, 0, 64), (32768, 0, 128)):
         stride = h + off + pad
         n = cold_sets(B, stride)
         bases = [make_set(torch, B, stride, torch.bfloat16, 9500 + i, "cuda:0") for i in range(n)]
