@@ -316,9 +316,10 @@ def main():
                          "forced bench-library ones (CFG = lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags)")
     ap.add_argument("--hot", action="store_true",
                     help="with --ab: one buffer set, the same every call (resident in the Infinity Cache)")
-    ap.add_argument("--ab-layout", default="0,0", metavar="OFF,PAD",
-                    help="with --ab: input and residual rows start OFF elements into rows of H + OFF + PAD "
-                         "elements (rows off the 128-byte grid take the configurations' off-grid variants)")
+    ap.add_argument("--layout", default="0,0", metavar="OFF,PAD",
+                    help="with --ab, or --profile of the fused op: input and residual rows start OFF elements "
+                         "into rows of H + OFF + PAD elements (rows off the 128-byte grid take the "
+                         "configurations' off-grid variants)")
     ap.add_argument("--profile-op", default="fused",
                     choices=("fused", "fp8", "plain", "mxfp8", "mxfp4", "copy", "relu"),
                     help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, plain RMSNorm, "
@@ -344,7 +345,7 @@ def main():
     if args.sweep:
         return sweep(torch, abi, op, args)
     if args.ab:
-        off, pad = (int(v) for v in args.ab_layout.split(","))
+        off, pad = (int(v) for v in args.layout.split(","))
         return ab_trials(torch, abi, op, args.ab, args.hot, off, pad)
     if args.ceiling:
         hs = [int(v) for v in args.ceiling.split(",")]
@@ -541,14 +542,26 @@ def profile_driver(torch, abi, op, args):
 
         def op(x, w, r, eps):  # noqa: F811  (streamer: reads x, writes r; w and eps unused)
             stream_fn(r, x)
-    us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup, trials=1)[0][0]
+    off, pad = (int(v) for v in args.layout.split(","))
+    if (off, pad) == (0, 0):
+        us = time_shapes(torch, op, [(B, hidden, torch.bfloat16, "bench")], args.steps, args.warmup, trials=1)[0][0]
+    else:
+        # rows at element offset `off` of rows of hidden + off + pad elements
+        stride = hidden + off + pad
+        bases = [make_set(torch, B, stride, torch.bfloat16, 9500 + i, "cuda:0") for i in range(cold_sets(B, stride))]
+        sets = [(x[:, off:off + hidden], r[:, off:off + hidden]) for x, r in bases]
+        w = make_weight(torch, hidden, torch.bfloat16, 1, "cuda:0")
+        us = time_rotating(torch, lambda i: op(sets[i][0], w, sets[i][1], EPS), len(sets), args.steps,
+                           args.warmup)
+        del bases, sets
     n = 1 << 29
     src = torch.empty(n, dtype=torch.bfloat16, device="cuda:0").normal_()
     dst = torch.empty_like(src)
     for _ in range(args.steps):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"profile: (4096, {hidden}) {us:.2f} us/call; then {args.steps} copies of {2 * n} bytes")
+    log(f"profile: (4096, {hidden}) layout {off},{pad}: {us:.2f} us/call; then {args.steps} copies of "
+        f"{2 * n} bytes")
 
 
 def sweep(torch, abi, op, args):
