@@ -628,6 +628,10 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
                 the op's bytes as flat 4 KiB-per-workgroup streams: one tensor
                 rewritten in place, x and r rewritten in place, x and r
                 copied to two other tensors
+      inplace_2stream_off16 / _off64
+                x and r rewritten in place from 16 / 64 bytes past their
+                starts, so every wave's 1 KiB access shares its first and
+                last 128-byte line with its neighbours
     and one timeline launch of the table's kernel (per-workgroup start/end)."""
     import numpy as np
     bench = abi.BENCH
@@ -669,13 +673,19 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
                                                                 bufs[(i + 1) % n][1].data_ptr(), nb, stream),
                                           "copy_2stream"),
         }
+        for off in (16, 64):
+            kinds[f"inplace_2stream_off{off}"] = (
+                lambda i, off=off: chk(BL.hprms_ceil_streams(1, bufs[i][0].data_ptr() + off,
+                                                             bufs[i][1].data_ptr() + off, None, None, nb - 128,
+                                                             stream), f"inplace_2stream_off{off}"))
         samples = {k: [] for k in kinds}
         for t in range(trials):
             for k, fn in (kinds.items() if t % 2 == 0 else reversed(list(kinds.items()))):
                 samples[k].append(time_rotating(torch, fn, n, steps, warmup))
         us = {k: statistics.median(v) for k, v in samples.items()}
         nbytes = {"fused": fused_bytes(B, h), "skeleton": 4 * nb, "copy": 4 * nb, "read": 2 * nb, "write": 2 * nb,
-                  "inplace_1stream": 4 * nb, "inplace_2stream": 4 * nb, "copy_2stream": 4 * nb}
+                  "inplace_1stream": 4 * nb, "inplace_2stream": 4 * nb, "copy_2stream": 4 * nb,
+                  "inplace_2stream_off16": 4 * (nb - 128), "inplace_2stream_off64": 4 * (nb - 128)}
         row = {"hidden": h, "rows": B,
                "kernel": {"lanes_per_row": cfg.lanes_per_row, "vec_per_lane": cfg.vec_per_lane,
                           "lds_vec_per_lane": cfg.lds_vec_per_lane, "block": cfg.block_threads,

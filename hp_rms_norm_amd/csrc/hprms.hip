@@ -481,9 +481,9 @@ Phase shift_phase(const Problem& p) {
 // Rotated rows (FusedArgs::rot_*, the off-grid variants of modes 0, 1, 3, 4).  With
 // rows off the 128-byte grid, a wave's 1 KiB access to a row shares its first
 // and last cache line with the neighbouring accesses: such half-written lines
-// cost 7-11% against whole ones (a flat two-stream in-place probe at a 16-byte
-// offset, 256 MiB per tensor; 24-27% with sc1 stores), and the rows' own
-// measured 10-17% at 16K-32K.  The kernel rotates each row's lane mapping so
+// cost 9-13% against whole ones (a flat two-stream in-place rewrite 16 bytes
+// off, 4096 x 4K-32K bf16), and the rows' own measured 10-17% at 16K-32K
+// before the rotation.  The kernel rotates each row's lane mapping so
 // that every access starts on a cache line of one written stream: the stream
 // the shift aligns when rows are shifted, otherwise the first written stream
 // whose rows are 16-byte aligned but off the grid.  Returns that stream's

@@ -36,7 +36,7 @@
 // phase is not a multiple of 16 bytes), slot k * LPR + lane holds body vector
 // k * LPR + lane - rp and the first rp slots the row's last rp vectors, so
 // every wave's 1 KiB access starts on a cache line and writes whole lines
-// (partial lines written by two accesses cost 7-11% on HBM).
+// (lines written in two parts by two accesses cost 9-13% at a 16-byte offset).
 // Bit 6 selects the tail variant (TAIL), for widths that are not a multiple
 // of 8 (hidden >= 8) and for shifted rows (hidden >= 16).  Row r is shifted by
 // delta = (shift_base + r * shift_step) mod 8 elements (both 0: no shift): the
