@@ -291,6 +291,47 @@ def test_rotated_rows_every_phase_every_mode(abi, hidden):
             assert_output_close(bits(ov.view), p_out, dtype, "reduce output " + tag)
 
 
+@pytest.mark.parametrize("hidden,off,pad", [(8192, 8, 8), (16384, 1, 8), (4097, 0, 0)])
+def test_off_grid_rows_in_a_hip_graph(abi, hidden, off, pad):
+    """Rotated (16-byte aligned off the grid), shifted (2 bytes off) and odd-width rows captured
+    in a HIP graph: each replay, with fresh inputs copied in and eager work between replays,
+    gives the same bits as the eager call on the same layout."""
+    import hp_rms_norm_amd
+    dtype, rows, eps = torch.bfloat16, 300, 1e-6
+    stride = hidden + off + pad
+    bx = torch.zeros(rows, stride, dtype=dtype, device=DEV)
+    br = torch.zeros_like(bx)
+    xs, rs = bx[:, off:off + hidden], br[:, off:off + hidden]
+    wd = make_inputs(1, hidden, dtype, 0)[2].to(DEV)
+    print("off-grid graph", hidden, off, pad, flush=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hp_rms_norm_amd.hp_rms_norm(xs, wd, rs, eps)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hp_rms_norm_amd.hp_rms_norm(xs, wd, rs, eps)
+    ex, er = torch.zeros_like(bx), torch.zeros_like(br)
+    xe, re_ = ex[:, off:off + hidden], er[:, off:off + hidden]
+    for rep in range(4):
+        x, r, _ = make_inputs(rows, hidden, dtype, 200 + rep)
+        xs.copy_(x.to(DEV))
+        rs.copy_(r.to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_x, got_r = u16(xs), u16(rs)
+        xe.copy_(x.to(DEV))
+        re_.copy_(r.to(DEV))
+        hp_rms_norm_amd.hp_rms_norm(xe, wd, re_, eps)
+        torch.cuda.synchronize()
+        assert torch.equal(got_x, u16(xe)), f"replay {rep} output"
+        assert torch.equal(got_r, u16(re_)), f"replay {rep} residual"
+    o_out, o_res = oracle_fused(x, r, wd.cpu(), eps, dtype)
+    assert_residual_exact(got_r.numpy().view(np.uint16), o_res, dtype, "graph residual")
+    assert_output_close(got_x.numpy().view(np.uint16), o_out, dtype, "graph output")
+
+
 # ---- modes 1-4 -------------------------------------------------------------------------
 OTHER_WIDTHS = [8, 1000, 1001, 4096, 4103, 12288, 16384, 16391, 32768, 32775, 65536]
 
