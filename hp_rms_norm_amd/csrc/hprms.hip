@@ -599,28 +599,24 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
                 c.block_threads, c.flags);
   if (p.rows == 0) return HPRMS_OK;
 
+  // the kernel's leading scalar arguments (preloaded into SGPRs), then FusedArgs
+  const uint16_t* x_rows = (const uint16_t*)p.x;
+  uint16_t* res_rows = (uint16_t*)p.res;
+  const uint16_t* weight = (const uint16_t*)p.w;
+  const int64_t rpb = c.block_threads / c.lanes_per_row;
   FusedArgs a = {};
-  a.x = (const uint16_t*)p.x;
+  a.ngroups = (p.rows + rpb - 1) / rpb;
   a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x : p.out);
   a.res_out = (uint16_t*)p.res_out;
   a.res_out_stride = p.res_out_stride;
   a.nparts = p.nparts;
   for (int g = 0; g < p.nparts && p.parts; ++g) a.parts[g] = (const uint16_t*)p.parts[g];
-  a.res = (uint16_t*)p.res;
-  a.w = (const uint16_t*)p.w;
-  a.rows = p.rows;
   a.q = p.mode == 2 || is_mx(p.mode) ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
   a.q_stride = p.mode == 2 || is_mx(p.mode) ? p.out_stride : 0;
   a.mx_scale = (uint8_t*)p.mx_scales;
   a.mx_scale_stride = p.mx_scale_stride;
-  const int64_t rpb = c.block_threads / c.lanes_per_row;
-  a.ngroups = (p.rows + rpb - 1) / rpb;
-  a.x_stride = p.x_stride;
   a.out_stride = p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x_stride : p.out_stride;
-  a.res_stride = p.res_stride;
-  a.hidden = (int32_t)p.hidden;
-  a.nvec = (int32_t)(p.hidden / 8);
   if (c.flags & 64) {
     const Phase ph = shift_phase(p);
     a.shift_base = ph.base;
@@ -640,7 +636,8 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   if (grid > kMaxGrid) grid = kMaxGrid;
   // flags bit 11: 96 KiB of (unused) dynamic LDS, so one workgroup holds a CU
   const unsigned lds = (c.flags & 2048) ? 96u * 1024u : 0u;
-  hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(c.block_threads), lds, stream, a);
+  hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(c.block_threads), lds, stream, x_rows, res_rows, weight,
+                     p.rows, p.x_stride, p.res_stride, (int32_t)p.hidden, (int32_t)grid, a);
   return check_launch("fused rmsnorm kernel");
 }
 

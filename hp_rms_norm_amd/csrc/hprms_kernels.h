@@ -83,18 +83,17 @@
 
 namespace hprms {
 
+// The kernel's arguments.  What a row group needs before its first loads
+// comes first, as scalar arguments (fused_vec_kernel's x_rows ... grid):
+// hipcc's -amdgpu-kernarg-preload-count has gfx950 preload the first 14 dwords
+// of the argument block into SGPRs at wave launch, so in the aligned kernels
+// the first row loads wait for no scalar memory load (a copy kernel measured
+// 0.2 us less per launch at 16-256 MB with its arguments preloaded; a by-value
+// struct is never preloaded).  FusedArgs holds the rest:
 struct FusedArgs {
-  const uint16_t* x;     // input rows (MODE 0: also the output; MODE 4: part 0)
   uint16_t* out;         // 16-bit output rows (MODES 1, 3, 4; MODE 0: == x)
-  uint16_t* res;         // residual rows (every mode but 1)
-  const uint16_t* w;     // weight [hidden]
-  int64_t rows;
-  int64_t ngroups;       // ceil(rows / RPB)
-  int64_t x_stride;      // elements
+  int64_t ngroups;       // ceil(rows / RPB); the grid never exceeds it
   int64_t out_stride;
-  int64_t res_stride;
-  int32_t hidden;
-  int32_t nvec;          // hidden / 8
   float hidden_f;
   float eps;
   uint8_t* q;            // MODES 2, 5, 6: quantised output rows
@@ -102,7 +101,7 @@ struct FusedArgs {
   int64_t q_stride;      // MODES 2, 5, 6: bytes between quantised rows
   uint16_t* res_out;     // MODE 3: residual output rows
   int64_t res_out_stride;
-  int32_t nparts;        // MODE 4: number of partial rows summed (x is part 0)
+  int32_t nparts;        // MODE 4: number of partial rows summed (x_rows is part 0)
   const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
   uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes, hidden / 32 per row
   int64_t mx_scale_stride;  // bytes between scale rows
@@ -126,7 +125,15 @@ constexpr int kMinWavesPerEU = ((FLAGS & 256) != 0 || ((FLAGS & 64) != 0 && BLOC
 
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<FLAGS, BLOCK, VPL>)))
-void fused_vec_kernel(FusedArgs a) {
+void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the output; MODE 4: part 0)
+                      uint16_t* res_rows,      // residual rows (every mode but 1)
+                      const uint16_t* w,       // weight [hidden]
+                      int64_t rows,
+                      int64_t x_stride, int64_t res_stride,  // elements
+                      int32_t hidden,
+                      int32_t grid,            // workgroups launched (<= FusedArgs::ngroups)
+                      FusedArgs a) {
+  const int32_t nvec = hidden >> 3;  // whole 16-byte vectors per row
   static_assert(LPR >= 16 && (LPR & (LPR - 1)) == 0 && BLOCK % LPR == 0 && BLOCK % 64 == 0, "shape");
   static_assert(LDSV >= 0 && LDSV <= VPL, "LDS share");
   using F = Fmt<DT>;
@@ -172,7 +179,7 @@ void fused_vec_kernel(FusedArgs a) {
   constexpr bool TIMELINE = (FLAGS & 512) != 0;
   const uint64_t t_start = TIMELINE ? __builtin_amdgcn_s_memrealtime() : 0;
 
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)a.hidden * 2u);
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, (uint32_t)hidden * 2u);
 
   // slots past the row's vectors: their row accesses and (in the tail
   // variant, whose shifted weight slot past the row could start inside the
@@ -181,25 +188,27 @@ void fused_vec_kernel(FusedArgs a) {
   // returns zeros
   bool vec_ok[VPL];
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < a.nvec;
+  for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < nvec;
 
   int buf = 0;
-  for (int64_t g = blockIdx.x; g < a.ngroups; g += gridDim.x) {
+  // the grid never exceeds ngroups, so every workgroup has a first row group
+  // and ngroups (not preloaded) is first needed at its end
+  for (int64_t g = blockIdx.x;;) {
     const int64_t row0 = g * RPB;
-    const int64_t left = a.rows - row0;
+    const int64_t left = rows - row0;
     const int nrows = left < RPB ? (int)left : RPB;
     const bool row_ok = rib < nrows;
 
     // TAIL: this row's shift delta (elements), its first body vector j0 and
     // its body vectors nb; without the tail every row is nvec whole vectors
-    int delta = 0, j0 = 0, nb = a.nvec, t = 0;
+    int delta = 0, j0 = 0, nb = nvec, t = 0;
     uint32_t wshift = 0;
     if constexpr (TAIL) {
       delta = (int)((a.shift_base + (uint32_t)(row0 + rib) * a.shift_step) & 7u);
       j0 = delta > 0 ? 1 : 0;
-      const int jend = (a.hidden + delta) >> 3;
+      const int jend = (hidden + delta) >> 3;
       nb = jend - j0;  // >= 1: hidden >= 8, and >= 16 when shifted
-      t = a.hidden + delta - 8 * jend;  // elements after the last body vector
+      t = hidden + delta - 8 * jend;  // elements after the last body vector
       wshift = 16u * (uint32_t)j0 - 2u * (uint32_t)delta;
     }
     // ROT: the row's rotation rp, in vectors, from the 128-byte phase of its
@@ -216,22 +225,22 @@ void fused_vec_kernel(FusedArgs a) {
     // byte offset of slot k's vector past the lane's first (16-byte vectors)
     auto vk = [&](int k) -> uint32_t { return (uint32_t)(k * CH) + (k == 0 ? wrap * 16u : 0u); };
 
-    const uint32_t xbytes = (uint32_t)(((int64_t)(nrows - 1) * a.x_stride + a.hidden) * 2);
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + row0 * a.x_stride, xbytes);
-    uint32_t xoff = (uint32_t)rib * (uint32_t)a.x_stride * 2u + lofs;
+    const uint32_t xbytes = (uint32_t)(((int64_t)(nrows - 1) * x_stride + hidden) * 2);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x_rows + row0 * x_stride, xbytes);
+    uint32_t xoff = (uint32_t)rib * (uint32_t)x_stride * 2u + lofs;
 
     // rrs/roff: residual loads; srs/soff: residual stores; ors/ooff: output
     __amdgpu_buffer_rsrc_t rrs = xrs, srs = xrs, ors = xrs;
     uint32_t roff = 0, soff = 0, ooff = xoff;
     if constexpr (RES) {
-      const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_stride + a.hidden) * 2);
-      rrs = make_rsrc(a.res + row0 * a.res_stride, rbytes);
-      roff = (uint32_t)rib * (uint32_t)a.res_stride * 2u + lofs;
+      const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * res_stride + hidden) * 2);
+      rrs = make_rsrc(res_rows + row0 * res_stride, rbytes);
+      roff = (uint32_t)rib * (uint32_t)res_stride * 2u + lofs;
       srs = rrs;
       soff = roff;
     }
     if constexpr (MODE == 3) {
-      const uint32_t sbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_out_stride + a.hidden) * 2);
+      const uint32_t sbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_out_stride + hidden) * 2);
       srs = make_rsrc(a.res_out + row0 * a.res_out_stride, sbytes);
       soff = (uint32_t)rib * (uint32_t)a.res_out_stride * 2u + lofs;
     }
@@ -240,18 +249,18 @@ void fused_vec_kernel(FusedArgs a) {
     uint32_t xsoff = 0;
     if constexpr (MODE == 2 || MX) {
       constexpr uint32_t QB = MODE == 6 ? 4u : 8u;  // output bytes per 8-element vector
-      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + a.hidden * (int64_t)QB / 8);
+      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + hidden * (int64_t)QB / 8);
       ors = make_rsrc(a.q + row0 * a.q_stride, qbytes);
       ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)(lane - rp) * QB;
     }
     if constexpr (MX) {
-      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * a.mx_scale_stride + a.hidden / 32);
+      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * a.mx_scale_stride + hidden / 32);
       xsrs = make_rsrc(a.mx_scale + row0 * a.mx_scale_stride, sbytes);
       // one lane of each quad writes its block's scale byte
       xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)a.mx_scale_stride + (uint32_t)lane / 4u : kOOB;
     }
     if constexpr (OUT16) {
-      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + a.hidden) * 2);
+      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + hidden) * 2);
       ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + lofs;
     }
@@ -284,8 +293,8 @@ void fused_vec_kernel(FusedArgs a) {
         eok = row_ok; elo = 0; ehi = 8 - delta;
       } else if (t > 0 && lane == tl) {
         eok = row_ok; elo = 8 - t; ehi = 8;
-        eb = 2u * (uint32_t)a.hidden - 16u;
-        eq = (uint32_t)a.hidden - 8u;
+        eb = 2u * (uint32_t)hidden - 16u;
+        eq = (uint32_t)hidden - 8u;
       }
       if (eok) {
         exoff = xrow + eb;
@@ -359,7 +368,7 @@ void fused_vec_kernel(FusedArgs a) {
 #pragma unroll
         for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
           if (g >= a.nparts) break;
-          const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * a.x_stride, xbytes);
+          const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * x_stride, xbytes);
           u32x4 pv[G], tpv = {};
 #pragma unroll
           for (int i = 0; i < G; ++i) {
@@ -590,6 +599,8 @@ void fused_vec_kernel(FusedArgs a) {
         store8<SAUX>(q, ors, eooff);
       }
     }
+    g += grid;
+    if (g >= a.ngroups) break;
   }
   if constexpr (TIMELINE) {
     __builtin_amdgcn_s_waitcnt(0);  // every load and store of this wave has completed
