@@ -316,6 +316,8 @@ def main():
                          "forced bench-library ones (CFG = lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags)")
     ap.add_argument("--hot", action="store_true",
                     help="with --ab: one buffer set, the same every call (resident in the Infinity Cache)")
+    ap.add_argument("--ab-rows", type=int, default=B, metavar="ROWS",
+                    help="with --ab: rows per call (default 4096)")
     ap.add_argument("--layout", default="0,0", metavar="OFF,PAD",
                     help="with --ab, or --profile of the fused op: input and residual rows start OFF elements "
                          "into rows of H + OFF + PAD elements (rows off the 128-byte grid take the "
@@ -346,7 +348,7 @@ def main():
         return sweep(torch, abi, op, args)
     if args.ab:
         off, pad = (int(v) for v in args.layout.split(","))
-        return ab_trials(torch, abi, op, args.ab, args.hot, off, pad)
+        return ab_trials(torch, abi, op, args.ab, args.hot, off, pad, rows=args.ab_rows)
     if args.ceiling:
         hs = [int(v) for v in args.ceiling.split(",")]
         rows = ceiling(torch, abi, hp_rms_norm_amd, hs, max(args.steps, 10), args.warmup,
@@ -447,8 +449,8 @@ def time_rotating(torch, call, n, steps, warmup):
     return e0.elapsed_time(e1) * 1e3 / ncalls
 
 
-def ab_trials(torch, abi, op, specs, hot, off=0, pad=0, trials=7):
-    """A/B of the fused op at (4096, H) bf16: the table's configuration and
+def ab_trials(torch, abi, op, specs, hot, off=0, pad=0, trials=7, rows=B):
+    """A/B of the fused op at (rows, H) bf16 (rows = 4096 by default): the table's configuration and
     forced configurations of the bench library, timed in one process in
     `trials` interleaved rounds (the order reversed every other round); each
     timing is back-to-back calls between one HIP event pair, over buffer sets
@@ -472,18 +474,18 @@ def ab_trials(torch, abi, op, specs, hot, off=0, pad=0, trials=7):
     stream = torch.cuda.current_stream().cuda_stream
     for h, forced in plan:
         stride = h + off + pad
-        n = 1 if hot else cold_sets(B, stride)
-        bufs = [torch.empty((2, B, stride), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
+        n = 1 if hot else cold_sets(rows, stride)
+        bufs = [torch.empty((2, rows, stride), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
         sets = [b[:, :, off:off + h] for b in bufs]
         w = (1 + 0.1 * torch.randn(h, device="cuda:0")).to(torch.bfloat16)
-        base = abi.select_config(B, h, abi.DTYPE_BF16)
+        base = abi.select_config(rows, h, abi.DTYPE_BF16)
 
         def table_call(i):
             op(sets[i][0], w, sets[i][1], EPS)
 
         def forced_call(cfg):
             return lambda i: abi.BENCH.fused_add_rmsnorm(sets[i][0].data_ptr(), w.data_ptr(), sets[i][1].data_ptr(),
-                                                         B, h, stride, stride, abi.DTYPE_BF16, EPS, stream, cfg)
+                                                         rows, h, stride, stride, abi.DTYPE_BF16, EPS, stream, cfg)
         runs = [("table", table_call)] + [(c, forced_call(cfg)) for c, cfg in forced]
         res = {k: [] for k, _ in runs}
         for t in range(trials):
@@ -494,9 +496,9 @@ def ab_trials(torch, abi, op, specs, hot, off=0, pad=0, trials=7):
             m = statistics.median(v)
             cfg = "table " + ",".join(str(x) for x in (base.lanes_per_row, base.vec_per_lane, base.lds_vec_per_lane,
                                                         base.block_threads, base.flags)) if k == "table" else k
-            print(json.dumps({"hidden": h, "rows": B, "row_offset": off, "row_stride": stride, "hot": hot,
+            print(json.dumps({"hidden": h, "rows": rows, "row_offset": off, "row_stride": stride, "hot": hot,
                               "cfg": cfg, "us": round(m, 2),
-                              "gbs": round(fused_bytes(B, h) / m / 1e3, 1), "vs_table": round(m / tab - 1, 4),
+                              "gbs": round(fused_bytes(rows, h) / m / 1e3, 1), "vs_table": round(m / tab - 1, 4),
                               "spread": round((max(v) - min(v)) / m, 4)}), flush=True)
         del sets, bufs
         torch.cuda.empty_cache()

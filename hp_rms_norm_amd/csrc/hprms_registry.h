@@ -124,7 +124,8 @@ struct FusedEntry {
 // candidates of the table's rows (bf16): +256 = held to 8 waves per SIMD,
 // +2048 = one workgroup per CU (the launch reserves 96 KiB of LDS), other
 // cache policies of the 3K-12K rows (sc1 on the stores alone: +16; sc0 on the
-// stores: +8192; no nt on the loads, the stores or either)
+// stores: +8192; no nt on the loads, the stores or either), and the latency
+// rows of 4K-8K with the weight loaded with the row (flags 3)
 #define HPRMS_CANDIDATE_SHAPES(X, DT, MODE)                                                          \
   X(DT, MODE, 32, 4, 0, 256, 135) X(DT, MODE, 64, 4, 0, 256, 131) X(DT, MODE, 128, 2, 0, 256, 135)    \
   X(DT, MODE, 128, 4, 0, 256, 135) X(DT, MODE, 128, 4, 0, 256, 159) X(DT, MODE, 128, 4, 0, 256, 391) \
@@ -140,7 +141,8 @@ struct FusedEntry {
   X(DT, MODE, 256, 2, 0, 256, 8339) X(DT, MODE, 512, 2, 0, 512, 8215)                                        \
   X(DT, MODE, 256, 2, 0, 256, 128) X(DT, MODE, 256, 2, 0, 256, 129) X(DT, MODE, 256, 2, 0, 256, 130)           \
   X(DT, MODE, 32, 4, 0, 256, 128) X(DT, MODE, 32, 4, 0, 256, 129) X(DT, MODE, 32, 4, 0, 256, 130)              \
-  X(DT, MODE, 512, 2, 0, 512, 4) X(DT, MODE, 512, 2, 0, 512, 5) X(DT, MODE, 512, 2, 0, 512, 6)
+  X(DT, MODE, 512, 2, 0, 512, 4) X(DT, MODE, 512, 2, 0, 512, 5) X(DT, MODE, 512, 2, 0, 512, 6)          \
+  X(DT, MODE, 256, 2, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 3)
 
 // the bandwidth table's rows with the output phase's separate unpack (+4096)
 #define HPRMS_SHARED_UNPACK_SHAPES(X, DT, MODE)                                                        \
