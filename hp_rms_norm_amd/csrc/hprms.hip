@@ -655,7 +655,8 @@ int launch_stream(const StreamArgs& base, bool flat, hipStream_t stream) {
     if (grid < 1) grid = 1;
     if (grid > kMaxGrid)
       return fail(HPRMS_E_RANGE, "streamer: %lld elements exceed the grid limit", (long long)(a.rows * a.hidden));
-    stream_chunk_kernel<DT, OP, kUnroll, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(a);
+    stream_chunk_kernel<DT, OP, kUnroll, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(a.in, a.out,
+                                                                                                 a.nvec, a);
   } else {
     // strided or misaligned rows: 4 KiB chunks of a row per workgroup
     constexpr int kBlock = 256;
@@ -663,7 +664,8 @@ int launch_stream(const StreamArgs& base, bool flat, hipStream_t stream) {
     const int64_t chunks = a.nvec > 0 ? (a.nvec + kBlock - 1) / kBlock : 1;
     const int64_t units = a.rows * chunks;
     const int64_t grid = units < kMaxGrid ? units : kMaxGrid;
-    stream_rows_kernel<DT, OP, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(a);
+    stream_rows_kernel<DT, OP, kBlock><<<dim3((unsigned)grid), dim3(kBlock), 0, stream>>>(
+        a.in, a.out, a.rows, a.in_stride, a.out_stride, (int32_t)a.hidden, (int32_t)a.nvec, (int32_t)grid);
   }
   return check_launch("streamer kernel");
 }

@@ -861,20 +861,23 @@ __device__ __forceinline__ uint16_t stream_op1(uint16_t h) {
 // 1 KiB), all loads before all stores, non-temporal both ways.  One
 // workgroup per chunk, no grid-stride loop.
 template <int DT, int OP, int UNROLL, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void stream_chunk_kernel(StreamArgs a) {
-  const u32x4* in = reinterpret_cast<const u32x4*>(a.in);
-  u32x4* out = reinterpret_cast<u32x4*>(a.out);
+// in, out and the vector count lead the arguments, so that gfx950 preloads
+// them into SGPRs (the first loads wait for no scalar memory load)
+__global__ __launch_bounds__(BLOCK) void stream_chunk_kernel(const uint16_t* in16, uint16_t* out16, int64_t nvec,
+                                                             StreamArgs a) {
+  const u32x4* in = reinterpret_cast<const u32x4*>(in16);
+  u32x4* out = reinterpret_cast<u32x4*>(out16);
   const int64_t base = (int64_t)blockIdx.x * (UNROLL * BLOCK) + threadIdx.x;
   u32x4 v[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
     const int64_t i = base + u * BLOCK;
-    if (i < a.nvec) v[u] = __builtin_nontemporal_load(in + i);
+    if (i < nvec) v[u] = __builtin_nontemporal_load(in + i);
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
     const int64_t i = base + u * BLOCK;
-    if (i < a.nvec) {
+    if (i < nvec) {
       u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[j] = stream_op2<DT, OP>(v[u][j]);
@@ -883,8 +886,8 @@ __global__ __launch_bounds__(BLOCK) void stream_chunk_kernel(StreamArgs a) {
   }
   if (blockIdx.x == gridDim.x - 1) {  // elements past the last whole vector
     const int64_t total = a.rows * a.hidden;
-    for (int64_t e = a.nvec * 8 + threadIdx.x; e < total; e += BLOCK)
-      a.out[e] = stream_op1<DT, OP>(a.in[e]);
+    for (int64_t e = nvec * 8 + threadIdx.x; e < total; e += BLOCK)
+      out16[e] = stream_op1<DT, OP>(in16[e]);
   }
 }
 
@@ -892,30 +895,34 @@ __global__ __launch_bounds__(BLOCK) void stream_chunk_kernel(StreamArgs a) {
 // (row, chunk): BLOCK lanes, one 16-byte vector each (4 KiB per workgroup, as
 // the flat kernel), accesses through buffer resources sized to the row
 // (unaligned 16-byte accesses are legal here, see fused_vec_kernel), so the
-// range check drops everything past the row's whole vectors (a.nvec per
+// range check drops everything past the row's whole vectors (nvec per
 // row).  hidden % 8 != 0: the lane holding the last whole vector also moves
 // the 16 bytes that end at the row's end; they overlap that vector, whose
 // elements it writes again with the same values (both ops are idempotent, so
 // this holds in place too).  hidden < 8: the first hidden lanes move one
 // element each.
 template <int DT, int OP, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void stream_rows_kernel(StreamArgs a) {
-  const int64_t chunks = a.nvec > 0 ? (a.nvec + BLOCK - 1) / BLOCK : 1;
-  const uint32_t rowbytes = (uint32_t)a.hidden * 2u;
-  const int tcount = (int)(a.hidden - a.nvec * 8);
-  for (int64_t u = blockIdx.x; u < a.rows * chunks; u += gridDim.x) {
+// every field leads as a scalar argument (preloaded into SGPRs on gfx950),
+// with the launched grid, which never exceeds rows * chunks
+__global__ __launch_bounds__(BLOCK) void stream_rows_kernel(const uint16_t* in16, uint16_t* out16, int64_t rows,
+                                                            int64_t in_stride, int64_t out_stride, int32_t hidden,
+                                                            int32_t nvec, int32_t grid) {
+  const int64_t chunks = nvec > 0 ? (nvec + BLOCK - 1) / BLOCK : 1;
+  const uint32_t rowbytes = (uint32_t)hidden * 2u;
+  const int tcount = (int)(hidden - nvec * 8);
+  for (int64_t u = blockIdx.x; u < rows * chunks; u += grid) {
     const int64_t row = u / chunks;
     const int64_t v = (u - row * chunks) * BLOCK + threadIdx.x;
-    const __amdgpu_buffer_rsrc_t irs = make_rsrc(a.in + row * a.in_stride, rowbytes);
-    const __amdgpu_buffer_rsrc_t ors = make_rsrc(a.out + row * a.out_stride, rowbytes);
-    if (a.nvec == 0) {  // hidden < 8
+    const __amdgpu_buffer_rsrc_t irs = make_rsrc(in16 + row * in_stride, rowbytes);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(out16 + row * out_stride, rowbytes);
+    if (nvec == 0) {  // hidden < 8
       const uint32_t off = (uint32_t)threadIdx.x * 2u;
       __builtin_amdgcn_raw_buffer_store_b16(stream_op1<DT, OP>(__builtin_amdgcn_raw_buffer_load_b16(irs, off, 0, 0)),
                                             ors, off, 0, 0);
       continue;
     }
-    const bool ok = v < a.nvec;
-    const bool tail = tcount > 0 && v == a.nvec - 1;
+    const bool ok = v < nvec;
+    const bool tail = tcount > 0 && v == nvec - 1;
     const uint32_t off = ok ? (uint32_t)v * 16u : kOOB;
     const uint32_t toff = tail ? rowbytes - 16u : kOOB;
     const u32x4 x = load16<kAuxNT>(irs, off);
