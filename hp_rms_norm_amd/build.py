@@ -33,12 +33,13 @@ BENCH_LIB = os.path.join(PKG, "libhprms_bench.so")
 ARCH = "gfx950"
 # Packed fp32 VALU ops stay off: plain fp32 code is what the kernels need, and
 # it keeps the generated arithmetic to ordinary IEEE binary32 instructions.
-# The first 14 dwords of every kernel's argument block are preloaded into
-# SGPRs at wave launch (gfx950 kernarg preload): the fused kernels put what
-# their first loads need there.
+# The leading scalar arguments of every kernel (up to 10 arguments within the
+# first 14 dwords of the argument block) are preloaded into SGPRs at wave
+# launch (gfx950 kernarg preload): the fused kernels put what their row loop
+# needs there.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-             "-mllvm", "-amdgpu-kernarg-preload-count=8"]
+             "-mllvm", "-amdgpu-kernarg-preload-count=10"]
 
 
 def _report(cmd, p_returncode, text):

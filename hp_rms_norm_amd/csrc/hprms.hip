@@ -380,6 +380,9 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
         if (!aligned16(p.parts[g])) return false;
   }
   if ((int64_t)c.lanes_per_row * c.vec_per_lane < p.hidden / 8) return false;  // whole vectors
+  // the kernels take the input and residual (plain RMSNorm: output) row strides as 32-bit scalars
+  if (p.x_stride > INT32_MAX || (has_res(p.mode) && p.res_stride > INT32_MAX)) return false;
+  if (p.mode == 1 && p.out_stride > INT32_MAX) return false;
   // every buffer resource of a row group spans < 2^31 bytes
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   int64_t smax = p.x_stride > p.out_stride ? p.x_stride : p.out_stride;
@@ -420,7 +423,7 @@ struct Phase {
 Phase phase16(const void* p, int64_t stride) { return {(uint32_t)(((uintptr_t)p >> 1) & 7u), (uint32_t)(stride & 7)}; }
 Phase phase8(const void* p, int64_t stride) { return {(uint32_t)((uintptr_t)p & 7u), (uint32_t)(stride & 7)}; }
 
-// Shifted rows (the tail variant's FusedArgs::shift_*), modes 0-4 from 513
+// Shifted rows (the tail variant's shift phases), modes 0-4 from 513
 // whole vectors up, when no stream of the call (the weight aside: it stays in
 // L2) has all its rows on 16-byte boundaries.  The rows are shifted to the
 // phase of the first written stream (input / residual in place, the output
@@ -478,7 +481,7 @@ Phase shift_phase(const Problem& p) {
   return s[0];
 }
 
-// Rotated rows (FusedArgs::rot_*, the off-grid variants of modes 0, 1, 3, 4).  With
+// Rotated rows (the rotation phases of the off-grid variants of modes 0, 1, 3, 4).  With
 // rows off the 128-byte grid, a wave's 1 KiB access to a row shares its first
 // and last cache line with the neighbouring accesses: such half-written lines
 // cost 9-13% against whole ones (a flat two-stream in-place rewrite 16 bytes
@@ -577,8 +580,9 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
     return fail(HPRMS_E_INVALID, "flags bit 9 (timeline) needs hprms_bench_fused_timeline and its buffer");
   if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
     return fail(HPRMS_E_INVALID,
-                "MX output needs 2-byte aligned input, residual and weight and a row group's rows "
-                "(strides times rows per workgroup) within 2 GiB");
+                "MX output needs 2-byte aligned input, residual and weight, input and residual row "
+                "strides below 2^31 elements and a row group's rows (strides times rows per "
+                "workgroup) within 2 GiB");
   if (c.tier != 3 && !vec_fits(p, c)) {
     if (forced && forced->tier != 0)
       return fail(HPRMS_E_INVALID,
@@ -601,11 +605,13 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
 
   // the kernel's leading scalar arguments (preloaded into SGPRs), then FusedArgs
   const uint16_t* x_rows = (const uint16_t*)p.x;
-  uint16_t* res_rows = (uint16_t*)p.res;
+  // plain RMSNorm has no residual: the output takes its place
+  uint16_t* res_rows = (uint16_t*)(p.mode == 1 ? p.out : p.res);
+  const int64_t res_stride = p.mode == 1 ? p.out_stride : p.res_stride;
   const uint16_t* weight = (const uint16_t*)p.w;
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   FusedArgs a = {};
-  a.ngroups = (p.rows + rpb - 1) / rpb;
+  const int64_t ngroups = (p.rows + rpb - 1) / rpb;
   a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x : p.out);
   a.res_out = (uint16_t*)p.res_out;
   a.res_out_stride = p.res_out_stride;
@@ -617,27 +623,19 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   a.mx_scale = (uint8_t*)p.mx_scales;
   a.mx_scale_stride = p.mx_scale_stride;
   a.out_stride = p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x_stride : p.out_stride;
-  if (c.flags & 64) {
-    const Phase ph = shift_phase(p);
-    a.shift_base = ph.base;
-    a.shift_step = ph.step;
-  }
-  if (c.flags & 32) {
-    const Phase rot = rot_phase(p);
-    a.rot_base = rot.base;
-    a.rot_step = rot.step;
-  }
-  a.hidden_f = (float)p.hidden;
-  a.eps = (float)p.eps;
+  const Phase shift = (c.flags & 64) ? shift_phase(p) : Phase{0, 0};
+  const Phase rot = (c.flags & 32) ? rot_phase(p) : Phase{0, 0};
+  const uint32_t phases = pack_phases(rot.base, rot.step, shift.base, shift.step);
   a.timeline = p.timeline;
 
-  int64_t grid = a.ngroups;
+  int64_t grid = ngroups;
   if (c.grid_blocks > 0 && c.grid_blocks < grid) grid = c.grid_blocks;
   if (grid > kMaxGrid) grid = kMaxGrid;
   // flags bit 11: 96 KiB of (unused) dynamic LDS, so one workgroup holds a CU
   const unsigned lds = (c.flags & 2048) ? 96u * 1024u : 0u;
   hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(c.block_threads), lds, stream, x_rows, res_rows, weight,
-                     p.rows, p.x_stride, p.res_stride, (int32_t)p.hidden, (int32_t)grid, a);
+                     p.rows, (int32_t)p.x_stride, (int32_t)res_stride, (int32_t)p.hidden, (int32_t)grid, phases,
+                     (float)p.eps, a);
   return check_launch("fused rmsnorm kernel");
 }
 

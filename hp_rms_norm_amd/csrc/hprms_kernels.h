@@ -32,14 +32,14 @@
 // runtime, which runs them in unaligned mode, and hipcc relies on the same for
 // ordinary code).  In modes 0, 1, 3 and 4 these variants also rotate each
 // row's lane mapping: with the row's first body vector rp 16-byte steps past a
-// 128-byte boundary of the rotation stream (FusedArgs::rot_*; rp = 0 when that
+// 128-byte boundary of the rotation stream (`phases`, below; rp = 0 when that
 // phase is not a multiple of 16 bytes), slot k * LPR + lane holds body vector
 // k * LPR + lane - rp and the first rp slots the row's last rp vectors, so
 // every wave's 1 KiB access starts on a cache line and writes whole lines
 // (lines written in two parts by two accesses cost 9-13% at a 16-byte offset).
 // Bit 6 selects the tail variant (TAIL), for widths that are not a multiple
 // of 8 (hidden >= 8) and for shifted rows (hidden >= 16).  Row r is shifted by
-// delta = (shift_base + r * shift_step) mod 8 elements (both 0: no shift): the
+// delta = (shift base + r * shift step) mod 8 elements (`phases`; both 0: no shift): the
 // lanes' "body" vectors start at element 8j - delta (j >= 1 when delta > 0),
 // so a stream whose row r starts delta elements past a vector boundary (16
 // bytes; 8 bytes for the FP8 output) is accessed aligned; the elements before the first body
@@ -83,19 +83,25 @@
 
 namespace hprms {
 
-// The kernel's arguments.  What a row group needs before its first loads
-// comes first, as scalar arguments (fused_vec_kernel's x_rows ... grid):
-// hipcc's -amdgpu-kernarg-preload-count has gfx950 preload the first 14 dwords
-// of the argument block into SGPRs at wave launch, so in the aligned kernels
-// the first row loads wait for no scalar memory load (a copy kernel measured
-// 0.2 us less per launch at 16-256 MB with its arguments preloaded; a by-value
-// struct is never preloaded).  FusedArgs holds the rest:
+// The kernel's arguments.  Everything the in-place op and the plain RMSNorm
+// (MODES 0 and 1) read comes first, as scalar arguments (fused_vec_kernel's x_rows ... eps, 14 dwords):
+// hipcc's -amdgpu-kernarg-preload-count has gfx950 preload up to the first 14
+// dwords of the argument block into SGPRs at wave launch, so its first row
+// loads wait for no scalar memory load (the compiler waits for every scalar
+// load the row loop uses before the loop's first iteration; a copy kernel
+// measured 0.2 us less per launch at 16-256 MB with its arguments preloaded;
+// a by-value struct is never preloaded).  The row strides are 32-bit (the
+// host sends larger strides to the general kernel); the off-grid variants'
+// per-row phases take one dword:
+__host__ __device__ constexpr uint32_t pack_phases(uint32_t rot_base, uint32_t rot_step, uint32_t shift_base,
+                                                   uint32_t shift_step) {
+  return (rot_base & 127u) | (rot_step & 127u) << 8 | (shift_base & 7u) << 16 | (shift_step & 7u) << 24;
+}
+
+// FusedArgs holds the rest:
 struct FusedArgs {
   uint16_t* out;         // 16-bit output rows (MODES 1, 3, 4; MODE 0: == x)
-  int64_t ngroups;       // ceil(rows / RPB); the grid never exceeds it
   int64_t out_stride;
-  float hidden_f;
-  float eps;
   uint8_t* q;            // MODES 2, 5, 6: quantised output rows
   float* scale;          // MODE 2: per-row scales
   int64_t q_stride;      // MODES 2, 5, 6: bytes between quantised rows
@@ -105,13 +111,7 @@ struct FusedArgs {
   const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
   uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes, hidden / 32 per row
   int64_t mx_scale_stride;  // bytes between scale rows
-  uint32_t shift_base;   // tail variant: row r is shifted by (shift_base + r * shift_step) mod 8 elements
-  uint32_t shift_step;
   int64_t* timeline;     // FLAGS bit 9 only (bench library): 4 values per workgroup
-  // FLAGS bit 5 (modes 0, 1, 3, 4): the rotation stream's row r starts (rot_base +
-  // r * rot_step) mod 128 bytes past a 128-byte boundary (both 0: no rotation)
-  uint32_t rot_base;
-  uint32_t rot_step;
 };
 
 // Waves per SIMD the compiler must leave room for: the tail variant of the
@@ -126,12 +126,14 @@ constexpr int kMinWavesPerEU = ((FLAGS & 256) != 0 || ((FLAGS & 64) != 0 && BLOC
 template <int DT, int MODE, int LPR, int VPL, int LDSV, int BLOCK, int FLAGS, int WLATE>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<FLAGS, BLOCK, VPL>)))
 void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the output; MODE 4: part 0)
-                      uint16_t* res_rows,      // residual rows (every mode but 1)
+                      uint16_t* res_rows,      // residual rows (MODE 1: the output rows)
                       const uint16_t* w,       // weight [hidden]
                       int64_t rows,
-                      int64_t x_stride, int64_t res_stride,  // elements
+                      int32_t x_stride, int32_t res_stride,  // elements
                       int32_t hidden,
-                      int32_t grid,            // workgroups launched (<= FusedArgs::ngroups)
+                      int32_t grid,            // workgroups launched (<= ceil(rows / RPB))
+                      uint32_t phases,         // off-grid variants: rotation and shift (pack_phases)
+                      float eps,
                       FusedArgs a) {
   const int32_t nvec = hidden >> 3;  // whole 16-byte vectors per row
   static_assert(LPR >= 16 && (LPR & (LPR - 1)) == 0 && BLOCK % LPR == 0 && BLOCK % 64 == 0, "shape");
@@ -148,7 +150,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
   constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // shifted rows, head and tail vectors
   // rows off the 128-byte grid: each row's lane mapping rotated so that every
-  // wave's 1 KiB access starts on a cache line (FusedArgs::rot_*)
+  // wave's 1 KiB access starts on a cache line (`phases` bits 0-14)
   // (not the FP8 and MX outputs: the FP8 form's 1024 x 2 tail kernel,
   // held to 64 VGPRs, would spill, and an MX block must stay one quad's)
   constexpr bool ROT = (FLAGS & 32) != 0 && !MX && MODE != 2;
@@ -191,8 +193,14 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < nvec;
 
   int buf = 0;
-  // the grid never exceeds ngroups, so every workgroup has a first row group
-  // and ngroups (not preloaded) is first needed at its end
+  // the grid never exceeds the row group count, so every workgroup has a
+  // first row group
+  const int64_t ngroups = (rows + RPB - 1) / RPB;
+  // hidden as binary32 (exact: 1 <= hidden < 2^24), built with integer
+  // operations so that it stays in an SGPR (a conversion would take a VGPR)
+  const uint32_t hb = (uint32_t)hidden;
+  const int he = 31 - __builtin_clz(hb);
+  const float hidden_f = __builtin_bit_cast(float, (uint32_t)(127 + he) << 23 | ((hb << (23 - he)) & 0x7fffffu));
   for (int64_t g = blockIdx.x;;) {
     const int64_t row0 = g * RPB;
     const int64_t left = rows - row0;
@@ -204,7 +212,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     int delta = 0, j0 = 0, nb = nvec, t = 0;
     uint32_t wshift = 0;
     if constexpr (TAIL) {
-      delta = (int)((a.shift_base + (uint32_t)(row0 + rib) * a.shift_step) & 7u);
+      delta = (int)((((phases >> 16) & 7u) + (uint32_t)(row0 + rib) * (phases >> 24)) & 7u);
       j0 = delta > 0 ? 1 : 0;
       const int jend = (hidden + delta) >> 3;
       nb = jend - j0;  // >= 1: hidden >= 8, and >= 16 when shifted
@@ -217,7 +225,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     // and the first rp slots (k = 0, lane < rp) the row's last rp vectors
     int rp = 0;
     if constexpr (ROT) {
-      const uint32_t ph = (a.rot_base + (uint32_t)(row0 + rib) * a.rot_step + wshift) & 127u;
+      const uint32_t ph = ((phases & 127u) + (uint32_t)(row0 + rib) * ((phases >> 8) & 127u) + wshift) & 127u;
       if ((ph & 15u) == 0 && nb >= 8) rp = (int)(ph >> 4);
     }
     const uint32_t lofs = (uint32_t)(lane - rp) * 16u;        // lane * 16 without rotation
@@ -259,7 +267,12 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       // one lane of each quad writes its block's scale byte
       xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)a.mx_scale_stride + (uint32_t)lane / 4u : kOOB;
     }
-    if constexpr (OUT16) {
+    if constexpr (MODE == 1) {
+      // no residual: its (preloaded) arguments carry the output rows
+      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * res_stride + hidden) * 2);
+      ors = make_rsrc(res_rows + row0 * res_stride, obytes);
+      ooff = (uint32_t)rib * (uint32_t)res_stride * 2u + lofs;
+    } else if constexpr (OUT16) {
       const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + hidden) * 2);
       ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
       ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + lofs;
@@ -466,7 +479,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       for (int j = 1; j < WPR; ++j) tot += red[buf][w0 + j];
       buf ^= 1;
     }
-    const float inv = 1.0f / __builtin_sqrtf(tot / a.hidden_f + a.eps);
+    const float inv = 1.0f / __builtin_sqrtf(tot / hidden_f + eps);
 
     if constexpr (MX) {
       constexpr int EMAX = MODE == 5 ? 8 : 2;
@@ -600,7 +613,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       }
     }
     g += grid;
-    if (g >= a.ngroups) break;
+    if (g >= ngroups) break;
   }
   if constexpr (TIMELINE) {
     __builtin_amdgcn_s_waitcnt(0);  // every load and store of this wave has completed

@@ -9,8 +9,8 @@
 
 namespace hprms {
 
-typedef void (*fused_fn)(const uint16_t*, uint16_t*, const uint16_t*, int64_t, int64_t, int64_t, int32_t, int32_t,
-                         FusedArgs);
+typedef void (*fused_fn)(const uint16_t*, uint16_t*, const uint16_t*, int64_t, int32_t, int32_t, int32_t, int32_t,
+                         uint32_t, float, FusedArgs);
 
 struct FusedEntry {
   int dtype, mode, lpr, vpl, ldsv, block, flags;

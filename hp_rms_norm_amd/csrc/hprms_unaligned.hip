@@ -7,7 +7,7 @@
 // and such partial lines written with sc1 measured 13-24% slower at 16K-32K
 // (4096 rows, row stride hidden + 8).  In modes 0, 1, 3 and 4 the variants
 // rotate each row's lane mapping so that the chunks start on cache lines
-// (FusedArgs::rot_*).  Kept in its own translation unit so that the
+// (the kernel's rotation phases).  Kept in its own translation unit so that the
 // build compiles it in parallel with hprms.hip; hprms_tail.hip holds the same
 // shapes with the tail vector for hidden % 8 != 0.
 #include <hip/hip_runtime.h>

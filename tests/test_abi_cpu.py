@@ -300,6 +300,12 @@ def test_mx_entry_rejects_bad_arguments():
     assert "2 GiB" in abi.last_error()
     assert L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, 256, 128, 1 << 20, 256, 256, abi.MX_FP4_E2M1, 0, 1e-6,
                                         None) == abi.HPRMS_OK
+    # the vector kernels take 32-bit input and residual row strides, also with one row per workgroup
+    assert L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, 32768, 32768, 1024, 1 << 31, 32768, abi.MX_FP4_E2M1, 0,
+                                        1e-6, None) == abi.HPRMS_E_INVALID
+    assert "2^31" in abi.last_error()
+    assert L.hprms_fused_add_rmsnorm_mx(0, 0, 0, 0, 0, 0, 32768, 32768, 1024, (1 << 31) - 8, 32768,
+                                        abi.MX_FP4_E2M1, 0, 1e-6, None) == abi.HPRMS_OK
     for mode in (abi.MODE_MXFP8, abi.MODE_MXFP4):
         c = abi.select_config(4096, 4096, abi.DTYPE_BF16, mode)
         assert c.tier in (1, 2) and c.lanes_per_row % 4 == 0

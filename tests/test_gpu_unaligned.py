@@ -533,8 +533,11 @@ def strided_rows(t, stride):
 # row stride of 2^27 elements: its table shape puts 16 rows in a workgroup, whose buffer
 # resources would span 4 GiB, so the vector shapes are refused and the register kernel takes
 # the call.  1001 with a stride of 2^28 stays on the vector tier: with 2 rows the latency
-# table gives one row per workgroup, so huge strides fit its resources.
-GENERAL_CASES = [(7, 5, 7), (70001, 3, 70001), (101, 2, 1 << 27), (1001, 2, 1 << 28)]
+# table gives one row per workgroup, so huge strides fit its resources.  The vector kernels
+# take 32-bit row strides: 4096 with 2^31 - 8 (the largest, rows 16 bytes off the grid) stays
+# on the vector tier, 1001 with 2^31 goes to the register kernel (4 GiB buffers).
+GENERAL_CASES = [(7, 5, 7), (70001, 3, 70001), (101, 2, 1 << 27), (1001, 2, 1 << 28), (4096, 2, (1 << 31) - 8),
+                 (1001, 2, 1 << 31)]
 
 
 @pytest.mark.parametrize("hidden,rows,stride", GENERAL_CASES)
