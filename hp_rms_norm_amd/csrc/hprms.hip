@@ -486,11 +486,15 @@ Phase shift_phase(const Problem& p) {
 // and last cache line with the neighbouring accesses: such half-written lines
 // cost 9-13% against whole ones (a flat two-stream in-place rewrite 16 bytes
 // off, 4096 x 4K-32K bf16), and the rows' own measured 10-17% at 16K-32K
-// before the rotation.  The kernel rotates each row's lane mapping so
-// that every access starts on a cache line of one written stream: the stream
-// the shift aligns when rows are shifted, otherwise the first written stream
-// whose rows are 16-byte aligned but off the grid.  Returns that stream's
-// 128-byte phase {base, step} in bytes, or {0, 0} (no rotation).
+// before the rotation.  The kernel rotates each row's lane mapping so that
+// every access starts on a 512-byte boundary of one written stream (4096 rows
+// at stride H + 8: 0.1-1% faster than 128-byte boundaries at 16K-32K; 1 KiB
+// boundaries measured up to 1% faster still, but would make the result's
+// bits depend on where torch's allocator, which aligns to 512 bytes, puts a
+// buffer): the stream the shift aligns when rows are shifted, otherwise the
+// first written stream whose rows are 16-byte aligned but off the 128-byte
+// grid, else off the 512-byte grid.  Returns that stream's phase
+// {base, step} modulo 512 bytes, or {0, 0} (no rotation).
 Phase rot_phase(const Problem& p) {
   const Phase none = {0, 0};
   if (p.mode == 2 || p.mode > 4) return none;
@@ -503,20 +507,37 @@ Phase rot_phase(const Problem& p) {
     case 3: w[n++] = {p.out, p.out_stride}; w[n++] = {p.res_out, p.res_out_stride}; break;
     default: w[n++] = {p.out, p.out_stride}; w[n++] = {p.res, p.res_stride}; break;
   }
-  auto phase128 = [](const Stream& s) {
-    return Phase{(uint32_t)((uintptr_t)s.ptr & 127u), (uint32_t)((s.stride * 2) & 127)};
+  auto phase512 = [](const Stream& s) {
+    return Phase{(uint32_t)((uintptr_t)s.ptr & 511u), (uint32_t)((s.stride * 2) & 511)};
   };
-  if (p.hidden % 8 != 0 || !(shift_phase(p) == none)) return phase128(w[0]);  // the shifted stream
+  if (p.hidden % 8 != 0 || !(shift_phase(p) == none)) return phase512(w[0]);  // the shifted stream
+  // 16-byte aligned rows, not all on a `grid`-byte boundary
+  auto off = [](const Stream& s, int grid) {
+    return aligned16(s.ptr) && s.stride % 8 == 0 && !((uintptr_t)s.ptr % grid == 0 && (s.stride * 2) % grid == 0);
+  };
   for (int i = 0; i < n; ++i)
-    if (aligned16(w[i].ptr) && w[i].stride % 8 == 0 && !rows_aligned128(w[i].ptr, w[i].stride * 2))
-      return phase128(w[i]);
+    if (off(w[i], 128)) return phase512(w[i]);
+  for (int i = 0; i < n; ++i)
+    if (off(w[i], 512)) return phase512(w[i]);
   return none;
 }
 
-// the variant of a table entry for rows needs_unaligned() reports
+// The variant of a table entry for rows needs_unaligned() reports (or for
+// calls skip_sc1() takes off the sc1 bits).  The variants of modes 0, 1, 3
+// and 4 rotate their rows onto whole lines and keep the entry's sc1 bits for
+// calls past 16 Mi elements: with 4096 rows 16 bytes off the grid (stride
+// H + 8), sc1 and the 512-byte rotation measured 1.1-2.6% faster than
+// neither at 12K-32K.  The tail variants keep them only past 2048 whole
+// vectors (the 1024-lane rows: 1.1% faster at H = 32775; the LDS tier's tail
+// variant at 16K measured 0.3-0.9% slower with them).  Smaller calls, and the
+// FP8 and MX variants, which write partial lines (13-24% slower with sc1 at
+// 16K-32K), go without.
 int unaligned_flags(const Problem& p, int flags) {
-  return p.hidden % 8 != 0 || !(shift_phase(p) == Phase{0, 0}) ? HPRMS_TAIL_FLAGS(flags)
-                                                               : HPRMS_UNALIGNED_FLAGS(flags);
+  const bool tail = p.hidden % 8 != 0 || !(shift_phase(p) == Phase{0, 0});
+  const bool rotated = p.mode == 0 || p.mode == 1 || p.mode == 3 || p.mode == 4;
+  const bool keep_sc1 = rotated && p.rows * p.hidden > (int64_t(1) << 24) && (!tail || p.hidden / 8 > 2048);
+  const int f = keep_sc1 ? flags : flags & ~24;
+  return tail ? f | 96 : f | 32;
 }
 
 // Calls that update the residual in place and whose input and residual rows
@@ -752,10 +773,12 @@ int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms
   // the choice for rows off it
   table_config(rows, hidden, mode, hidden % 8 == 0, config);
   if (hidden % 8 != 0) {
-    if (config->tier != 3 && hidden >= 8 && mode <= 4)
-      config->flags = HPRMS_TAIL_FLAGS(config->flags);
-    else
+    if (config->tier != 3 && hidden >= 8 && mode <= 4) {
+      Problem p{mode, nullptr, nullptr, nullptr, nullptr, rows, hidden, hidden, hidden, hidden, dtype, 0.0};
+      config->flags = unaligned_flags(p, config->flags);
+    } else {
       config->tier = 3;
+    }
   }
   return HPRMS_OK;
 }

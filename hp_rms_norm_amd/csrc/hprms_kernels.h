@@ -32,11 +32,16 @@
 // runtime, which runs them in unaligned mode, and hipcc relies on the same for
 // ordinary code).  In modes 0, 1, 3 and 4 these variants also rotate each
 // row's lane mapping: with the row's first body vector rp 16-byte steps past a
-// 128-byte boundary of the rotation stream (`phases`, below; rp = 0 when that
-// phase is not a multiple of 16 bytes), slot k * LPR + lane holds body vector
-// k * LPR + lane - rp and the first rp slots the row's last rp vectors, so
-// every wave's 1 KiB access starts on a cache line and writes whole lines
-// (lines written in two parts by two accesses cost 9-13% at a 16-byte offset).
+// 512-byte boundary of the rotation stream (`phases`, below; a 16 * LPR-byte
+// boundary for LPR < 32; rp = 0 when that phase is not a multiple of 16
+// bytes), slot k * LPR + lane holds body vector k * LPR + lane - rp and the
+// first rp slots the row's last rp vectors, so every wave's 1 KiB access
+// starts on a 512-byte boundary and writes whole cache lines (lines written
+// in two parts by two accesses cost 9-13% at a 16-byte offset; 512-byte
+// boundaries rather than 128-byte ones measured up to 1% faster at 16K-32K).
+// The phase depends on a buffer's address only modulo 512 bytes, which
+// torch's allocator fixes, so the result's bits (the lanes' summation order)
+// do not depend on where a buffer was allocated.
 // Bit 6 selects the tail variant (TAIL), for widths that are not a multiple
 // of 8 (hidden >= 8) and for shifted rows (hidden >= 16).  Row r is shifted by
 // delta = (shift base + r * shift step) mod 8 elements (`phases`; both 0: no shift): the
@@ -84,18 +89,23 @@
 namespace hprms {
 
 // The kernel's arguments.  Everything the in-place op and the plain RMSNorm
-// (MODES 0 and 1) read comes first, as scalar arguments (fused_vec_kernel's x_rows ... eps, 14 dwords):
-// hipcc's -amdgpu-kernarg-preload-count has gfx950 preload up to the first 14
-// dwords of the argument block into SGPRs at wave launch, so its first row
-// loads wait for no scalar memory load (the compiler waits for every scalar
-// load the row loop uses before the loop's first iteration; a copy kernel
-// measured 0.2 us less per launch at 16-256 MB with its arguments preloaded;
-// a by-value struct is never preloaded).  The row strides are 32-bit (the
-// host sends larger strides to the general kernel); the off-grid variants'
-// per-row phases take one dword:
+// (MODES 0 and 1) read comes first, as scalar arguments (fused_vec_kernel's
+// x_rows ... eps, 14 dwords): hipcc's -amdgpu-kernarg-preload-count has gfx950
+// preload up to the first 14 dwords of the argument block into SGPRs at wave
+// launch, so their first row loads wait for no scalar memory load (the
+// compiler waits for every scalar load the row loop uses before the loop's
+// first iteration; a copy kernel measured 0.2 us less per launch at 16-256 MB
+// with its arguments preloaded; a by-value struct is never preloaded).  The
+// row strides are 32-bit (the host sends larger strides to the general
+// kernel); the off-grid variants' per-row phases take one dword:
+//   bits 0-9   rotation (FLAGS bit 5, modes 0, 1, 3, 4): the rotation
+//   bits 10-19 stream's row r starts (base + r * step) mod 512 bytes past a
+//              512-byte boundary (both < 512; both 0: no rotation)
+//   bits 20-22 shift (FLAGS bit 6): row r is shifted by (base + r * step)
+//   bits 24-26 mod 8 elements (both 0: no shift)
 __host__ __device__ constexpr uint32_t pack_phases(uint32_t rot_base, uint32_t rot_step, uint32_t shift_base,
                                                    uint32_t shift_step) {
-  return (rot_base & 127u) | (rot_step & 127u) << 8 | (shift_base & 7u) << 16 | (shift_step & 7u) << 24;
+  return (rot_base & 1023u) | (rot_step & 1023u) << 10 | (shift_base & 7u) << 20 | (shift_step & 7u) << 24;
 }
 
 // FusedArgs holds the rest:
@@ -150,7 +160,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
   constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // shifted rows, head and tail vectors
   // rows off the 128-byte grid: each row's lane mapping rotated so that every
-  // wave's 1 KiB access starts on a cache line (`phases` bits 0-14)
+  // wave's 1 KiB access starts on a 512-byte boundary (`phases` bits 0-19)
   // (not the FP8 and MX outputs: the FP8 form's 1024 x 2 tail kernel,
   // held to 64 VGPRs, would spill, and an MX block must stay one quad's)
   constexpr bool ROT = (FLAGS & 32) != 0 && !MX && MODE != 2;
@@ -212,21 +222,23 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     int delta = 0, j0 = 0, nb = nvec, t = 0;
     uint32_t wshift = 0;
     if constexpr (TAIL) {
-      delta = (int)((((phases >> 16) & 7u) + (uint32_t)(row0 + rib) * (phases >> 24)) & 7u);
+      delta = (int)((((phases >> 20) & 7u) + (uint32_t)(row0 + rib) * (phases >> 24)) & 7u);
       j0 = delta > 0 ? 1 : 0;
       const int jend = (hidden + delta) >> 3;
       nb = jend - j0;  // >= 1: hidden >= 8, and >= 16 when shifted
       t = hidden + delta - 8 * jend;  // elements after the last body vector
       wshift = 16u * (uint32_t)j0 - 2u * (uint32_t)delta;
     }
-    // ROT: the row's rotation rp, in vectors, from the 128-byte phase of its
-    // first body vector in the rotation stream (when that is a multiple of 16
-    // bytes); slot k * LPR + lane then holds body vector k * LPR + lane - rp,
-    // and the first rp slots (k = 0, lane < rp) the row's last rp vectors
+    // ROT: the row's rotation rp, in vectors, from the phase of its first
+    // body vector in the rotation stream modulo RG bytes (when that is a
+    // multiple of 16 bytes); slot k * LPR + lane then holds body vector
+    // k * LPR + lane - rp, and the first rp slots (k = 0, lane < rp < LPR)
+    // the row's last rp vectors
     int rp = 0;
     if constexpr (ROT) {
-      const uint32_t ph = ((phases & 127u) + (uint32_t)(row0 + rib) * ((phases >> 8) & 127u) + wshift) & 127u;
-      if ((ph & 15u) == 0 && nb >= 8) rp = (int)(ph >> 4);
+      constexpr uint32_t RG = LPR * 16 < 512 ? LPR * 16 : 512;
+      const uint32_t ph = ((phases & 1023u) + (uint32_t)(row0 + rib) * ((phases >> 10) & 1023u) + wshift) & (RG - 1);
+      if ((ph & 15u) == 0 && nb >= (int)(RG / 16)) rp = (int)(ph >> 4);
     }
     const uint32_t lofs = (uint32_t)(lane - rp) * 16u;        // lane * 16 without rotation
     const uint32_t wrap = (ROT && lane < rp) ? (uint32_t)nb : 0u;  // vectors added to slot k = 0

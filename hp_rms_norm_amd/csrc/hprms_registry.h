@@ -30,17 +30,20 @@ struct FusedEntry {
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
 
 // The unaligned variants of a shape: the same lanes, vectors and weight
-// timing, no sc1 bits (partial cache lines written with sc1 measured 13-24%
-// slower at 16K-32K), bit 5 set (which also rotates each row's lane mapping
-// onto the cache lines in modes 0, 1, 3 and 4); and the same with the tail
-// (bit 6), which costs about 30 VGPRs and so is kept apart from the rows that
-// need no tail.
-#define HPRMS_UNALIGNED_FLAGS(FLAGS) ((((FLAGS) & ~24) | 32))
-#define HPRMS_TAIL_FLAGS(FLAGS) ((((FLAGS) & ~24) | 96))
+// timing, bit 5 set (which also rotates each row's lane mapping onto 512-byte
+// boundaries in modes 0, 1, 3 and 4); and the same with the tail (bit 6),
+// which costs about 30 VGPRs and so is kept apart from the rows that need no
+// tail.  Every shape has them without the sc1 bits (the FP8 and MX variants,
+// which write partial cache lines, and calls small enough to stay in the
+// Infinity Cache); the rotated modes' shapes with sc1 also have them with it.
 #define HPRMS_UNALIGNED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
-  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, HPRMS_UNALIGNED_FLAGS(FLAGS))
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, ((FLAGS) & ~24) | 32)
 #define HPRMS_TAIL_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
-  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, HPRMS_TAIL_FLAGS(FLAGS))
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, ((FLAGS) & ~24) | 96)
+#define HPRMS_UNALIGNED_SC1_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) | 32)
+#define HPRMS_TAIL_SC1_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) | 96)
 
 // (lanes per row, vectors per lane, of which in LDS, block, flags).  flags 3 =
 // nt on the row loads and stores, 7 = the same with the weight loaded late,
@@ -91,6 +94,26 @@ struct FusedEntry {
 #define HPRMS_ALL_MODES(ENTRY, DT) HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_ALL_MODES_OFFGRID(ENTRY, DT) HPRMS_MODE0_OFFGRID_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
+
+// The shapes with sc1 bits among the lists of modes 0, 1, 3 and 4 (their
+// off-grid variants keep them for calls past the Infinity Cache)
+#define HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) \
+  X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 8, 4, 1024, 31)
+#define HPRMS_SC1_FUSED_SHAPES(X, DT, MODE)                                                       \
+  HPRMS_SC1_COMMON_SHAPES(X, DT, MODE)                                                            \
+  X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 4, 0, 1024, 159)
+#define HPRMS_SC1_MODE1_SHAPES(X, DT, MODE) \
+  HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31)
+#define HPRMS_ROTATED_MODES_SC1(ENTRY, DT)                                                         \
+  HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 0) HPRMS_SC1_MODE1_SHAPES(ENTRY, DT, 1)                      \
+  HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 3) HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 4)
+// the same for the tail variants, which keep sc1 only past 2048 whole vectors
+#define HPRMS_SC1_TAIL_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 8, 4, 1024, 31)
+#define HPRMS_SC1_TAIL_FUSED_SHAPES(X, DT, MODE) \
+  HPRMS_SC1_TAIL_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 4, 0, 1024, 159)
+#define HPRMS_ROTATED_MODES_SC1_TAIL(ENTRY, DT)                                                    \
+  HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 0) HPRMS_SC1_TAIL_SHAPES(ENTRY, DT, 1)                  \
+  HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 3) HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 4)
 
 // Bench library: the shapes the other modes choose, as in-place (mode 0)
 // kernels, so a test can run the 16-bit op with another form's lane mapping
@@ -160,8 +183,8 @@ struct FusedEntry {
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every
-// entry the tables can choose, with HPRMS_UNALIGNED_FLAGS / HPRMS_TAIL_FLAGS
-// applied.
+// entry the tables can choose, as HPRMS_UNALIGNED_ENTRY / HPRMS_TAIL_ENTRY
+// (and the _SC1_ forms) make them.
 extern const FusedEntry kFusedUnaligned[];
 extern const int kFusedUnalignedCount;
 extern const FusedEntry kFusedTail[];

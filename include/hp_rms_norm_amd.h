@@ -63,8 +63,8 @@ typedef enum {
  * (the reference assumes contiguous rows).  rows == 0 is a no-op.
  * hidden may be any value in [1, 2^24] and rows may start at any 2-byte
  * boundary.  The vector tiers take every hidden in [8, 65543]: rows off the
- * 128-byte grid run a variant without the sc1 cache-policy bit that rotates
- * each row's lane mapping onto the input's cache lines, hidden % 8 != 0 adds
+ * 128-byte grid run a variant that rotates each row's lane mapping onto
+ * 512-byte boundaries of the input (whole cache lines), hidden % 8 != 0 adds
  * a tail vector, and from hidden 4104 up, when neither input nor residual has
  * its rows on 16-byte boundaries, the rows are shifted so that the input is
  * accessed aligned (flags bits 5 and 6 of hprms_config); other shapes take a

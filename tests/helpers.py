@@ -71,9 +71,10 @@ def assert_output_close(got_bits, want_bits, dtype, what="output"):
 def as_dispatched(abi, cfg, hidden):
     """`cfg`, a table configuration, as the dispatch runs it on contiguous rows
     of `hidden` elements: rows off the 128-byte grid (hidden * 2 % 128 != 0)
-    take its unaligned variant (flags bit 5 set, the sc1 bits cleared), which
-    rotates each row's lane mapping by the row's 128-byte phase, and so sums
-    the squares in another order than the table's kernel forced on them."""
+    take its unaligned variant (flags bit 5 set, the sc1 bits cleared: they do
+    not change results), which rotates each row's lane mapping by the row's
+    phase modulo 512 bytes, and so sums the squares in another order than the
+    table's kernel forced on them."""
     if cfg.tier == 3 or hidden % 8 != 0 or (hidden * 2) % 128 == 0:
         return cfg
     c = abi.Config(*cfg.as_tuple())

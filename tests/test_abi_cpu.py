@@ -102,14 +102,6 @@ def test_errors_are_thread_local():
     assert "dtype" in abi.last_error()
 
 
-def variant_flags(flags, hidden):
-    """The flags of the kernel the dispatch runs for rows off the 128-byte grid
-    (hprms.hip, needs_unaligned / unaligned_flags): no sc1 bits, and bit 6 (the
-    tail variant) when hidden % 8 != 0, else bit 5 (bit 6 also for input rows
-    off 16-byte boundaries from 513 whole vectors up: the shifted rows)."""
-    return (flags & ~24) | (96 if hidden % 8 else 32)
-
-
 def entry_points_find_kernels(L, hidden, dtype, base):
     """Every entry point with rows = 0 validates and looks its kernel up without
     launching; `base` 0 gives 128-byte aligned rows, 2 rows at a 2-byte boundary
@@ -155,13 +147,19 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 cm = abi.select_config(rows, hidden, dtype, mode)
                 t = cm.as_tuple()
                 assert t in built[(dtype, mode)], (hidden, mode, t)
-                # the choice for rows off the grid (odd widths report it) in its
-                # unaligned and tail variants
-                off = abi.select_config(rows, hidden + (1 if hidden % 8 == 0 and mode <= 4 else 0), dtype,
-                                        mode).as_tuple()
+                # the choice for rows off the grid (odd widths report it: the tail
+                # variant, with the sc1 bits the dispatch keeps) in its unaligned and
+                # tail variants, with and without sc1
+                hw = hidden + (1 if hidden % 8 == 0 and mode <= 4 else 0)
+                off = abi.select_config(rows, hw, dtype, mode).as_tuple()
                 assert off[:6] + ((off[6] & ~(24 | 64)) | 32,) in built[(dtype, mode)], (hidden, mode, off)
                 if mode <= 4:
-                    assert off[:6] + (variant_flags(off[6], 9),) in built[(dtype, mode)], (hidden, mode, off)
+                    assert off[6] & 96 == 96, (hidden, mode, off)
+                    if mode == 2 or rows * hw <= 1 << 24 or hw // 8 <= 2048:
+                        assert off[6] & 24 == 0, (hidden, mode, off)
+                    assert off in built[(dtype, mode)], (hidden, mode, off)
+                    assert off[:6] + ((off[6] & ~64) | 32,) in built[(dtype, mode)], (hidden, mode, off)
+                    assert off[:6] + ((off[6] & ~24) | 96,) in built[(dtype, mode)], (hidden, mode, off)
             if hidden % 8 == 0 and hidden % 32 and hidden > 1024 and hidden not in (4104, 16392, 65528):
                 continue   # the lookups are exercised at every size class below and at the odd sizes
             entry_points_find_kernels(L, hidden, dtype, 0)
@@ -373,7 +371,9 @@ def _reachable(dtype, mode):
     mode): at each width and at both sides of each latency row's row-count
     limit, the choice for rows on the 128-byte grid (aligned, and unaligned
     when sc1 is dropped for small calls) and the choice for rows off it
-    (reported for odd widths) in its unaligned and (modes 0-4) tail variants."""
+    (reported for odd widths, with the sc1 bits the dispatch keeps for calls
+    past 16 Mi elements in modes 0, 1, 3 and 4) in its unaligned and (modes
+    0-4) tail variants."""
     out = set()
     for rows in (1, 256, 257, 384, 385, 768, 769, 1024, 1025, 4096):
         for nvec in range(1, 8193):
@@ -389,6 +389,10 @@ def _reachable(dtype, mode):
                 tshape = (t.tier, t.lanes_per_row, t.vec_per_lane, t.lds_vec_per_lane, t.block_threads, 0)
                 out.add(tshape + (t.flags,))
                 out.add(tshape + (t.flags & ~64,))
+                # rows of this width off the grid: the rotated variant keeps sc1 past 16 Mi
+                # elements (the rows with sc1 bits take the same shape on and off the grid)
+                if mode != 2 and c.flags & 24 and rows * nvec * 8 > 1 << 24:
+                    out.add(shape + (c.flags | 32,))
             else:
                 out.add(shape + ((c.flags & ~24) | 32,))
     return out

@@ -5,8 +5,8 @@ all start on a 128-byte boundary to a variant of the table's shape:
   * hidden % 8 == 0: the unaligned variant (flags bit 5: rows at any 2-byte
     boundary, no sc1 bits), which keeps the shape's arithmetic; on rows whose
     written stream is 16-byte aligned it rotates each row's lane mapping so
-    that every wave's 1 KiB access starts on a cache line (the first few
-    lanes take the row's last vectors), so its sum of squares runs in another
+    that every wave's 1 KiB access starts on a 512-byte boundary (the first
+    up to 31 lanes take the row's last vectors), so its sum of squares runs in another
     order there and its output is held to the oracle's bar, its residual to
     the aligned kernel's bits; on rows that are not rotated it gives the same
     bits as the table's kernel on contiguous aligned copies;
@@ -235,11 +235,12 @@ ROT_WIDTHS = [48, 64, 1000, 1024, 4096, 5120, 8192, 12288, 16376, 16384, 24576, 
 @pytest.mark.parametrize("hidden", ROT_WIDTHS)
 def test_rotated_rows_every_phase_every_mode(abi, hidden):
     """Written streams 16-byte aligned off the 128-byte grid: first elements at
-    8j (j = 0 ... 7) and a row stride of hidden + 8, so consecutive rows take
-    consecutive 16-byte phases and every rotation of the lane mapping, on the
-    bandwidth table (300 rows) and the latency table (5 rows); outliers so
-    that every element's square matters; each mode against the oracle, and
-    nothing written outside the views."""
+    8j (j = 0 ... 7) and a row stride of 8j + hidden + 8 elements, so the rows
+    take many 16-byte phases modulo 512 bytes (with j = 0 and hidden a multiple
+    of 256, all 32 of them: every rotation of the lane mapping), on the bandwidth
+    table (300 rows) and the latency table (5 rows); outliers so that every
+    element's square matters; each mode against the oracle, and nothing
+    written outside the views."""
     dtype = torch.bfloat16
     th = min(16, oracle.max_threads())
     for rows in (300, 5):
