@@ -350,16 +350,23 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + vk(k) : kOOB);
       }
     }
+    // TAIL: the edge vector's loads, by the lanes that hold one only (a
+    // branch, so that the other waves issue none: measured up to 12% faster
+    // than loads at out-of-range offsets from every lane, at 16K-17K)
     u32x4 txv = {}, trv = {}, twv = {};
     if constexpr (TAIL) {
-      txv = load16<LAUX>(xrs, exoff);
-      if constexpr (RES) trv = load16<LAUX>(rrs, eroff);
+      if (eok) {
+        txv = load16<LAUX>(xrs, exoff);
+        if constexpr (RES) trv = load16<LAUX>(rrs, eroff);
+      }
     }
     if constexpr (!WLATE) {
 #pragma unroll
       for (int k = 0; k < VPL; ++k)
         wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
-      if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
+      if constexpr (TAIL) {
+        if (eok) twv = load16<0>(wrs, ewoff);
+      }
     }
 
     if constexpr (MODE == 4) {
@@ -400,7 +407,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
             const int k = k0 + i < VPL ? k0 + i : 0;
             pv[i] = load16<LAUX>(prs, (k0 + i < VPL && row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
           }
-          if (with_tail) tpv = load16<LAUX>(prs, exoff);
+          if (with_tail && eok) tpv = load16<LAUX>(prs, exoff);
 #pragma unroll
           for (int i = 0; i < G; ++i)
 #pragma unroll
@@ -478,7 +485,9 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
 #pragma unroll
       for (int k = 0; k < VPL; ++k)
         wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
-      if constexpr (TAIL) twv = load16<0>(wrs, ewoff);
+      if constexpr (TAIL) {
+        if (eok) twv = load16<0>(wrs, ewoff);
+      }
     }
 
     float tot = group_sum<GW>(ss0 + ss1);
