@@ -60,11 +60,13 @@ struct FusedEntry {
   X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)      \
   X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
 
-// the fused op in place (mode 0) and its out-of-place (3) and partial-sum (4) forms
-#define HPRMS_FUSED_SHAPES(X, DT, MODE)                                                          \
+// the fused op in place (mode 0) and its out-of-place (3) and partial-sum (4)
+// forms; the tail variants have no LDS-tier 256 x 8 (hprms.hip, tail_shape)
+#define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE)                                                     \
   HPRMS_COMMON_SHAPES(X, DT, MODE)                                                               \
   X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
-  X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 4, 0, 1024, 159)
+  X(DT, MODE, 1024, 4, 0, 1024, 159)
+#define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) X(DT, MODE, 256, 8, 4, 256, 27)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
 #define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
@@ -93,6 +95,11 @@ struct FusedEntry {
   HPRMS_MODE4_SHAPES(ENTRY, DT, 4)
 #define HPRMS_ALL_MODES(ENTRY, DT) HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_ALL_MODES_OFFGRID(ENTRY, DT) HPRMS_MODE0_OFFGRID_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
+#define HPRMS_ALL_MODES_TAIL(ENTRY, DT)                                                           \
+  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 0) ENTRY(DT, 0, 128, 4, 0, 256, 131)                        \
+  HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2)                              \
+  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 3) ENTRY(DT, 3, 128, 4, 0, 256, 131)                        \
+  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 4) ENTRY(DT, 4, 128, 4, 0, 256, 131) ENTRY(DT, 4, 256, 4, 0, 256, 3)
 #define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
 
 // The shapes with sc1 bits among the lists of modes 0, 1, 3 and 4 (their

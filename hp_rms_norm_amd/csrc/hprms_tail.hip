@@ -10,8 +10,8 @@
 namespace hprms {
 
 const FusedEntry kFusedTail[] = {
-    HPRMS_ALL_MODES_OFFGRID(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16)
-    HPRMS_ALL_MODES_OFFGRID(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_ALL_MODES_TAIL(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES_TAIL(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16)
     HPRMS_ROTATED_MODES_SC1_TAIL(HPRMS_TAIL_SC1_ENTRY, HPRMS_DTYPE_BF16)
     HPRMS_ROTATED_MODES_SC1_TAIL(HPRMS_TAIL_SC1_ENTRY, HPRMS_DTYPE_FP16)
 };
