@@ -292,6 +292,63 @@ def test_rotated_rows_every_phase_every_mode(abi, hidden):
             assert_output_close(bits(ov.view), p_out, dtype, "reduce output " + tag)
 
 
+# calls past 16 Mi elements: the rotated variants keep the table row's sc1 bits (the tail
+# variants on the 1024-lane rows past 2048 vectors only)
+@pytest.mark.parametrize("hidden,off,pad", [(16384, 8, 0), (24576, 1, 8), (32775, 0, 0)])
+def test_large_off_grid_calls_every_rotated_mode(abi, hidden, off, pad):
+    """1100 rows (past 16 Mi elements) 16 bytes off the grid, 2 bytes off
+    (shifted) and of an odd width: modes 0, 1, 3 and 4 against the oracle, and
+    nothing written outside the views."""
+    dtype, rows = torch.bfloat16, 1100
+    th = min(16, oracle.max_threads())
+    x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + off)
+    o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+    wd = w.to(DEV)
+    tag = f"{rows}x{hidden} off {off} pad {pad}"
+    print("large off-grid call", tag, flush=True)
+    xv, rv = View(x, off, pad), View(r, off, pad)
+    abi.fused_add_rmsnorm(xv.ptr, wd.data_ptr(), rv.ptr, rows, hidden, xv.stride, rv.stride, DT[dtype], EPS,
+                          _stream())
+    torch.cuda.synchronize()
+    xv.check_outside("input " + tag)
+    rv.check_outside("residual " + tag)
+    assert_residual_exact(bits(rv.view), o_res, dtype, "fused residual " + tag)
+    assert_output_close(bits(xv.view), o_out, dtype, "fused output " + tag)
+    del xv, rv
+
+    xa, ov = View(x, off, pad), View(torch.zeros_like(x), off, pad)
+    abi.rmsnorm(ov.ptr, xa.ptr, wd.data_ptr(), rows, hidden, ov.stride, xa.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("plain output " + tag)
+    assert_output_close(bits(ov.view), oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=th), dtype,
+                        "plain " + tag)
+    del ov
+
+    ra = View(r, off, pad)
+    ov, rov = View(torch.zeros_like(x), off, pad), View(torch.zeros_like(x), off, pad)
+    abi.fused_add_rmsnorm_out(ov.ptr, rov.ptr, xa.ptr, ra.ptr, wd.data_ptr(), rows, hidden, ov.stride, rov.stride,
+                              xa.stride, ra.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("out " + tag)
+    rov.check_outside("residual_out " + tag)
+    assert_residual_exact(bits(rov.view), o_res, dtype, "out residual " + tag)
+    assert_output_close(bits(ov.view), o_out, dtype, "out output " + tag)
+    del xa, ra, ov, rov
+
+    half = (x.float() / 2).to(dtype)
+    parts = [View(half, off, pad), View(half, off, pad)]
+    rv, ov = View(r, off, pad), View(torch.zeros_like(x), off, pad)
+    abi.reduce_add_rmsnorm(ov.ptr, [p.ptr for p in parts], wd.data_ptr(), rv.ptr, rows, hidden, ov.stride,
+                           parts[0].stride, rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("reduce output " + tag)
+    rv.check_outside("reduce residual " + tag)
+    p_out, p_res = oracle.reduce_add_rmsnorm([bits(half), bits(half)], bits(w), bits(r), EPS, DT[dtype],
+                                             threads=th)
+    assert_residual_exact(bits(rv.view), p_res, dtype, "reduce residual " + tag)
+    assert_output_close(bits(ov.view), p_out, dtype, "reduce output " + tag)
+
+
 @pytest.mark.parametrize("hidden,off,pad", [(8192, 8, 8), (16384, 1, 8), (4097, 0, 0)])
 def test_off_grid_rows_in_a_hip_graph(abi, hidden, off, pad):
     """Rotated (16-byte aligned off the grid), shifted (2 bytes off) and odd-width rows captured
