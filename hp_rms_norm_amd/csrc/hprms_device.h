@@ -47,6 +47,15 @@ __device__ __forceinline__ void store16(u32x4 v, __amdgpu_buffer_rsrc_t r, uint3
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, AUX);
 }
 
+// v through an empty asm statement (no instruction): what is computed from it
+// can neither move ahead of this point nor be hoisted out of a loop.  The
+// kernels read their non-preloaded arguments this way after the row loads.
+template <typename T>
+__device__ __forceinline__ T opaque(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
 // ---- element formats --------------------------------------------------------
 template <int DT>
 struct Fmt;

@@ -249,71 +249,32 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x_rows + row0 * x_stride, xbytes);
     uint32_t xoff = (uint32_t)rib * (uint32_t)x_stride * 2u + lofs;
 
-    // rrs/roff: residual loads; srs/soff: residual stores; ors/ooff: output
-    __amdgpu_buffer_rsrc_t rrs = xrs, srs = xrs, ors = xrs;
-    uint32_t roff = 0, soff = 0, ooff = xoff;
+    // rrs/roff: residual loads (the stores' resources come after the loads)
+    __amdgpu_buffer_rsrc_t rrs = xrs;
+    uint32_t roff = 0;
     if constexpr (RES) {
       const uint32_t rbytes = (uint32_t)(((int64_t)(nrows - 1) * res_stride + hidden) * 2);
       rrs = make_rsrc(res_rows + row0 * res_stride, rbytes);
       roff = (uint32_t)rib * (uint32_t)res_stride * 2u + lofs;
-      srs = rrs;
-      soff = roff;
-    }
-    if constexpr (MODE == 3) {
-      const uint32_t sbytes = (uint32_t)(((int64_t)(nrows - 1) * a.res_out_stride + hidden) * 2);
-      srs = make_rsrc(a.res_out + row0 * a.res_out_stride, sbytes);
-      soff = (uint32_t)rib * (uint32_t)a.res_out_stride * 2u + lofs;
-    }
-    // MX: the scale bytes of the row group
-    __amdgpu_buffer_rsrc_t xsrs = xrs;
-    uint32_t xsoff = 0;
-    if constexpr (MODE == 2 || MX) {
-      constexpr uint32_t QB = MODE == 6 ? 4u : 8u;  // output bytes per 8-element vector
-      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * a.q_stride + hidden * (int64_t)QB / 8);
-      ors = make_rsrc(a.q + row0 * a.q_stride, qbytes);
-      ooff = (uint32_t)rib * (uint32_t)a.q_stride + (uint32_t)(lane - rp) * QB;
-    }
-    if constexpr (MX) {
-      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * a.mx_scale_stride + hidden / 32);
-      xsrs = make_rsrc(a.mx_scale + row0 * a.mx_scale_stride, sbytes);
-      // one lane of each quad writes its block's scale byte
-      xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)a.mx_scale_stride + (uint32_t)lane / 4u : kOOB;
-    }
-    if constexpr (MODE == 1) {
-      // no residual: its (preloaded) arguments carry the output rows
-      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * res_stride + hidden) * 2);
-      ors = make_rsrc(res_rows + row0 * res_stride, obytes);
-      ooff = (uint32_t)rib * (uint32_t)res_stride * 2u + lofs;
-    } else if constexpr (OUT16) {
-      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * a.out_stride + hidden) * 2);
-      ors = make_rsrc(a.out + row0 * a.out_stride, obytes);
-      ooff = (uint32_t)rib * (uint32_t)a.out_stride * 2u + lofs;
     }
 
     // TAIL: the lane's edge vector (head or tail); the e*off offsets address
     // the edge vector in each stream, kOOB elsewhere
-    uint32_t exoff = kOOB, eroff = kOOB, esoff = kOOB, eooff = kOOB, ewoff = kOOB;
+    uint32_t exoff = kOOB, eroff = kOOB, ewoff = kOOB, eb = 0, eq = 0;
     int elo = 0, ehi = 0;
     bool eok = false;
     if constexpr (TAIL) {
-      const uint32_t xrow = xoff - lofs;
-      const uint32_t rrow = roff - lofs, srow = soff - lofs;
-      const uint32_t orow = ooff - (MODE == 2 ? (uint32_t)(lane - rp) * 8u : lofs);
+      const uint32_t xrow = xoff - lofs, rrow = roff - lofs;
 #pragma unroll
       for (int k = 0; k < VPL; ++k) vec_ok[k] = (k * LPR + lane) < nb;
       xoff += wshift;
-      if constexpr (RES) {
-        roff += wshift;
-        soff += wshift;
-      }
-      ooff += MODE == 2 ? (uint32_t)(8 * j0 - delta) : wshift;
+      if constexpr (RES) roff += wshift;
       // the head goes to the lane holding body vector 0 (slot rp), the tail
       // to the lane holding body vector nb - 1 (slot rp - 1, or nb - 1
       // unrotated), or to the next lane when that is the head's
       const int hl = rp;
       int tl = rp > 0 ? rp - 1 : (nb - 1) & (LPR - 1);
       if (delta > 0 && tl == hl) tl = hl + 1;
-      uint32_t eb = 0, eq = 0;
       if (delta > 0 && lane == hl) {
         eok = row_ok; elo = 0; ehi = 8 - delta;
       } else if (t > 0 && lane == tl) {
@@ -323,11 +284,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       }
       if (eok) {
         exoff = xrow + eb;
-        if constexpr (RES) {
-          eroff = rrow + eb;
-          esoff = srow + eb;
-        }
-        eooff = orow + (MODE == 2 ? eq : eb);
+        if constexpr (RES) eroff = rrow + eb;
         ewoff = eb;
       }
     }
@@ -369,6 +326,62 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       }
     }
 
+    // The written streams' resources, after the row loads have been issued:
+    // the arguments of modes 2-6 come from FusedArgs (not preloaded), read
+    // here through opaque() so that neither they nor what is computed from
+    // them moves ahead of the loads, which then wait for no scalar load.
+    // Modes 0 and 1 write through preloaded arguments and take no barrier
+    // (with it the compiler kept 64 x 8's unpacked rows live, 120 -> 189
+    // VGPRs), nor does the LDS tier, whose weight loads then trail the row
+    // loads (1-1.6% slower at 16K-32K, two builds side by side).
+    // srs/soff: residual stores; ors/ooff: output; xsrs/xsoff: MX scales
+    if constexpr (MODE >= 2 && LDSV == 0) __builtin_amdgcn_sched_barrier(0);
+    __amdgpu_buffer_rsrc_t srs = rrs, ors = xrs, xsrs = xrs;
+    uint32_t soff = roff, ooff = xoff, xsoff = 0, esoff = eroff, eooff = exoff;
+    if constexpr (MODE == 3) {
+      uint16_t* const ro = opaque(a.res_out);
+      const int64_t rs = opaque(a.res_out_stride);
+      const uint32_t sbytes = (uint32_t)(((int64_t)(nrows - 1) * rs + hidden) * 2);
+      srs = make_rsrc(ro + row0 * rs, sbytes);
+      const uint32_t srow = (uint32_t)rib * (uint32_t)rs * 2u;
+      soff = srow + lofs + wshift;
+      esoff = eok ? srow + eb : kOOB;
+    }
+    if constexpr (MODE == 2 || MX) {
+      constexpr uint32_t QB = MODE == 6 ? 4u : 8u;  // output bytes per 8-element vector
+      uint8_t* const qp = opaque(a.q);
+      const int64_t qs = opaque(a.q_stride);
+      const uint32_t qbytes = (uint32_t)((int64_t)(nrows - 1) * qs + hidden * (int64_t)QB / 8);
+      ors = make_rsrc(qp + row0 * qs, qbytes);
+      const uint32_t qrow = (uint32_t)rib * (uint32_t)qs;
+      ooff = qrow + (uint32_t)(lane - rp) * QB + (TAIL ? (uint32_t)(8 * j0 - delta) : 0u);
+      eooff = eok ? qrow + eq : kOOB;
+    }
+    if constexpr (MX) {
+      uint8_t* const sp = opaque(a.mx_scale);
+      const int64_t ss = opaque(a.mx_scale_stride);
+      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * ss + hidden / 32);
+      xsrs = make_rsrc(sp + row0 * ss, sbytes);
+      // one lane of each quad writes its block's scale byte
+      xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)ss + (uint32_t)lane / 4u : kOOB;
+    }
+    if constexpr (MODE == 1) {
+      // no residual: its (preloaded) arguments carry the output rows
+      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * res_stride + hidden) * 2);
+      ors = make_rsrc(res_rows + row0 * res_stride, obytes);
+      const uint32_t orow = (uint32_t)rib * (uint32_t)res_stride * 2u;
+      ooff = orow + lofs + wshift;
+      eooff = eok ? orow + eb : kOOB;
+    } else if constexpr (OUT16) {
+      uint16_t* const op = opaque(a.out);
+      const int64_t os = opaque(a.out_stride);
+      const uint32_t obytes = (uint32_t)(((int64_t)(nrows - 1) * os + hidden) * 2);
+      ors = make_rsrc(op + row0 * os, obytes);
+      const uint32_t orow = (uint32_t)rib * (uint32_t)os * 2u;
+      ooff = orow + lofs + wshift;
+      eooff = eok ? orow + eb : kOOB;
+    }
+
     if constexpr (MODE == 4) {
       // x := rne(sum of the parts), accumulated in fp32 in part order and
       // rounded once, for groups of at most 2 vector slots at a time when a
@@ -399,8 +412,8 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         }
 #pragma unroll
         for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
-          if (g >= a.nparts) break;
-          const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.parts[g] + row0 * x_stride, xbytes);
+          if (g >= opaque(a.nparts)) break;
+          const __amdgpu_buffer_rsrc_t prs = make_rsrc(opaque(a.parts[g]) + row0 * x_stride, xbytes);
           u32x4 pv[G], tpv = {};
 #pragma unroll
           for (int i = 0; i < G; ++i) {
@@ -609,7 +622,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       float sc = amax / 448.0f;
       if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
       const float isc = 1.0f / sc;
-      if (row_ok && lane == 0) a.scale[row0 + rib] = sc;
+      if (row_ok && lane == 0) opaque(a.scale)[row0 + rib] = sc;
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         u32x2 q;
