@@ -218,6 +218,18 @@ bool reduce_config(int64_t nvec, hprms_config* c) {
   return true;
 }
 
+// The table's 1024 x 2 and 1024 x 3 rows (12K < H <= 24.5K) load the weight
+// together with the row in the fused op and its out-of-place and partial-sum
+// forms (modes 0, 3, 4): 0.8-1.6% faster (bf16 and fp16, on the 128-byte grid
+// and rotated off it; 4096 rows, two builds side by side, 9 interleaved
+// trials; one row: 2% slower).  Plain RMSNorm measured the same either way;
+// the FP8 and MX outputs ran 12-23% slower with it and the tail variants
+// 2-4% (tail_shape): they load it late.
+bool weight_late_1024(int mode, const hprms_config& c) {
+  if (c.lanes_per_row != 1024 || (c.vec_per_lane != 2 && c.vec_per_lane != 3)) return false;
+  return !(mode == 0 || mode == 3 || mode == 4);
+}
+
 // `grid`: every row of every stream starts on the 128-byte grid (only the
 // in-place op's rows depend on it).
 void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_config* c) {
@@ -243,9 +255,9 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_confi
       {512, 128, 4, 0, 256, 131},    // H <= 4096
       {1024, 512, 2, 0, 512, 7},     // H <= 8192:  one row per 8-wave workgroup
       {1536, 512, 3, 0, 512, 159},   // H <= 12288
-      {2047, 1024, 2, 0, 1024, 31},  // H <= 16376
+      {2047, 1024, 2, 0, 1024, 27},  // H <= 16376
       {2048, 256, 8, 4, 256, 27},    // H = 16384: LDS tier, half the row in LDS
-      {3072, 1024, 3, 0, 1024, 159}, // H <= 24576
+      {3072, 1024, 3, 0, 1024, 155}, // H <= 24576
       {4096, 1024, 4, 0, 1024, 159}, // H <= 32768
       {8192, 1024, 8, 4, 1024, 31},  // H <= 65536: LDS tier
   };
@@ -257,6 +269,7 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_confi
       c->block_threads = r.block;
       c->flags = r.flags;
       c->tier = r.ldsv > 0 ? 2 : 1;
+      if (weight_late_1024(mode, *c)) c->flags |= 4;
       return;
     }
   }
@@ -544,10 +557,14 @@ int unaligned_flags(const Problem& p, int flags) {
 // the LDS tier's 256 x 8, whose edge registers (135 VGPRs) leave room for
 // three workgroups per CU: 4096 rows of 16384 two bytes off the grid and of
 // 16391, 4.4-5.1% faster in bf16 and fp16 (the unaligned variant, without
-// the tail, keeps the LDS tier: within 0.5%).
+// the tail, keeps the LDS tier: within 0.5%).  The tail variants of 1024 x 2
+// and 1024 x 3 load the weight late in every mode.
 void tail_shape(const Problem& p, hprms_config* c) {
-  if (c->tier != 2 || !(c->flags & 64) || c->lanes_per_row != 256) return;
-  *c = hprms_config{1, 1024, 2, 0, 1024, c->grid_blocks, unaligned_flags(p, 31)};
+  if (!(c->flags & 64)) return;
+  if (c->tier == 2 && c->lanes_per_row == 256)
+    *c = hprms_config{1, 1024, 2, 0, 1024, c->grid_blocks, unaligned_flags(p, 31)};
+  else if (c->lanes_per_row == 1024 && (c->vec_per_lane == 2 || c->vec_per_lane == 3))
+    c->flags |= 4;
 }
 
 // Calls that update the residual in place and whose input and residual rows

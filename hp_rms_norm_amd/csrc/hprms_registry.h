@@ -55,18 +55,20 @@ struct FusedEntry {
 // tables and checks that these lists hold every reachable shape and no other.
 #define HPRMS_COMMON_SHAPES(X, DT, MODE)                                                         \
   X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)      \
-  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 3, 0, 1024, 159) \
-  X(DT, MODE, 1024, 8, 4, 1024, 31)                                                              \
+  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 8, 4, 1024, 31) \
   X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)      \
   X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
 
 // the fused op in place (mode 0) and its out-of-place (3) and partial-sum (4)
-// forms; the tail variants have no LDS-tier 256 x 8 (hprms.hip, tail_shape)
-#define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE)                                                     \
-  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                               \
-  X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
-  X(DT, MODE, 1024, 4, 0, 1024, 159)
-#define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) X(DT, MODE, 256, 8, 4, 256, 27)
+// forms.  In 1024 x 2 and 1024 x 3 these modes load the weight with the row
+// (flags 27 / 155) except in the tail variants (31 / 159), which have no
+// LDS-tier 256 x 8 either (hprms.hip, table_config and tail_shape).
+#define HPRMS_FUSED_ROWS(X, DT, MODE, F2, F3)                                                     \
+  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                                \
+  X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, F2) \
+  X(DT, MODE, 1024, 3, 0, 1024, F3) X(DT, MODE, 1024, 4, 0, 1024, 159)
+#define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159)
+#define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155) X(DT, MODE, 256, 8, 4, 256, 27)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
 #define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
@@ -76,13 +78,13 @@ struct FusedEntry {
 
 // plain RMSNorm (mode 1)
 #define HPRMS_MODE1_SHAPES(X, DT, MODE)                                                           \
-  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                                \
+  HPRMS_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 3, 0, 1024, 159)                              \
   X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 256, 3, 0, 256, 7)      \
   X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31) X(DT, MODE, 512, 8, 0, 512, 7)
 
 // the FP8 output (mode 2) and the OCP MX outputs (modes 5 and 6)
 #define HPRMS_QUANT_SHAPES(X, DT, MODE)                                                           \
-  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                                \
+  HPRMS_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 3, 0, 1024, 159)                              \
   X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 256, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, 31)
 #define HPRMS_MODE2_SHAPES(X, DT, MODE) HPRMS_QUANT_SHAPES(X, DT, MODE) X(DT, MODE, 512, 8, 4, 512, 159)
 #define HPRMS_MX_SHAPES(X, DT, MODE) HPRMS_QUANT_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 4, 0, 1024, 159)
@@ -104,13 +106,13 @@ struct FusedEntry {
 
 // The shapes with sc1 bits among the lists of modes 0, 1, 3 and 4 (their
 // off-grid variants keep them for calls past the Infinity Cache)
-#define HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) \
-  X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 8, 4, 1024, 31)
+#define HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 8, 4, 1024, 31)
 #define HPRMS_SC1_FUSED_SHAPES(X, DT, MODE)                                                       \
-  HPRMS_SC1_COMMON_SHAPES(X, DT, MODE)                                                            \
-  X(DT, MODE, 1024, 2, 0, 1024, 31) X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 4, 0, 1024, 159)
-#define HPRMS_SC1_MODE1_SHAPES(X, DT, MODE) \
-  HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31)
+  HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 3, 0, 1024, 155)                         \
+  X(DT, MODE, 1024, 2, 0, 1024, 27) X(DT, MODE, 256, 8, 4, 256, 27) X(DT, MODE, 1024, 4, 0, 1024, 159)
+#define HPRMS_SC1_MODE1_SHAPES(X, DT, MODE)                                                       \
+  HPRMS_SC1_COMMON_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 3, 0, 1024, 159)                         \
+  X(DT, MODE, 512, 2, 0, 512, 31) X(DT, MODE, 512, 4, 0, 512, 31)
 #define HPRMS_ROTATED_MODES_SC1(ENTRY, DT)                                                         \
   HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 0) HPRMS_SC1_MODE1_SHAPES(ENTRY, DT, 1)                      \
   HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 3) HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 4)
@@ -128,7 +130,8 @@ struct FusedEntry {
 #define HPRMS_OTHER_MODE_SHAPES(X, DT, MODE)                                                      \
   X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3) X(DT, MODE, 256, 3, 0, 256, 7)  \
   X(DT, MODE, 512, 8, 4, 512, 159) X(DT, MODE, 64, 8, 0, 256, 3) X(DT, MODE, 512, 2, 0, 512, 31)  \
-  X(DT, MODE, 512, 4, 0, 512, 31) X(DT, MODE, 512, 8, 0, 512, 7)
+  X(DT, MODE, 512, 4, 0, 512, 31) X(DT, MODE, 512, 8, 0, 512, 7) X(DT, MODE, 1024, 2, 0, 1024, 31) \
+  X(DT, MODE, 1024, 3, 0, 1024, 159)
 
 // The shapes below are built only into the bench library libhprms_bench.so
 // (hprms.hip compiled with HPRMS_BENCH_BUILD), never into libhprms.so: no
@@ -185,7 +188,7 @@ struct FusedEntry {
 #define HPRMS_TIMELINE_SHAPES(X, DT, MODE)                                                        \
   X(DT, MODE, 32, 4, 0, 256, 643) X(DT, MODE, 64, 4, 0, 256, 647) X(DT, MODE, 128, 3, 0, 256, 519) \
   X(DT, MODE, 256, 2, 0, 256, 643) X(DT, MODE, 512, 2, 0, 512, 519) X(DT, MODE, 512, 3, 0, 512, 671) \
-  X(DT, MODE, 1024, 2, 0, 1024, 543) X(DT, MODE, 256, 8, 4, 256, 539) X(DT, MODE, 1024, 3, 0, 1024, 671) \
+  X(DT, MODE, 1024, 2, 0, 1024, 539) X(DT, MODE, 256, 8, 4, 256, 539) X(DT, MODE, 1024, 3, 0, 1024, 667) \
   X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 643)
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants

@@ -152,13 +152,17 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 # tail variants, with and without sc1
                 hw = hidden + (1 if hidden % 8 == 0 and mode <= 4 else 0)
                 off = abi.select_config(rows, hw, dtype, mode).as_tuple()
-                assert off[:6] + ((off[6] & ~(24 | 64)) | 32,) in built[(dtype, mode)], (hidden, mode, off)
+                u = (off[6] & ~(24 | 64)) | 32
+                if mode in (0, 3, 4) and off[1] == 1024 and off[2] in (2, 3):
+                    u &= ~4   # the weight loaded late by the tail variant only
+                assert off[:6] + (u,) in built[(dtype, mode)], (hidden, mode, off)
                 if mode <= 4:
                     assert off[6] & 96 == 96, (hidden, mode, off)
                     if mode == 2 or rows * hw <= 1 << 24 or hw // 8 <= 2048:
                         assert off[6] & 24 == 0, (hidden, mode, off)
                     assert off in built[(dtype, mode)], (hidden, mode, off)
-                    assert off[:6] + ((off[6] & ~64) | 32,) in built[(dtype, mode)], (hidden, mode, off)
+                    us = ((off[6] & ~64) | 32) & ~4 | (u & 4)   # with sc1, the weight as in u
+                    assert off[:6] + (us,) in built[(dtype, mode)], (hidden, mode, off)
                     assert off[:6] + ((off[6] & ~24) | 96,) in built[(dtype, mode)], (hidden, mode, off)
             if hidden % 8 == 0 and hidden % 32 and hidden > 1024 and hidden not in (4104, 16392, 65528):
                 continue   # the lookups are exercised at every size class below and at the odd sizes
@@ -388,7 +392,12 @@ def _reachable(dtype, mode):
                 t = abi.select_config(rows, nvec * 8 + 1, dtype, mode)   # off the grid: its tail variant
                 tshape = (t.tier, t.lanes_per_row, t.vec_per_lane, t.lds_vec_per_lane, t.block_threads, 0)
                 out.add(tshape + (t.flags,))
-                out.add(tshape + (t.flags & ~64,))
+                # its unaligned sibling; in 1024 x 2 and x 3 only the tail loads the weight late
+                # in modes 0, 3 and 4
+                u = t.flags & ~64
+                if mode in (0, 3, 4) and t.lanes_per_row == 1024 and t.vec_per_lane in (2, 3):
+                    u &= ~4
+                out.add(tshape + (u,))
                 # rows of this width off the grid: the rotated variant keeps sc1 past 16 Mi
                 # elements (the rows with sc1 bits take the same shape on and off the grid)
                 if mode != 2 and c.flags & 24 and rows * nvec * 8 > 1 << 24:
