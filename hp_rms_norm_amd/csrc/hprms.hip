@@ -559,12 +559,36 @@ int unaligned_flags(const Problem& p, int flags) {
 // 16391, 4.4-5.1% faster in bf16 and fp16 (the unaligned variant, without
 // the tail, keeps the LDS tier: within 0.5%).  The tail variants of 1024 x 2
 // and 1024 x 3 load the weight late in every mode.
+//
+// A shifted row reads its weight 2-14 bytes off the weight's 16-byte vectors;
+// from 1024 rows (plain RMSNorm: 384) the tail variants of 512 x 2-4 and
+// 1024 x 2-3 instead stage the whole weight in LDS with aligned loads, once
+// per workgroup (flags bit 14), where the fused op, its out-of-place and
+// partial-sum forms measured 1.5-5% faster and plain RMSNorm 8-17% (4096
+// rows, odd widths and rows two bytes off at 8K-20K).  Not below: the
+// staging sits on a single row's critical path (1-256 rows: 3-23% slower);
+// not in 1024 x 4 (1.7-3.5% slower: one workgroup per CU either way, VGPRs
+// 80 -> 96), in the fused op's 1024 x 3 (62 -> 66 VGPRs: one workgroup per
+// CU instead of two, -1.5% to +1.7%), nor the partial sums' 1024 x 2 (spills).
+bool weight_in_lds(const Problem& p, const hprms_config& c) {
+  if (c.lds_vec_per_lane != 0 || c.block_threads != c.lanes_per_row) return false;
+  const int l = c.lanes_per_row, v = c.vec_per_lane;
+  switch (p.mode) {
+    case 0:
+    case 3: return p.rows >= 1024 && ((l == 512 && (v == 2 || v == 3)) || (l == 1024 && v == 2));
+    case 4: return p.rows >= 1024 && l == 512 && v == 3;
+    case 1: return p.rows >= 384 && ((l == 512 && v >= 2 && v <= 4) || (l == 1024 && v == 3));
+    default: return false;
+  }
+}
+
 void tail_shape(const Problem& p, hprms_config* c) {
   if (!(c->flags & 64)) return;
   if (c->tier == 2 && c->lanes_per_row == 256)
     *c = hprms_config{1, 1024, 2, 0, 1024, c->grid_blocks, unaligned_flags(p, 31)};
   else if (c->lanes_per_row == 1024 && (c->vec_per_lane == 2 || c->vec_per_lane == 3))
     c->flags |= 4;
+  if (weight_in_lds(p, *c)) c->flags |= 16384;
 }
 
 // Calls that update the residual in place and whose input and residual rows

@@ -56,6 +56,13 @@
 // issues all its loads before its stores.  Bit 7 issues all
 // of a lane's residual loads before its input loads (otherwise the two
 // streams alternate per vector); which is faster depends on the shape.
+// Bit 14 (tail variants with the late weight and rows of several waves, not
+// the FP8 output): a shifted row reads its weight 2 * delta bytes off the
+// weight's 16-byte vectors, and such loads cost the L1 path.  With the bit the
+// workgroup loads the whole weight once, aligned, before its first row
+// group's loads, writes it to LDS after them, and every row reads its
+// vectors from there (five dwords each, funnel-shifted by the row's 2-byte
+// phase) after the row-sum barrier.
 //
 // The residual is stored as soon as it is formed: deferring it to the output
 // phase (one write burst per workgroup) measured up to 5% slower.
@@ -180,6 +187,13 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
 
   __shared__ float red[2][WPR > 1 ? NW : 1];
   __shared__ u32x4 spill[LDSV > 0 ? LDSV * BLOCK : 1];
+  // WLDS: the weight staged in LDS (FLAGS bit 14): the row's whole vectors,
+  // its partial last vector and one vector of slack for the five-dword reads
+  constexpr bool WLDS = (FLAGS & 16384) != 0;
+  static_assert(!WLDS || (TAIL && WLATE && LDSV == 0 && WPR > 1 && MODE != 2), "weight staged in LDS");
+  constexpr int NST = WLDS ? (LPR * VPL + BLOCK - 1) / BLOCK : 1;  // staged vectors per thread
+  __shared__ u32x4 wlds[WLDS ? LPR * VPL + 2 : 1];
+  bool staged = false;
 
   const int tid = threadIdx.x;
   const int lane = tid & (LPR - 1);
@@ -289,6 +303,21 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       }
     }
 
+    // WLDS: the first row group loads the whole weight (aligned) before its
+    // row loads and writes it to LDS after them; the values stay live only
+    // within this iteration
+    u32x4 wst[NST], wtl = {};
+    if constexpr (WLDS) {
+      if (!staged) {
+#pragma unroll
+        for (int i = 0; i < NST; ++i) {
+          const int v = tid + i * BLOCK;
+          wst[i] = load16<0>(wrs, v < nvec ? (uint32_t)v * 16u : kOOB);
+        }
+        // the elements past the last whole vector, from the weight's last 16 bytes
+        if ((hidden & 7) != 0 && tid == BLOCK - 1) wtl = load16<0>(wrs, 2u * (uint32_t)hidden - 16u);
+      }
+    }
     u32x4 xv[VPL], rv[VPL], wv[VPL];
     if constexpr (RFIRST) {
       // all of the residual's vectors, then all of the input's (the
@@ -323,6 +352,28 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
       if constexpr (TAIL) {
         if (eok) twv = load16<0>(wrs, ewoff);
+      }
+    }
+    if constexpr (WLDS) {
+      // (the row-sum barrier below makes these writes visible to the workgroup)
+      if (!staged) {
+#pragma unroll
+        for (int i = 0; i < NST; ++i) {
+          const int v = tid + i * BLOCK;
+          if (v < nvec) wlds[v] = wst[i];
+        }
+        if ((hidden & 7) != 0 && tid == BLOCK - 1) {
+          uint16_t* const w16 = reinterpret_cast<uint16_t*>(wlds);
+          const int r = hidden & 7;
+#pragma unroll
+          for (int i = 0; i < 7; ++i) {
+            if (i < r) {
+              const int e = i + 8 - r;  // element 8 * nvec + i among the last 8
+              w16[8 * nvec + i] = (uint16_t)(wtl[e >> 1] >> ((e & 1) * 16));
+            }
+          }
+        }
+        staged = true;
       }
     }
 
@@ -495,9 +546,11 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     }
 
     if constexpr (WLATE) {
+      if constexpr (!WLDS) {
 #pragma unroll
-      for (int k = 0; k < VPL; ++k)
-        wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
+        for (int k = 0; k < VPL; ++k)
+          wv[k] = load16<0>(wrs, (TAIL && !vec_ok[k]) ? kOOB : lofs + vk(k) + wshift);
+      }
       if constexpr (TAIL) {
         if (eok) twv = load16<0>(wrs, ewoff);
       }
@@ -512,6 +565,22 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
 #pragma unroll
       for (int j = 1; j < WPR; ++j) tot += red[buf][w0 + j];
       buf ^= 1;
+    }
+    if constexpr (WLDS) {
+      // slot k's vector starts at byte lofs + vk(k) + wshift of the weight:
+      // the five dwords from the one holding its first element, shifted by
+      // 0 or 16 bits (wshift is even; the same phase for every slot)
+      const uint32_t* const wd = reinterpret_cast<const uint32_t*>(wlds);
+      const uint32_t sh = (wshift & 3u) * 8u;
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const uint32_t i = vec_ok[k] ? (lofs + vk(k) + wshift) >> 2 : 0u;
+        uint32_t d[5];
+#pragma unroll
+        for (int j = 0; j < 5; ++j) d[j] = wd[i + j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wv[k][j] = __builtin_amdgcn_alignbit(d[j + 1], d[j], sh);
+      }
     }
     const float inv = 1.0f / __builtin_sqrtf(tot / hidden_f + eps);
 

@@ -44,6 +44,11 @@ struct FusedEntry {
   HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) | 32)
 #define HPRMS_TAIL_SC1_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
   HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) | 96)
+// tail variants with the weight staged in LDS (flags bit 14)
+#define HPRMS_TAIL_WLDS_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, ((FLAGS) & ~24) | 96 | 16384)
+#define HPRMS_TAIL_WLDS_SC1_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS) \
+  HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) | 96 | 16384)
 
 // (lanes per row, vectors per lane, of which in LDS, block, flags).  flags 3 =
 // nt on the row loads and stores, 7 = the same with the weight loaded late,
@@ -117,12 +122,25 @@ struct FusedEntry {
   HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 0) HPRMS_SC1_MODE1_SHAPES(ENTRY, DT, 1)                      \
   HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 3) HPRMS_SC1_FUSED_SHAPES(ENTRY, DT, 4)
 // the same for the tail variants, which keep sc1 only past 2048 whole vectors
-#define HPRMS_SC1_TAIL_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 8, 4, 1024, 31)
-#define HPRMS_SC1_TAIL_FUSED_SHAPES(X, DT, MODE) \
-  HPRMS_SC1_TAIL_SHAPES(X, DT, MODE) X(DT, MODE, 1024, 4, 0, 1024, 159)
+// (plain RMSNorm's 1024 x 3 tail then stages its weight in LDS: HPRMS_WLDS_TAIL_SC1)
+#define HPRMS_SC1_TAIL_FUSED_SHAPES(X, DT, MODE)                                                  \
+  X(DT, MODE, 1024, 3, 0, 1024, 159) X(DT, MODE, 1024, 8, 4, 1024, 31) X(DT, MODE, 1024, 4, 0, 1024, 159)
 #define HPRMS_ROTATED_MODES_SC1_TAIL(ENTRY, DT)                                                    \
-  HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 0) HPRMS_SC1_TAIL_SHAPES(ENTRY, DT, 1)                  \
+  HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 0) ENTRY(DT, 1, 1024, 8, 4, 1024, 31)                   \
   HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 3) HPRMS_SC1_TAIL_FUSED_SHAPES(ENTRY, DT, 4)
+
+// The tail shapes that stage the weight in LDS from 1024 rows (plain RMSNorm:
+// 384; hprms.hip, tail_shape): 512 x 2, 512 x 3 and 1024 x 2 in the fused op
+// in place and out of place, 512 x 3 in the partial-sum form, and 512 x 2, 3
+// and 4 and 1024 x 3 in plain RMSNorm (its 1024 x 3 also with sc1).
+#define HPRMS_WLDS_FUSED_SHAPES(X, DT, MODE) \
+  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 2, 0, 1024, 31)
+#define HPRMS_ALL_MODES_WLDS_TAIL(ENTRY, DT)                                                      \
+  HPRMS_WLDS_FUSED_SHAPES(ENTRY, DT, 0) HPRMS_WLDS_FUSED_SHAPES(ENTRY, DT, 3)                    \
+  ENTRY(DT, 4, 512, 3, 0, 512, 159)                                                              \
+  ENTRY(DT, 1, 512, 2, 0, 512, 31) ENTRY(DT, 1, 512, 3, 0, 512, 159) ENTRY(DT, 1, 512, 4, 0, 512, 31) \
+  ENTRY(DT, 1, 1024, 3, 0, 1024, 159)
+#define HPRMS_WLDS_TAIL_SC1(ENTRY, DT) ENTRY(DT, 1, 1024, 3, 0, 1024, 159)
 
 // Bench library: the shapes the other modes choose, as in-place (mode 0)
 // kernels, so a test can run the 16-bit op with another form's lane mapping

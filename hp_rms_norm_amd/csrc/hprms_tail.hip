@@ -14,6 +14,10 @@ const FusedEntry kFusedTail[] = {
     HPRMS_ALL_MODES_TAIL(HPRMS_TAIL_ENTRY, HPRMS_DTYPE_FP16)
     HPRMS_ROTATED_MODES_SC1_TAIL(HPRMS_TAIL_SC1_ENTRY, HPRMS_DTYPE_BF16)
     HPRMS_ROTATED_MODES_SC1_TAIL(HPRMS_TAIL_SC1_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_ALL_MODES_WLDS_TAIL(HPRMS_TAIL_WLDS_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_ALL_MODES_WLDS_TAIL(HPRMS_TAIL_WLDS_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_WLDS_TAIL_SC1(HPRMS_TAIL_WLDS_SC1_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_WLDS_TAIL_SC1(HPRMS_TAIL_WLDS_SC1_ENTRY, HPRMS_DTYPE_FP16)
 };
 
 const int kFusedTailCount = (int)(sizeof(kFusedTail) / sizeof(kFusedTail[0]));

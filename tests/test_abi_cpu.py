@@ -122,6 +122,28 @@ def entry_points_find_kernels(L, hidden, dtype, base):
         assert rc == want, (h, fmt, abi.last_error())
 
 
+def test_tail_weight_staged_in_lds_from_a_row_count():
+    """The tail variants of 512 x 2-4 and 1024 x 2-3 stage the weight in LDS
+    (flags bit 14) from 1024 rows (plain RMSNorm: 384), never in 1024 x 4, the
+    fused op's 1024 x 3, the partial sums' 1024 x 2, the FP8 output or the
+    variants without the tail."""
+    bf = abi.DTYPE_BF16
+    for hidden in (8191, 12289, 16391):
+        assert not abi.select_config(1023, hidden, bf, 0).flags & 16384
+        assert abi.select_config(1024, hidden, bf, 0).flags & 16384
+        assert abi.select_config(1024, hidden, bf, 3).flags & 16384
+        assert not abi.select_config(4096, hidden, bf, 2).flags & 16384
+    assert not abi.select_config(383, 16391, bf, 1).flags & 16384
+    assert abi.select_config(384, 16391, bf, 1).flags & 16384
+    assert abi.select_config(4096, 12289, bf, 4).flags & 16384
+    assert not abi.select_config(4096, 16391, bf, 4).flags & 16384       # 1024 x 2
+    assert not abi.select_config(4096, 20479, bf, 0).flags & 16384       # 1024 x 3
+    assert abi.select_config(4096, 20479, bf, 1).flags & 16384
+    assert not abi.select_config(4096, 32775, bf, 0).flags & 16384       # 1024 x 4
+    for hidden in (8192, 12288, 16384):
+        assert not abi.select_config(4096, hidden, bf, 0).flags & 16384  # no tail
+
+
 def test_table_covers_every_hidden_with_a_built_kernel():
     """Every hidden size maps either to a built vector-tier kernel that covers
     it, or (hidden < 8 or > 65543) to the general kernel; the choice for rows
@@ -152,7 +174,7 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 # tail variants, with and without sc1
                 hw = hidden + (1 if hidden % 8 == 0 and mode <= 4 else 0)
                 off = abi.select_config(rows, hw, dtype, mode).as_tuple()
-                u = (off[6] & ~(24 | 64)) | 32
+                u = (off[6] & ~(24 | 64 | 16384)) | 32
                 if mode in (0, 3, 4) and off[1] == 1024 and off[2] in (2, 3):
                     u &= ~4   # the weight loaded late by the tail variant only
                 assert off[:6] + (u,) in built[(dtype, mode)], (hidden, mode, off)
@@ -161,7 +183,7 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                     if mode == 2 or rows * hw <= 1 << 24 or hw // 8 <= 2048:
                         assert off[6] & 24 == 0, (hidden, mode, off)
                     assert off in built[(dtype, mode)], (hidden, mode, off)
-                    us = ((off[6] & ~64) | 32) & ~4 | (u & 4)   # with sc1, the weight as in u
+                    us = ((off[6] & ~(64 | 16384)) | 32) & ~4 | (u & 4)   # with sc1, the weight as in u
                     assert off[:6] + (us,) in built[(dtype, mode)], (hidden, mode, off)
                     assert off[:6] + ((off[6] & ~24) | 96,) in built[(dtype, mode)], (hidden, mode, off)
             if hidden % 8 == 0 and hidden % 32 and hidden > 1024 and hidden not in (4104, 16392, 65528):
@@ -394,7 +416,7 @@ def _reachable(dtype, mode):
                 out.add(tshape + (t.flags,))
                 # its unaligned sibling; in 1024 x 2 and x 3 only the tail loads the weight late
                 # in modes 0, 3 and 4
-                u = t.flags & ~64
+                u = t.flags & ~(64 | 16384)   # (only tails stage the weight in LDS)
                 if mode in (0, 3, 4) and t.lanes_per_row == 1024 and t.vec_per_lane in (2, 3):
                     u &= ~4
                 out.add(tshape + (u,))

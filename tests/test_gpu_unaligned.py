@@ -349,6 +349,80 @@ def test_large_off_grid_calls_every_rotated_mode(abi, hidden, off, pad):
     assert_output_close(bits(ov.view), p_out, dtype, "reduce output " + tag)
 
 
+# (hidden, element offset, row padding, dtype): odd widths (every tail length, the
+# weight's partial last vector staged) and shifted rows on each staged shape
+WLDS_CASES = [(4105, 0, 0, torch.bfloat16), (8191, 0, 0, torch.float16), (8192, 1, 8, torch.bfloat16),
+              (12289, 0, 0, torch.bfloat16), (12288, 3, 5, torch.float16), (12294, 0, 0, torch.bfloat16),
+              (16383, 0, 0, torch.float16), (16391, 0, 0, torch.bfloat16), (16384, 5, 11, torch.bfloat16),
+              (20479, 0, 0, torch.bfloat16), (20483, 0, 0, torch.float16)]
+
+
+@pytest.mark.parametrize("hidden,off,pad,dtype", WLDS_CASES)
+def test_tail_weight_staged_in_lds(abi, hidden, off, pad, dtype):
+    """From 1024 rows (plain RMSNorm: 384) the tail variants of 512 x 2-4 and
+    1024 x 2-3 load the whole weight into LDS once per workgroup (flags bit
+    14) and read each row's shifted vectors from there: modes 0, 1, 3 and 4
+    at 1024 rows against the oracle, nothing written outside the views, and
+    the dispatch's choice for the odd widths carrying the bit where the
+    table stages the weight."""
+    rows = 1024
+    th = min(16, oracle.max_threads())
+    x, r, w = make_inputs(rows, hidden, dtype, seed=hidden + 3 * off)
+    o_out, o_res = oracle_fused(x, r, w, EPS, dtype)
+    wd = w.to(DEV)
+    tag = f"{rows}x{hidden} off {off} pad {pad} {dtype}"
+    print("weight staged in LDS", tag, flush=True)
+    if hidden % 8:
+        # the fused op's staged shapes end with 1024 x 2 (16K), the partial sums' are
+        # 512 x 3 (8K-12K), plain RMSNorm's start with 512 x 2 (from 641 vectors)
+        staged = {m: bool(abi.select_config(rows, hidden, DT[dtype], m).flags & 16384) for m in (0, 1, 3, 4)}
+        assert staged[0] == staged[3] == (hidden < 16384 + 8), staged
+        assert staged[4] == (8 * 1025 <= hidden < 8 * 1537), staged
+        assert staged[1] == (hidden >= 8 * 641), staged
+
+    xv, rv = View(x, off, pad), View(r, off, pad)
+    abi.fused_add_rmsnorm(xv.ptr, wd.data_ptr(), rv.ptr, rows, hidden, xv.stride, rv.stride, DT[dtype], EPS,
+                          _stream())
+    torch.cuda.synchronize()
+    xv.check_outside("input " + tag)
+    rv.check_outside("residual " + tag)
+    assert_residual_exact(bits(rv.view), o_res, dtype, "fused residual " + tag)
+    assert_output_close(bits(xv.view), o_out, dtype, "fused output " + tag)
+    del xv, rv
+
+    xa, ov = View(x, off, pad), View(torch.zeros_like(x), off, pad)
+    abi.rmsnorm(ov.ptr, xa.ptr, wd.data_ptr(), rows, hidden, ov.stride, xa.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("plain output " + tag)
+    assert_output_close(bits(ov.view), oracle.rmsnorm(bits(x), bits(w), EPS, DT[dtype], threads=th), dtype,
+                        "plain " + tag)
+    del ov
+
+    ra = View(r, off, pad)
+    ov, rov = View(torch.zeros_like(x), off, pad), View(torch.zeros_like(x), off, pad)
+    abi.fused_add_rmsnorm_out(ov.ptr, rov.ptr, xa.ptr, ra.ptr, wd.data_ptr(), rows, hidden, ov.stride, rov.stride,
+                              xa.stride, ra.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("out " + tag)
+    rov.check_outside("residual_out " + tag)
+    assert_residual_exact(bits(rov.view), o_res, dtype, "out residual " + tag)
+    assert_output_close(bits(ov.view), o_out, dtype, "out output " + tag)
+    del xa, ra, ov, rov
+
+    half = (x.float() / 2).to(dtype)
+    parts = [View(half, off, pad), View(half, off, pad)]
+    rv, ov = View(r, off, pad), View(torch.zeros_like(x), off, pad)
+    abi.reduce_add_rmsnorm(ov.ptr, [p.ptr for p in parts], wd.data_ptr(), rv.ptr, rows, hidden, ov.stride,
+                           parts[0].stride, rv.stride, DT[dtype], EPS, _stream())
+    torch.cuda.synchronize()
+    ov.check_outside("reduce output " + tag)
+    rv.check_outside("reduce residual " + tag)
+    p_out, p_res = oracle.reduce_add_rmsnorm([bits(half), bits(half)], bits(w), bits(r), EPS, DT[dtype],
+                                             threads=th)
+    assert_residual_exact(bits(rv.view), p_res, dtype, "reduce residual " + tag)
+    assert_output_close(bits(ov.view), p_out, dtype, "reduce output " + tag)
+
+
 @pytest.mark.parametrize("hidden,off,pad", [(8192, 8, 8), (16384, 1, 8), (4097, 0, 0)])
 def test_off_grid_rows_in_a_hip_graph(abi, hidden, off, pad):
     """Rotated (16-byte aligned off the grid), shifted (2 bytes off) and odd-width rows captured
