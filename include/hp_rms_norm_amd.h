@@ -204,7 +204,10 @@ typedef struct {
                                first written tensor), bit 6 (with bit 5): head and tail vectors, for
                                hidden % 8 != 0 and (from hidden 4104 up, modes 0-4) rows
                                shifted to the first written tensor's 16-byte phase;
-                               bit 7: a lane's residual loads issued before its input loads */
+                               bit 7: a lane's residual loads issued before its input loads;
+                               bit 14 (with bit 6, late weight, rows of several waves, not
+                               the FP8 output): the whole weight loaded once per workgroup
+                               with aligned loads into LDS, where shifted rows read it */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
@@ -222,7 +225,10 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * rows on the 128-byte grid: rows off it run the same shape (mode 0 at
  * 384 < hidden / 8 <= 512 excepted: 128 lanes x 4 vectors, flags 131, where
  * rows on the grid take 256 x 2) with flags
- * (flags & ~24) | 32, or | 96 (the tail variant) for hidden % 8 != 0 and, in
+ * (flags & ~24) | 32, or | 96 (the tail variant, which adds bit 2 to the
+ * 1024 x 2 and 1024 x 3 rows and, from 1024 rows (plain RMSNorm: 384), bit
+ * 14 to 512 x 2-4 and 1024 x 2-3 in the modes that stage the weight in LDS)
+ * for hidden % 8 != 0 and, in
  * modes 0-4 from hidden 4104 up, for calls none of whose tensors (the weight
  * aside) has its rows on 16-byte boundaries (the kernel then shifts its
  * vectors to align the first written tensor; plain RMSNorm with input and
