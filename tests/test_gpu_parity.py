@@ -128,6 +128,21 @@ def test_persistent_grid(abi):
         check_case(abi, 1000, 4096, torch.bfloat16, seed=grid, config=cfg)
 
 
+@pytest.mark.parametrize("hidden", [12289, 16391])
+def test_persistent_grid_weight_staged_in_lds(abi, hidden):
+    """A persistent grid over a tail variant that stages the weight in LDS
+    (flags bit 14; rows of odd width, each shifted by its own amount): every
+    workgroup stages the weight in its first row group and reads it there for
+    all its later ones."""
+    from hp_rms_norm_amd.abi import Config
+    base = abi.select_config(1024, hidden, DT[torch.bfloat16])
+    assert base.flags & 16384, base.as_tuple()
+    for grid in (1, 7, 64):
+        cfg = Config(*base.as_tuple())
+        cfg.grid_blocks = grid
+        check_case(abi, 1024, hidden, torch.bfloat16, seed=grid + hidden, config=cfg)
+
+
 # ---- odd widths, misalignment, row strides, the general tier --------------------------
 # odd widths (the vector tiers' tail variants from 8 up, the general tier below 8 and above
 # 65543) on both sides of the table's rows and of the general kernels' block sizes
