@@ -423,19 +423,21 @@ def test_tail_weight_staged_in_lds(abi, hidden, off, pad, dtype):
     assert_output_close(bits(ov.view), p_out, dtype, "reduce output " + tag)
 
 
-@pytest.mark.parametrize("hidden,off,pad", [(8192, 8, 8), (16384, 1, 8), (4097, 0, 0)])
-def test_off_grid_rows_in_a_hip_graph(abi, hidden, off, pad):
+@pytest.mark.parametrize("hidden,off,pad,rows", [(8192, 8, 8, 300), (16384, 1, 8, 300), (4097, 0, 0, 300),
+                                                 (16384, 1, 8, 1024)])
+def test_off_grid_rows_in_a_hip_graph(abi, hidden, off, pad, rows):
     """Rotated (16-byte aligned off the grid), shifted (2 bytes off) and odd-width rows captured
-    in a HIP graph: each replay, with fresh inputs copied in and eager work between replays,
-    gives the same bits as the eager call on the same layout."""
+    in a HIP graph (at 1024 rows the shifted rows' weight staged in LDS): each replay, with fresh
+    inputs copied in and eager work between replays, gives the same bits as the eager call on the
+    same layout."""
     import hp_rms_norm_amd
-    dtype, rows, eps = torch.bfloat16, 300, 1e-6
+    dtype, eps = torch.bfloat16, 1e-6
     stride = hidden + off + pad
     bx = torch.zeros(rows, stride, dtype=dtype, device=DEV)
     br = torch.zeros_like(bx)
     xs, rs = bx[:, off:off + hidden], br[:, off:off + hidden]
     wd = make_inputs(1, hidden, dtype, 0)[2].to(DEV)
-    print("off-grid graph", hidden, off, pad, flush=True)
+    print("off-grid graph", hidden, off, pad, rows, flush=True)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
