@@ -119,7 +119,8 @@ bool latency_config(int64_t rows, int64_t nvec, int mode, hprms_config* c) {
     const Row& r = lat[i];
     if (nvec <= r.max_nvec) {
       if (rows > max_rows[cls][i]) return false;
-      *c = hprms_config{1, r.lpr, r.vpl, 0, r.lpr, 0, nvec <= 256 ? 3 : 7};
+      // (the partial sums load all their parts before adding them: flags bit 15)
+      *c = hprms_config{1, r.lpr, r.vpl, 0, r.lpr, 0, (nvec <= 256 ? 3 : 7) | (mode == 4 ? 32768 : 0)};
       return true;
     }
   }

@@ -62,7 +62,8 @@
 // workgroup loads the whole weight once, aligned, before its first row
 // group's loads, writes it to LDS after them, and every row reads its
 // vectors from there (five dwords each, funnel-shifted by the row's 2-byte
-// phase) after the row-sum barrier.
+// phase) after the row-sum barrier.  Bit 15 (MODE 4): each group of vectors
+// loads every part before adding the first (the latency rows).
 //
 // The residual is stored as soon as it is formed: deferring it to the output
 // phase (one write burst per workgroup) measured up to 5% slower.
@@ -191,6 +192,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   // its partial last vector and one vector of slack for the five-dword reads
   constexpr bool WLDS = (FLAGS & 16384) != 0;
   static_assert(!WLDS || (TAIL && WLATE && LDSV == 0 && WPR > 1 && MODE != 2), "weight staged in LDS");
+  static_assert((FLAGS & 32768) == 0 || MODE == 4, "parts prefetched: partial sums only");
   constexpr int NST = WLDS ? (LPR * VPL + BLOCK - 1) / BLOCK : 1;  // staged vectors per thread
   __shared__ u32x4 wlds[WLDS ? LPR * VPL + 2 : 1];
   bool staged = false;
@@ -440,7 +442,12 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       // lane: past the VGPR budget of the wide shapes); the tail goes with the
       // last group.  The unrolled loops keep every parts[] and slot index a
       // constant.
-      constexpr int G = VPL <= 4 ? VPL : 2;
+      // FLAGS bit 15 (the latency rows, few rows per call): each group's loads
+      // of every part are issued before the first part is added, so the parts
+      // cost one memory round trip rather than one each (G <= 2: at most 7 x 2
+      // vectors in flight per lane)
+      constexpr bool PF = (FLAGS & 32768) != 0;
+      constexpr int G = PF ? (VPL < 2 ? VPL : 2) : (VPL <= 4 ? VPL : 2);
 #pragma unroll
       for (int k0 = 0; k0 < VPL; k0 += G) {
         const bool with_tail = TAIL && k0 + G >= VPL;
@@ -461,8 +468,46 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
             tacc[2 * j + 1] = F::hi(txv[j]);
           }
         }
+        if constexpr (PF) {
+          const int np = opaque(a.nparts);
+          u32x4 ppv[HPRMS_MAX_PARTS - 1][G], ptv[HPRMS_MAX_PARTS - 1];
+#pragma unroll
+          for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+            if (g < np) {
+              const __amdgpu_buffer_rsrc_t prs = make_rsrc(opaque(a.parts[g]) + row0 * x_stride, xbytes);
+#pragma unroll
+              for (int i = 0; i < G; ++i) {
+                const int k = k0 + i < VPL ? k0 + i : 0;
+                ppv[g - 1][i] = load16<LAUX>(prs, (k0 + i < VPL && row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
+              }
+              ptv[g - 1] = u32x4{};
+              if (with_tail && eok) ptv[g - 1] = load16<LAUX>(prs, exoff);
+            }
+          }
+          // added in part order, as below
+#pragma unroll
+          for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+            if (g < np) {
+#pragma unroll
+              for (int i = 0; i < G; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                  acc[i][2 * j] += F::lo(ppv[g - 1][i][j]);
+                  acc[i][2 * j + 1] += F::hi(ppv[g - 1][i][j]);
+                }
+              if (with_tail) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                  tacc[2 * j] += F::lo(ptv[g - 1][j]);
+                  tacc[2 * j + 1] += F::hi(ptv[g - 1][j]);
+                }
+              }
+            }
+          }
+        }
 #pragma unroll
         for (int g = 1; g < HPRMS_MAX_PARTS; ++g) {
+          if (PF) break;
           if (g >= opaque(a.nparts)) break;
           const __amdgpu_buffer_rsrc_t prs = make_rsrc(opaque(a.parts[g]) + row0 * x_stride, xbytes);
           u32x4 pv[G], tpv = {};

@@ -58,28 +58,34 @@ struct FusedEntry {
 // Per mode, exactly the shapes its dispatch table (hprms.hip) can choose:
 // the rows every mode shares, then each mode's own.  A CPU test enumerates the
 // tables and checks that these lists hold every reachable shape and no other.
-#define HPRMS_COMMON_SHAPES(X, DT, MODE)                                                         \
+#define HPRMS_COMMON_BW_SHAPES(X, DT, MODE)                                                      \
   X(DT, MODE, 16, 1, 0, 256, 3) X(DT, MODE, 32, 1, 0, 256, 3) X(DT, MODE, 64, 1, 0, 256, 3)      \
-  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 8, 4, 1024, 31) \
-  X(DT, MODE, 64, 2, 0, 64, 3) X(DT, MODE, 128, 2, 0, 128, 3) X(DT, MODE, 256, 2, 0, 256, 7)      \
-  X(DT, MODE, 512, 2, 0, 512, 7) X(DT, MODE, 512, 4, 0, 512, 7)
+  X(DT, MODE, 32, 4, 0, 256, 131) X(DT, MODE, 512, 3, 0, 512, 159) X(DT, MODE, 1024, 8, 4, 1024, 31)
+// the latency rows (hprms.hip, latency_config; FL = 32768 for the partial sums,
+// which load all parts before adding them)
+#define HPRMS_LATENCY_SHAPES(X, DT, MODE, FL)                                                     \
+  X(DT, MODE, 64, 2, 0, 64, 3 | FL) X(DT, MODE, 128, 2, 0, 128, 3 | FL) X(DT, MODE, 256, 2, 0, 256, 7 | FL) \
+  X(DT, MODE, 512, 2, 0, 512, 7 | FL) X(DT, MODE, 512, 4, 0, 512, 7 | FL)
+#define HPRMS_COMMON_SHAPES(X, DT, MODE) HPRMS_COMMON_BW_SHAPES(X, DT, MODE) HPRMS_LATENCY_SHAPES(X, DT, MODE, 0)
 
 // the fused op in place (mode 0) and its out-of-place (3) and partial-sum (4)
 // forms.  In 1024 x 2 and 1024 x 3 these modes load the weight with the row
 // (flags 27 / 155) except in the tail variants (31 / 159), which have no
 // LDS-tier 256 x 8 either (hprms.hip, table_config and tail_shape).
-#define HPRMS_FUSED_ROWS(X, DT, MODE, F2, F3)                                                     \
-  HPRMS_COMMON_SHAPES(X, DT, MODE)                                                                \
+#define HPRMS_FUSED_ROWS(X, DT, MODE, F2, F3, FL)                                                 \
+  HPRMS_COMMON_BW_SHAPES(X, DT, MODE) HPRMS_LATENCY_SHAPES(X, DT, MODE, FL)                        \
   X(DT, MODE, 64, 4, 0, 256, 135) X(DT, MODE, 128, 3, 0, 256, 7) X(DT, MODE, 1024, 2, 0, 1024, F2) \
   X(DT, MODE, 1024, 3, 0, 1024, F3) X(DT, MODE, 1024, 4, 0, 1024, 159)
-#define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159)
-#define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155) X(DT, MODE, 256, 8, 4, 256, 27)
+#define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159, 0)
+#define HPRMS_MODE4_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159, 32768)
+#define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155, 0) X(DT, MODE, 256, 8, 4, 256, 27)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
 #define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
 #define HPRMS_MODE3_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
-#define HPRMS_MODE4_SHAPES(X, DT, MODE) \
-  HPRMS_MODE3_SHAPES(X, DT, MODE) X(DT, MODE, 256, 4, 0, 256, 3)
+#define HPRMS_MODE4_SHAPES(X, DT, MODE)                                                           \
+  HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155, 32768) X(DT, MODE, 256, 8, 4, 256, 27)                   \
+  X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3)
 
 // plain RMSNorm (mode 1)
 #define HPRMS_MODE1_SHAPES(X, DT, MODE)                                                           \
@@ -106,7 +112,7 @@ struct FusedEntry {
   HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 0) ENTRY(DT, 0, 128, 4, 0, 256, 131)                        \
   HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2)                              \
   HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 3) ENTRY(DT, 3, 128, 4, 0, 256, 131)                        \
-  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 4) ENTRY(DT, 4, 128, 4, 0, 256, 131) ENTRY(DT, 4, 256, 4, 0, 256, 3)
+  HPRMS_MODE4_TAIL_SHAPES(ENTRY, DT, 4) ENTRY(DT, 4, 128, 4, 0, 256, 131) ENTRY(DT, 4, 256, 4, 0, 256, 3)
 #define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
 
 // The shapes with sc1 bits among the lists of modes 0, 1, 3 and 4 (their

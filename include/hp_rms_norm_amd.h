@@ -207,7 +207,9 @@ typedef struct {
                                bit 7: a lane's residual loads issued before its input loads;
                                bit 14 (with bit 6, late weight, rows of several waves, not
                                the FP8 output): the whole weight loaded once per workgroup
-                               with aligned loads into LDS, where shifted rows read it */
+                               with aligned loads into LDS, where shifted rows read it;
+                               bit 15 (partial sums, the latency rows): every part's loads
+                               issued before the first part is added */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,

@@ -164,6 +164,7 @@ def test_reduce_every_table_row(abi, dtype, nparts):
                 # the in-place op with the reduce form's shape and variant (the same fp32
                 # summation order)
                 cfg = as_dispatched(abi, abi.select_config(rows, hidden, DT[dtype], abi.MODE_REDUCE), hidden)
+                cfg.flags &= ~32768   # (the partial sums' part prefetch: no in-place counterpart)
                 xd, rd2 = parts[0].to(DEV), r.to(DEV)
                 abi.BENCH.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd2.data_ptr(), rows, hidden, hidden, hidden,
                                             DT[dtype], 1e-6, _stream(), cfg)
