@@ -905,6 +905,29 @@ def run_extra(torch, ops, args):
         del sets
         torch.cuda.empty_cache()
     out["reduce_parts_bf16"] = red
+    # the same form at decode sizes (a tensor-parallel step's all-reduce with a few rows): the
+    # latency rows load every part before adding them; the fused op beside them (0 parts)
+    redd = []
+    for h in (4096, 8192):
+        for rows in (1, 32):
+            g = torch.Generator(device="cuda:0").manual_seed(h + rows)
+            w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+            for nparts in (0, 2, 8):
+                sets = [([torch.randn(rows, h, device="cuda:0", generator=g).to(torch.bfloat16)
+                          for _ in range(max(nparts, 1))],
+                         torch.randn(rows, h, device="cuda:0", generator=g).to(torch.bfloat16),
+                         torch.empty(rows, h, dtype=torch.bfloat16, device="cuda:0")) for _ in range(16)]
+
+                def call(i, sets=sets, w=w, nparts=nparts):
+                    parts, r, o = sets[i]
+                    if nparts:
+                        ops.reduce_add_rms_norm(o, parts, w, r, EPS)
+                    else:
+                        ops.hp_rms_norm(parts[0], w, r, EPS)
+                us = time_rotating(torch, call, len(sets), steps, args.warmup)
+                redd.append({"parts": nparts, "rows": rows, "hidden": h, "us_per_call": round(us, 2)})
+                del sets
+    out["reduce_parts_decode_bf16"] = redd
     # streamer (the reference "relu" = copy, and the true ReLU) at (4096, 14336)
     rows, h = B, 14336
     res = []
