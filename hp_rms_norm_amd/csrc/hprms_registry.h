@@ -24,7 +24,8 @@ struct FusedEntry {
 // bit 8 = held to 8 waves per SIMD, bit 9 = timeline instrumentation (bench
 // library only), bit 11 = one workgroup per CU (the launch reserves LDS),
 // bit 12 = the output phase's separate unpack (bench library), bit 13 = sc0 on
-// the stores (bench library)
+// the stores (bench library), bit 14 = the tail variant's weight staged in
+// LDS, bit 15 = the partial sums' parts loaded before any is added
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
