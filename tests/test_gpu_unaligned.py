@@ -542,8 +542,9 @@ SHIFT_WIDTHS = [4104, 4105, 8195, 16384, 32773]
 
 
 @pytest.mark.parametrize("hidden", SHIFT_WIDTHS)
-@pytest.mark.parametrize("dtype,rows,nparts", [(torch.bfloat16, 21, 3), (torch.float16, 300, 8)],
-                         ids=["bf16-latency-table", "fp16-bandwidth-table"])
+@pytest.mark.parametrize("dtype,rows,nparts", [(torch.bfloat16, 21, 3), (torch.float16, 300, 8),
+                                               (torch.float16, 64, 8)],
+                         ids=["bf16-latency-table", "fp16-bandwidth-table", "fp16-latency-table-8-parts"])
 def test_shifted_rows_every_mode(abi, hidden, dtype, rows, nparts):
     """From 513 whole vectors up, rows of calls whose streams are all off
     16-byte alignment (element offsets 1-7; row strides not a multiple of 8,
