@@ -80,10 +80,18 @@ struct FusedEntry {
 #define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159, 0)
 #define HPRMS_MODE4_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159, 32768)
 #define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155, 0) X(DT, MODE, 256, 8, 4, 256, 27)
-#define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131)
+// 32 lanes x 5-10 vectors, two rows per one-wave workgroup: the fused op in
+// and out of place at 1K-2.5K and 1024 < rows <= 4096 (hprms.hip, wide_rows)
+#define HPRMS_WIDE_ROWS(X, DT, MODE)                                                              \
+  X(DT, MODE, 32, 5, 0, 64, 135) X(DT, MODE, 32, 6, 0, 64, 135) X(DT, MODE, 32, 7, 0, 64, 135)     \
+  X(DT, MODE, 32, 8, 0, 64, 135) X(DT, MODE, 32, 9, 0, 64, 135) X(DT, MODE, 32, 10, 0, 64, 135)
+#define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
+  HPRMS_WIDE_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
-#define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
-#define HPRMS_MODE3_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131)
+#define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) \
+  HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(X, DT, MODE)
+#define HPRMS_MODE3_SHAPES(X, DT, MODE) \
+  HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(X, DT, MODE)
 #define HPRMS_MODE4_SHAPES(X, DT, MODE)                                                           \
   HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155, 32768) X(DT, MODE, 256, 8, 4, 256, 27)                   \
   X(DT, MODE, 128, 4, 0, 256, 131) X(DT, MODE, 256, 4, 0, 256, 3)
@@ -110,9 +118,9 @@ struct FusedEntry {
 #define HPRMS_ALL_MODES(ENTRY, DT) HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_ALL_MODES_OFFGRID(ENTRY, DT) HPRMS_MODE0_OFFGRID_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_ALL_MODES_TAIL(ENTRY, DT)                                                           \
-  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 0) ENTRY(DT, 0, 128, 4, 0, 256, 131)                        \
+  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 0) ENTRY(DT, 0, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(ENTRY, DT, 0) \
   HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2)                              \
-  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 3) ENTRY(DT, 3, 128, 4, 0, 256, 131)                        \
+  HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 3) ENTRY(DT, 3, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(ENTRY, DT, 3) \
   HPRMS_MODE4_TAIL_SHAPES(ENTRY, DT, 4) ENTRY(DT, 4, 128, 4, 0, 256, 131) ENTRY(DT, 4, 256, 4, 0, 256, 3)
 #define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
 

@@ -122,6 +122,30 @@ def entry_points_find_kernels(L, hidden, dtype, base):
         assert rc == want, (h, fmt, abi.last_error())
 
 
+def test_wide_rows_at_1k_to_2_5k():
+    """At 1K-2.5K and 1024 < rows <= 4096 the fused op in and out of place take
+    32 lanes x ceil(H / 256) vectors, two rows per one-wave workgroup, except
+    at 1K-2K where the table's 64 x 4 (four rows per workgroup) comes out in
+    even rounds over the 256 CUs at up to 3072 rows; the other forms, other
+    row counts and 2.5K-3K keep the table's rows."""
+    bf = abi.DTYPE_BF16
+    wide = {1032: (1280, 1536, 2304, 2560, 3584, 4096), 2048: (1280, 1536, 2304, 2560, 3584, 4096),
+            2056: (1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096),
+            2560: (1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096)}
+    for hidden, rows_wide in wide.items():
+        for rows in (512, 1024, 1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096, 5120, 8192):
+            for mode in (abi.MODE_FUSED, abi.MODE_OUT):
+                c = abi.select_config(rows, hidden, bf, mode)
+                if rows in rows_wide:
+                    assert (c.lanes_per_row, c.vec_per_lane, c.block_threads, c.flags & ~96) == \
+                        (32, -(-hidden // 256), 64, 135), (hidden, rows, mode)
+                else:
+                    assert c.lanes_per_row != 32 or c.block_threads != 64, (hidden, rows, mode)
+            for mode in (abi.MODE_PLAIN, abi.MODE_FP8, abi.MODE_REDUCE, abi.MODE_MXFP8):
+                assert abi.select_config(rows, hidden, bf, mode).lanes_per_row != 32, (hidden, rows, mode)
+    assert abi.select_config(4096, 3072, bf, abi.MODE_FUSED).lanes_per_row == 128
+
+
 def test_tail_weight_staged_in_lds_from_a_row_count():
     """The tail variants of 512 x 2-4 and 1024 x 2-3 stage the weight in LDS
     (flags bit 14) from 1024 rows (plain RMSNorm: 384), never in 1024 x 4, the
@@ -194,13 +218,16 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 rc = L.hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype, 1e-6,
                                                       ctypes.byref(c), None)
                 assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
-                # the bench library also has the FP8 table's choice as a fused (mode 0)
-                # kernel, so the 16-bit op can be run with the same lane mapping
-                c8 = abi.select_config(rows, hidden, dtype, 2)
-                assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
-                rc = abi.BENCH.lib().hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden, dtype,
-                                                                    1e-6, ctypes.byref(c8), None)
-                assert rc == abi.HPRMS_OK, (hidden, c8.as_tuple(), abi.BENCH.last_error())
+                # the bench library also has the FP8 and partial-sum tables' choices as
+                # fused (mode 0) kernels, so the 16-bit op can be run with the same lane
+                # mapping (the partial sums' part prefetch has no in-place form)
+                for other in (2, 4):
+                    c8 = abi.select_config(rows, hidden, dtype, other)
+                    c8.flags &= ~32768
+                    assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
+                    rc = abi.BENCH.lib().hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden,
+                                                                        dtype, 1e-6, ctypes.byref(c8), None)
+                    assert rc == abi.HPRMS_OK, (hidden, other, c8.as_tuple(), abi.BENCH.last_error())
 
 
 def test_config_entry_rejects_unbuilt_and_misfit_configs():
@@ -337,7 +364,8 @@ def test_mx_entry_rejects_bad_arguments():
 
 def test_latency_rows_end_at_the_per_mode_limits():
     """The latency rows take calls up to a per-mode, per-width row count; the
-    next row count takes the bandwidth table (the same choice as 4096 rows)."""
+    next row count takes the bandwidth table (the same choice as 4096 rows, or
+    as 8192 rows where 4096 rows take the wide rows of 1K-2.5K)."""
     fp8_mx = {1024: 1024, 2048: 768, 4096: 768, 8192: 256, 16384: 256}
     limits = {abi.MODE_FUSED: {1024: 1024, 2048: 768, 4096: 768, 8192: 256, 16384: 384},
               abi.MODE_PLAIN: {1024: 1024, 2048: 256, 4096: 768, 8192: 256, 16384: 256},
@@ -349,7 +377,10 @@ def test_latency_rows_end_at_the_per_mode_limits():
                 lat = abi.select_config(1, hidden, dtype, mode).as_tuple()
                 assert abi.select_config(limit, hidden, dtype, mode).as_tuple() == lat, (mode, hidden)
                 past = abi.select_config(limit + 1, hidden, dtype, mode).as_tuple()
-                assert past == abi.select_config(4096, hidden, dtype, mode).as_tuple(), (mode, hidden)
+                want = abi.select_config(4096, hidden, dtype, mode)
+                if (want.lanes_per_row, want.block_threads) == (32, 64):
+                    want = abi.select_config(8192, hidden, dtype, mode)
+                assert past == want.as_tuple(), (mode, hidden)
 
 
 def test_bench_library_is_apart_from_the_product():

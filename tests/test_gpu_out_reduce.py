@@ -80,6 +80,37 @@ def test_out_of_place_every_table_row(abi, dtype):
             assert np.array_equal(bits(rod), ip_res), "residual differs from the in-place op " + tag
 
 
+# the wide rows of 1K-2.5K (32 lanes x ceil(H / 256) vectors, two rows per one-wave
+# workgroup) at row counts the dispatch gives them, on and off the 128-byte grid
+WIDE_CASES = [(1280, 1032), (1536, 2048), (4096, 1536), (2048, 2560), (3072, 2304), (1100, 1288), (4096, 2049)]
+
+
+@pytest.mark.parametrize("rows,hidden", WIDE_CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_wide_rows_in_and_out_of_place(abi, rows, hidden, dtype):
+    print("wide", rows, hidden, dtype, flush=True)
+    for mode in (abi.MODE_FUSED, abi.MODE_OUT):
+        c = abi.select_config(rows, hidden, DT[dtype], mode)
+        assert (c.lanes_per_row, c.block_threads) == (32, 64), (mode, c.as_tuple())
+    x, r, w = make_inputs(rows, hidden, dtype, seed=rows + hidden)
+    want_out, want_res = oracle_fused(x, r, w, 1e-6, dtype)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    od, rod = torch.empty_like(xd), torch.empty_like(rd)
+    run_out(abi, xd, rd, wd, od, rod, 1e-6)
+    torch.cuda.synchronize()
+    tag = f"{rows}x{hidden} {dtype}"
+    assert np.array_equal(bits(xd), bits(x)) and np.array_equal(bits(rd), bits(r)), "inputs modified " + tag
+    assert_residual_exact(bits(rod), want_res, dtype, "residual_out " + tag)
+    assert_output_close(bits(od), want_out, dtype, "out " + tag)
+    # the in-place op through its own dispatch: the same shape, so the same bits
+    abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
+                          1e-6, _stream())
+    torch.cuda.synchronize()
+    assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
+    assert np.array_equal(bits(xd), bits(od)), "in place differs from out of place " + tag
+    assert np.array_equal(bits(rd), bits(rod)), "residual differs from out of place " + tag
+
+
 def test_out_of_place_torch_ops_and_aliases(abi):
     import hp_rms_norm_amd
     x, r, w = make_inputs(300, 4096, torch.bfloat16, seed=5)
