@@ -231,19 +231,25 @@ bool weight_late_1024(int mode, const hprms_config& c) {
   return !(mode == 0 || mode == 3 || mode == 4);
 }
 
-// Rows of 1K-2.5K (128 < H / 8 <= 320) in the fused op in and out of place,
+// Rows of 1K-3K (128 < H / 8 <= 384) in the fused op in and out of place,
 // 1024 < rows <= 4096: 32 lanes x ceil(H / 256) vectors, two rows per one-wave
 // workgroup (flags 135: residual first, weight late), in place of the table's
-// 128 x 3 (two rows per 256-lane workgroup) and, where its last round of
-// workgroups leaves CUs idle or past 3072 rows, of its 64 x 4 (four).  Two
-// builds side by side, 7 interleaved trials, both dtypes, H = 1536 / 2048 /
-// 2304 / 2560: 5-15% faster at 1280-1536, 2304-2560 and 3584-4096 rows and at
-// 2048-3072 rows past 2K; within 3% at 1280 rows past 2K.  Kept out of: 64 x 4
-// with even rounds at 1024 / 1792-2048 / 3072 rows (0-16% slower), 1024 rows
-// and fewer (up to 27% slower out of place), and 5120 rows and more (fp16 and
-// the out-of-place op up to 14% slower, bf16 in place up to 8% faster).  Eight
-// rows per 256-lane workgroup, 32 x 11 and x 12 (2.5K-3K), and the FP8, MX
-// and partial-sum forms measured slower with the wider rows.
+// 128 x 3 (2K-3K) and, where its last round of workgroups leaves CUs idle or
+// past 3072 rows, of its 64 x 4 (four rows per 256-lane workgroup, 1K-2K).
+// Two builds side by side, 7 interleaved trials, both dtypes: at 1K-2.5K
+// 5-15% faster at 1280-1536, 2304-2560 and 3584-4096 rows and at 2048-3072
+// rows past 2K, within 3% at 1280 rows past 2K; at 2.5K-3K 7-16% faster at
+// 1536-4096 rows (4096 x 3072 bf16: 18.07 -> 16.66 us) but 3-7% slower for
+// fp16 in place at 4096 rows (2816, and rows off the 128-byte grid); at
+// 1280-1536 rows 8-14% faster out of place, 0-6% slower in place (which
+// keeps the table there).  Kept out of: 64 x 4 with even
+// rounds at 1024 / 1792-2048 / 3072 rows (0-16% slower), 1024 rows and fewer
+// (up to 27% slower out of place), 5120 rows and more (fp16 and the
+// out-of-place op up to 14% slower, 32 x 11 and x 12 6-8% at 8192 rows), and
+// past 3K, where 32 x 13 and x 14 need the whole register file in some forms
+// (one wave per SIMD: 2-7% slower there; held to two waves they spill).
+// Eight rows per 256-lane workgroup, and the FP8, MX and partial-sum forms,
+// measured slower with the wider rows.
 constexpr int64_t kCUs = 256;   // MI355X
 
 // rows per CU with `rows_per_wg` rows per workgroup, whole rounds of workgroups
@@ -252,7 +258,8 @@ int64_t rows_per_cu(int64_t rows, int64_t rows_per_wg) {
 }
 
 bool wide_rows(int64_t rows, int64_t nvec, int mode) {
-  if ((mode != 0 && mode != 3) || nvec <= 128 || nvec > 320 || rows <= 1024 || rows > 4096) return false;
+  if ((mode != 0 && mode != 3) || nvec <= 128 || nvec > 384 || rows <= 1024 || rows > 4096) return false;
+  if (nvec > 320) return mode == 3 || rows > 1536;
   return nvec > 256 || rows > 3072 || rows_per_cu(rows, 2) < rows_per_cu(rows, 4);
 }
 
@@ -261,6 +268,10 @@ bool wide_rows(int64_t rows, int64_t nvec, int mode) {
 void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_config* c) {
   const int64_t nvec = hidden / 8;
   if (latency_config(rows, nvec, mode, c)) return;
+  if (wide_rows(rows, nvec, mode)) {
+    *c = hprms_config{1, 32, (int)((nvec + 31) / 32), 0, 64, 0, 135};
+    return;
+  }
   if (mode == 0 && grid && inplace_config(nvec, c)) return;
   if (mode == 1 && plain_config(nvec, c)) return;
   if (mode == 4 && reduce_config(nvec, c)) return;
@@ -296,7 +307,6 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_confi
       c->flags = r.flags;
       c->tier = r.ldsv > 0 ? 2 : 1;
       if (weight_late_1024(mode, *c)) c->flags |= 4;
-      if (wide_rows(rows, nvec, mode)) *c = hprms_config{1, 32, (int)((nvec + 31) / 32), 0, 64, 0, 135};
       return;
     }
   }

@@ -80,11 +80,12 @@ struct FusedEntry {
 #define HPRMS_FUSED_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159, 0)
 #define HPRMS_MODE4_TAIL_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 31, 159, 32768)
 #define HPRMS_FUSED_SHAPES(X, DT, MODE) HPRMS_FUSED_ROWS(X, DT, MODE, 27, 155, 0) X(DT, MODE, 256, 8, 4, 256, 27)
-// 32 lanes x 5-10 vectors, two rows per one-wave workgroup: the fused op in
-// and out of place at 1K-2.5K and 1024 < rows <= 4096 (hprms.hip, wide_rows)
+// 32 lanes x 5-12 vectors, two rows per one-wave workgroup: the fused op in
+// and out of place at 1K-3K and 1024 < rows <= 4096 (hprms.hip, wide_rows)
 #define HPRMS_WIDE_ROWS(X, DT, MODE)                                                              \
   X(DT, MODE, 32, 5, 0, 64, 135) X(DT, MODE, 32, 6, 0, 64, 135) X(DT, MODE, 32, 7, 0, 64, 135)     \
-  X(DT, MODE, 32, 8, 0, 64, 135) X(DT, MODE, 32, 9, 0, 64, 135) X(DT, MODE, 32, 10, 0, 64, 135)
+  X(DT, MODE, 32, 8, 0, 64, 135) X(DT, MODE, 32, 9, 0, 64, 135) X(DT, MODE, 32, 10, 0, 64, 135)    \
+  X(DT, MODE, 32, 11, 0, 64, 135) X(DT, MODE, 32, 12, 0, 64, 135)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
   HPRMS_WIDE_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)

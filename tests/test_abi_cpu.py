@@ -122,28 +122,32 @@ def entry_points_find_kernels(L, hidden, dtype, base):
         assert rc == want, (h, fmt, abi.last_error())
 
 
-def test_wide_rows_at_1k_to_2_5k():
-    """At 1K-2.5K and 1024 < rows <= 4096 the fused op in and out of place take
+def test_wide_rows_at_1k_to_3k():
+    """At 1K-3K and 1024 < rows <= 4096 the fused op in and out of place take
     32 lanes x ceil(H / 256) vectors, two rows per one-wave workgroup, except
     at 1K-2K where the table's 64 x 4 (four rows per workgroup) comes out in
-    even rounds over the 256 CUs at up to 3072 rows; the other forms, other
-    row counts and 2.5K-3K keep the table's rows."""
+    even rounds over the 256 CUs at up to 3072 rows, and past 2.5K in place
+    at up to 1536 rows; the other forms, other row counts and widths past 3K
+    keep the table's rows."""
     bf = abi.DTYPE_BF16
+    every = (1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096)
     wide = {1032: (1280, 1536, 2304, 2560, 3584, 4096), 2048: (1280, 1536, 2304, 2560, 3584, 4096),
-            2056: (1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096),
-            2560: (1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096)}
+            2056: every, 2560: every, 2816: every, 3072: every}
     for hidden, rows_wide in wide.items():
-        for rows in (512, 1024, 1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096, 5120, 8192):
+        for rows in (512, 1024) + every + (5120, 8192):
             for mode in (abi.MODE_FUSED, abi.MODE_OUT):
                 c = abi.select_config(rows, hidden, bf, mode)
-                if rows in rows_wide:
+                # past 2.5K the in-place op starts above 1536 rows
+                if rows in rows_wide and not (hidden > 2560 and mode == abi.MODE_FUSED and rows <= 1536):
                     assert (c.lanes_per_row, c.vec_per_lane, c.block_threads, c.flags & ~96) == \
                         (32, -(-hidden // 256), 64, 135), (hidden, rows, mode)
                 else:
                     assert c.lanes_per_row != 32 or c.block_threads != 64, (hidden, rows, mode)
             for mode in (abi.MODE_PLAIN, abi.MODE_FP8, abi.MODE_REDUCE, abi.MODE_MXFP8):
                 assert abi.select_config(rows, hidden, bf, mode).lanes_per_row != 32, (hidden, rows, mode)
-    assert abi.select_config(4096, 3072, bf, abi.MODE_FUSED).lanes_per_row == 128
+    for mode in (abi.MODE_FUSED, abi.MODE_OUT):
+        for hidden in (3080, 3584, 4096):
+            assert abi.select_config(4096, hidden, bf, mode).lanes_per_row != 32
 
 
 def test_tail_weight_staged_in_lds_from_a_row_count():

@@ -80,9 +80,10 @@ def test_out_of_place_every_table_row(abi, dtype):
             assert np.array_equal(bits(rod), ip_res), "residual differs from the in-place op " + tag
 
 
-# the wide rows of 1K-2.5K (32 lanes x ceil(H / 256) vectors, two rows per one-wave
+# the wide rows of 1K-3K (32 lanes x ceil(H / 256) vectors, two rows per one-wave
 # workgroup) at row counts the dispatch gives them, on and off the 128-byte grid
-WIDE_CASES = [(1280, 1032), (1536, 2048), (4096, 1536), (2048, 2560), (3072, 2304), (1100, 1288), (4096, 2049)]
+WIDE_CASES = [(1280, 1032), (1536, 2048), (4096, 1536), (2048, 2560), (3072, 2304), (1100, 1288), (4096, 2049),
+              (4096, 3072), (1600, 2817), (2000, 3064)]
 
 
 @pytest.mark.parametrize("rows,hidden", WIDE_CASES)
