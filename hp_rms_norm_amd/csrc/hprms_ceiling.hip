@@ -3,7 +3,7 @@
 // the fused add + RMSNorm op in simpler ways, so that the op's time can be
 // set beside what the same hardware needs for the same traffic:
 //
-//   hprms_ceil_empty     a grid of empty workgroups of 256, 512 or 1024 lanes
+//   hprms_ceil_empty     a grid of empty workgroups of 64, 256, 512 or 1024 lanes
 //                        (launch, dispatch and teardown of a kernel of that
 //                        grid, no memory traffic)
 //   hprms_ceil_read      read two tensors of n bytes (the op's two read streams)
@@ -182,7 +182,7 @@ const SkelEntry kSkel[] = {
     HPRMS_SKEL_FLAGS(128, 4, 256) HPRMS_SKEL_FLAGS(256, 2, 256) HPRMS_SKEL_FLAGS(256, 4, 256)
     HPRMS_SKEL_FLAGS(512, 2, 512) HPRMS_SKEL_FLAGS(512, 3, 512) HPRMS_SKEL_FLAGS(512, 4, 512)
     HPRMS_SKEL_FLAGS(1024, 2, 1024) HPRMS_SKEL_FLAGS(256, 8, 256) HPRMS_SKEL_FLAGS(1024, 3, 1024)
-    HPRMS_SKEL_FLAGS(1024, 4, 1024)
+    HPRMS_SKEL_FLAGS(1024, 4, 1024) HPRMS_SKEL_FLAGS(32, 8, 64) HPRMS_SKEL_FLAGS(32, 12, 64)
 };
 
 int launched() { return hipGetLastError() == hipSuccess ? HPRMS_OK : HPRMS_E_LAUNCH; }
@@ -200,11 +200,13 @@ using namespace hprms;
 
 extern "C" {
 
-// block: 256, 512 or 1024 lanes (the table's workgroup sizes)
+// block: 64, 256, 512 or 1024 lanes (the table's workgroup sizes)
 int hprms_ceil_empty(int64_t grid, int block, hipStream_t stream) {
   if (grid < 1 || grid > 0x7fffffff) return HPRMS_E_INVALID;
   const dim3 g((unsigned)grid);
-  if (block == 256)
+  if (block == 64)
+    ceil_empty_kernel<64><<<g, dim3(64), 0, stream>>>();
+  else if (block == 256)
     ceil_empty_kernel<256><<<g, dim3(256), 0, stream>>>();
   else if (block == 512)
     ceil_empty_kernel<512><<<g, dim3(512), 0, stream>>>();

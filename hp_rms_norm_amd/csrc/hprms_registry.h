@@ -223,7 +223,8 @@ struct FusedEntry {
   X(DT, MODE, 32, 4, 0, 256, 643) X(DT, MODE, 64, 4, 0, 256, 647) X(DT, MODE, 128, 3, 0, 256, 519) \
   X(DT, MODE, 256, 2, 0, 256, 643) X(DT, MODE, 512, 2, 0, 512, 519) X(DT, MODE, 512, 3, 0, 512, 671) \
   X(DT, MODE, 1024, 2, 0, 1024, 539) X(DT, MODE, 256, 8, 4, 256, 539) X(DT, MODE, 1024, 3, 0, 1024, 667) \
-  X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 643)
+  X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 643) X(DT, MODE, 32, 8, 0, 64, 647)   \
+  X(DT, MODE, 32, 12, 0, 64, 647)
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every

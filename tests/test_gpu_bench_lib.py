@@ -94,7 +94,7 @@ def test_ceiling_kernels_move_what_they_claim(abi):
     assert L.hprms_ceil_read(a.data_ptr(), b.data_ptr(), n, sink.data_ptr(), s) == 0
     wa, wb = torch.zeros_like(a), torch.zeros_like(a)
     assert L.hprms_ceil_write(wa.data_ptr(), wb.data_ptr(), n, s) == 0
-    for block in (256, 512, 1024):
+    for block in (64, 256, 512, 1024):
         assert L.hprms_ceil_empty(1000, block, s) == 0
     torch.cuda.synchronize()
     v = np.arange(n // 16, dtype=np.uint32).repeat(4)
@@ -102,7 +102,8 @@ def test_ceiling_kernels_move_what_they_claim(abi):
     assert np.array_equal(wb.cpu().numpy().view(np.uint32), ~v)
 
 
-@pytest.mark.parametrize("shape", [(128, 4, 256, 131), (512, 2, 512, 3), (1024, 4, 1024, 155), (64, 4, 256, 27)])
+@pytest.mark.parametrize("shape", [(128, 4, 256, 131), (512, 2, 512, 3), (1024, 4, 1024, 155), (64, 4, 256, 27),
+                                   (32, 12, 64, 131)])
 def test_skeleton_moves_the_ops_bytes(abi, shape):
     """r <- x + r and x <- x ^ (r_new + t) per 32-bit word, t the binary32 bits of
     the row's sum of the low bytes of r_new's words (exact in fp32 at these sizes)."""
