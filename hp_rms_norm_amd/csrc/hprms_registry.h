@@ -86,8 +86,13 @@ struct FusedEntry {
   X(DT, MODE, 32, 5, 0, 64, 135) X(DT, MODE, 32, 6, 0, 64, 135) X(DT, MODE, 32, 7, 0, 64, 135)     \
   X(DT, MODE, 32, 8, 0, 64, 135) X(DT, MODE, 32, 9, 0, 64, 135) X(DT, MODE, 32, 10, 0, 64, 135)    \
   X(DT, MODE, 32, 11, 0, 64, 135) X(DT, MODE, 32, 12, 0, 64, 135)
+// 64 lanes x 7-10 vectors, one row per one-wave workgroup: the fused op in
+// place at 3K-5K up to 2048 rows on the 128-byte grid (hprms.hip, wave_rows)
+#define HPRMS_WAVE_ROWS(X, DT, MODE) \
+  X(DT, MODE, 64, 7, 0, 64, 135) X(DT, MODE, 64, 8, 0, 64, 135) X(DT, MODE, 64, 9, 0, 64, 135) \
+  X(DT, MODE, 64, 10, 0, 64, 135)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
-  HPRMS_WIDE_ROWS(X, DT, MODE)
+  HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
 #define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) \
   HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(X, DT, MODE)

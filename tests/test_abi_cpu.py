@@ -150,6 +150,25 @@ def test_wide_rows_at_1k_to_3k():
             assert abi.select_config(4096, hidden, bf, mode).lanes_per_row != 32
 
 
+def test_wave_rows_at_3k_to_5k():
+    """The in-place op on rows on the 128-byte grid at 3K-5K takes one row per
+    one-wave workgroup (64 lanes x ceil(H / 512) vectors) from the latency
+    rows' limit up to 2048 rows; rows off the grid, the other forms and more
+    rows keep the table."""
+    for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+        for hidden in (3080, 3584, 4096, 4608, 5120):
+            for rows in (769, 1024, 1536, 2048):
+                c = abi.select_config(rows, hidden, dtype, abi.MODE_FUSED)
+                assert c.as_tuple() == (1, 64, -(-hidden // 512), 0, 64, 0, 135), (hidden, rows)
+                for mode in (abi.MODE_OUT, abi.MODE_REDUCE, abi.MODE_PLAIN, abi.MODE_FP8):
+                    assert abi.select_config(rows, hidden, dtype, mode).block_threads != 64, (hidden, rows, mode)
+                odd = abi.select_config(rows, hidden + 1, dtype, abi.MODE_FUSED)   # off the grid
+                assert odd.block_threads != 64, (hidden, rows)
+            assert abi.select_config(2049, hidden, dtype, abi.MODE_FUSED).block_threads != 64
+        for hidden in (3072, 5128, 6144):
+            assert abi.select_config(1024, hidden, dtype, abi.MODE_FUSED).lanes_per_row != 64
+
+
 def test_tail_weight_staged_in_lds_from_a_row_count():
     """The tail variants of 512 x 2-4 and 1024 x 2-3 stage the weight in LDS
     (flags bit 14) from 1024 rows (plain RMSNorm: 384), never in 1024 x 4, the
@@ -369,7 +388,8 @@ def test_mx_entry_rejects_bad_arguments():
 def test_latency_rows_end_at_the_per_mode_limits():
     """The latency rows take calls up to a per-mode, per-width row count; the
     next row count takes the bandwidth table (the same choice as 4096 rows, or
-    as 8192 rows where 4096 rows take the wide rows of 1K-2.5K)."""
+    as 8192 rows where 4096 rows take the wide rows of 1K-3K), or, in place at
+    3K-5K, one row per one-wave workgroup."""
     fp8_mx = {1024: 1024, 2048: 768, 4096: 768, 8192: 256, 16384: 256}
     limits = {abi.MODE_FUSED: {1024: 1024, 2048: 768, 4096: 768, 8192: 256, 16384: 384},
               abi.MODE_PLAIN: {1024: 1024, 2048: 256, 4096: 768, 8192: 256, 16384: 256},
@@ -384,6 +404,8 @@ def test_latency_rows_end_at_the_per_mode_limits():
                 want = abi.select_config(4096, hidden, dtype, mode)
                 if (want.lanes_per_row, want.block_threads) == (32, 64):
                     want = abi.select_config(8192, hidden, dtype, mode)
+                if mode == abi.MODE_FUSED and 3072 < hidden <= 5120:
+                    want = abi.Config(1, 64, hidden // 512, 0, 64, 0, 135)
                 assert past == want.as_tuple(), (mode, hidden)
 
 

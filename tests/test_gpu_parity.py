@@ -143,6 +143,16 @@ def test_persistent_grid_weight_staged_in_lds(abi, hidden):
         check_case(abi, 1024, hidden, torch.bfloat16, seed=grid + hidden, config=cfg)
 
 
+# one row per one-wave workgroup: the in-place op at 3K-5K, on the 128-byte grid, from the
+# latency rows' limit up to 2048 rows
+@pytest.mark.parametrize("rows,hidden", [(1000, 4096), (1536, 3584), (2048, 5120), (800, 4608)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_wave_rows_through_the_table(abi, rows, hidden, dtype):
+    c = abi.select_config(rows, hidden, DT[dtype])
+    assert (c.lanes_per_row, c.block_threads) == (64, 64), c.as_tuple()
+    check_case(abi, rows, hidden, dtype, seed=rows + hidden)
+
+
 # ---- odd widths, misalignment, row strides, the general tier --------------------------
 # odd widths (the vector tiers' tail variants from 8 up, the general tier below 8 and above
 # 65543) on both sides of the table's rows and of the general kernels' block sizes
