@@ -263,18 +263,18 @@ bool wide_rows(int64_t rows, int64_t nvec, int mode) {
   return nvec > 256 || rows > 3072 || rows_per_cu(rows, 2) < rows_per_cu(rows, 4);
 }
 
-// Rows of 3K-5K (384 < H / 8 <= 640) in the fused op in place on the
-// 128-byte grid, from the latency rows' limit up to 2048 rows: one row per
-// one-wave workgroup, 64
+// Rows of 3K-5K (384 < H / 8 <= 640) in the fused op in and out of place on
+// the 128-byte grid, 768 < rows <= 2048: one row per one-wave workgroup, 64
 // lanes x ceil(H / 512) vectors (flags 135), in place of the table's 256 x 2
-// / 128 x 4 (one row per 256-lane workgroup) and 512 x 2.  Forced shapes, 7
-// interleaved trials, bf16: 8-15% faster at 1024-2048 rows (4096 wide: 7.32
-// -> 6.41 us at 1024 rows), fp16 8% at 2048 x 4096; 1-5% faster at 2560 and
-// 3072 rows, 3% slower at 4096.  Past 5K the fp16 kernels need the whole
-// register file (64 x 12: one wave per SIMD) and lost 2-7% at 2048 rows.
-// Rows off the grid keep the table (inplace_config: two rows per workgroup).
+// / 128 x 4 and 512 x 2.  Two builds side by side, 7 interleaved trials, both
+// dtypes, H = 3584-5120: in place 2-18% faster at 769-2048 rows (1024 x 4096
+// bf16: 7.36 -> 6.43 us), out of place 3-20%; out of place at 300-512 rows
+// 0-12% slower; with forced shapes 1-5% faster at 2560-3072 rows and 3%
+// slower at 4096.  Past 5K the fp16 kernels need the whole register file
+// (64 x 12: one wave per SIMD) and lost 2-7% at 2048 rows.  Rows off the grid
+// keep the table (inplace_config: two rows per workgroup).
 bool wave_rows(int64_t rows, int64_t nvec, int mode, bool grid) {
-  return mode == 0 && grid && nvec > 384 && nvec <= 640 && rows <= 2048;
+  return (mode == 0 || mode == 3) && grid && nvec > 384 && nvec <= 640 && rows > 768 && rows <= 2048;
 }
 
 // `grid`: every row of every stream starts on the 128-byte grid (only the
