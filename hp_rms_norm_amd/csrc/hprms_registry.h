@@ -92,8 +92,13 @@ struct FusedEntry {
 #define HPRMS_WAVE_ROWS(X, DT, MODE) \
   X(DT, MODE, 64, 7, 0, 64, 135) X(DT, MODE, 64, 8, 0, 64, 135) X(DT, MODE, 64, 9, 0, 64, 135) \
   X(DT, MODE, 64, 10, 0, 64, 135)
+// 128 lanes x 6-8 vectors, one row per two-wave workgroup: the fused op in
+// place at 5K-8K and 512 < rows <= 1280 on the 128-byte grid (hprms.hip,
+// pair_rows)
+#define HPRMS_PAIR_ROWS(X, DT, MODE) \
+  X(DT, MODE, 128, 6, 0, 128, 135) X(DT, MODE, 128, 7, 0, 128, 135) X(DT, MODE, 128, 8, 0, 128, 135)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
-  HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE)
+  HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE) HPRMS_PAIR_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
 #define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) \
   HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(X, DT, MODE)

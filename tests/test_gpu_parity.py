@@ -145,11 +145,14 @@ def test_persistent_grid_weight_staged_in_lds(abi, hidden):
 
 # one row per one-wave workgroup: the in-place op at 3K-5K, on the 128-byte grid, from the
 # latency rows' limit up to 2048 rows
-@pytest.mark.parametrize("rows,hidden", [(1000, 4096), (1536, 3584), (2048, 5120), (800, 4608)])
+# (64 lanes), and one row per two-wave workgroup at 5K-8K, 512 < rows <= 1280 (128 lanes)
+@pytest.mark.parametrize("rows,hidden,lanes", [(1000, 4096, 64), (1536, 3584, 64), (2048, 5120, 64),
+                                               (800, 4608, 64), (1024, 6144, 128), (600, 8192, 128),
+                                               (1280, 5248, 128)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
-def test_wave_rows_through_the_table(abi, rows, hidden, dtype):
+def test_wave_rows_through_the_table(abi, rows, hidden, lanes, dtype):
     c = abi.select_config(rows, hidden, DT[dtype])
-    assert (c.lanes_per_row, c.block_threads) == (64, 64), c.as_tuple()
+    assert (c.lanes_per_row, c.block_threads) == (lanes, lanes), c.as_tuple()
     check_case(abi, rows, hidden, dtype, seed=rows + hidden)
 
 
