@@ -277,15 +277,15 @@ bool wave_rows(int64_t rows, int64_t nvec, int mode, bool grid) {
   return (mode == 0 || mode == 3) && grid && nvec > 384 && nvec <= 640 && rows > 768 && rows <= 2048;
 }
 
-// Rows of 5K-8K (640 < H / 8 <= 1024) in the fused op in place on the
-// 128-byte grid, 512 < rows <= 1280: one row per two-wave workgroup, 128
+// Rows of 5K-8K (640 < H / 8 <= 1024) in the fused op in and out of place on
+// the 128-byte grid, 512 < rows <= 1280: one row per two-wave workgroup, 128
 // lanes x ceil(H / 1024) vectors (flags 135), in place of the table's 512 x 2
-// (one row per 8-wave workgroup).  Forced shapes, 7 interleaved trials, both
-// dtypes: 2-15% faster at 768-1280 rows (1024 x 6144 bf16: 10.26 -> 9.16 us;
-// fp16 at 768 x 8192 level); at 300 rows 3-14% slower, at 512 rows -10% to
-// +2%, at 1536-2560 rows -2% to +7%.
+// (one row per 8-wave workgroup).  Two builds side by side, 7 interleaved
+// trials, H = 5632-8192: in place 2-14% faster (bf16; 1024 x 6144: 10.26 ->
+// 9.07 us), out of place 3-18%; fp16 at 513 x 7-8K 2-5% slower.  Forced
+// shapes: 3-14% slower at 300 rows, -2% to +7% at 1536-2560 rows.
 bool pair_rows(int64_t rows, int64_t nvec, int mode, bool grid) {
-  return mode == 0 && grid && nvec > 640 && nvec <= 1024 && rows > 512 && rows <= 1280;
+  return (mode == 0 || mode == 3) && grid && nvec > 640 && nvec <= 1024 && rows > 512 && rows <= 1280;
 }
 
 // `grid`: every row of every stream starts on the 128-byte grid (only the

@@ -93,8 +93,8 @@ struct FusedEntry {
   X(DT, MODE, 64, 7, 0, 64, 135) X(DT, MODE, 64, 8, 0, 64, 135) X(DT, MODE, 64, 9, 0, 64, 135) \
   X(DT, MODE, 64, 10, 0, 64, 135)
 // 128 lanes x 6-8 vectors, one row per two-wave workgroup: the fused op in
-// place at 5K-8K and 512 < rows <= 1280 on the 128-byte grid (hprms.hip,
-// pair_rows)
+// and out of place at 5K-8K and 512 < rows <= 1280 on the 128-byte grid
+// (hprms.hip, pair_rows; aligned registry only)
 #define HPRMS_PAIR_ROWS(X, DT, MODE) \
   X(DT, MODE, 128, 6, 0, 128, 135) X(DT, MODE, 128, 7, 0, 128, 135) X(DT, MODE, 128, 8, 0, 128, 135)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
@@ -128,7 +128,8 @@ struct FusedEntry {
   HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2) HPRMS_MODE3_SHAPES(ENTRY, DT, 3) \
   HPRMS_MODE4_SHAPES(ENTRY, DT, 4)
 #define HPRMS_ALL_MODES(ENTRY, DT) \
-  HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT) HPRMS_WAVE_ROWS(ENTRY, DT, 3)
+  HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT) HPRMS_WAVE_ROWS(ENTRY, DT, 3) \
+  HPRMS_PAIR_ROWS(ENTRY, DT, 3)
 #define HPRMS_ALL_MODES_OFFGRID(ENTRY, DT) HPRMS_MODE0_OFFGRID_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_ALL_MODES_TAIL(ENTRY, DT)                                                           \
   HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 0) ENTRY(DT, 0, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(ENTRY, DT, 0) \

@@ -173,20 +173,22 @@ def test_wave_rows_at_3k_to_5k():
 
 
 def test_pair_rows_at_5k_to_8k():
-    """The in-place op on rows on the 128-byte grid at 5K-8K takes one row per
-    two-wave workgroup (128 lanes x ceil(H / 1024) vectors) at 512 < rows <=
-    1280; rows off the grid, the other forms and other row counts keep the
-    table."""
+    """The fused op in and out of place on rows on the 128-byte grid at 5K-8K
+    takes one row per two-wave workgroup (128 lanes x ceil(H / 1024) vectors)
+    at 512 < rows <= 1280; rows off the grid, the other forms and other row
+    counts keep the table."""
     for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
         for hidden in (5184, 6144, 7168, 8192):
             for rows in (513, 768, 1024, 1280):
-                c = abi.select_config(rows, hidden, dtype, abi.MODE_FUSED)
-                assert c.as_tuple() == (1, 128, -(-hidden // 1024), 0, 128, 0, 135), (hidden, rows)
-                assert abi.select_config(rows, hidden + 1, dtype, abi.MODE_FUSED).block_threads != 128
-                for mode in (abi.MODE_OUT, abi.MODE_REDUCE, abi.MODE_PLAIN, abi.MODE_FP8):
+                for mode in (abi.MODE_FUSED, abi.MODE_OUT):
+                    c = abi.select_config(rows, hidden, dtype, mode)
+                    assert c.as_tuple() == (1, 128, -(-hidden // 1024), 0, 128, 0, 135), (hidden, rows, mode)
+                    assert abi.select_config(rows, hidden + 1, dtype, mode).block_threads != 128
+                for mode in (abi.MODE_REDUCE, abi.MODE_PLAIN, abi.MODE_FP8):
                     assert abi.select_config(rows, hidden, dtype, mode).block_threads != 128, (hidden, rows, mode)
             for rows in (300, 512, 1281, 4096):
-                assert abi.select_config(rows, hidden, dtype, abi.MODE_FUSED).block_threads != 128, (hidden, rows)
+                for mode in (abi.MODE_FUSED, abi.MODE_OUT):
+                    assert abi.select_config(rows, hidden, dtype, mode).block_threads != 128, (hidden, rows)
 
 
 def test_tail_weight_staged_in_lds_from_a_row_count():

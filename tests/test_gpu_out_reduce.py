@@ -86,17 +86,18 @@ WIDE_CASES = [(1280, 1032), (1536, 2048), (4096, 1536), (2048, 2560), (3072, 230
               (4096, 3072), (1600, 2817), (2000, 3064)]
 
 
-# and one row per one-wave workgroup (64 lanes) at 3K-5K, 768 < rows <= 2048
-WAVE_CASES = [(1000, 4096), (2048, 3584), (800, 5120)]
+# one row per one-wave workgroup (64 lanes) at 3K-5K, 768 < rows <= 2048, and one row per
+# two-wave workgroup (128 lanes) at 5K-8K, 512 < rows <= 1280
+WAVE_CASES = [(1000, 4096, 64), (2048, 3584, 64), (800, 5120, 64), (1024, 6144, 128), (600, 8192, 128)]
 
 
-@pytest.mark.parametrize("rows,hidden,lanes", [c + (32,) for c in WIDE_CASES] + [c + (64,) for c in WAVE_CASES])
+@pytest.mark.parametrize("rows,hidden,lanes", [c + (32,) for c in WIDE_CASES] + WAVE_CASES)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_wide_rows_in_and_out_of_place(abi, rows, hidden, lanes, dtype):
     print("wide", rows, hidden, dtype, flush=True)
     for mode in (abi.MODE_FUSED, abi.MODE_OUT):
         c = abi.select_config(rows, hidden, DT[dtype], mode)
-        assert (c.lanes_per_row, c.block_threads) == (lanes, 64), (mode, c.as_tuple())
+        assert (c.lanes_per_row, c.block_threads) == (lanes, max(lanes, 64)), (mode, c.as_tuple())
     x, r, w = make_inputs(rows, hidden, dtype, seed=rows + hidden)
     want_out, want_res = oracle_fused(x, r, w, 1e-6, dtype)
     xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
