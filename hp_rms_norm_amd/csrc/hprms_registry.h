@@ -87,7 +87,8 @@ struct FusedEntry {
   X(DT, MODE, 32, 8, 0, 64, 135) X(DT, MODE, 32, 9, 0, 64, 135) X(DT, MODE, 32, 10, 0, 64, 135)    \
   X(DT, MODE, 32, 11, 0, 64, 135) X(DT, MODE, 32, 12, 0, 64, 135)
 // 64 lanes x 7-10 vectors, one row per one-wave workgroup: the fused op in
-// and out of place at 3K-5K and 768 < rows <= 2048 on the 128-byte grid
+// and out of place and plain RMSNorm at 3K-5K and 768 < rows <= 2048 on the
+// 128-byte grid
 // (hprms.hip, wave_rows; aligned registry only)
 #define HPRMS_WAVE_ROWS(X, DT, MODE) \
   X(DT, MODE, 64, 7, 0, 64, 135) X(DT, MODE, 64, 8, 0, 64, 135) X(DT, MODE, 64, 9, 0, 64, 135) \
@@ -129,6 +130,7 @@ struct FusedEntry {
   HPRMS_MODE4_SHAPES(ENTRY, DT, 4)
 #define HPRMS_ALL_MODES(ENTRY, DT) \
   HPRMS_MODE0_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT) HPRMS_WAVE_ROWS(ENTRY, DT, 3) \
+  HPRMS_WAVE_ROWS(ENTRY, DT, 1) \
   HPRMS_PAIR_ROWS(ENTRY, DT, 3)
 #define HPRMS_ALL_MODES_OFFGRID(ENTRY, DT) HPRMS_MODE0_OFFGRID_SHAPES(ENTRY, DT, 0) HPRMS_MODES_1_TO_4(ENTRY, DT)
 #define HPRMS_ALL_MODES_TAIL(ENTRY, DT)                                                           \

@@ -462,6 +462,22 @@ def test_plain_rmsnorm(abi, hidden, dtype):
     assert torch.equal(xd.view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("rows,hidden", [(1024, 4096), (2048, 3584), (800, 5120)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_plain_rmsnorm_wave_rows(abi, rows, hidden, dtype):
+    """Plain RMSNorm at 3K-5K, 768 < rows <= 2048: one row per one-wave workgroup."""
+    import hp_rms_norm_amd
+    c = abi.select_config(rows, hidden, DT[dtype], abi.MODE_PLAIN)
+    assert (c.lanes_per_row, c.block_threads) == (64, 64), c.as_tuple()
+    x, _, w = make_inputs(rows, hidden, dtype, rows + hidden)
+    want = oracle.rmsnorm(bits(x), bits(w), 1e-6, DT[dtype], threads=8)
+    xd, wd = x.to(DEV), w.to(DEV)
+    out = torch.empty_like(xd)
+    hp_rms_norm_amd.rms_norm(out, xd, wd, 1e-6)
+    torch.cuda.synchronize()
+    assert_output_close(bits(out), want, dtype)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_plain_rmsnorm_every_table_row(abi, dtype):
     """Enough rows for the bandwidth table (its plain-RMSNorm rows included),
