@@ -23,13 +23,16 @@ cpu_baseline = the reference's CPU path: its test's torch formula
                cores, on the whole workload; core count and CPU model stated.
 cpu_oracle   = the CPU oracle (a scalar C restatement, OpenMP over rows) on a
                bounded sample of the same shapes.
-extra      = BASELINE.json's other configs (decode, fp16, streamer) and the other
-             operators (FP8 / MX outputs, out-of-place, plain RMSNorm, rows
-             off the 128-byte grid, partial sums), µs/call; and a copy moving
-             the fused op's bytes at six of the widths, with the fused op's
-             time as a fraction of it.
+details    = printed before the bench line, one JSON line per section
+             ({"bench_detail": name, "data": ...}): BASELINE.json's other
+             configs (decode, fp16, streamer) and the other operators (FP8 /
+             MX outputs, out-of-place, plain RMSNorm, rows off the 128-byte
+             grid, partial sums), µs/call; a copy moving the fused op's bytes
+             at six of the widths, with the fused op's time as a fraction of
+             it; the ceiling leg; the CPU baseline per shape.  The bench line
+             itself (the last stdout line) stays under HEADLINE_MAX_BYTES.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--full-json PATH]
        python bench.py --sweep STEP [--sweep-max H]   (per-H table sweep, one JSON line per H)
        python bench.py --ab 'H:lpr,vpl,ldsv,block,flags;...' ... [--hot]
                       (forced bench-library configurations against the table's, one JSON line each)
@@ -74,7 +77,8 @@ def make_weight(torch, hidden, dtype, seed, dev):
 
 
 def kernel_key(abi, rows, hidden, dtype_code):
-    c = abi.select_config(rows, hidden, dtype_code)
+    """The table's configuration for contiguous rows on this device's CUs."""
+    c = abi.select_config(rows, hidden, dtype_code, cus=abi.device_cu_count())
     return c.as_tuple()
 
 
@@ -297,6 +301,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--full-json", default="", metavar="PATH",
+                    help="also write the bench line and every detail section to PATH as one JSON document")
     ap.add_argument("--profile", type=int, default=0, metavar="H",
                     help="profiling driver: only run (4096, H) bf16 calls, then a 1 GiB device copy "
                          "(the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -413,9 +419,38 @@ def main():
         log("bench: CPU oracle")
         cpu_oracle = cpu_oracle_baseline(torch)
 
+    details = detail_lines(extra, cpu)
+    line = headline(value=value, steps=args.steps, warmup=args.warmup, step_ms=step_ms, step_bytes=step_bytes,
+                    per_shape=per_shape, roofline=roofline, cpu=cpu, cpu_oracle=cpu_oracle,
+                    details=[d["bench_detail"] for d in details])
+    if args.full_json:
+        with open(args.full_json, "w") as f:
+            json.dump({"headline": line, "details": details}, f)
+    for d in details:
+        print(json.dumps(d), flush=True)
+    print(json.dumps(line), flush=True)
+
+
+# The bench line (the last line on stdout) stays well below what a driver
+# keeps of a run's output; everything else goes on the lines before it.
+HEADLINE_MAX_BYTES = 8192
+
+
+def kernel_name(k):
+    """A per_shape kernel dict as 'lanes x vectors (in LDS) /block flags F'."""
+    lds = f" ({k['lds_vec_per_lane']})" if k.get("lds_vec_per_lane") else ""
+    return f"{k['lanes_per_row']}x{k['vec_per_lane']}{lds}/{k['block']} f{k['flags']}"
+
+
+def headline(*, value, steps, warmup, step_ms, step_bytes, per_shape, roofline, cpu, cpu_oracle, details=()):
+    """The bench line: the metric, the per-shape figures (hidden, µs with
+    p10/p90, GB/s, kernel), the dominant kernel's roofline and the CPU
+    baselines without their per-shape lists.  Raises if it would exceed
+    HEADLINE_MAX_BYTES."""
+    cpu_keys = ("value", "unit", "cores", "kind", "what", "sample", "torch_threads", "os_cpu_count", "cpu_model")
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 4),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(step_ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "fused add+RMSNorm bf16 (4096, H), H in configs[1] (1024..12288 step 1024) "
@@ -424,13 +459,26 @@ def main():
                    "inputs": "input, residual ~ N(0,1), weight ~ N(1,0.1), generated on device",
                    "buffer_sets_per_shape": 2, "bytes_per_step": step_bytes,
                    "per_shape_timing": "back-to-back calls over buffer sets spanning >= 1 GiB"},
-        "per_shape": per_shape,
+        "per_shape": [{"hidden": p["hidden"], "us": p["us_per_call"], "us_p10_p90": [p["us_p10"], p["us_p90"]],
+                       "gbs": p["gbs"], "kernel": kernel_name(p["kernel"])} for p in per_shape],
         "roofline": roofline,
-        "cpu_baseline": cpu,
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in cpu_keys if k in cpu},
         "cpu_oracle": cpu_oracle,
-        "extra": extra,
+        "details_on_earlier_lines": list(details),
     }
-    print(json.dumps(line), flush=True)
+    n = len(json.dumps(line).encode())
+    if n > HEADLINE_MAX_BYTES:
+        raise RuntimeError(f"bench line of {n} bytes exceeds {HEADLINE_MAX_BYTES}")
+    return line
+
+
+def detail_lines(extra, cpu):
+    """The measurements that do not go into the bench line, one JSON object
+    per section ({"bench_detail": name, "data": ...}), printed before it."""
+    out = [{"bench_detail": k, "data": v} for k, v in extra.items()]
+    if cpu is not None and "per_shape" in cpu:
+        out.append({"bench_detail": "cpu_baseline_per_shape", "data": cpu["per_shape"]})
+    return out
 
 
 def time_rotating(torch, call, n, steps, warmup):
@@ -645,7 +693,7 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
         n = cold_sets(B, h)
         bufs = [torch.empty((2, B, h), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
         w = make_weight(torch, h, torch.bfloat16, 0, "cuda:0")
-        cfg = abi.select_config(B, h, abi.DTYPE_BF16)
+        cfg = abi.select_config(B, h, abi.DTYPE_BF16, cus=abi.device_cu_count())
         rpb = cfg.block_threads // cfg.lanes_per_row
         grid = (B + rpb - 1) // rpb
         nb = B * h * 2   # bytes of one [B, H] tensor
@@ -701,14 +749,20 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
         tcfg.flags = cfg.flags | 512
         tl = torch.zeros((grid, 4), dtype=torch.int64, device="cuda:0")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for k in range(n):  # leave set 0 the least recently used
+
+        def timeline_launch(k):
+            return BL.hprms_bench_fused_timeline(bufs[k][0].data_ptr(), w.data_ptr(), bufs[k][1].data_ptr(), B, h,
+                                                 abi.DTYPE_BF16, EPS, ctypes.byref(tcfg), tl.data_ptr(), stream)
+        # the instrumented kernel's first launch loads its code: once untimed, on another set
+        rc = timeline_launch(n - 1)
+        for k in range(1, n):  # leave set 0 the least recently used
             kinds["fused"](k)
         torch.cuda.synchronize()
         prefill(torch, 5)
-        e0.record()
-        rc = BL.hprms_bench_fused_timeline(bufs[0][0].data_ptr(), w.data_ptr(), bufs[0][1].data_ptr(), B, h,
-                                           abi.DTYPE_BF16, EPS, ctypes.byref(tcfg), tl.data_ptr(), stream)
-        e1.record()
+        if rc == 0:
+            e0.record()
+            rc = timeline_launch(0)
+            e1.record()
         torch.cuda.synchronize()
         if rc == 0:
             tlh = tl.cpu().numpy()
