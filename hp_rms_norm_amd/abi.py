@@ -36,6 +36,8 @@ SYMBOLS = (
     "hprms_rmsnorm",
     "hprms_fused_add_rmsnorm_config",
     "hprms_select_config",
+    "hprms_select_config_cu",
+    "hprms_device_cu_count",
     "hprms_kernel_configs",
     "hprms_last_error",
     "hprms_abi_version",
@@ -71,13 +73,16 @@ def _bind(L, bench):
     L.hprms_fused_add_rmsnorm_mx.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, cd, vp]
     L.hprms_streamer.argtypes = [vp, vp, i64, i64, i64, i64, ci, ci, vp]
     L.hprms_select_config.argtypes = [i64, i64, ci, ci, ctypes.POINTER(Config)]
+    L.hprms_select_config_cu.argtypes = [i64, i64, ci, ci, ci, ctypes.POINTER(Config)]
+    L.hprms_device_cu_count.argtypes = [ci]
     L.hprms_kernel_configs.argtypes = [ci, ci, ctypes.POINTER(Config), ci]
     L.hprms_last_error.restype = ctypes.c_char_p
     L.hprms_last_error.argtypes = []
     L.hprms_abi_version.restype = ci
     names = ["hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
              "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_out", "hprms_reduce_add_rmsnorm",
-             "hprms_fused_add_rmsnorm_mx", "hprms_streamer", "hprms_select_config", "hprms_kernel_configs"]
+             "hprms_fused_add_rmsnorm_mx", "hprms_streamer", "hprms_select_config", "hprms_select_config_cu",
+             "hprms_device_cu_count", "hprms_kernel_configs"]
     if bench:
         L.hprms_bench_fused_timeline.argtypes = [vp, vp, vp, i64, i64, ci, cd, ctypes.POINTER(Config), vp, vp]
         L.hprms_ceil_empty.argtypes = [i64, ci, vp]
@@ -173,11 +178,24 @@ class Library:
         return self._check(self.lib().hprms_streamer(out_ptr, in_ptr, rows, hidden, out_stride, in_stride, dtype,
                                                      op, stream))
 
-    def select_config(self, rows, hidden, dtype, mode=0):
-        """The table's configuration for a MODE_* entry point."""
+    def select_config(self, rows, hidden, dtype, mode=0, cus=None):
+        """The table's configuration for a MODE_* entry point, on a device of
+        `cus` compute units (None: 256, a whole MI355X)."""
         c = Config()
-        self._check(self.lib().hprms_select_config(rows, hidden, dtype, mode, ctypes.byref(c)))
+        L = self.lib()
+        if cus is None:
+            self._check(L.hprms_select_config(rows, hidden, dtype, mode, ctypes.byref(c)))
+        else:
+            self._check(L.hprms_select_config_cu(rows, hidden, dtype, mode, cus, ctypes.byref(c)))
         return c
+
+    def device_cu_count(self, device=-1):
+        """Compute units of a HIP device (-1: the current one) as the entry
+        points use them."""
+        n = self.lib().hprms_device_cu_count(device)
+        if n < 0:
+            raise HprmsError(n, self.last_error())
+        return n
 
     def bench_fused_timeline(self, input_ptr, weight_ptr, residual_ptr, rows, hidden, dtype, eps, config,
                              timeline_ptr, stream=0):
@@ -218,4 +236,5 @@ fused_add_rmsnorm_mx = PRODUCT.fused_add_rmsnorm_mx
 rmsnorm = PRODUCT.rmsnorm
 streamer = PRODUCT.streamer
 select_config = PRODUCT.select_config
+device_cu_count = PRODUCT.device_cu_count
 kernel_configs = PRODUCT.kernel_configs

@@ -10,6 +10,8 @@
 // reduction) have no reference counterpart and share the fused kernels.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -85,6 +87,54 @@ const FusedEntry* find_fused(int dtype, int mode, const hprms_config& c) {
   for (int i = 0; i < r.count; ++i)
     if (entry_is(r.entries[i], dtype, mode, c)) return &r.entries[i];
   return nullptr;
+}
+
+// ---- compute units ------------------------------------------------------------------
+// The table's row-count rules (below) were measured on a whole MI355X, 256 CUs.
+// What they depend on is rows per CU, so on a device with another count (a
+// partition of an MI355X, say) each rule sees the equivalent row count on 256
+// CUs, rows * 256 / CUs rounded up; rounds of workgroups are counted on the
+// device's own CUs.  (The reference sizes its persistent grid from the
+// device's multiProcessorCount, hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:550.)
+constexpr int kRefCUs = 256;
+constexpr int kMaxDevices = 64;
+// CUs per device ordinal, 0 until queried.  Threads that race on a first query
+// store the same value.
+std::atomic<int> g_cus[kMaxDevices];
+
+// CUs of device `dev` (queried once per ordinal), or a negative status
+int device_cus(int dev) {
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int n = g_cus[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+  }
+  int n = 0;
+  const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess || n < 1) {
+    (void)hipGetLastError();  // not left for the next launch check to report
+    return fail(HPRMS_E_LAUNCH, "CU count of device %d: %s", dev,
+                e != hipSuccess ? hipGetErrorString(e) : "no compute units reported");
+  }
+  if (dev >= 0 && dev < kMaxDevices) g_cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// CUs of the current device; 256 when there is no device to ask (a launch
+// would then fail and report why)
+int current_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return kRefCUs;
+  }
+  const int n = device_cus(dev);
+  return n > 0 ? n : kRefCUs;
+}
+
+// `rows` on a device of `cus` CUs as the row count with as many rows per CU on 256
+int64_t rows_at_ref(int64_t rows, int cus) {
+  if (cus == kRefCUs || rows > (int64_t(1) << 40)) return rows;
+  return (rows * kRefCUs + cus - 1) / cus;
 }
 
 // ---- the gfx950 table -------------------------------------------------------------
@@ -250,17 +300,18 @@ bool weight_late_1024(int mode, const hprms_config& c) {
 // (one wave per SIMD: 2-7% slower there; held to two waves they spill).
 // Eight rows per 256-lane workgroup, and the FP8, MX and partial-sum forms,
 // measured slower with the wider rows.
-constexpr int64_t kCUs = 256;   // MI355X
-
+// (`r`: the row count scaled to 256 CUs, rows_at_ref; `rows` and `cus`: the
+// call's own, for the rounds of workgroups.)
+//
 // rows per CU with `rows_per_wg` rows per workgroup, whole rounds of workgroups
-int64_t rows_per_cu(int64_t rows, int64_t rows_per_wg) {
-  return ((rows + rows_per_wg - 1) / rows_per_wg + kCUs - 1) / kCUs * rows_per_wg;
+int64_t rows_per_cu(int64_t rows, int64_t rows_per_wg, int cus) {
+  return ((rows + rows_per_wg - 1) / rows_per_wg + cus - 1) / cus * rows_per_wg;
 }
 
-bool wide_rows(int64_t rows, int64_t nvec, int mode) {
-  if ((mode != 0 && mode != 3) || nvec <= 128 || nvec > 384 || rows <= 1024 || rows > 4096) return false;
-  if (nvec > 320) return mode == 3 || rows > 1536;
-  return nvec > 256 || rows > 3072 || rows_per_cu(rows, 2) < rows_per_cu(rows, 4);
+bool wide_rows(int64_t rows, int64_t r, int64_t nvec, int mode, int cus) {
+  if ((mode != 0 && mode != 3) || nvec <= 128 || nvec > 384 || r <= 1024 || r > 4096) return false;
+  if (nvec > 320) return mode == 3 || r > 1536;
+  return nvec > 256 || r > 3072 || rows_per_cu(rows, 2, cus) < rows_per_cu(rows, 4, cus);
 }
 
 // Rows of 3K-5K (384 < H / 8 <= 640) in the fused op in and out of place and
@@ -291,19 +342,20 @@ bool pair_rows(int64_t rows, int64_t nvec, int mode, bool grid) {
 }
 
 // `grid`: every row of every stream starts on the 128-byte grid (only the
-// in-place op's rows depend on it).
-void table_config(int64_t rows, int64_t hidden, int mode, bool grid, hprms_config* c) {
+// in-place op's rows depend on it); `cus`: the device's compute units.
+void table_config(int64_t rows, int64_t hidden, int mode, bool grid, int cus, hprms_config* c) {
   const int64_t nvec = hidden / 8;
-  if (latency_config(rows, nvec, mode, c)) return;
-  if (wide_rows(rows, nvec, mode)) {
+  const int64_t r = rows_at_ref(rows, cus);
+  if (latency_config(r, nvec, mode, c)) return;
+  if (wide_rows(rows, r, nvec, mode, cus)) {
     *c = hprms_config{1, 32, (int)((nvec + 31) / 32), 0, 64, 0, 135};
     return;
   }
-  if (wave_rows(rows, nvec, mode, grid)) {
+  if (wave_rows(r, nvec, mode, grid)) {
     *c = hprms_config{1, 64, (int)((nvec + 63) / 64), 0, 64, 0, 135};
     return;
   }
-  if (pair_rows(rows, nvec, mode, grid)) {
+  if (pair_rows(r, nvec, mode, grid)) {
     *c = hprms_config{1, 128, (int)((nvec + 127) / 128), 0, 128, 0, 135};
     return;
   }
@@ -642,25 +694,27 @@ int unaligned_flags(const Problem& p, int flags) {
 // not in 1024 x 4 (1.7-3.5% slower: one workgroup per CU either way, VGPRs
 // 80 -> 96), in the fused op's 1024 x 3 (62 -> 66 VGPRs: one workgroup per
 // CU instead of two, -1.5% to +1.7%), nor the partial sums' 1024 x 2 (spills).
-bool weight_in_lds(const Problem& p, const hprms_config& c) {
+// (row counts on 256 CUs, as in table_config)
+bool weight_in_lds(const Problem& p, int cus, const hprms_config& c) {
   if (c.lds_vec_per_lane != 0 || c.block_threads != c.lanes_per_row) return false;
   const int l = c.lanes_per_row, v = c.vec_per_lane;
+  const int64_t r = rows_at_ref(p.rows, cus);
   switch (p.mode) {
     case 0:
-    case 3: return p.rows >= 1024 && ((l == 512 && (v == 2 || v == 3)) || (l == 1024 && v == 2));
-    case 4: return p.rows >= 1024 && l == 512 && v == 3;
-    case 1: return p.rows >= 384 && ((l == 512 && v >= 2 && v <= 4) || (l == 1024 && v == 3));
+    case 3: return r >= 1024 && ((l == 512 && (v == 2 || v == 3)) || (l == 1024 && v == 2));
+    case 4: return r >= 1024 && l == 512 && v == 3;
+    case 1: return r >= 384 && ((l == 512 && v >= 2 && v <= 4) || (l == 1024 && v == 3));
     default: return false;
   }
 }
 
-void tail_shape(const Problem& p, hprms_config* c) {
+void tail_shape(const Problem& p, int cus, hprms_config* c) {
   if (!(c->flags & 64)) return;
   if (c->tier == 2 && c->lanes_per_row == 256)
     *c = hprms_config{1, 1024, 2, 0, 1024, c->grid_blocks, unaligned_flags(p, 31)};
   else if (c->lanes_per_row == 1024 && (c->vec_per_lane == 2 || c->vec_per_lane == 3))
     c->flags |= 4;
-  if (weight_in_lds(p, *c)) c->flags |= 16384;
+  if (weight_in_lds(p, cus, *c)) c->flags |= 16384;
 }
 
 // Calls that update the residual in place and whose input and residual rows
@@ -716,11 +770,13 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   if (forced && forced->tier != 0) {
     c = *forced;
   } else {
+    // (a call with no rows runs no kernel and asks no device)
+    const int cus = p.rows > 0 ? current_cus() : kRefCUs;
     const bool off_grid = needs_unaligned(p);
-    table_config(p.rows, p.hidden, p.mode, !off_grid, &c);
+    table_config(p.rows, p.hidden, p.mode, !off_grid, cus, &c);
     if (c.tier != 3 && (off_grid || ((c.flags & 24) && skip_sc1(p)))) {
       c.flags = unaligned_flags(p, c.flags);
-      tail_shape(p, &c);
+      tail_shape(p, cus, &c);
     }
   }
   if ((c.flags & 512) && !p.timeline)
@@ -889,25 +945,41 @@ int hprms_rmsnorm(void* out, const void* in, const void* weight, int64_t rows, i
   return run(p, nullptr, stream);
 }
 
-int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config) {
+int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, int cu_count,
+                           hprms_config* config) {
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
   if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
+  if (cu_count < 1 || cu_count > 65536) return fail(HPRMS_E_INVALID, "cu_count must be in [1, 65536] (got %d)", cu_count);
   // the choice for rows on the 128-byte grid; odd widths: the tail variant of
   // the choice for rows off it
-  table_config(rows, hidden, mode, hidden % 8 == 0, config);
+  table_config(rows, hidden, mode, hidden % 8 == 0, cu_count, config);
   if (hidden % 8 != 0) {
     if (config->tier != 3 && hidden >= 8 && mode <= 4) {
       Problem p{mode, nullptr, nullptr, nullptr, nullptr, rows, hidden, hidden, hidden, hidden, dtype, 0.0};
       config->flags = unaligned_flags(p, config->flags);
-      tail_shape(p, config);
+      tail_shape(p, cu_count, config);
     } else {
       config->tier = 3;
     }
   }
   return HPRMS_OK;
+}
+
+int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config) {
+  return hprms_select_config_cu(rows, hidden, dtype, mode, kRefCUs, config);
+}
+
+int hprms_device_cu_count(int device) {
+  if (device < 0) {
+    if (hipGetDevice(&device) != hipSuccess) {
+      const hipError_t e = hipGetLastError();
+      return fail(HPRMS_E_LAUNCH, "no current device: %s", hipGetErrorString(e));
+    }
+  }
+  return device_cus(device);
 }
 
 int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int64_t out_row_stride,

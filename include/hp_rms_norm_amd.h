@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 4
+#define HPRMS_ABI_VERSION 5
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -170,9 +170,11 @@ int hprms_reduce_add_rmsnorm(void* out, const void* const* parts, int nparts, co
  * `format` is HPRMS_MX_FP8_E4M3 (out: hidden bytes per row) or
  * HPRMS_MX_FP4_E2M1 (out: hidden / 2 bytes per row); `scales` holds hidden / 32
  * bytes per row; both row strides are in bytes.  `input` is only read.  Needs
- * hidden % 32 == 0 and 2-byte aligned input, residual and weight (`out` and
- * `scales` may start at any byte); there is no general-tier fallback, so a
- * row group (rows per workgroup times the row strides) must span < 2 GiB.
+ * hidden % 32 == 0, 2-byte aligned input, residual and weight (`out` and
+ * `scales` may start at any byte), and input and residual row strides below
+ * 2^31 elements; there is no general-tier fallback, so a row group (rows per
+ * workgroup times the row strides) must also span < 2 GiB.  Other calls
+ * return HPRMS_E_INVALID.
  * No counterpart in the reference.
  */
 int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const void* weight,
@@ -222,25 +224,57 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * `mode` (0: hprms_fused_add_rmsnorm, 1: hprms_rmsnorm, 2:
  * hprms_fused_add_rmsnorm_fp8, 3: hprms_fused_add_rmsnorm_out, 4:
  * hprms_reduce_add_rmsnorm, 5 / 6: hprms_fused_add_rmsnorm_mx with
- * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1), written to *config (tier 3 when only the
- * general kernel fits hidden; with hidden % 8 != 0 the tail variant).  For
- * rows on the 128-byte grid: rows off it run the same shape (mode 0 at
- * 384 < hidden / 8 <= 512 excepted: 128 lanes x 4 vectors, flags 131, where
- * rows on the grid take 256 x 2) with flags
- * (flags & ~24) | 32, or | 96 (the tail variant, which adds bit 2 to the
- * 1024 x 2 and 1024 x 3 rows and, from 1024 rows (plain RMSNorm: 384), bit
- * 14 to 512 x 2-4 and 1024 x 2-3 in the modes that stage the weight in LDS)
- * for hidden % 8 != 0 and, in
- * modes 0-4 from hidden 4104 up, for calls none of whose tensors (the weight
- * aside) has its rows on 16-byte boundaries (the kernel then shifts its
- * vectors to align the first written tensor; plain RMSNorm with input and
- * output off by different amounts from hidden 16384 up, the FP8 output only
- * for odd hidden with every tensor off by the same amount).  Calls of modes
- * 0, 2, 4, 5 and 6 with rows * hidden <= 2^24 also run the shape with flags
- * (flags & ~24) | 32 when the reported flags carry the sc1 bits (8, 16): the
- * same kernel without them.  Pure function of its arguments; touches no
- * device. */
+ * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1) on a device of 256 CUs (a whole
+ * MI355X), written to *config; tier 3 when only the general kernel fits
+ * hidden.  It is the choice for contiguous rows on the 128-byte grid (for
+ * hidden % 8 != 0: the tail variant of the choice for rows off it).  A call's
+ * layout changes it as follows:
+ *   - Rows off the 128-byte grid (any tensor's rows, or the weight) run the
+ *     bandwidth table's shape for their hidden: never 256 lanes x 2 (mode 0,
+ *     384 < hidden / 8 <= 512: 128 x 4, flags 131 instead), the one-wave rows
+ *     (modes 0, 1, 3; 384 < hidden / 8 <= 640; 768 < rows <= 2048) or the
+ *     two-wave rows (modes 0, 3; 640 < hidden / 8 <= 1024; 512 < rows <=
+ *     1280).  Its flags gain bit 5 (the unaligned variant; in modes 0, 1, 3
+ *     and 4 it rotates each row's lane mapping onto 512-byte boundaries of
+ *     the first written tensor, which changes the order in which a row's
+ *     squares are summed, within the same 1-ulp bar), or bits 5 and 6 (the
+ *     tail variant) for hidden % 8 != 0 and for shifted rows: modes 0-4 from
+ *     hidden 4104 up when no tensor but the weight has its rows on 16-byte
+ *     boundaries (plain RMSNorm with input and output at different 16-byte
+ *     phases only from hidden 16384; the FP8 output only for odd hidden with
+ *     every tensor at one phase).  The sc1 bits (8, 16) are dropped, except
+ *     in modes 0, 1, 3 and 4 for calls of more than 2^24 elements (tail
+ *     variants only past 2048 whole vectors).  The tail variant adds bit 2 to
+ *     1024 x 2 and 1024 x 3, runs 1024 x 2 (flags 31, adjusted as above) in
+ *     place of the LDS tier's 256 x 8, and adds bit 14 to 512 x 2-3 and
+ *     1024 x 2 (modes 0, 3; from 1024 rows), 512 x 3 (mode 4; from 1024 rows)
+ *     and 512 x 2-4 and 1024 x 3 (mode 1; from 384 rows).
+ *   - Calls of modes 0, 2, 4, 5 and 6 on the grid with rows * hidden <= 2^24
+ *     whose configuration carries the sc1 bits run the same shape with flags
+ *     (flags & ~24) | 32: the unaligned variant without sc1 (rows off a
+ *     512-byte boundary are then rotated, as above).
+ * Pure function of its arguments; touches no device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
+
+/* hprms_select_config() for a device of `cu_count` compute units (1 ...
+ * 65536).  The row-count rules above were measured on 256 CUs and depend on
+ * rows per CU: on `cu_count` CUs each sees rows * 256 / cu_count rounded up,
+ * and workgroup rounds are counted on `cu_count` CUs.  The entry points apply
+ * it with the current device's count (hprms_device_cu_count).  With
+ * cu_count = 256 it equals hprms_select_config().  No counterpart in the
+ * reference, which sizes its persistent grid from the device's
+ * multiProcessorCount (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:550).  Touches
+ * no device. */
+int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, int cu_count,
+                           hprms_config* config);
+
+/* Compute units of HIP device `device` (< 0: the current device) as the
+ * entry points use them: hipDeviceAttributeMultiprocessorCount, queried once
+ * per device ordinal and cached (safe to call from any thread).  Returns the
+ * count, or a negative status when the runtime cannot report it.  Replaces
+ * the reference's per-call device-property query
+ * (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:550,571). */
+int hprms_device_cu_count(int device);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
  * mode, numbered as for hprms_select_config).  Writes up to `capacity`

@@ -67,6 +67,14 @@ int main(void) {
   EXPECT(hprms_select_config(4096, 4097, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 1 && (c.flags & 96) == 96);
   EXPECT(hprms_select_config(4096, 15, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 1 && (c.flags & 96) == 96);
   EXPECT(hprms_select_config(4096, 7, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 3);
+  /* on a 256-CU device the per-CU table is hprms_select_config's; a CU count of 0 is refused */
+  {
+    hprms_config d;
+    EXPECT(hprms_select_config_cu(4096, 4096, HPRMS_DTYPE_BF16, 0, 256, &d) == HPRMS_OK);
+    EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK);
+    EXPECT(c.lanes_per_row == d.lanes_per_row && c.vec_per_lane == d.vec_per_lane && c.flags == d.flags);
+    EXPECT(hprms_select_config_cu(4096, 4096, HPRMS_DTYPE_BF16, 0, 0, &d) == HPRMS_E_INVALID);
+  }
 
   if (failures) return 1;
   printf("c abi caller: ok\n");

@@ -191,6 +191,56 @@ def test_pair_rows_at_5k_to_8k():
                     assert abi.select_config(rows, hidden, dtype, mode).block_threads != 128, (hidden, rows)
 
 
+def ref_rows(rows, cus):
+    """rows on `cus` CUs as the row count with as many rows per CU on 256"""
+    return -(-rows * 256 // cus)
+
+
+def test_row_rules_scale_with_the_cu_count():
+    """The table's row-count rules at 32, 80 and 256 CUs: on C CUs a call of
+    R rows takes what a 256-CU device gives ceil(R * 256 / C) rows (the wide
+    rows' comparison of workgroup rounds aside, checked below), so the
+    latency rows, one- and two-wave rows, wide rows and LDS-staged weight
+    keep their rows per CU; at 256 CUs the choice is hprms_select_config's."""
+    bf = abi.DTYPE_BF16
+    hiddens = (512, 1024, 1032, 2048, 2056, 3072, 4096, 5120, 6144, 8192, 8191, 12289, 16384, 16391, 32768)
+    rowss = (1, 8, 32, 100, 128, 129, 256, 300, 400, 512, 640, 768, 1000, 1024, 1280, 2048, 4096, 8192)
+    for mode in range(7):
+        for hidden in hiddens:
+            if mode >= 5 and hidden % 32:
+                continue
+            for rows in rowss:
+                assert abi.select_config(rows, hidden, bf, mode, cus=256).as_tuple() == \
+                    abi.select_config(rows, hidden, bf, mode).as_tuple(), (mode, hidden, rows)
+                for cus in (32, 80):
+                    r = ref_rows(rows, cus)
+                    if mode in (0, 3) and 128 < hidden // 8 <= 256 and 1024 < r <= 3072:
+                        continue   # workgroup rounds counted on the call's own CUs
+                    assert abi.select_config(rows, hidden, bf, mode, cus=cus).as_tuple() == \
+                        abi.select_config(r, hidden, bf, mode).as_tuple(), (mode, hidden, rows, cus)
+    # the fused op's latency rows at H = 1024 end at 1024 rows on 256 CUs, 128 on 32
+    lat = abi.select_config(1, 1024, bf, 0).as_tuple()
+    assert abi.select_config(128, 1024, bf, 0, cus=32).as_tuple() == lat
+    assert abi.select_config(129, 1024, bf, 0, cus=32).as_tuple() != lat
+    assert abi.select_config(1024, 1024, bf, 0).as_tuple() == lat
+    # wide rows at 1K-2K where 64 x 4's rounds come out uneven on the device's CUs: on 80 CUs,
+    # 400 rows are 3 rounds of two-row workgroups (6 rows per CU) against 2 of four-row ones (8)
+    assert abi.select_config(400, 2048, bf, 0, cus=80).lanes_per_row == 32
+    # 640 rows: 4 rounds of two-row workgroups and 2 of four-row ones, 8 rows per CU either way
+    assert abi.select_config(640, 2048, bf, 0, cus=80).as_tuple() == abi.select_config(4096, 2048, bf, 0, cus=80).as_tuple()
+    assert abi.select_config(640, 2048, bf, 0, cus=80).lanes_per_row == 64
+    # the weight staged in LDS (odd widths): from 1024 rows on 256 CUs, from 128 on 32
+    assert not abi.select_config(127, 12289, bf, 0, cus=32).flags & 16384
+    assert abi.select_config(128, 12289, bf, 0, cus=32).flags & 16384
+
+
+@pytest.mark.parametrize("cus", [0, -1, 65537])
+def test_select_config_cu_rejects_bad_cu_counts(cus):
+    c = abi.Config()
+    assert abi.lib().hprms_select_config_cu(4096, 4096, abi.DTYPE_BF16, 0, cus, ctypes.byref(c)) == abi.HPRMS_E_INVALID
+    assert "cu_count" in abi.last_error()
+
+
 def test_tail_weight_staged_in_lds_from_a_row_count():
     """The tail variants of 512 x 2-4 and 1024 x 2-3 stage the weight in LDS
     (flags bit 14) from 1024 rows (plain RMSNorm: 384), never in 1024 x 4, the

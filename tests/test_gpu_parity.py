@@ -571,3 +571,27 @@ def test_small_in_place_calls_without_sc1_give_the_table_kernels_bits(abi, rows,
         outs.append((bits(xd), bits(rd)))
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
     check_case(abi, rows, hidden, torch.bfloat16, seed=hidden + rows)
+
+
+# ---- the device's CU count ---------------------------------------------------------------
+def test_device_cu_count_is_the_devices(abi):
+    """The CU count the entry points size their row rules by is the device's
+    own (hipDeviceAttributeMultiprocessorCount, cached per device): torch
+    reports the same count, and a call at a row count where the rules depend
+    on it gives the bits of the table's choice at that count, forced, and
+    meets the oracle's bar."""
+    n = abi.device_cu_count(0)
+    assert n == torch.cuda.get_device_properties(0).multi_processor_count
+    assert abi.device_cu_count(-1) == n and abi.device_cu_count(0) == n   # cached, current device
+    rows, hidden = 1280, 2048   # wide rows on 256 CUs
+    c = abi.select_config(rows, hidden, abi.DTYPE_BF16, cus=n)
+    print("cus", n, "config", c.as_tuple(), flush=True)
+    x, r, w = make_inputs(rows, hidden, torch.bfloat16, seed=n)
+    outs = []
+    for config in (None, c):
+        xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+        run_abi(abi, xd, wd, rd, 1e-6, config)
+        torch.cuda.synchronize()
+        outs.append((bits(xd), bits(rd)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    check_case(abi, rows, hidden, torch.bfloat16, seed=n)
