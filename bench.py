@@ -315,6 +315,17 @@ def main():
     ap.add_argument("--ceiling", default="", metavar="H,H,...",
                     help="only the ceiling leg: the fused op beside the skeleton, copy, read, write and empty "
                          "kernels of the bench library at (4096, H), one JSON line")
+    ap.add_argument("--flat", default="", metavar="H,H,...",
+                    help="only the flat-stream leg: one and two in-place streams of each workgroup shape and load "
+                         "order at the fused op's bytes, one JSON line per H")
+    ap.add_argument("--placement", default="", metavar="H,H,...",
+                    help="only the placement leg: the fused op and the flat two-stream rewrite with the residual "
+                         "at each of --gaps relative to the input, one JSON line per H")
+    ap.add_argument("--gaps", default="0,512,4096,8192,16384,65536,262144,1048576,r0",
+                    help="with --placement: bytes from the end of x to the start of r (rG: r first)")
+    ap.add_argument("--fillmap", action="store_true",
+                    help="only the fill-and-drain map at (4096, 4096): empty grid, skeleton and fused op for every "
+                         "split of the row into lanes x vectors and rows per workgroup, one JSON line")
     ap.add_argument("--timeline-dump", default="", metavar="DIR",
                     help="with --ceiling: also save each H's raw per-workgroup timeline as DIR/timeline_H.npy")
     ap.add_argument("--ab", nargs="+", default=None, metavar="H:CFG;CFG",
@@ -355,6 +366,14 @@ def main():
     if args.ab:
         off, pad = (int(v) for v in args.layout.split(","))
         return ab_trials(torch, abi, op, args.ab, args.hot, off, pad, rows=args.ab_rows)
+    if args.flat:
+        return flat_leg(torch, abi, hp_rms_norm_amd, [int(v) for v in args.flat.split(",")], max(args.steps, 10),
+                        args.warmup)
+    if args.placement:
+        return placement_leg(torch, abi, hp_rms_norm_amd, [int(v) for v in args.placement.split(",")],
+                             args.gaps.split(","), max(args.steps, 10), args.warmup)
+    if args.fillmap:
+        return fill_leg(torch, abi, hp_rms_norm_amd, max(args.steps, 10), args.warmup)
     if args.ceiling:
         hs = [int(v) for v in args.ceiling.split(",")]
         rows = ceiling(torch, abi, hp_rms_norm_amd, hs, max(args.steps, 10), args.warmup,
@@ -776,6 +795,142 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
         del bufs, tl
         torch.cuda.empty_cache()
     return out
+
+
+def interleaved(torch, kinds, n, steps, warmup, trials):
+    """Median µs per call of each kind (a function of the buffer-set index),
+    timed in `trials` interleaved rounds, the order reversed every other one."""
+    samples = {k: [] for k in kinds}
+    items = list(kinds.items())
+    for t in range(trials):
+        for k, fn in (items if t % 2 == 0 else items[::-1]):
+            samples[k].append(time_rotating(torch, fn, n, steps, warmup))
+    return {k: statistics.median(v) for k, v in samples.items()}
+
+
+def chk(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: status {rc}")
+
+
+FLAT_SHAPES = [(64, 1), (128, 1), (256, 1), (512, 1), (1024, 1), (256, 2), (512, 2), (1024, 2), (256, 4), (1024, 4)]
+# the shapes also built with the workgroups in xcd_order's maps 1 and 2 (hprms_ceil_flat orders 4 and 5)
+FLAT_MAPPED = [(256, 1), (512, 1), (1024, 1), (256, 2), (1024, 4)]
+
+
+def flat_leg(torch, abi, ops, hs, steps, warmup, trials=5):
+    """The fused op's bytes at (4096, H) as flat in-place streams of each
+    workgroup shape (hprms_ceil_flat): one stream `a` of 2*B*H*2 bytes, and
+    two streams `x`, `r` of B*H*2 bytes each (adjacent in one allocation) in
+    four load orders (o0-o3), and for FLAT_MAPPED shapes with the workgroups
+    in xcd_order's maps 1 and 2 (o4, o5); beside them the fused op and a
+    copy.  Cold (rotating buffer sets spanning >= 1 GiB).  One JSON line per
+    H."""
+    BL = abi.BENCH.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    for h in hs:
+        nb = B * h * 2
+        n = cold_sets(B, h)
+        bufs = [torch.empty((2, B, h), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
+        w = make_weight(torch, h, torch.bfloat16, 0, "cuda:0")
+        kinds = {"fused": lambda i: ops.hp_rms_norm(bufs[i][0], w, bufs[i][1], EPS),
+                 "copy": lambda i: chk(BL.hprms_ceil_copy(bufs[(i + 1) % n].data_ptr(), bufs[i].data_ptr(), 2 * nb,
+                                                          stream), "copy")}
+        for blk, vpl in FLAT_SHAPES:
+            kinds[f"one_{blk}x{vpl}"] = (lambda i, blk=blk, vpl=vpl: chk(
+                BL.hprms_ceil_flat(0, blk, vpl, 0, bufs[i].data_ptr(), None, nb, stream), "flat"))
+            for order in range(4) if (blk, vpl) not in FLAT_MAPPED else range(6):
+                kinds[f"two_{blk}x{vpl}_o{order}"] = (lambda i, blk=blk, vpl=vpl, order=order: chk(
+                    BL.hprms_ceil_flat(1, blk, vpl, order, bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nb,
+                                       stream), "flat"))
+            if (blk, vpl) in FLAT_MAPPED:
+                for order in (4, 5):
+                    kinds[f"one_{blk}x{vpl}_o{order}"] = (lambda i, blk=blk, vpl=vpl, order=order: chk(
+                        BL.hprms_ceil_flat(0, blk, vpl, order, bufs[i].data_ptr(), None, nb, stream), "flat"))
+        us = interleaved(torch, kinds, n, steps, warmup, trials)
+        nbytes = {k: (fused_bytes(B, h) if k == "fused" else 4 * nb) for k in kinds}
+        print(json.dumps({"flat_hidden": h, "rows": B, "us": {k: round(v, 2) for k, v in us.items()},
+                          "gbs": {k: round(nbytes[k] / (us[k] * 1e-6) / 1e9, 1) for k in us}}), flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+
+
+def placement_leg(torch, abi, ops, hs, gaps, steps, warmup, trials=5):
+    """The fused op and the flat two-stream rewrite (256 lanes x 1 vector,
+    alternating loads) with the residual placed relative to the input inside
+    one allocation: gap "G" puts r G bytes after the end of x, "rG" puts r
+    first and x G bytes after it.  Cold, interleaved over the gaps.  One JSON
+    line per H."""
+    BL = abi.BENCH.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    for h in hs:
+        nb = B * h * 2
+        n = cold_sets(B, h)
+        w = make_weight(torch, h, torch.bfloat16, 0, "cuda:0")
+        kinds, keep = {}, []
+        for gap in gaps:
+            rfirst = gap.startswith("r")
+            g = int(gap[1:] if rfirst else gap)
+            if g % 512:
+                raise SystemExit(f"--gaps: {gap} is not a multiple of 512 bytes")
+            sets = []
+            for _ in range(n):
+                raw = torch.empty(2 * nb + g, dtype=torch.uint8, device="cuda:0")
+                lo = raw[:nb].view(torch.bfloat16).view(B, h)
+                hi = raw[nb + g:].view(torch.bfloat16).view(B, h)
+                x, r = (hi, lo) if rfirst else (lo, hi)
+                x.normal_()
+                r.normal_()
+                sets.append((x, r))
+            keep.append(sets)
+            kinds[f"fused_{gap}"] = lambda i, s=sets: ops.hp_rms_norm(s[i][0], w, s[i][1], EPS)
+            kinds[f"flat2_{gap}"] = lambda i, s=sets: chk(
+                BL.hprms_ceil_flat(1, 256, 1, 0, s[i][0].data_ptr(), s[i][1].data_ptr(), nb, stream), "flat")
+        us = interleaved(torch, kinds, n, steps, warmup, trials)
+        print(json.dumps({"placement_hidden": h, "rows": B, "gaps": gaps,
+                          "us": {k: round(v, 2) for k, v in us.items()}}), flush=True)
+        del keep, kinds
+        torch.cuda.empty_cache()
+
+
+FILL_SHAPES = [(64, 8, 64), (64, 8, 128), (64, 8, 256), (64, 8, 512), (128, 4, 128), (128, 4, 256), (128, 4, 512),
+               (256, 2, 256), (256, 2, 512), (512, 1, 512)]
+
+
+def fill_leg(torch, abi, ops, steps, warmup, trials=7, h=4096):
+    """Fill-and-drain map at (4096, 4096) bf16: for every split of a row into
+    lanes x vectors in workgroups of one to eight rows (grids of 512 to 4096
+    workgroups of 64 to 512 lanes), the empty grid, the skeleton (the op's
+    data movement, no arithmetic) and the fused op forced to that shape (nt,
+    residual loads first, weight with the row: flags 131); beside them the
+    table's op and a copy of the same bytes.  Cold, interleaved.  One JSON
+    line."""
+    BB = abi.BENCH
+    BL = BB.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    nb = B * h * 2
+    n = cold_sets(B, h)
+    bufs = [torch.empty((2, B, h), dtype=torch.bfloat16, device="cuda:0").normal_() for _ in range(n)]
+    w = make_weight(torch, h, torch.bfloat16, 0, "cuda:0")
+    kinds = {"table": lambda i: ops.hp_rms_norm(bufs[i][0], w, bufs[i][1], EPS),
+             "copy": lambda i: chk(BL.hprms_ceil_copy(bufs[(i + 1) % n].data_ptr(), bufs[i].data_ptr(), 2 * nb,
+                                                      stream), "copy")}
+    for lpr, vpl, blk in FILL_SHAPES:
+        grid = B // (blk // lpr)
+        tag = f"{lpr}x{vpl}/{blk}"
+        cfg = abi.Config(1, lpr, vpl, 0, blk, 0, 131)
+        kinds[f"empty {tag}"] = lambda i, g=grid, b=blk: chk(BL.hprms_ceil_empty(g, b, stream), "empty")
+        kinds[f"skeleton {tag}"] = lambda i, lpr=lpr, vpl=vpl, blk=blk: chk(
+            BL.hprms_ceil_skeleton(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), B, h, lpr, vpl, blk, 131, stream),
+            "skeleton")
+        kinds[f"fused {tag}"] = lambda i, cfg=cfg: BB.fused_add_rmsnorm(
+            bufs[i][0].data_ptr(), w.data_ptr(), bufs[i][1].data_ptr(), B, h, h, h, abi.DTYPE_BF16, EPS, stream, cfg)
+    us = interleaved(torch, kinds, n, steps, warmup, trials)
+    grids = {f"{lpr}x{vpl}/{blk}": B // (blk // lpr) for lpr, vpl, blk in FILL_SHAPES}
+    print(json.dumps({"fill_hidden": h, "rows": B, "grids": grids, "us": {k: round(v, 2) for k, v in us.items()}}),
+          flush=True)
+    del bufs
+    torch.cuda.empty_cache()
 
 
 def load_traffic(key):

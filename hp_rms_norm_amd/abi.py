@@ -91,8 +91,9 @@ def _bind(L, bench):
         L.hprms_ceil_copy.argtypes = [vp, vp, i64, vp]
         L.hprms_ceil_skeleton.argtypes = [vp, vp, i64, i64, ci, ci, ci, ci, vp]
         L.hprms_ceil_streams.argtypes = [ci, vp, vp, vp, vp, i64, vp]
+        L.hprms_ceil_flat.argtypes = [ci, ci, ci, ci, vp, vp, i64, vp]
         names += ["hprms_bench_fused_timeline", "hprms_ceil_empty", "hprms_ceil_read", "hprms_ceil_write",
-                  "hprms_ceil_copy", "hprms_ceil_skeleton", "hprms_ceil_streams"]
+                  "hprms_ceil_copy", "hprms_ceil_skeleton", "hprms_ceil_streams", "hprms_ceil_flat"]
     for name in names:
         getattr(L, name).restype = ci
 

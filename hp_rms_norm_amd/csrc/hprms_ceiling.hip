@@ -3,13 +3,15 @@
 // the fused add + RMSNorm op in simpler ways, so that the op's time can be
 // set beside what the same hardware needs for the same traffic:
 //
-//   hprms_ceil_empty     a grid of empty workgroups of 64, 256, 512 or 1024 lanes
+//   hprms_ceil_empty     a grid of empty workgroups of 64 ... 1024 lanes
 //                        (launch, dispatch and teardown of a kernel of that
 //                        grid, no memory traffic)
 //   hprms_ceil_read      read two tensors of n bytes (the op's two read streams)
 //   hprms_ceil_write     write two tensors of n bytes (the op's two write streams)
 //   hprms_ceil_copy      copy n bytes (one read and one write stream)
 //   hprms_ceil_streams   the op's bytes as flat in-place or copying streams
+//   hprms_ceil_flat      flat in-place streams (one or two) with a chosen
+//                        workgroup shape and load order
 //   hprms_ceil_skeleton  the op's own data movement in place on [rows, hidden]
 //                        x and r with the lane mapping of a table row: every
 //                        load first, r <- x + r stored as soon as it is formed,
@@ -79,6 +81,80 @@ __global__ __launch_bounds__(kFlatBlock) void ceil_streams_kernel(u32x4* a, u32x
     __builtin_nontemporal_store(u ^ v, KIND == 1 ? b + i : d + i);
   }
 }
+
+// The flat streams with a workgroup shape and load order of their own, to
+// tell which of them the two-stream cost follows: BLOCK lanes, VPL 16-byte
+// vectors per lane of each stream (lane t holds vectors t, t + BLOCK, ...),
+// loads then stores as the fused op orders them (b's stores as soon as its
+// sums are formed, then a's).  KIND 0 rewrites one stream `a` of 2 * VPL
+// vectors per lane in place, KIND 1 rewrites `a` and `b` in place.  ORDER
+// (KIND 1): 0 a and b alternating per vector, 1 all of b then all of a, 2 the
+// two orders alternating per wave, 3 alternating per workgroup (consecutive
+// workgroups go to different XCDs); MAP 1 / 2: the workgroups in
+// xcd_xor's / xcd_runs<3>'s order.  Buffer resources span each stream
+// (< 2 GiB), so the last workgroup's vectors past the end read zeros and
+// drop their stores.
+template <int KIND, int BLOCK, int VPL, int ORDER, int MAP = 0>
+__global__ __launch_bounds__(BLOCK) void ceil_flat_kernel(uint8_t* a, uint8_t* b, uint32_t nbytes) {
+  constexpr int NA = KIND == 0 ? 2 * VPL : VPL;  // vectors of `a` per lane
+  const __amdgpu_buffer_rsrc_t ars = make_rsrc(a, KIND == 0 ? 2 * nbytes : nbytes);
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(b, nbytes);
+  const uint32_t chunk = (uint32_t)(MAP == 1 ? xcd_xor(blockIdx.x, gridDim.x) : xcd_runs<MAP == 2 ? 3 : 0>(blockIdx.x, gridDim.x));
+  const uint32_t base = (chunk * (BLOCK * NA) + threadIdx.x) * 16u;
+  u32x4 u[NA], v[VPL];
+  if constexpr (KIND == 0) {
+#pragma unroll
+    for (int k = 0; k < NA; ++k) u[k] = load16<kAuxNT>(ars, base + k * BLOCK * 16u);
+#pragma unroll
+    for (int k = 0; k < NA; ++k) store16<kAuxNT>(u[k] + 1u, ars, base + k * BLOCK * 16u);
+  } else {
+    const bool bfirst = ORDER == 1 || (ORDER == 2 && ((threadIdx.x >> 6) & 1)) || (ORDER == 3 && (blockIdx.x & 1));
+    if (ORDER == 0) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        u[k] = load16<kAuxNT>(ars, base + k * BLOCK * 16u);
+        v[k] = load16<kAuxNT>(brs, base + k * BLOCK * 16u);
+      }
+    } else if (bfirst) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) v[k] = load16<kAuxNT>(brs, base + k * BLOCK * 16u);
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) u[k] = load16<kAuxNT>(ars, base + k * BLOCK * 16u);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) u[k] = load16<kAuxNT>(ars, base + k * BLOCK * 16u);
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) v[k] = load16<kAuxNT>(brs, base + k * BLOCK * 16u);
+    }
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) store16<kAuxNT>(u[k] + v[k], brs, base + k * BLOCK * 16u);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) store16<kAuxNT>(u[k] ^ v[k], ars, base + k * BLOCK * 16u);
+  }
+}
+
+typedef void (*flat_fn)(uint8_t*, uint8_t*, uint32_t);
+struct FlatEntry {
+  int kind, block, vpl, order, map;
+  flat_fn fn;
+};
+#define HPRMS_FLAT(KIND, BLOCK, VPL, ORDER) {KIND, BLOCK, VPL, ORDER, 0, &ceil_flat_kernel<KIND, BLOCK, VPL, ORDER>},
+#define HPRMS_FLAT_MAPPED(KIND, BLOCK, VPL, MAP) \
+  {KIND, BLOCK, VPL, 0, MAP, &ceil_flat_kernel<KIND, BLOCK, VPL, 0, MAP>},
+#define HPRMS_FLAT_ORDERS(BLOCK, VPL) \
+  HPRMS_FLAT(0, BLOCK, VPL, 0) HPRMS_FLAT(1, BLOCK, VPL, 0) HPRMS_FLAT(1, BLOCK, VPL, 1) \
+  HPRMS_FLAT(1, BLOCK, VPL, 2) HPRMS_FLAT(1, BLOCK, VPL, 3)
+// the workgroup orders of xcd_xor (map 1) and xcd_runs<3> (map 2) for one and two streams
+#define HPRMS_FLAT_MAPS(BLOCK, VPL) \
+  HPRMS_FLAT_MAPPED(0, BLOCK, VPL, 1) HPRMS_FLAT_MAPPED(0, BLOCK, VPL, 2) HPRMS_FLAT_MAPPED(1, BLOCK, VPL, 1) \
+  HPRMS_FLAT_MAPPED(1, BLOCK, VPL, 2)
+const FlatEntry kFlat[] = {
+    HPRMS_FLAT_ORDERS(64, 1) HPRMS_FLAT_ORDERS(128, 1) HPRMS_FLAT_ORDERS(256, 1) HPRMS_FLAT_ORDERS(512, 1)
+    HPRMS_FLAT_ORDERS(1024, 1) HPRMS_FLAT_ORDERS(256, 2) HPRMS_FLAT_ORDERS(512, 2) HPRMS_FLAT_ORDERS(1024, 2)
+    HPRMS_FLAT_ORDERS(256, 4) HPRMS_FLAT_ORDERS(1024, 4)
+    HPRMS_FLAT_MAPS(256, 1) HPRMS_FLAT_MAPS(512, 1) HPRMS_FLAT_MAPS(1024, 1) HPRMS_FLAT_MAPS(256, 2)
+    HPRMS_FLAT_MAPS(1024, 4)
+};
 
 struct SkelArgs {
   uint16_t* x;
@@ -183,6 +259,10 @@ const SkelEntry kSkel[] = {
     HPRMS_SKEL_FLAGS(512, 2, 512) HPRMS_SKEL_FLAGS(512, 3, 512) HPRMS_SKEL_FLAGS(512, 4, 512)
     HPRMS_SKEL_FLAGS(1024, 2, 1024) HPRMS_SKEL_FLAGS(256, 8, 256) HPRMS_SKEL_FLAGS(1024, 3, 1024)
     HPRMS_SKEL_FLAGS(1024, 4, 1024) HPRMS_SKEL_FLAGS(32, 8, 64) HPRMS_SKEL_FLAGS(32, 12, 64)
+    // the other splits of a 512-vector row (H = 4096), one to eight rows per workgroup
+    HPRMS_SKEL(64, 8, 64, 131) HPRMS_SKEL(64, 8, 128, 131) HPRMS_SKEL(64, 8, 256, 131) HPRMS_SKEL(64, 8, 512, 131)
+    HPRMS_SKEL(128, 4, 128, 131) HPRMS_SKEL(128, 4, 512, 131) HPRMS_SKEL(256, 2, 512, 131)
+    HPRMS_SKEL(512, 1, 512, 131)
 };
 
 int launched() { return hipGetLastError() == hipSuccess ? HPRMS_OK : HPRMS_E_LAUNCH; }
@@ -200,12 +280,14 @@ using namespace hprms;
 
 extern "C" {
 
-// block: 64, 256, 512 or 1024 lanes (the table's workgroup sizes)
+// block: 64, 128, 256, 512 or 1024 lanes (the workgroup sizes of the table and the fill map)
 int hprms_ceil_empty(int64_t grid, int block, hipStream_t stream) {
   if (grid < 1 || grid > 0x7fffffff) return HPRMS_E_INVALID;
   const dim3 g((unsigned)grid);
   if (block == 64)
     ceil_empty_kernel<64><<<g, dim3(64), 0, stream>>>();
+  else if (block == 128)
+    ceil_empty_kernel<128><<<g, dim3(128), 0, stream>>>();
   else if (block == 256)
     ceil_empty_kernel<256><<<g, dim3(256), 0, stream>>>();
   else if (block == 512)
@@ -256,6 +338,27 @@ int hprms_ceil_streams(int kind, void* a, void* b, void* c, void* d, int64_t nby
   else
     ceil_streams_kernel<2><<<g, dim3(kFlatBlock), 0, stream>>>(pa, pb, pc, pd, nvec);
   return launched();
+}
+
+// kind 0: a (2 * nbytes) rewritten in place; kind 1: a and b (nbytes each)
+// rewritten in place; block lanes x vpl vectors per lane per stream, load
+// order `order` (ceil_flat_kernel).  nbytes % 16 == 0, below 1 GiB.
+// order 4 / 5: alternating loads (order 0) with the workgroups in xcd_xor's
+// order / in xcd_runs<3>'s (for kind 0 too).
+int hprms_ceil_flat(int kind, int block, int vpl, int order, void* a, void* b, int64_t nbytes, hipStream_t stream) {
+  if (!flat_ok(a, nbytes) || (kind == 1 && !flat_ok(b, nbytes)) || nbytes >= (int64_t(1) << 30))
+    return HPRMS_E_INVALID;
+  const int map = order >= 4 ? order - 3 : 0;
+  const int ord = order >= 4 || kind == 0 ? 0 : order;
+  for (const FlatEntry& e : kFlat) {
+    if (e.kind != kind || e.block != block || e.vpl != vpl || e.order != ord || e.map != map) continue;
+    const int64_t per_wg = (int64_t)block * vpl * 16;  // bytes of each stream per workgroup (kind 0: of half `a`)
+    const int64_t grid = (nbytes + per_wg - 1) / per_wg;
+    hipLaunchKernelGGL(e.fn, dim3((unsigned)grid), dim3(block), 0, stream, (uint8_t*)a,
+                       (uint8_t*)(kind == 0 ? a : b), (uint32_t)nbytes);
+    return launched();
+  }
+  return HPRMS_E_INVALID;
 }
 
 // x and r: contiguous [rows, hidden] 16-bit tensors, 16-byte aligned, hidden %

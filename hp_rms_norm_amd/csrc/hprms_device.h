@@ -143,6 +143,29 @@ __device__ __forceinline__ uint32_t cvt_e2m1x2(uint32_t w, float a, float b) {
   return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, 1.0f, SEL);
 }
 
+// ---- workgroup order ------------------------------------------------------------
+// The hardware hands consecutive workgroups of a grid to the 8 XCDs in turn,
+// so with work unit g = blockIdx.x XCD k always takes the units g % 8 == k.
+// xcd_xor: unit g ^ ((g >> 3) & 7), so an XCD's units cycle through all 8
+// residues modulo 8 in every run of 64.  xcd_runs<V>: in every block of
+// 8 * 2^V units each XCD takes 2^V consecutive units (V = 3: each 8 x 8 block
+// transposed).  Both permute each whole run or block of the n units; a
+// trailing partial one keeps its order.
+__device__ __forceinline__ int64_t xcd_xor(int64_t g, int64_t n) {
+  return (g | 63) >= n ? g : g ^ ((g >> 3) & 7);
+}
+
+template <int V>
+__device__ __forceinline__ int64_t xcd_runs(int64_t g, int64_t n) {
+  if constexpr (V == 0) {
+    return g;
+  } else {
+    constexpr int64_t R = int64_t(1) << V;
+    if ((g | (8 * R - 1)) >= n) return g;
+    return (g & ~(8 * R - 1)) | ((g & 7) << V) | ((g >> 3) & (R - 1));
+  }
+}
+
 // ---- reductions ---------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {

@@ -177,6 +177,11 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0) | ((FLAGS & 8192) ? kAuxSC0 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
+  // FLAGS bit 10 (bench library): row groups in xcd_xor's order; bits 16-18
+  // (bench library), V > 0: in xcd_runs<V>'s order (runs of 2^V row groups
+  // per XCD)
+  constexpr bool WXOR = (FLAGS & 1024) != 0;
+  constexpr int WRUNS = (FLAGS >> 16) & 7;
   // The output phase's unpack of the held row.  With the square phase's lo /
   // hi the compiler merges the two and keeps the row's unpacked floats live
   // across the reduction (more VGPRs); FLAGS bit 12 (bench library) unpacks
@@ -228,7 +233,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   const int he = 31 - __builtin_clz(hb);
   const float hidden_f = __builtin_bit_cast(float, (uint32_t)(127 + he) << 23 | ((hb << (23 - he)) & 0x7fffffu));
   for (int64_t g = blockIdx.x;;) {
-    const int64_t row0 = g * RPB;
+    const int64_t row0 = (WXOR ? xcd_xor(g, ngroups) : xcd_runs<WRUNS>(g, ngroups)) * RPB;
     const int64_t left = rows - row0;
     const int nrows = left < RPB ? (int)left : RPB;
     const bool row_ok = rib < nrows;

@@ -22,10 +22,12 @@ struct FusedEntry {
 // rows that are not 128-byte aligned (any 2-byte boundary), bit 6 = with the
 // tail vector for hidden % 8 != 0 (with bit 5), bit 7 = residual loads first,
 // bit 8 = held to 8 waves per SIMD, bit 9 = timeline instrumentation (bench
-// library only), bit 11 = one workgroup per CU (the launch reserves LDS),
+// library only), bit 10 = row groups in the xor XCD order (bench library),
+// bit 11 = one workgroup per CU (the launch reserves LDS),
 // bit 12 = the output phase's separate unpack (bench library), bit 13 = sc0 on
 // the stores (bench library), bit 14 = the tail variant's weight staged in
-// LDS, bit 15 = the partial sums' parts loaded before any is added
+// LDS, bit 15 = the partial sums' parts loaded before any is added, bits
+// 16-18 = V > 0: row groups in runs of 2^V per XCD (xcd_runs; bench library)
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
@@ -240,6 +242,25 @@ struct FusedEntry {
   X(DT, MODE, 1024, 2, 0, 1024, 539) X(DT, MODE, 256, 8, 4, 256, 539) X(DT, MODE, 1024, 3, 0, 1024, 667) \
   X(DT, MODE, 1024, 4, 0, 1024, 671) X(DT, MODE, 128, 4, 0, 256, 643) X(DT, MODE, 32, 8, 0, 64, 647)   \
   X(DT, MODE, 32, 12, 0, 64, 647)
+
+// every split of a 512-vector row (H = 4096) into lanes x vectors, in
+// workgroups of one to eight rows (the grid-size map of the fill-and-drain
+// cost at 4096 rows; nt, residual loads first, weight with the row)
+#define HPRMS_FILL_SHAPES(X, DT, MODE)                                                            \
+  X(DT, MODE, 64, 8, 0, 64, 131) X(DT, MODE, 64, 8, 0, 128, 131) X(DT, MODE, 64, 8, 0, 256, 131)   \
+  X(DT, MODE, 64, 8, 0, 512, 131) X(DT, MODE, 128, 4, 0, 128, 131) X(DT, MODE, 128, 4, 0, 256, 131) \
+  X(DT, MODE, 128, 4, 0, 512, 131) X(DT, MODE, 256, 2, 0, 512, 131) X(DT, MODE, 512, 1, 0, 512, 131)
+
+// the bandwidth table's rows with their row groups in xcd_xor's order
+// (+1024) and in xcd_runs<V>'s (+V << 16: runs of 2^V row groups per XCD)
+#define HPRMS_XCD_ORDER_ROWS(X, DT, MODE, F)                                                       \
+  X(DT, MODE, 256, 2, 0, 256, 131 | F) X(DT, MODE, 512, 2, 0, 512, 7 | F) X(DT, MODE, 512, 3, 0, 512, 159 | F) \
+  X(DT, MODE, 1024, 2, 0, 1024, 27 | F) X(DT, MODE, 256, 8, 4, 256, 27 | F)                              \
+  X(DT, MODE, 1024, 3, 0, 1024, 155 | F) X(DT, MODE, 1024, 4, 0, 1024, 159 | F)
+#define HPRMS_XCD_ORDER_SHAPES(X, DT, MODE)                                                        \
+  HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 1024) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 65536)                 \
+  HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 131072) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 196608)              \
+  HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 262144) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 327680)
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every

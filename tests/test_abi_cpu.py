@@ -490,7 +490,7 @@ def test_bench_library_is_apart_from_the_product():
     for n in declared_functions():
         assert hasattr(bench, n), n
     extra = ("hprms_bench_fused_timeline", "hprms_ceil_empty", "hprms_ceil_read", "hprms_ceil_write",
-             "hprms_ceil_copy", "hprms_ceil_skeleton")
+             "hprms_ceil_copy", "hprms_ceil_skeleton", "hprms_ceil_streams", "hprms_ceil_flat")
     for n in extra:
         assert hasattr(bench, n), n
         assert not hasattr(abi.lib(), n), f"{n} must not be in the product library"
@@ -507,7 +507,10 @@ def test_bench_library_is_apart_from_the_product():
 def test_bench_entry_points_reject_bad_arguments():
     L = abi.BENCH.lib()
     assert L.hprms_ceil_empty(0, 256, None) == abi.HPRMS_E_INVALID
-    assert L.hprms_ceil_empty(4, 128, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_ceil_empty(4, 96, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_ceil_flat(1, 256, 3, 0, 0x1000, 0x2000, 4096, None) == abi.HPRMS_E_INVALID   # no such shape
+    assert L.hprms_ceil_flat(1, 256, 1, 0, 0x1000, 0x2008, 4096, None) == abi.HPRMS_E_INVALID   # misaligned
+    assert L.hprms_ceil_flat(1, 256, 1, 0, 0x1000, 0x2000, 1 << 30, None) == abi.HPRMS_E_INVALID
     assert L.hprms_ceil_copy(0x1000, 0x2008, 4096, None) == abi.HPRMS_E_INVALID   # misaligned source
     assert L.hprms_ceil_read(0x1000, 0x2000, 4095, 0x3000, None) == abi.HPRMS_E_INVALID
     assert L.hprms_ceil_skeleton(0x1000, 0x2000, 4, 4096, 128, 3, 256, 3, None) == abi.HPRMS_E_INVALID

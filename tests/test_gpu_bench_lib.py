@@ -94,7 +94,7 @@ def test_ceiling_kernels_move_what_they_claim(abi):
     assert L.hprms_ceil_read(a.data_ptr(), b.data_ptr(), n, sink.data_ptr(), s) == 0
     wa, wb = torch.zeros_like(a), torch.zeros_like(a)
     assert L.hprms_ceil_write(wa.data_ptr(), wb.data_ptr(), n, s) == 0
-    for block in (64, 256, 512, 1024):
+    for block in (64, 128, 256, 512, 1024):
         assert L.hprms_ceil_empty(1000, block, s) == 0
     torch.cuda.synchronize()
     v = np.arange(n // 16, dtype=np.uint32).repeat(4)
@@ -103,7 +103,7 @@ def test_ceiling_kernels_move_what_they_claim(abi):
 
 
 @pytest.mark.parametrize("shape", [(128, 4, 256, 131), (512, 2, 512, 3), (1024, 4, 1024, 155), (64, 4, 256, 27),
-                                   (32, 12, 64, 131)])
+                                   (32, 12, 64, 131), (64, 8, 512, 131), (512, 1, 512, 131), (128, 4, 128, 131)])
 def test_skeleton_moves_the_ops_bytes(abi, shape):
     """r <- x + r and x <- x ^ (r_new + t) per 32-bit word, t the binary32 bits of
     the row's sum of the low bytes of r_new's words (exact in fp32 at these sizes)."""
@@ -147,3 +147,30 @@ def test_stream_pattern_kernels(abi):
     assert L.hprms_ceil_streams(0, ab.data_ptr(), None, None, None, n, s) == 0
     torch.cuda.synchronize()
     assert np.array_equal(ab.cpu().numpy().view(np.uint32), ab0 + 1)
+
+
+def test_flat_stream_kernels(abi):
+    """hprms_ceil_flat at every built shape and load order, on a size that
+    leaves the last workgroup partly past the end: kind 0 adds 1 to every
+    32-bit word of a (2n bytes) in place; kind 1 stores a + b to b and
+    a ^ b to a."""
+    import bench
+    L = abi.BENCH.lib()
+    s = _stream()
+    n = (1 << 20) + 3 * 4096 + 48
+    g = torch.Generator(device=DEV).manual_seed(5)
+    a0 = torch.randint(0, 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device=DEV, generator=g)
+    b0 = torch.randint(0, 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device=DEV, generator=g)
+    ua, ub = a0.cpu().numpy().view(np.uint32), b0.cpu().numpy().view(np.uint32)
+    for block, vpl in bench.FLAT_SHAPES:
+        ab = torch.cat([a0, b0])
+        assert L.hprms_ceil_flat(0, block, vpl, 0, ab.data_ptr(), None, n, s) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(ab.cpu().numpy().view(np.uint32), np.concatenate([ua, ub]) + 1), (block, vpl)
+        for order in range(4):
+            print("flat", block, vpl, order, flush=True)
+            a, b = a0.clone(), b0.clone()
+            assert L.hprms_ceil_flat(1, block, vpl, order, a.data_ptr(), b.data_ptr(), n, s) == 0
+            torch.cuda.synchronize()
+            assert np.array_equal(b.cpu().numpy().view(np.uint32), ua + ub), (block, vpl, order)
+            assert np.array_equal(a.cpu().numpy().view(np.uint32), ua ^ ub), (block, vpl, order)
