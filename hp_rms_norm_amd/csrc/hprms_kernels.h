@@ -174,6 +174,11 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr bool ROT = (FLAGS & 32) != 0 && !MX && MODE != 2;
   // residual loads issued first (not for the partial-sum form, where it measured 0.1-1.8% slower)
   constexpr bool RFIRST = (FLAGS & 128) != 0 && RES && MODE != 4;
+  // FLAGS bit 20 / bit 21 (bench library, with bit 7): the residual-first and
+  // input-first orders alternating per wave / per workgroup (consecutive
+  // workgroups run on different XCDs)
+  constexpr bool ALTW = RFIRST && (FLAGS & 1048576) != 0;
+  constexpr bool ALTG = RFIRST && (FLAGS & 2097152) != 0;
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0) | ((FLAGS & 8192) ? kAuxSC0 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
@@ -326,7 +331,23 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       }
     }
     u32x4 xv[VPL], rv[VPL], wv[VPL];
-    if constexpr (RFIRST) {
+    if constexpr (ALTW || ALTG) {
+      if (ALTW ? (wave & 1) != 0 : (blockIdx.x & 1) != 0) {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (RFIRST) {
       // all of the residual's vectors, then all of the input's (the
       // scheduling barriers keep the two groups apart)
 #pragma unroll
@@ -633,6 +654,8 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       }
     }
     const float inv = 1.0f / __builtin_sqrtf(tot / hidden_f + eps);
+    // FLAGS bit 19 (bench library): the output phase at raised wave priority
+    if constexpr ((FLAGS & 524288) != 0) __builtin_amdgcn_s_setprio(3);
 
     if constexpr (MX) {
       constexpr int EMAX = MODE == 5 ? 8 : 2;
@@ -765,6 +788,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         store8<SAUX>(q, ors, eooff);
       }
     }
+    if constexpr ((FLAGS & 524288) != 0) __builtin_amdgcn_s_setprio(0);
     g += grid;
     if (g >= ngroups) break;
   }

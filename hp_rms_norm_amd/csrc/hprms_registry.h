@@ -27,7 +27,10 @@ struct FusedEntry {
 // bit 12 = the output phase's separate unpack (bench library), bit 13 = sc0 on
 // the stores (bench library), bit 14 = the tail variant's weight staged in
 // LDS, bit 15 = the partial sums' parts loaded before any is added, bits
-// 16-18 = V > 0: row groups in runs of 2^V per XCD (xcd_runs; bench library)
+// 16-18 = V > 0: row groups in runs of 2^V per XCD (xcd_runs; bench library),
+// bit 19 = the output phase at raised wave priority (bench library), bits 20
+// / 21 = the two load orders alternating per wave / per workgroup (with bit 7;
+// bench library)
 #define HPRMS_FUSED_ENTRY(DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS)                             \
   {DT, MODE, LPR, VPL, LDSV, BLOCK, FLAGS,                                                   \
    &fused_vec_kernel<DT, MODE, LPR, VPL, LDSV, BLOCK, (FLAGS) & ~4, ((FLAGS) >> 2) & 1>},
@@ -261,6 +264,27 @@ struct FusedEntry {
   HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 1024) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 65536)                 \
   HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 131072) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 196608)              \
   HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 262144) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 327680)
+
+// candidates at 16384 (LDS splits and weight timing for fewer VGPRs), shapes
+// that fit the widths 5K-11K that are not powers of two, and the table's rows
+// with the output phase at raised wave priority (+524288)
+#define HPRMS_SHAPE_CANDIDATES(X, DT, MODE)                                                        \
+  X(DT, MODE, 256, 8, 4, 256, 31) X(DT, MODE, 256, 8, 4, 256, 287) X(DT, MODE, 256, 8, 6, 256, 31)    \
+  X(DT, MODE, 256, 8, 6, 256, 27) X(DT, MODE, 512, 4, 2, 512, 31) X(DT, MODE, 512, 4, 2, 512, 27)      \
+  X(DT, MODE, 512, 4, 0, 512, 27) X(DT, MODE, 128, 5, 0, 128, 135) X(DT, MODE, 128, 5, 0, 256, 135)    \
+  X(DT, MODE, 128, 6, 0, 256, 135) X(DT, MODE, 128, 7, 0, 256, 135) X(DT, MODE, 128, 9, 0, 256, 135)   \
+  X(DT, MODE, 256, 5, 0, 256, 135) X(DT, MODE, 128, 10, 0, 256, 135) X(DT, MODE, 256, 3, 0, 256, 135)  \
+  X(DT, MODE, 256, 2, 0, 256, 524419) X(DT, MODE, 512, 2, 0, 512, 524295) X(DT, MODE, 512, 3, 0, 512, 524447) \
+  X(DT, MODE, 1024, 2, 0, 1024, 524315) X(DT, MODE, 256, 8, 4, 256, 524315)                             \
+  X(DT, MODE, 1024, 3, 0, 1024, 524443) X(DT, MODE, 1024, 4, 0, 1024, 524447)
+// the bandwidth table's rows with the residual-first and input-first loads
+// alternating per wave (+1048576, with +128) and per workgroup (+2097152)
+#define HPRMS_ALT_ORDER_ROWS(X, DT, MODE, F)                                                          \
+  X(DT, MODE, 256, 2, 0, 256, 131 | F) X(DT, MODE, 512, 2, 0, 512, 135 | F) X(DT, MODE, 512, 3, 0, 512, 159 | F) \
+  X(DT, MODE, 1024, 2, 0, 1024, 155 | F) X(DT, MODE, 256, 8, 4, 256, 155 | F)                              \
+  X(DT, MODE, 1024, 3, 0, 1024, 155 | F) X(DT, MODE, 1024, 4, 0, 1024, 159 | F)
+#define HPRMS_ALT_ORDER_SHAPES(X, DT, MODE) \
+  HPRMS_ALT_ORDER_ROWS(X, DT, MODE, 1048576) HPRMS_ALT_ORDER_ROWS(X, DT, MODE, 2097152)
 
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every
