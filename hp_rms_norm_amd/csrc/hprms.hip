@@ -406,6 +406,37 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, int cus, hp
   c->block_threads = 256;
 }
 
+// Row groups in runs per XCD (hprms_device.h, xcd_runs; flags bits 16-18 =
+// V: each XCD takes 2^V consecutive row groups in place of every 8th).  The
+// in-place op on rows on the 128-byte grid whose input and residual share a
+// row pitch in this table, with the table's kernel for that pitch, measured
+// faster this way (bf16, cold, interleaved trials, repeated on fresh boxes):
+// 8 KiB rows (H = 4096) with runs of 32, 0.6-1.1% at 4096-16384 rows; 16 KiB
+// (H = 8192) with runs of 64, 1.1-1.9% at 2048-8192 rows (0.4% at 16384).
+// At the other 17 widths of the benchmark sweep (4096 rows) every run length
+// from 2 to 128 was as fast or slower (up to 16%) or less than 1% faster
+// (56 KiB, H = 28672: runs of 8, 0.2-1.0% at 2048-16384 rows; left out), and
+// at 64 KiB (H = 32768) runs of 8 ranged from 3.6% faster to 4% slower with
+// the row count.  The order only changes which workgroup takes a row, so the
+// bits are the same.
+struct RunsRow {
+  int64_t pitch_bytes;
+  int lpr, vpl, block, flags, v;
+  int64_t min_rows;  // on 256 CUs
+};
+constexpr RunsRow kRuns[] = {{8192, 256, 2, 256, 131, 5, 4096}, {16384, 512, 2, 512, 7, 6, 2048}};
+
+// flags bits 16-18 for configuration c of the in-place op (mode 0) on rows
+// `pitch_bytes` apart in both streams, on the 128-byte grid; 0 for others
+int xcd_runs_flags(int mode, int64_t rows, int64_t pitch_bytes, int cus, const hprms_config& c) {
+  if (mode != 0 || c.tier != 1 || c.lds_vec_per_lane != 0) return 0;
+  for (const RunsRow& r : kRuns)
+    if (r.pitch_bytes == pitch_bytes && r.lpr == c.lanes_per_row && r.vpl == c.vec_per_lane &&
+        r.block == c.block_threads && r.flags == c.flags && rows_at_ref(rows, cus) >= r.min_rows)
+      return r.v << 16;
+  return 0;
+}
+
 constexpr int64_t kMaxHidden = int64_t(1) << 24;
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
@@ -781,6 +812,8 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
     if (c.tier != 3 && (off_grid || ((c.flags & 24) && skip_sc1(p)))) {
       c.flags = unaligned_flags(p, c.flags);
       tail_shape(p, cus, &c);
+    } else if (!off_grid && p.x_stride == p.res_stride) {
+      c.flags |= xcd_runs_flags(p.mode, p.rows, p.x_stride * 2, cus, c);
     }
   }
   if ((c.flags & 512) && !p.timeline)
@@ -960,6 +993,7 @@ int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, in
   // the choice for rows on the 128-byte grid; odd widths: the tail variant of
   // the choice for rows off it
   table_config(rows, hidden, mode, hidden % 8 == 0, cu_count, config);
+  if (hidden % 8 == 0) config->flags |= xcd_runs_flags(mode, rows, hidden * 2, cu_count, *config);
   if (hidden % 8 != 0) {
     if (config->tier != 3 && hidden >= 8 && mode <= 4) {
       Problem p{mode, nullptr, nullptr, nullptr, nullptr, rows, hidden, hidden, hidden, hidden, dtype, 0.0};

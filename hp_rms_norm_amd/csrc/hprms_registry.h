@@ -27,7 +27,8 @@ struct FusedEntry {
 // bit 12 = the output phase's separate unpack (bench library), bit 13 = sc0 on
 // the stores (bench library), bit 14 = the tail variant's weight staged in
 // LDS, bit 15 = the partial sums' parts loaded before any is added, bits
-// 16-18 = V > 0: row groups in runs of 2^V per XCD (xcd_runs; bench library),
+// 16-18 = V > 0: row groups in runs of 2^V per XCD (xcd_runs; the product
+// has two, hprms.hip kRuns),
 // bit 19 = the output phase at raised wave priority (bench library), bits 20
 // / 21 = the two load orders alternating per wave / per workgroup (with bit 7;
 // bench library)
@@ -103,8 +104,10 @@ struct FusedEntry {
 // (hprms.hip, pair_rows; aligned registry only)
 #define HPRMS_PAIR_ROWS(X, DT, MODE) \
   X(DT, MODE, 128, 6, 0, 128, 135) X(DT, MODE, 128, 7, 0, 128, 135) X(DT, MODE, 128, 8, 0, 128, 135)
+// the in-place op's rows with their row groups in runs per XCD (hprms.hip, kRuns)
+#define HPRMS_RUNS_ROWS(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131 | 327680) X(DT, MODE, 512, 2, 0, 512, 7 | 393216)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
-  HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE) HPRMS_PAIR_ROWS(X, DT, MODE)
+  HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE) HPRMS_PAIR_ROWS(X, DT, MODE) HPRMS_RUNS_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)
 #define HPRMS_MODE0_OFFGRID_SHAPES(X, DT, MODE) \
   HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(X, DT, MODE)
@@ -257,13 +260,15 @@ struct FusedEntry {
 // the bandwidth table's rows with their row groups in xcd_xor's order
 // (+1024) and in xcd_runs<V>'s (+V << 16: runs of 2^V row groups per XCD)
 #define HPRMS_XCD_ORDER_ROWS(X, DT, MODE, F)                                                       \
+  X(DT, MODE, 32, 4, 0, 256, 131 | F) X(DT, MODE, 32, 8, 0, 64, 135 | F) X(DT, MODE, 32, 12, 0, 64, 135 | F) \
   X(DT, MODE, 256, 2, 0, 256, 131 | F) X(DT, MODE, 512, 2, 0, 512, 7 | F) X(DT, MODE, 512, 3, 0, 512, 159 | F) \
   X(DT, MODE, 1024, 2, 0, 1024, 27 | F) X(DT, MODE, 256, 8, 4, 256, 27 | F)                              \
   X(DT, MODE, 1024, 3, 0, 1024, 155 | F) X(DT, MODE, 1024, 4, 0, 1024, 159 | F)
 #define HPRMS_XCD_ORDER_SHAPES(X, DT, MODE)                                                        \
   HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 1024) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 65536)                 \
   HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 131072) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 196608)              \
-  HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 262144) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 327680)
+  HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 262144) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 327680)              \
+  HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 393216) HPRMS_XCD_ORDER_ROWS(X, DT, MODE, 458752)
 
 // candidates at 16384 (LDS splits and weight timing for fewer VGPRs), shapes
 // that fit the widths 5K-11K that are not powers of two, and the table's rows

@@ -211,7 +211,10 @@ typedef struct {
                                the FP8 output): the whole weight loaded once per workgroup
                                with aligned loads into LDS, where shifted rows read it;
                                bit 15 (partial sums, the latency rows): every part's loads
-                               issued before the first part is added */
+                               issued before the first part is added;
+                               bits 16-18, V > 0 (the in-place op at two row pitches):
+                               each XCD takes runs of 2^V consecutive row groups rather
+                               than every 8th (the same results) */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
@@ -253,6 +256,11 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  *     whose configuration carries the sc1 bits run the same shape with flags
  *     (flags & ~24) | 32: the unaligned variant without sc1 (rows off a
  *     512-byte boundary are then rotated, as above).
+ *   - Mode 0 reports bits 16-18 (row groups in runs per XCD) for hidden 4096
+ *     from 4096 rows and hidden 8192 from 2048 rows; calls take them when
+ *     their input and residual rows are on the grid with that pitch (8 KiB,
+ *     16 KiB) and the table's shape.  Every variant above takes its row
+ *     groups in the default order.
  * Pure function of its arguments; touches no device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 

@@ -595,3 +595,25 @@ def test_device_cu_count_is_the_devices(abi):
         outs.append((bits(xd), bits(rd)))
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
     check_case(abi, rows, hidden, torch.bfloat16, seed=n)
+
+
+# ---- row groups in runs per XCD ------------------------------------------------------------
+@pytest.mark.parametrize("rows,hidden", [(4096, 4096), (4100, 4096), (2048, 8192), (4133, 8192), (16384, 8192)])
+def test_xcd_runs_rows_give_the_default_orders_bits(abi, rows, hidden):
+    """At the row pitches where the in-place op takes its row groups in runs
+    per XCD (flags bits 16-18), the bits equal those of the same kernel in
+    the default order (forced), also with a partial last block of runs, and
+    the oracle's bar holds."""
+    c = abi.select_config(rows, hidden, abi.DTYPE_BF16, cus=abi.device_cu_count())
+    assert (c.flags >> 16) & 7, c.as_tuple()
+    plain = abi.Config(*c.as_tuple())
+    plain.flags = c.flags & 0xffff
+    x, r, w = make_inputs(rows, hidden, torch.bfloat16, seed=hidden + rows)
+    outs = []
+    for config in (None, plain):
+        xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+        run_abi(abi, xd, wd, rd, 1e-6, config)
+        torch.cuda.synchronize()
+        outs.append((bits(xd), bits(rd)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    check_case(abi, rows, hidden, torch.bfloat16, seed=hidden + rows)
