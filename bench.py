@@ -331,6 +331,9 @@ def main():
     ap.add_argument("--ab", nargs="+", default=None, metavar="H:CFG;CFG",
                     help="only an A/B of the fused op at (4096, H) bf16: the table's configuration against "
                          "forced bench-library ones (CFG = lanes_per_row,vec_per_lane,lds_vec_per_lane,block,flags)")
+    ap.add_argument("--xcd-sweep", action="store_true",
+                    help="only an A/B at every H of the sweep: the table's shape with its row groups in each "
+                         "xcd_runs order (runs of 1, 2, ..., 128 per XCD; flags bits 16-18) against the table")
     ap.add_argument("--hot", action="store_true",
                     help="with --ab: one buffer set, the same every call (resident in the Infinity Cache)")
     ap.add_argument("--ab-rows", type=int, default=B, metavar="ROWS",
@@ -363,6 +366,19 @@ def main():
         return profile_driver(torch, abi, op, args)
     if args.sweep:
         return sweep(torch, abi, op, args)
+    if args.xcd_sweep:
+        # (widths whose table shape at this row count has no such variants in the bench library are left out)
+        built = {c.as_tuple() for c in abi.BENCH.kernel_configs(abi.DTYPE_BF16, abi.MODE_FUSED)}
+        specs = []
+        for h in H_SWEEP:
+            c = abi.select_config(args.ab_rows, h, abi.DTYPE_BF16)
+            c.flags &= ~(7 << 16)
+            if not all(c.as_tuple()[:6] + (c.flags | (v << 16),) in built for v in range(8)):
+                log(f"--xcd-sweep: no run-order variants of {c.as_tuple()} for H = {h}")
+                continue
+            base = ",".join(str(v) for v in (c.lanes_per_row, c.vec_per_lane, c.lds_vec_per_lane, c.block_threads))
+            specs.append(f"{h}:" + ";".join(f"{base},{c.flags | (v << 16)}" for v in range(8)))
+        return ab_trials(torch, abi, op, specs, args.hot, rows=args.ab_rows)
     if args.ab:
         off, pad = (int(v) for v in args.layout.split(","))
         return ab_trials(torch, abi, op, args.ab, args.hot, off, pad, rows=args.ab_rows)
@@ -763,9 +779,10 @@ def ceiling(torch, abi, ops, hs, steps, warmup, trials=5, dump=None):
                "gbs": {k: round(nbytes[k] / (us[k] * 1e-6) / 1e9, 1) for k in nbytes},
                "fused_over_skeleton": round(us["fused"] / us["skeleton"], 3),
                "fused_over_copy": round(us["fused"] / us["copy"], 3)}
-        # one timeline launch of the table's kernel on a cold buffer set
+        # one timeline launch of the table's kernel on a cold buffer set (in the default row-group
+        # order: the instrumented kernels have no runs-per-XCD variants)
         tcfg = abi.Config(*cfg.as_tuple())
-        tcfg.flags = cfg.flags | 512
+        tcfg.flags = (cfg.flags & ~(7 << 16)) | 512
         tl = torch.zeros((grid, 4), dtype=torch.int64, device="cuda:0")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
