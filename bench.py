@@ -942,6 +942,11 @@ def fill_leg(torch, abi, ops, steps, warmup, trials=7, h=4096):
             "skeleton")
         kinds[f"fused {tag}"] = lambda i, cfg=cfg: BB.fused_add_rmsnorm(
             bufs[i][0].data_ptr(), w.data_ptr(), bufs[i][1].data_ptr(), B, h, h, h, abi.DTYPE_BF16, EPS, stream, cfg)
+    # every row resident in one round: 128 x 4 held to 8 waves per SIMD (flags +256; the compiler then
+    # keeps 64 VGPRs and spills), so the 2048 two-row workgroups fit the chip's wave slots at once
+    every = abi.Config(1, 128, 4, 0, 256, 0, 391)
+    kinds["fused 128x4/256 at 8 waves per SIMD"] = lambda i: BB.fused_add_rmsnorm(
+        bufs[i][0].data_ptr(), w.data_ptr(), bufs[i][1].data_ptr(), B, h, h, h, abi.DTYPE_BF16, EPS, stream, every)
     us = interleaved(torch, kinds, n, steps, warmup, trials)
     grids = {f"{lpr}x{vpl}/{blk}": B // (blk // lpr) for lpr, vpl, blk in FILL_SHAPES}
     print(json.dumps({"fill_hidden": h, "rows": B, "grids": grids, "us": {k: round(v, 2) for k, v in us.items()}}),
