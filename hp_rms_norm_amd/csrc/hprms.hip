@@ -759,9 +759,12 @@ void tail_shape(const Problem& p, int cus, hprms_config* c) {
 // not: the fused op 1-31% faster (9216 x 512 resident: 9.16 -> 6.36 us), the
 // FP8 and MX outputs and the partial sums up to 9.5% (within +2.5% in the
 // worst case).  Plain RMSNorm (+3-37%) and the out-of-place form (up to +13%
-// with resident rows), whose inputs sc1 keeps in the cache, keep it.  The
-// variant for rows off the 128-byte grid is that kernel (the same code; bit 5
-// only selects it).
+// with resident rows), whose inputs sc1 keeps in the cache, keep it.  Such
+// calls run the shape's unaligned variant (flags bit 5, sc1 bits cleared; the
+// registry has no aligned kernel of the shape without sc1): for rows on a
+// 512-byte boundary it is the table kernel's mapping; rows on the 128-byte
+// grid but off a 512-byte boundary are rotated onto one (rot_phase), which
+// changes the order of the row's sum of squares, within the same bar.
 bool skip_sc1(const Problem& p) {
   return p.mode != 1 && p.mode != 3 && p.rows * p.hidden <= (int64_t(1) << 24);
 }
