@@ -234,6 +234,28 @@ def test_row_rules_scale_with_the_cu_count():
     assert abi.select_config(128, 12289, bf, 0, cus=32).flags & 16384
 
 
+def test_row_groups_in_runs_per_xcd_at_two_pitches():
+    """The in-place op takes its row groups in runs per XCD (flags bits 16-18)
+    at H = 4096 from 4096 rows (runs of 32) and H = 8192 from 2048 rows (runs
+    of 64), in both dtypes, on the table's shape; no other mode, width or row
+    count, and no variant for rows off the grid, takes them."""
+    for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
+        for hidden, v, first in ((4096, 5, 4096), (8192, 6, 2048)):
+            for rows in (first, first + 1, 3 * first, 16384):
+                c = abi.select_config(rows, hidden, dtype)
+                assert (c.flags >> 16) & 7 == v and c.flags & 0xffff == (131 if hidden == 4096 else 7), c.as_tuple()
+            assert not abi.select_config(first - 1, hidden, dtype).flags >> 16
+            for mode in range(1, 7):
+                assert not abi.select_config(first, hidden, dtype, mode).flags >> 16, mode
+            assert not abi.select_config(first, hidden + 1, dtype).flags >> 16   # odd width: the tail variant
+        for hidden in (1024, 2048, 3072, 5120, 6144, 7168, 9216, 12288, 16384, 24576, 28672, 32768):
+            for rows in (2048, 4096, 16384):
+                assert not abi.select_config(rows, hidden, dtype).flags >> 16, (hidden, rows)
+    # on 32 CUs the row counts scale: H = 8192 from 256 rows
+    assert (abi.select_config(256, 8192, abi.DTYPE_BF16, cus=32).flags >> 16) & 7 == 6
+    assert not abi.select_config(255, 8192, abi.DTYPE_BF16, cus=32).flags >> 16
+
+
 @pytest.mark.parametrize("cus", [0, -1, 65537])
 def test_select_config_cu_rejects_bad_cu_counts(cus):
     c = abi.Config()
