@@ -63,7 +63,9 @@
 // group's loads, writes it to LDS after them, and every row reads its
 // vectors from there (five dwords each, funnel-shifted by the row's 2-byte
 // phase) after the row-sum barrier.  Bit 15 (MODE 4): each group of vectors
-// loads every part before adding the first (the latency rows).
+// loads every part before adding the first (the latency rows).  Bits 16-18
+// (V > 0): workgroup g takes row group xcd_runs<V>(g) rather than g, so each
+// XCD works on runs of 2^V consecutive row groups (hprms_device.h).
 //
 // The residual is stored as soon as it is formed: deferring it to the output
 // phase (one write burst per workgroup) measured up to 5% slower.
@@ -182,9 +184,10 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0) | ((FLAGS & 8192) ? kAuxSC0 : 0);
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
-  // FLAGS bit 10 (bench library): row groups in xcd_xor's order; bits 16-18
-  // (bench library), V > 0: in xcd_runs<V>'s order (runs of 2^V row groups
-  // per XCD)
+  // FLAGS bit 10 (bench library): row groups in xcd_xor's order; bits 16-18,
+  // V > 0: in xcd_runs<V>'s order (runs of 2^V row groups per XCD; the table
+  // takes it for the in-place op at two row pitches, the bench library for
+  // its sweeps)
   constexpr bool WXOR = (FLAGS & 1024) != 0;
   constexpr int WRUNS = (FLAGS >> 16) & 7;
   // The output phase's unpack of the held row.  With the square phase's lo /
