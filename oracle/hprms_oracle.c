@@ -18,9 +18,12 @@
  *
  * Arithmetic, element by element, in IEEE binary32 with round-to-nearest-even:
  *   s   = rne16(f32(x) + f32(r))                 stored to residual
- *   ms  = fp32 mean of f32(s)^2 over the row     (summed in binary64, then
- *                                                 rounded once to binary32:
- *                                                 no reduction-order error)
+ *   ms  = fp32 mean of f32(s)^2 over the row     (each square a binary32
+ *                                                 product, summed in binary64,
+ *                                                 then rounded once to
+ *                                                 binary32: no reduction-order
+ *                                                 error; a sum past binary32's
+ *                                                 range is +inf, see mean_square)
  *   inv = 1 / sqrt(ms + (float)eps)              two correctly rounded ops
  *   out = rne16((f32(s) * inv) * f32(w))          stored to input
  * The 16-bit conversions below are written from the IEEE 754 definitions
@@ -138,11 +141,26 @@ enum {
   MUT_NORM_INPUT = 5,      /* normalise the pre-add input instead of the sum */
   MUT_L1_MEAN = 6,         /* mean of |s| instead of s^2 (then squared) */
   MUT_UNROUNDED_SQUARES = 7, /* squares of the unrounded fp32 sum (the reference kernel's order) */
-  MUT_WEIGHT_TWICE = 8     /* (s * inv) * w * w */
+  MUT_WEIGHT_TWICE = 8,    /* (s * inv) * w * w */
+  MUT_BINARY64_SQUARES = 9 /* squares and mean in binary64: no binary32 overflow */
 };
 
 static int check_rows(int64_t rows, int64_t hidden, int64_t s0, int64_t s1) {
   return rows >= 0 && hidden >= 1 && s0 >= hidden && s1 >= hidden;
+}
+
+/* The mean of a row's squares as the reference's formula forms it in
+ * binary32 (test/test_hp_rms_norm.py:13-18: torch.rms_norm upcasts the row
+ * to fp32 and takes the mean of its squares).  The caller adds each square
+ * as a binary32 product, which is exact for 16-bit inputs unless it
+ * overflows to +inf or falls below the normal range, where it rounds as
+ * binary32 does.  sum_sq is their sum in binary64, free of reduction-order
+ * error.  A sum past binary32's range is +inf, as any binary32 summation of
+ * the same squares gives (a row of 256 values of 3e18 has finite squares
+ * and an infinite fp32 sum); otherwise the mean is rounded once. */
+static inline float mean_square(double sum_sq, double n) {
+  if (isinf((float)sum_sq)) return INFINITY;
+  return (float)(sum_sq / n);
 }
 
 /* One row of the fused op.  x: input row (overwritten with the output),
@@ -157,12 +175,13 @@ static void fused_row(uint16_t* x, const uint16_t* w, uint16_t* r, int64_t H,
     if (mutation == MUT_UNROUNDED_SQUARES) sf = sum;
     if (mutation == MUT_NORM_INPUT) sf = to_f32(x[j], dtype);
     if (mutation == MUT_L1_MEAN) acc += fabs((double)sf);
-    else acc += (double)sf * (double)sf;
+    else if (mutation == MUT_BINARY64_SQUARES) acc += (double)sf * (double)sf;
+    else acc += (double)(sf * sf);
     r[j] = s;
   }
   if (mutation == MUT_L1_MEAN) acc = (acc / (double)H) * (acc / (double)H) * (double)H;
   double denom = mutation == MUT_MEAN_H_MINUS_1 && H > 1 ? (double)(H - 1) : (double)H;
-  float ms = (float)(acc / denom);
+  float ms = mutation == MUT_BINARY64_SQUARES ? (float)(acc / denom) : mean_square(acc, denom);
   float v = mutation == MUT_DROP_EPS ? ms : ms + epsf;
   float inv = 1.0f / sqrtf(v);
   for (int64_t j = 0; j < H; ++j) {
@@ -214,10 +233,10 @@ int hprms_oracle_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* weig
     uint16_t* o = out + i * out_row_stride;
     double acc = 0.0;
     for (int64_t j = 0; j < hidden; ++j) {
-      double v = (double)to_f32(x[j], dtype);
-      acc += v * v;
+      float v = to_f32(x[j], dtype);
+      acc += (double)(v * v);
     }
-    float inv = 1.0f / sqrtf((float)(acc / (double)hidden) + epsf);
+    float inv = 1.0f / sqrtf(mean_square(acc, (double)hidden) + epsf);
     for (int64_t j = 0; j < hidden; ++j)
       o[j] = from_f32((to_f32(x[j], dtype) * inv) * to_f32(weight[j], dtype), dtype);
   }

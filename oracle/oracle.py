@@ -27,6 +27,7 @@ MUTATIONS = {
     "l1_mean": 6,
     "unrounded_squares": 7,
     "weight_twice": 8,
+    "binary64_squares": 9,
 }
 
 # planted mistakes of the partial-sum step (reduce_add_rmsnorm)

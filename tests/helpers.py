@@ -40,6 +40,73 @@ def make_inputs(rows, hidden, dtype, seed, dist="bench"):
     return x.to(dtype), r.to(dtype), w.to(dtype)
 
 
+# Rows of special values, one pattern per row (row i takes pattern i % len):
+# where the sum of squares is infinite the inverse is 0 and finite elements
+# give +-0; zero rows with eps = 0 give 0 * inf = NaN; subnormal sums are
+# exact in binary32, so their rows are as well defined as normal ones.
+SPECIAL_PATTERNS = (
+    "normal",            # N(0, 1) row, the control
+    "zeros",             # x = r = 0
+    "nan",               # one NaN in x
+    "inf",               # one +inf in x: the row's sum of squares is +inf
+    "inf_minus_inf",     # x = +inf, r = -inf at one element: a NaN sum
+    "one_huge",          # one element whose square overflows binary32 (fp16: 60000)
+    "sum_overflows",     # every square finite, their binary32 sum infinite (fp16: 60000s)
+    "large_finite",      # a sum of squares near a quarter of FLT_MAX (fp16: 200s)
+    "subnormal",         # bf16 subnormals 1e-39 (fp16: 1e-7), r = 0
+    "squares_subnormal", # 1e-20: the squares are binary32 subnormals (fp16: 1e-4)
+    "sum_is_inf",        # x + r overflows the 16-bit type at one element
+    "cancels",           # x = -r everywhere: a zero row from large values
+    "negative_zeros",    # x = r = -0
+    "half_subnormal",    # the first half subnormal, the rest N(0, 1)
+)
+
+
+def special_inputs(rows, hidden, dtype, seed):
+    """input, residual, weight (CPU, `dtype`) whose row i holds
+    SPECIAL_PATTERNS[i % len] on top of an N(0, 1) row; the special element
+    of the one-element patterns moves with the row (the last element for
+    rows = 2 mod 3)."""
+    bf = dtype == torch.bfloat16
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((rows, hidden), generator=g)
+    r = torch.randn((rows, hidden), generator=g)
+    w = 1 + 0.1 * torch.randn((hidden,), generator=g)
+    inf, nan = float("inf"), float("nan")
+    safe = (3.4e38 / (4 * hidden)) ** 0.5
+    for i in range(rows):
+        p = SPECIAL_PATTERNS[i % len(SPECIAL_PATTERNS)]
+        j = hidden - 1 if i % 3 == 2 else (i * 37) % hidden
+        if p == "zeros":
+            x[i], r[i] = 0.0, 0.0
+        elif p == "nan":
+            x[i, j] = nan
+        elif p == "inf":
+            x[i, j] = inf
+        elif p == "inf_minus_inf":
+            x[i, j], r[i, j] = inf, -inf
+        elif p == "one_huge":
+            x[i, j], r[i, j] = (1e20 if bf else 6e4), 0.0
+        elif p == "sum_overflows":
+            x[i], r[i] = (3e18 if bf else 6e4), 0.0
+        elif p == "large_finite":
+            x[i], r[i] = (safe if bf else 200.0), 0.0
+        elif p == "subnormal":
+            x[i], r[i] = (1e-39 if bf else 1e-7), 0.0
+        elif p == "squares_subnormal":
+            x[i], r[i] = (1e-20 if bf else 1e-4), 0.0
+        elif p == "sum_is_inf":
+            x[i, j] = r[i, j] = 3e38 if bf else 6e4
+        elif p == "cancels":
+            x[i] = (1e30 if bf else 3e4) * torch.sign(x[i])
+            r[i] = -x[i]
+        elif p == "negative_zeros":
+            x[i], r[i] = -0.0, -0.0
+        elif p == "half_subnormal":
+            x[i, : hidden // 2], r[i, : hidden // 2] = (1e-39 if bf else 1e-7), 0.0
+    return x.to(dtype), r.to(dtype), w.to(dtype)
+
+
 def oracle_fused(x, r, w, eps, dtype, threads=None):
     if threads is None:
         threads = min(16, oracle.max_threads())

@@ -9,6 +9,8 @@ Each check is independent of the oracle's own code:
     exactly; scaling a row by a power of two leaves the output unchanged,
   * the 16-bit conversions against numpy's binary16 and torch's bfloat16
     conversions on exhaustive and random bit patterns,
+  * rows of special values (NaN, infinities, zero rows with eps = 0, binary32
+    overflow of the squares and of their sum, subnormals) against torch,
 and every planted mistake the oracle can be asked to make is rejected by at
 least one of these pins.
 """
@@ -16,6 +18,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import SPECIAL_PATTERNS, special_inputs
 from oracle import oracle
 
 BF, HF = oracle.BF16, oracle.FP16
@@ -140,9 +143,30 @@ def pin_closed_forms(mutation=0):
     return None
 
 
+def pin_special_values(mutation=0):
+    """The live torch formula on rows of special values (helpers.SPECIAL_PATTERNS:
+    NaN, infinities, zero rows, binary32 overflow of a square and of the sum of
+    squares, subnormals) with eps = 0 and 1e-6: the residual bit-exact and the
+    output within 1 ulp, NaN where torch's is NaN (NaN bit patterns are not
+    compared: torch's own differ between its vectorised and scalar paths)."""
+    for code in (BF, HF):
+        for hidden in (300, 1024):
+            x, r, w = (tbits(t) for t in special_inputs(28, hidden, TDT[code], hidden))
+            for eps in (0.0, 1e-6):
+                want_out, want_res = torch_formula(x, r, w, eps, code)
+                out, res = oracle.fused_add_rmsnorm(x, w, r, eps, code, mutation=mutation)
+                if oracle.ulp_distance(res, want_res, code).max() != 0:
+                    return f"special {hidden} eps {eps}: residual differs"
+                d = oracle.ulp_distance(out, want_out, code)
+                if d.max() > 1:
+                    bad = SPECIAL_PATTERNS[int(np.argmax(d.max(axis=1))) % len(SPECIAL_PATTERNS)]
+                    return f"special {hidden} eps {eps}: output {d.max()} ulp in a {bad!r} row"
+    return None
+
+
 def all_pins(golden, mutation=0):
     return [m for m in (pin_golden(golden, mutation), pin_torch_live(mutation), pin_brute_force(mutation),
-                        pin_closed_forms(mutation)) if m]
+                        pin_closed_forms(mutation), pin_special_values(mutation)) if m]
 
 
 # ---- tests ---------------------------------------------------------------------------------
@@ -160,6 +184,19 @@ def test_oracle_matches_binary64_brute_force():
 
 def test_oracle_closed_forms():
     assert pin_closed_forms() is None
+
+
+def test_oracle_special_values_match_torch():
+    assert pin_special_values() is None
+
+
+def test_binary64_squares_are_caught_only_by_the_special_values():
+    """Summing the squares in binary64 (no binary32 overflow) agrees with
+    every other pin; only the rows whose binary32 sum of squares overflows
+    tell it from the reference's formula."""
+    m = oracle.MUTATIONS["binary64_squares"]
+    assert pin_special_values(m) is not None
+    assert pin_torch_live(m) is None and pin_brute_force(m) is None and pin_closed_forms(m) is None
 
 
 @pytest.mark.parametrize("name", sorted(oracle.MUTATIONS))
@@ -229,6 +266,15 @@ def test_oracle_rmsnorm_plain_matches_torch():
         want = tbits(torch.rms_norm(tfrom(x, code), (1536,), weight=tfrom(w, code), eps=1e-6))
         d = oracle.ulp_distance(oracle.rmsnorm(x, w, 1e-6, code), want, code)
         assert d.max() <= 1 and (d != 0).mean() < 1e-3
+
+
+def test_oracle_rmsnorm_plain_special_values_match_torch():
+    for code in (BF, HF):
+        x, r, w = (tbits(t) for t in special_inputs(28, 520, TDT[code], 5))
+        s = tbits(tfrom(x, code) + tfrom(r, code))          # the special rows as one input
+        for eps in (0.0, 1e-6):
+            want = tbits(torch.rms_norm(tfrom(s, code), (520,), weight=tfrom(w, code), eps=eps))
+            assert oracle.ulp_distance(oracle.rmsnorm(s, w, eps, code), want, code).max() <= 1, (code, eps)
 
 
 def test_oracle_strided_rows_and_threads():
