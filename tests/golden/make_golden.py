@@ -57,6 +57,18 @@ def sp_fp16_overflow(x, r, w):
     x[1].fill_(2.0 ** -20); r[1].fill_(2.0 ** -20)  # subnormal sums
 
 
+def sp_binary32_overflow(x, r, w):
+    """Rows whose binary32 sum of squares overflows while their mean would
+    not (torch's fp32 sum makes the inverse 0, a binary64 sum would not),
+    and rows of subnormals, with eps = 0."""
+    r.zero_()
+    x[0].fill_(3e18)                       # every square finite, the sum infinite
+    x[1, 7] = 1e20                         # one square infinite
+    x[2].fill_(1e-20)                      # squares that are binary32 subnormals
+    x[3, :256] = 1e-39                     # half the row bf16 subnormals
+    x[4].zero_()                           # zero row, eps = 0: 0 * inf = NaN
+
+
 def sp_constant_rows(x, r, w):
     x.zero_(); r.zero_()
     for i in range(x.shape[0]):
@@ -110,6 +122,7 @@ def main():
         fused_case("bf16_4x256_special", 4, 256, bf, 1e-6, "bench", 10, sp_zero_and_huge),
         fused_case("fp16_2x256_special", 2, 256, hf, 1e-6, "bench", 11, sp_fp16_overflow),
         fused_case("bf16_6x512_constant_eps0", 6, 512, bf, 0.0, "bench", 12, sp_constant_rows),
+        fused_case("bf16_6x512_binary32_overflow_eps0", 6, 512, bf, 0.0, "bench", 18, sp_binary32_overflow),
         fp8_case("fp8_bf16_4x4096", 4, 4096, bf, 1e-6, 15),
         fp8_case("fp8_fp16_3x5120", 3, 5120, hf, 1e-6, 16),
         fp8_case("fp8_bf16_4x1000_tail", 4, 1000, bf, 1e-6, 17, sp_fp8_rows),

@@ -190,12 +190,14 @@ def test_oracle_special_values_match_torch():
     assert pin_special_values() is None
 
 
-def test_binary64_squares_are_caught_only_by_the_special_values():
-    """Summing the squares in binary64 (no binary32 overflow) agrees with
-    every other pin; only the rows whose binary32 sum of squares overflows
-    tell it from the reference's formula."""
+def test_binary64_squares_are_caught_only_by_binary32_overflow_rows(golden):
+    """Summing the squares in binary64 (no binary32 overflow) agrees with the
+    pins on ordinary rows; only rows whose binary32 sum of squares overflows
+    (the special-value rows and the golden case made from them) tell it from
+    the reference's formula."""
     m = oracle.MUTATIONS["binary64_squares"]
     assert pin_special_values(m) is not None
+    assert "binary32_overflow" in (pin_golden(golden, m) or "")
     assert pin_torch_live(m) is None and pin_brute_force(m) is None and pin_closed_forms(m) is None
 
 
