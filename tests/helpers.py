@@ -107,6 +107,18 @@ def special_inputs(rows, hidden, dtype, seed):
     return x.to(dtype), r.to(dtype), w.to(dtype)
 
 
+def special_weight(w):
+    """`w` with zeros, a negative zero, infinities, a NaN, a subnormal and the
+    largest finite magnitudes at spread-out elements (element 11 * k + 3)."""
+    bf = w.dtype == torch.bfloat16
+    big = 3e38 if bf else 6e4
+    vals = (0.0, -0.0, float("inf"), -float("inf"), float("nan"), 1e-39 if bf else 1e-7, big, -big)
+    wf = w.float()
+    for k, v in enumerate(vals):
+        wf[(11 * k + 3) % w.numel()] = v
+    return wf.to(w.dtype)
+
+
 def oracle_fused(x, r, w, eps, dtype, threads=None):
     if threads is None:
         threads = min(16, oracle.max_threads())

@@ -12,7 +12,8 @@ its vectorised and scalar code.
 import pytest
 import torch
 
-from helpers import DT, assert_output_close, assert_residual_exact, bits, oracle_fused, special_inputs
+from helpers import (DT, assert_output_close, assert_residual_exact, bits, oracle_fused, special_inputs,
+                     special_weight)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -33,6 +34,7 @@ FUSED_CASES = [
     (300, 32768, 0),     # 1024 x 4
     (300, 65536, 0),     # 1024 x 8 (4)
     (1200, 8192, 8),     # rows 16 bytes off the 128-byte grid: the rotated variant
+    (1024, 8192, 1),     # rows 2 bytes apart in phase: shifted rows, the weight staged in LDS
     (1024, 4097, 0),     # odd width: the tail variant
     (16, 70000, 0),      # past the vector tiers: the general kernel
 ]
@@ -71,6 +73,24 @@ def test_fused_special_values(abi, dtype, eps):
         xd, rd, wd = _on_device(x, pad), _on_device(r, pad), w.to(DEV)
         abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden, xd.stride(0),
                               rd.stride(0), DT[dtype], eps, _stream())
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
+        assert_output_close(bits(xd), want_out, dtype, "output " + tag)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_fused_special_weight(abi, dtype):
+    """The same rows with a weight of special values (helpers.special_weight):
+    zeros, infinities, a NaN, a subnormal and the largest magnitudes."""
+    for rows, hidden, pad in FUSED_CASES:
+        tag = f"special weight {rows}x{hidden}+{pad} {dtype}"
+        print(tag, flush=True)
+        x, r, w = special_inputs(rows, hidden, dtype, seed=rows + 2 * hidden)
+        w = special_weight(w)
+        want_out, want_res = oracle_fused(x, r, w, 1e-6, dtype)
+        xd, rd, wd = _on_device(x, pad), _on_device(r, pad), w.to(DEV)
+        abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden, xd.stride(0),
+                              rd.stride(0), DT[dtype], 1e-6, _stream())
         torch.cuda.synchronize()
         assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
         assert_output_close(bits(xd), want_out, dtype, "output " + tag)

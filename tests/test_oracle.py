@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import SPECIAL_PATTERNS, special_inputs
+from helpers import SPECIAL_PATTERNS, special_inputs, special_weight
 from oracle import oracle
 
 BF, HF = oracle.BF16, oracle.FP16
@@ -146,12 +146,16 @@ def pin_closed_forms(mutation=0):
 def pin_special_values(mutation=0):
     """The live torch formula on rows of special values (helpers.SPECIAL_PATTERNS:
     NaN, infinities, zero rows, binary32 overflow of a square and of the sum of
-    squares, subnormals) with eps = 0 and 1e-6: the residual bit-exact and the
+    squares, subnormals), also with a weight of special values
+    (helpers.special_weight), with eps = 0 and 1e-6: the residual bit-exact and the
     output within 1 ulp, NaN where torch's is NaN (NaN bit patterns are not
     compared: torch's own differ between its vectorised and scalar paths)."""
     for code in (BF, HF):
-        for hidden in (300, 1024):
-            x, r, w = (tbits(t) for t in special_inputs(28, hidden, TDT[code], hidden))
+        for hidden, weight in ((300, "plain"), (1024, "plain"), (520, "special")):
+            x, r, w = special_inputs(28, hidden, TDT[code], hidden)
+            if weight == "special":
+                w = special_weight(w)
+            x, r, w = tbits(x), tbits(r), tbits(w)
             for eps in (0.0, 1e-6):
                 want_out, want_res = torch_formula(x, r, w, eps, code)
                 out, res = oracle.fused_add_rmsnorm(x, w, r, eps, code, mutation=mutation)
@@ -160,7 +164,7 @@ def pin_special_values(mutation=0):
                 d = oracle.ulp_distance(out, want_out, code)
                 if d.max() > 1:
                     bad = SPECIAL_PATTERNS[int(np.argmax(d.max(axis=1))) % len(SPECIAL_PATTERNS)]
-                    return f"special {hidden} eps {eps}: output {d.max()} ulp in a {bad!r} row"
+                    return f"special {hidden} eps {eps} {weight} weight: output {d.max()} ulp in a {bad!r} row"
     return None
 
 
