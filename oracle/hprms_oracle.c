@@ -50,10 +50,12 @@
  * codes pack two to a byte, the even element in the low nibble.
  *
  * Parity pins (tests/test_oracle.py): golden vectors made by the reference's
- * own formula in torch (tests/golden/), the live torch formula, a binary64
- * brute force, closed forms (constant rows, power-of-two scaling), numpy's
- * binary16 conversion, and planted mistakes (the `mutation` argument) that
- * each pin must reject.
+ * own formula in torch (tests/golden/), the live torch formula on ordinary
+ * rows and on rows of special values (NaN, infinities, zero rows with
+ * eps = 0, binary32 overflow of the squares and of their sum, subnormals), a
+ * binary64 brute force, closed forms (constant rows, power-of-two scaling),
+ * numpy's binary16 conversion, and planted mistakes (the `mutation`
+ * argument) that the pins must reject.
  */
 #include <float.h>
 #include <math.h>
