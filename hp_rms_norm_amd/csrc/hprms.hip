@@ -466,6 +466,18 @@ int64_t q_row_bytes(int mode, int64_t hidden) { return mode == 6 ? hidden / 2 : 
 bool has_res(int mode) { return mode != 1; }
 bool has_out(int mode) { return mode != 0; }
 
+// No buffer on any GPU spans more bytes (virtual addresses have at most 57
+// bits), and under this bound the kernels' 64-bit row offsets cannot overflow.
+constexpr int64_t kMaxExtentBytes = int64_t(1) << 56;
+
+// `rows` rows of `width` elements of `elem` bytes, `stride` elements apart,
+// span at most kMaxExtentBytes
+bool extent_ok(int64_t rows, int64_t stride, int64_t elem, int64_t width) {
+  if (rows <= 1) return true;
+  if (stride > kMaxExtentBytes / elem) return false;
+  return rows - 1 <= (kMaxExtentBytes / elem - width) / stride;
+}
+
 int check_problem(const Problem& p) {
   if (p.dtype != HPRMS_DTYPE_BF16 && p.dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", p.dtype);
@@ -494,6 +506,13 @@ int check_problem(const Problem& p) {
     return fail(HPRMS_E_INVALID, "nparts must be in [1, %d] (got %d)", HPRMS_MAX_PARTS, p.nparts);
   if (!(p.eps >= 0.0)) return fail(HPRMS_E_INVALID, "eps must be >= 0");
   if (p.rows == 0) return HPRMS_OK;
+  const int64_t ob = (p.mode == 2 || is_mx(p.mode)) ? 1 : 2;  // bytes per output element
+  if (!extent_ok(p.rows, p.x_stride, 2, p.hidden) ||
+      (has_res(p.mode) && !extent_ok(p.rows, p.res_stride, 2, p.hidden)) ||
+      (has_out(p.mode) && !extent_ok(p.rows, p.out_stride, ob, q_row_bytes(p.mode, p.hidden))) ||
+      (p.mode == 3 && !extent_ok(p.rows, p.res_out_stride, 2, p.hidden)) ||
+      (is_mx(p.mode) && !extent_ok(p.rows, p.mx_scale_stride, 1, p.hidden / 32)))
+    return fail(HPRMS_E_RANGE, "%lld rows at these row strides span more than 2^56 bytes", (long long)p.rows);
   if (p.mode == 4 && !p.parts) return fail(HPRMS_E_INVALID, "null parts array");
   if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) || (p.mode == 2 && !p.scale) ||
       (p.mode == 3 && !p.res_out) || (is_mx(p.mode) && !p.mx_scales))
@@ -1036,6 +1055,8 @@ int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int6
   if (hidden >= (int64_t(1) << 30))  // a row's buffer resource spans 2 * hidden < 2^31 bytes
     return fail(HPRMS_E_RANGE, "hidden %lld exceeds the streamer's row limit 2^30 - 1", (long long)hidden);
   if (rows == 0) return HPRMS_OK;
+  if (!extent_ok(rows, out_row_stride, 2, hidden) || !extent_ok(rows, in_row_stride, 2, hidden))
+    return fail(HPRMS_E_RANGE, "%lld rows at these row strides span more than 2^56 bytes", (long long)rows);
   if (!out || !in) return fail(HPRMS_E_INVALID, "null tensor pointer");
   StreamArgs a{(uint16_t*)out, (const uint16_t*)in, rows, hidden, out_row_stride, in_row_stride, 0};
   const bool flat = out_row_stride == hidden && in_row_stride == hidden && aligned16(out) && aligned16(in);

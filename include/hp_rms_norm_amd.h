@@ -36,7 +36,8 @@ typedef enum {
 #define HPRMS_OK 0
 #define HPRMS_E_INVALID (-22)  /* bad argument: null pointer, size, stride, dtype */
 #define HPRMS_E_LAUNCH (-5)    /* the HIP runtime rejected a launch or query */
-#define HPRMS_E_RANGE (-34)    /* a size or stride does not fit the kernel's index width */
+#define HPRMS_E_RANGE (-34)    /* a size or stride does not fit the kernel's index width, or a
+                                  tensor's rows span more than 2^56 bytes */
 
 /* most partial buffers hprms_reduce_add_rmsnorm() sums */
 #define HPRMS_MAX_PARTS 8

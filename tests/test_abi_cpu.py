@@ -70,6 +70,20 @@ def test_fused_rejects_hidden_beyond_maximum():
     assert fused(hidden=(1 << 24) + 8, si=(1 << 24) + 8, sr=(1 << 24) + 8) == abi.HPRMS_E_RANGE
 
 
+def test_rows_spanning_more_than_2_pow_56_bytes_are_rejected():
+    """No buffer spans 2^56 bytes; such a call is a range error before any
+    launch (the kernels' 64-bit row offsets would overflow past it)."""
+    L = abi.lib()
+    big = 1 << 40                                          # elements between rows
+    assert fused(rows=1 << 16, si=big) == abi.HPRMS_E_RANGE    # 2^16 rows x 2^41 bytes = 2^57
+    assert "2^56" in abi.last_error()
+    assert fused(rows=1 << 16, sr=big) == abi.HPRMS_E_RANGE
+    assert fused(rows=2, si=(1 << 62) + 4096) == abi.HPRMS_E_RANGE       # the stride alone overflows
+    assert fused(rows=0, si=big) == abi.HPRMS_OK                         # nothing to do
+    assert L.hprms_streamer(0x1000, 0x2000, 1 << 16, 64, big, 64, 0, 0, None) == abi.HPRMS_E_RANGE
+    assert L.hprms_rmsnorm(0x1000, 0x2000, 0x3000, 1 << 16, 64, big, 64, 0, 1e-6, None) == abi.HPRMS_E_RANGE
+
+
 def test_zero_rows_is_a_no_op_without_pointers():
     assert fused(rows=0, input=0, weight=0, residual=0) == abi.HPRMS_OK
 
