@@ -38,6 +38,8 @@ SYMBOLS = (
     "hprms_select_config",
     "hprms_select_config_cu",
     "hprms_device_cu_count",
+    "hprms_set_batch_invariant",
+    "hprms_batch_invariant",
     "hprms_kernel_configs",
     "hprms_last_error",
     "hprms_abi_version",
@@ -75,6 +77,8 @@ def _bind(L, bench):
     L.hprms_select_config.argtypes = [i64, i64, ci, ci, ctypes.POINTER(Config)]
     L.hprms_select_config_cu.argtypes = [i64, i64, ci, ci, ci, ctypes.POINTER(Config)]
     L.hprms_device_cu_count.argtypes = [ci]
+    L.hprms_set_batch_invariant.argtypes = [ci]
+    L.hprms_batch_invariant.argtypes = []
     L.hprms_kernel_configs.argtypes = [ci, ci, ctypes.POINTER(Config), ci]
     L.hprms_last_error.restype = ctypes.c_char_p
     L.hprms_last_error.argtypes = []
@@ -82,7 +86,7 @@ def _bind(L, bench):
     names = ["hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
              "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_out", "hprms_reduce_add_rmsnorm",
              "hprms_fused_add_rmsnorm_mx", "hprms_streamer", "hprms_select_config", "hprms_select_config_cu",
-             "hprms_device_cu_count", "hprms_kernel_configs"]
+             "hprms_device_cu_count", "hprms_kernel_configs", "hprms_set_batch_invariant", "hprms_batch_invariant"]
     if bench:
         L.hprms_bench_fused_timeline.argtypes = [vp, vp, vp, i64, i64, ci, cd, ctypes.POINTER(Config), vp, vp]
         L.hprms_ceil_empty.argtypes = [i64, ci, vp]
@@ -190,6 +194,16 @@ class Library:
             self._check(L.hprms_select_config_cu(rows, hidden, dtype, mode, cus, ctypes.byref(c)))
         return c
 
+    def set_batch_invariant(self, enable):
+        """hprms_set_batch_invariant: returns the previous setting."""
+        rc = self.lib().hprms_set_batch_invariant(1 if enable else 0)
+        if rc < 0:
+            raise HprmsError(rc, self.last_error())
+        return bool(rc)
+
+    def batch_invariant(self):
+        return bool(self.lib().hprms_batch_invariant())
+
     def device_cu_count(self, device=-1):
         """Compute units of a HIP device (-1: the current one) as the entry
         points use them."""
@@ -238,4 +252,6 @@ rmsnorm = PRODUCT.rmsnorm
 streamer = PRODUCT.streamer
 select_config = PRODUCT.select_config
 device_cu_count = PRODUCT.device_cu_count
+set_batch_invariant = PRODUCT.set_batch_invariant
+batch_invariant = PRODUCT.batch_invariant
 kernel_configs = PRODUCT.kernel_configs

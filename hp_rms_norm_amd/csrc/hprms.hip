@@ -13,6 +13,7 @@
 #include <atomic>
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -134,6 +135,34 @@ int current_cus() {
   const int n = device_cus(dev);
   return n > 0 ? n : kRefCUs;
 }
+
+// ---- batch-invariant mode -----------------------------------------------------------
+// The row-count rules below pick, for one width, shapes whose lanes sum a
+// row's squares in different orders, so a row's output can differ by an ulp
+// between calls of different row counts.  In batch-invariant mode the shape
+// follows from the width, the dtype, the form and the layout alone (the
+// bandwidth table's choice for a large batch), as the reference's does
+// (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618), and the row's bits do not
+// depend on the call's row count.  Process-wide: -1 until first read, then
+// HPRMS_BATCH_INVARIANT from the environment ("1" turns it on) unless set
+// through hprms_set_batch_invariant; threads racing on the first read store
+// the same value.
+std::atomic<int> g_batch_invariant{-1};
+
+bool batch_invariant() {
+  int v = g_batch_invariant.load(std::memory_order_relaxed);
+  if (v < 0) {
+    const char* e = getenv("HPRMS_BATCH_INVARIANT");
+    v = (e && e[0] == '1' && e[1] == '\0') ? 1 : 0;
+    int expected = -1;
+    g_batch_invariant.compare_exchange_strong(expected, v, std::memory_order_relaxed);
+    v = g_batch_invariant.load(std::memory_order_relaxed);
+  }
+  return v == 1;
+}
+
+// the row count the table sees in batch-invariant mode: past every row-count rule
+constexpr int64_t kInvariantRows = int64_t(1) << 30;
 
 // `rows` on a device of `cus` CUs as the row count with as many rows per CU on 256
 int64_t rows_at_ref(int64_t rows, int cus) {
@@ -348,6 +377,7 @@ bool pair_rows(int64_t rows, int64_t nvec, int mode, bool grid) {
 // `grid`: every row of every stream starts on the 128-byte grid (only the
 // in-place op's rows depend on it); `cus`: the device's compute units.
 void table_config(int64_t rows, int64_t hidden, int mode, bool grid, int cus, hprms_config* c) {
+  if (batch_invariant()) rows = kInvariantRows;
   const int64_t nvec = hidden / 8;
   const int64_t r = rows_at_ref(rows, cus);
   if (latency_config(r, nvec, mode, c)) return;
@@ -708,6 +738,10 @@ Phase rot_phase(const Problem& p) {
   };
   for (int i = 0; i < n; ++i)
     if (off(w[i], 128)) return phase512(w[i]);
+  // (rows on the 128-byte grid reach here only from skip_sc1, which depends on
+  // the row count; in batch-invariant mode they keep the aligned kernel's
+  // lane mapping)
+  if (batch_invariant()) return none;
   for (int i = 0; i < n; ++i)
     if (off(w[i], 512)) return phase512(w[i]);
   return none;
@@ -1027,6 +1061,15 @@ int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, in
   }
   return HPRMS_OK;
 }
+
+int hprms_set_batch_invariant(int enable) {
+  if (enable != 0 && enable != 1) return fail(HPRMS_E_INVALID, "enable must be 0 or 1 (got %d)", enable);
+  const int previous = hprms::batch_invariant() ? 1 : 0;
+  hprms::g_batch_invariant.store(enable, std::memory_order_relaxed);
+  return previous;
+}
+
+int hprms_batch_invariant(void) { return hprms::batch_invariant() ? 1 : 0; }
 
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config) {
   return hprms_select_config_cu(rows, hidden, dtype, mode, kRefCUs, config);

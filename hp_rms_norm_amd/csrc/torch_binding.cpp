@@ -407,14 +407,36 @@ void rms_norm_mx_meta(at::Tensor& out, at::Tensor& scales, const at::Tensor& inp
   (void)eps;
 }
 
+// _C.set_batch_invariant(enable) -> previous setting; _C.batch_invariant()
+// -> current setting (hprms_set_batch_invariant / hprms_batch_invariant).
+PyObject* py_set_batch_invariant(PyObject*, PyObject* arg) {
+  const int on = PyObject_IsTrue(arg);
+  if (on < 0) return nullptr;
+  const int previous = hprms_set_batch_invariant(on);
+  if (previous < 0) {
+    PyErr_SetString(PyExc_RuntimeError, hprms_last_error());
+    return nullptr;
+  }
+  return PyBool_FromLong(previous);
+}
+
+PyObject* py_batch_invariant(PyObject*, PyObject*) { return PyBool_FromLong(hprms_batch_invariant()); }
+
+PyMethodDef kMethods[] = {
+    {"set_batch_invariant", py_set_batch_invariant, METH_O,
+     "set_batch_invariant(enable) -> bool: choose each call's kernel shape by the width alone (a row's bits "
+     "then do not depend on the call's row count); returns the previous setting"},
+    {"batch_invariant", py_batch_invariant, METH_NOARGS, "batch_invariant() -> bool: the current setting"},
+    {nullptr, nullptr, 0, nullptr}};
+
 }  // namespace
 
 // Module init of `hp_rms_norm_amd._C`.  The operators live in torch's
-// registry, so the module itself carries only the C ABI version it was built
-// against.
+// registry, so the module itself carries the C ABI version it was built
+// against and the batch-invariant mode's setter and getter.
 extern "C" PyObject* PyInit__C(void) {
   static PyModuleDef def = {PyModuleDef_HEAD_INIT, "_C",
-                            "torch.ops.hp_rms_norm.* on the gfx950 kernels of libhprms.so", -1, nullptr};
+                            "torch.ops.hp_rms_norm.* on the gfx950 kernels of libhprms.so", -1, kMethods};
   PyObject* m = PyModule_Create(&def);
   if (m && PyModule_AddIntConstant(m, "abi_version", hprms_abi_version()) != 0) {
     Py_DECREF(m);

@@ -5,7 +5,8 @@ import torch
 
 __all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "fused_add_rms_norm_out",
            "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "reduce_add_rms_norm", "hp_rms_norm_mx",
-           "fused_add_rms_norm_mxfp8", "fused_add_rms_norm_mxfp4", "MXFP8", "MXFP4"]
+           "fused_add_rms_norm_mxfp8", "fused_add_rms_norm_mxfp4", "MXFP8", "MXFP4",
+           "set_batch_invariant", "batch_invariant"]
 
 MXFP8, MXFP4 = 0, 1  # element formats of the OCP MX output
 
@@ -126,3 +127,23 @@ def fused_add_rms_norm_mxfp4(input, residual, weight, eps):
     q, scales = _mx_alloc(input, MXFP4)
     hp_rms_norm_mx(q, scales, input, weight, residual, eps, MXFP4)
     return q, scales
+
+
+def set_batch_invariant(enable):
+    """Process-wide: with ``enable`` true every call chooses its kernel shape by
+    the width (and dtype, form and layout) alone, as the reference's launcher
+    does (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618), so a row's output
+    bits do not depend on how many rows the call holds; calls with few rows
+    run slower.  By default the row count also picks the shape, and the same
+    row can come out one ulp apart between calls of different row counts.
+    Returns the previous setting.  ``HPRMS_BATCH_INVARIANT=1`` in the
+    environment turns it on until set.  No reference counterpart."""
+    from . import _C
+    return _C.set_batch_invariant(bool(enable))
+
+
+def batch_invariant():
+    """The current batch-invariant setting (see ``set_batch_invariant``)."""
+    from . import _C
+    return _C.batch_invariant()
+

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 5
+#define HPRMS_ABI_VERSION 6
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -284,6 +284,26 @@ int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, in
  * the reference's per-call device-property query
  * (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:550,571). */
 int hprms_device_cu_count(int device);
+
+/* Batch-invariant mode, process-wide.  By default the row count selects the
+ * shape (latency rows for few rows, wide, one- and two-wave rows for
+ * mid-size batches: up to 29% faster there), and shapes of one width sum a
+ * row's squares in different orders, so the same row can come out one ulp
+ * apart in calls of different row counts (in about 1e-5 of elements; both
+ * within the bar).  With the mode on, the shape follows from hidden, dtype,
+ * mode and layout alone -- the bandwidth table's choice for a large batch --
+ * as the reference's launcher chooses by hidden alone
+ * (hp_rms_norm/csrc/cuda/hp_rms_norm.cuh:562-618), so a row's bits do not
+ * depend on the call's row count; calls with few rows run slower.  Rows are
+ * compared at the same addresses modulo 512 bytes (torch's allocator aligns
+ * to 512): rows off the 128-byte grid take lane mappings that follow their
+ * addresses.  hprms_set_batch_invariant(0 or 1) returns the previous setting
+ * (or HPRMS_E_INVALID); hprms_batch_invariant() returns the current one.
+ * Until set, the environment variable HPRMS_BATCH_INVARIANT=1 turns it on.
+ * The setting is read once per call; hprms_select_config reports the
+ * configuration under it.  No counterpart in the reference. */
+int hprms_set_batch_invariant(int enable);
+int hprms_batch_invariant(void);
 
 /* Lists the vector-tier configurations built into the library for (dtype,
  * mode, numbered as for hprms_select_config).  Writes up to `capacity`

@@ -84,6 +84,40 @@ def test_rows_spanning_more_than_2_pow_56_bytes_are_rejected():
     assert L.hprms_rmsnorm(0x1000, 0x2000, 0x3000, 1 << 16, 64, big, 64, 0, 1e-6, None) == abi.HPRMS_E_RANGE
 
 
+def test_batch_invariant_mode_picks_the_shape_by_width_alone():
+    """With the mode on, every row count takes the configuration the table
+    gives a large batch (latency, wide, one- and two-wave rows are row-count
+    rules); with it off, few rows take the latency rows.  The mode is
+    process-wide and restored here."""
+    previous = abi.set_batch_invariant(False)
+    try:
+        assert not abi.batch_invariant()
+        for hidden in (1024, 2048, 3072, 4096, 6144, 8192, 16384, 32768, 4097):
+            default = {n: abi.select_config(n, hidden, abi.DTYPE_BF16, 0).as_tuple()[:5] for n in (1, 1500, 1 << 20)}
+            assert abi.set_batch_invariant(True) is False
+            inv = {n: abi.select_config(n, hidden, abi.DTYPE_BF16, 0).as_tuple()[:5]
+                   for n in (1, 8, 300, 1024, 1500, 2048, 3000, 4096, 1 << 20)}
+            assert abi.set_batch_invariant(False) is True
+            assert len(set(inv.values())) == 1, (hidden, inv)
+            assert inv[1 << 20] == default[1 << 20]
+        assert abi.select_config(8, 4096, abi.DTYPE_BF16, 0).as_tuple() != \
+            abi.select_config(1 << 20, 4096, abi.DTYPE_BF16, 0).as_tuple()
+        assert abi.lib().hprms_set_batch_invariant(2) == abi.HPRMS_E_INVALID
+    finally:
+        abi.set_batch_invariant(previous)
+
+
+def test_batch_invariant_mode_from_the_environment():
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); from hp_rms_norm_amd import abi; "
+            "print(abi.batch_invariant())") % ROOT
+    for env_value, want in (("1", "True"), ("0", "False"), ("", "False")):
+        env = dict(os.environ, HPRMS_BATCH_INVARIANT=env_value)
+        out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, check=True)
+        assert out.stdout.strip() == want, (env_value, out.stdout, out.stderr)
+
+
 def test_zero_rows_is_a_no_op_without_pointers():
     assert fused(rows=0, input=0, weight=0, residual=0) == abi.HPRMS_OK
 
