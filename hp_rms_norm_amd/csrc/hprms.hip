@@ -817,7 +817,8 @@ void tail_shape(const Problem& p, int cus, hprms_config* c) {
 // registry has no aligned kernel of the shape without sc1): for rows on a
 // 512-byte boundary it is the table kernel's mapping; rows on the 128-byte
 // grid but off a 512-byte boundary are rotated onto one (rot_phase), which
-// changes the order of the row's sum of squares, within the same bar.
+// changes the order of the row's sum of squares, within the same bar (not in
+// batch-invariant mode, where they keep the table kernel's mapping).
 bool skip_sc1(const Problem& p) {
   return p.mode != 1 && p.mode != 3 && p.rows * p.hidden <= (int64_t(1) << 24);
 }
