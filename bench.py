@@ -1008,6 +1008,20 @@ def run_extra(torch, ops, args):
         del g, bufs, sets
     torch.cuda.empty_cache()
     out["decode_bf16_hip_graph"] = graph
+    # the decode shapes and two mid-size batches with the batch-invariant mode on (every call
+    # takes its width's large-batch shape), beside the default mode's time for the same shape
+    mid = [(1024, 4096, torch.bfloat16, "bench"), (2048, 2048, torch.bfloat16, "bench")]
+    default_us = {(b, h): u for (b, h, _, _), (u, _, _) in zip(dec, us)}
+    for (b, h, _, _), (u, _, _) in zip(mid, time_shapes(torch, ops.hp_rms_norm, mid, steps, args.warmup)):
+        default_us[(b, h)] = u
+    previous = ops.set_batch_invariant(True)
+    try:
+        inv = time_shapes(torch, ops.hp_rms_norm, dec + mid, steps, args.warmup)
+    finally:
+        ops.set_batch_invariant(previous)
+    out["batch_invariant_mode_bf16"] = [
+        {"rows": b, "hidden": h, "us_per_call": round(u, 2), "default_mode_us_per_call": round(default_us[(b, h)], 2)}
+        for (b, h, _, _), (u, _, _) in zip(dec + mid, inv)]
     # fp16 non-power-of-two hidden
     f16 = [(B, 5120, torch.float16, "bench"), (B, 7168, torch.float16, "bench")]
     us = time_shapes(torch, ops.hp_rms_norm, f16, steps, args.warmup)
