@@ -67,6 +67,7 @@ const FusedEntry kFused[] = {
     HPRMS_XCD_ORDER_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_SHAPE_CANDIDATES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_ALT_ORDER_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_STREAM_POLICY_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_SHARED_UNPACK_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
 #endif
 };

@@ -198,14 +198,14 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
 
-// Unsigned maximum over aligned groups of WIDTH lanes, same lane pattern as
-// group_sum.  Must be called with every lane of the wave active.
 // Unsigned maximum over each aligned quad of lanes (every lane gets it).
 __device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
   v = __builtin_elementwise_max(v, dpp_u32<0xB1>(v));  // quad_perm [1,0,3,2]
   return __builtin_elementwise_max(v, dpp_u32<0x4E>(v));  // quad_perm [2,3,0,1]
 }
 
+// Unsigned maximum over aligned groups of WIDTH lanes, same lane pattern as
+// group_sum.  Must be called with every lane of the wave active.
 template <int WIDTH>
 __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
   static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group width");

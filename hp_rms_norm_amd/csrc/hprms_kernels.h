@@ -183,6 +183,14 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr bool ALTG = RFIRST && (FLAGS & 2097152) != 0;
   constexpr int LAUX = ((FLAGS & 1) ? kAuxNT : 0) | ((FLAGS & 8) ? kAuxSC1 : 0);
   constexpr int SAUX = ((FLAGS & 2) ? kAuxNT : 0) | ((FLAGS & 16) ? kAuxSC1 : 0) | ((FLAGS & 8192) ? kAuxSC0 : 0);
+  // FLAGS bits 22-25 (bench library): one stream's accesses without the
+  // policy bits the others keep: the input's loads (22) or the residual's
+  // (23) without nt and sc1, the residual's stores (24) or the output's (25)
+  // without nt
+  constexpr int XLAUX = (FLAGS & 4194304) ? 0 : LAUX;
+  constexpr int RLAUX = (FLAGS & 8388608) ? 0 : LAUX;
+  constexpr int RSAUX = (FLAGS & 16777216) ? (SAUX & ~kAuxNT) : SAUX;
+  constexpr int OSAUX = (FLAGS & 33554432) ? (SAUX & ~kAuxNT) : SAUX;
   constexpr uint32_t CH = LPR * 16;  // byte distance between a lane's vectors
   // FLAGS bit 10 (bench library): row groups in xcd_xor's order; bits 16-18,
   // V > 0: in xcd_runs<V>'s order (runs of 2^V row groups per XCD; the table
@@ -337,34 +345,34 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     if constexpr (ALTW || ALTG) {
       if (ALTW ? (wave & 1) != 0 : (blockIdx.x & 1) != 0) {
 #pragma unroll
-        for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
+        for (int k = 0; k < VPL; ++k) rv[k] = load16<RLAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
+        for (int k = 0; k < VPL; ++k) xv[k] = load16<XLAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
         __builtin_amdgcn_sched_barrier(0);
       } else {
 #pragma unroll
-        for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
+        for (int k = 0; k < VPL; ++k) xv[k] = load16<XLAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
+        for (int k = 0; k < VPL; ++k) rv[k] = load16<RLAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else if constexpr (RFIRST) {
       // all of the residual's vectors, then all of the input's (the
       // scheduling barriers keep the two groups apart)
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) rv[k] = load16<LAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
+      for (int k = 0; k < VPL; ++k) rv[k] = load16<RLAUX>(rrs, (row_ok && vec_ok[k]) ? roff + vk(k) : kOOB);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = 0; k < VPL; ++k) xv[k] = load16<LAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
+      for (int k = 0; k < VPL; ++k) xv[k] = load16<XLAUX>(xrs, (row_ok && vec_ok[k]) ? xoff + vk(k) : kOOB);
       __builtin_amdgcn_sched_barrier(0);
     } else {
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         const bool ok = row_ok && vec_ok[k];
-        xv[k] = load16<LAUX>(xrs, ok ? xoff + vk(k) : kOOB);
-        if constexpr (RES) rv[k] = load16<LAUX>(rrs, ok ? roff + vk(k) : kOOB);
+        xv[k] = load16<XLAUX>(xrs, ok ? xoff + vk(k) : kOOB);
+        if constexpr (RES) rv[k] = load16<RLAUX>(rrs, ok ? roff + vk(k) : kOOB);
       }
     }
     // TAIL: the edge vector's loads, by the lanes that hold one only (a
@@ -373,8 +381,8 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     u32x4 txv = {}, trv = {}, twv = {};
     if constexpr (TAIL) {
       if (eok) {
-        txv = load16<LAUX>(xrs, exoff);
-        if constexpr (RES) trv = load16<LAUX>(rrs, eroff);
+        txv = load16<XLAUX>(xrs, exoff);
+        if constexpr (RES) trv = load16<RLAUX>(rrs, eroff);
       }
     }
     if constexpr (!WLATE) {
@@ -590,7 +598,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
           ss1 = __builtin_fmaf(b1, b1, ss1);
         }
         const bool ok = row_ok && vec_ok[k];
-        store16<SAUX>(s, srs, ok ? soff + vk(k) : kOOB);
+        store16<RSAUX>(s, srs, ok ? soff + vk(k) : kOOB);
       } else {
         s = xv[k];
 #pragma unroll
@@ -616,7 +624,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         ss0 = __builtin_fmaf(b0, b0, ss0);
         ss1 = __builtin_fmaf(b1, b1, ss1);
       }
-      if constexpr (RES) store16<SAUX>(tsv, srs, esoff);
+      if constexpr (RES) store16<RSAUX>(tsv, srs, esoff);
     }
 
     if constexpr (WLATE) {
@@ -693,14 +701,14 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
             q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * mul), clamp_e4m3(F::hi(y0) * mul),
                                clamp_e4m3(F::lo(y1) * mul), clamp_e4m3(F::hi(y1) * mul));
           }
-          store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
+          store8<OSAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
         } else {
           uint32_t q = 0;
           q = cvt_e2m1x2<0>(q, F::lo(y[0]) * mul, F::hi(y[0]) * mul);
           q = cvt_e2m1x2<1>(q, F::lo(y[1]) * mul, F::hi(y[1]) * mul);
           q = cvt_e2m1x2<2>(q, F::lo(y[2]) * mul, F::hi(y[2]) * mul);
           q = cvt_e2m1x2<3>(q, F::lo(y[3]) * mul, F::hi(y[3]) * mul);
-          store4<SAUX>(q, ors, ok ? ooff + k * (LPR * 4u) : kOOB);
+          store4<OSAUX>(q, ors, ok ? ooff + k * (LPR * 4u) : kOOB);
         }
       }
     } else if constexpr (MODE != 2) {
@@ -712,14 +720,14 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         for (int j = 0; j < 4; ++j)
           o[j] = F::pack((olo(s[j]) * inv) * F::lo(wv[k][j]), (ohi(s[j]) * inv) * F::hi(wv[k][j]));
         const bool ok = row_ok && vec_ok[k];
-        store16<SAUX>(o, ors, ok ? ooff + vk(k) : kOOB);
+        store16<OSAUX>(o, ors, ok ? ooff + vk(k) : kOOB);
       }
       if constexpr (TAIL) {
         u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           o[j] = F::pack((olo(tsv[j]) * inv) * F::lo(twv[j]), (ohi(tsv[j]) * inv) * F::hi(twv[j]));
-        store16<SAUX>(o, ors, eooff);
+        store16<OSAUX>(o, ors, eooff);
       }
     } else {
       // y in 16-bit form, kept in the registers x came in; the row maximum of
@@ -778,7 +786,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
                              clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
         }
         const bool ok = row_ok && vec_ok[k];
-        store8<SAUX>(q, ors, ok ? ooff + k * (LPR * 8u) + (k == 0 ? wrap * 8u : 0u) : kOOB);
+        store8<OSAUX>(q, ors, ok ? ooff + k * (LPR * 8u) + (k == 0 ? wrap * 8u : 0u) : kOOB);
       }
       if constexpr (TAIL) {
         u32x2 q;
@@ -788,7 +796,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
           q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * isc), clamp_e4m3(F::hi(y0) * isc),
                              clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
         }
-        store8<SAUX>(q, ors, eooff);
+        store8<OSAUX>(q, ors, eooff);
       }
     }
     if constexpr ((FLAGS & 524288) != 0) __builtin_amdgcn_s_setprio(0);

@@ -291,6 +291,20 @@ struct FusedEntry {
 #define HPRMS_ALT_ORDER_SHAPES(X, DT, MODE) \
   HPRMS_ALT_ORDER_ROWS(X, DT, MODE, 1048576) HPRMS_ALT_ORDER_ROWS(X, DT, MODE, 2097152)
 
+// the latency rows of 4K-8K and the bandwidth rows of 12K-24K with one
+// stream's cache policy changed: the input's loads (+4194304) or the
+// residual's (+8388608) without nt / sc1, the residual's stores (+16777216)
+// or the output's (+33554432) without nt; and the 4K latency row without nt
+// on the loads or anywhere
+#define HPRMS_STREAM_POLICY_ROWS(X, DT, MODE, F)                                                   \
+  X(DT, MODE, 256, 2, 0, 256, 7 | F) X(DT, MODE, 512, 2, 0, 512, 7 | F)                          \
+  X(DT, MODE, 512, 3, 0, 512, 159 | F) X(DT, MODE, 1024, 2, 0, 1024, 27 | F)                     \
+  X(DT, MODE, 256, 8, 4, 256, 27 | F) X(DT, MODE, 1024, 3, 0, 1024, 155 | F)
+#define HPRMS_STREAM_POLICY_SHAPES(X, DT, MODE)                                                   \
+  HPRMS_STREAM_POLICY_ROWS(X, DT, MODE, 4194304) HPRMS_STREAM_POLICY_ROWS(X, DT, MODE, 8388608)  \
+  HPRMS_STREAM_POLICY_ROWS(X, DT, MODE, 16777216) HPRMS_STREAM_POLICY_ROWS(X, DT, MODE, 33554432) \
+  X(DT, MODE, 256, 2, 0, 256, 6) X(DT, MODE, 256, 2, 0, 256, 4)
+
 // The unaligned variants (hprms_unaligned.hip) and the tail variants
 // (hprms_tail.hip, modes 0-4: the MX outputs need hidden % 32 == 0): every
 // entry the tables can choose, as HPRMS_UNALIGNED_ENTRY / HPRMS_TAIL_ENTRY
