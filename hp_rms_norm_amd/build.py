@@ -8,10 +8,11 @@
                        the ceiling kernels (hprms_ceiling.hip)
 
 All land next to this file, so they travel with the source tree.  Run
-``python hp_rms_norm_amd/build.py [all|kernels|torch|oracle]`` (or
-``__graft_entry__.build()``) -- as a script, not with ``-m``: importing it
-through the package would run the package's __init__, which needs the
-libraries this builds.  No GPU is needed: hipcc cross-compiles for gfx950.
+``python hp_rms_norm_amd/build.py [all|product|kernels|torch|oracle]`` (or
+``__graft_entry__.build()``; ``product``, the two product libraries, is what
+``pip install`` builds) -- as a script, not with ``-m``: importing it through
+the package would run the package's __init__, which needs the libraries this
+builds.  No GPU is needed: hipcc cross-compiles for gfx950.
 """
 import os
 import shutil
@@ -73,21 +74,24 @@ def _atomic(dst, build_fn):
     os.replace(tmp, dst)
 
 
-def build_kernels():
+def build_kernels(bench=True):
     """Compiles every translation unit of csrc/ at once into a scratch
-    directory, then links libhprms.so and libhprms_bench.so.  The two share
-    the variant and general-tier objects; hprms.hip is compiled once per
-    library (HPRMS_BENCH_BUILD adds the bench-only shapes and entry point)."""
+    directory, then links libhprms.so and (with `bench`) libhprms_bench.so.
+    The two share the variant and general-tier objects; hprms.hip is compiled
+    once per library (HPRMS_BENCH_BUILD adds the bench-only shapes and entry
+    point)."""
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    units = [("hprms.hip", []), ("hprms_unaligned.hip", []), ("hprms_tail.hip", []), ("hprms_general.hip", []),
-             ("hprms.hip", ["-DHPRMS_BENCH_BUILD"]), ("hprms_ceiling.hip", [])]
+    units = [("hprms.hip", []), ("hprms_unaligned.hip", []), ("hprms_tail.hip", []), ("hprms_general.hip", [])]
+    if bench:
+        units += [("hprms.hip", ["-DHPRMS_BENCH_BUILD"]), ("hprms_ceiling.hip", [])]
     with tempfile.TemporaryDirectory(prefix="hprms_build_") as tmp:
         objs = [os.path.join(tmp, f"{i}_{name}.o") for i, (name, _) in enumerate(units)]
         _run_parallel([[hipcc, *HIP_FLAGS, *defs, "-c", f"-I{INCLUDE}", f"-I{CSRC}", os.path.join(CSRC, name),
                         "-o", obj] for (name, defs), obj in zip(units, objs)])
-        product, shared, bench = objs[0], objs[1:4], objs[4:]
+        product, shared, bench_objs = objs[0], objs[1:4], objs[4:]
         _atomic(KERNEL_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", product, *shared, "-o", out]))
-        _atomic(BENCH_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", *bench, *shared, "-o", out]))
+        if bench:
+            _atomic(BENCH_LIB, lambda out: _run([hipcc, *HIP_FLAGS, "-shared", *bench_objs, *shared, "-o", out]))
 
 
 def build_torch_binding():
@@ -119,8 +123,14 @@ def build_all():
     build_oracle()
 
 
+def build_product():
+    """libhprms.so and _C.so only: what an installed package holds."""
+    build_kernels(bench=False)
+    build_torch_binding()
+
+
 if __name__ == "__main__":
     what = sys.argv[1:] or ["all"]
     for w in what:
-        {"all": build_all, "kernels": build_kernels, "torch": build_torch_binding,
+        {"all": build_all, "product": build_product, "kernels": build_kernels, "torch": build_torch_binding,
          "oracle": build_oracle}[w]()
