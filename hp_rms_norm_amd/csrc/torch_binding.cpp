@@ -34,8 +34,15 @@ int dtype_code(const at::Tensor& t) {
 
 // Rows and row stride of a [..., hidden] tensor whose leading dims collapse
 // into one (the reference flattens with view({-1, hidden}),
-// hp_rms_norm/csrc/cuda/hp_rms_norm.cu:26).
+// hp_rms_norm/csrc/cuda/hp_rms_norm.cu:26).  Rows of width 0 hold no
+// element (the ops return at once); view cannot infer their count.
 void rows_of(const at::Tensor& t, int64_t hidden, int64_t* rows, int64_t* stride) {
+  if (hidden == 0) {
+    *rows = 1;
+    for (int64_t i = 0; i + 1 < t.dim(); ++i) *rows *= t.size(i);
+    *stride = 0;
+    return;
+  }
   at::Tensor flat = t.view({-1, hidden});
   *rows = flat.size(0);
   *stride = *rows <= 1 ? hidden : flat.stride(0);
@@ -78,7 +85,7 @@ FusedShape check_fused(const at::Tensor& input, const at::Tensor& weight, const 
 
 void rms_norm_hip(at::Tensor& input, const at::Tensor& weight, at::Tensor& residual, double eps) {
   const FusedShape s = check_fused(input, weight, residual);
-  if (s.rows == 0) return;
+  if (s.rows == 0 || s.hidden == 0) return;
   c10::DeviceGuard guard(input.device());
   hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
   check_status(hprms_fused_add_rmsnorm(input.data_ptr(), weight.data_ptr(), residual.data_ptr(), s.rows,
@@ -159,7 +166,7 @@ PlainShape check_plain(const at::Tensor& out, const at::Tensor& input, const at:
 
 void rms_norm_plain_hip(at::Tensor& out, const at::Tensor& input, const at::Tensor& weight, double eps) {
   const PlainShape s = check_plain(out, input, weight);
-  if (s.rows == 0) return;
+  if (s.rows == 0 || s.hidden == 0) return;
   c10::DeviceGuard guard(input.device());
   hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
   check_status(hprms_rmsnorm(out.data_ptr(), input.data_ptr(), weight.data_ptr(), s.rows, s.hidden,
@@ -206,7 +213,7 @@ Fp8Shape check_fp8(const at::Tensor& out, const at::Tensor& scale, const at::Ten
 void rms_norm_fp8_hip(at::Tensor& out, at::Tensor& scale, const at::Tensor& input, const at::Tensor& weight,
                       at::Tensor& residual, double eps) {
   const Fp8Shape s = check_fp8(out, scale, input, weight, residual);
-  if (s.f.rows == 0) return;
+  if (s.f.rows == 0 || s.f.hidden == 0) return;
   c10::DeviceGuard guard(input.device());
   hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
   check_status(hprms_fused_add_rmsnorm_fp8(out.data_ptr(), scale.data_ptr<float>(), input.data_ptr(),
@@ -260,7 +267,7 @@ FusedShape check_fused_out(const at::Tensor& out, const at::Tensor& residual_out
 void rms_norm_out_hip(at::Tensor& out, at::Tensor& residual_out, const at::Tensor& input, const at::Tensor& weight,
                       const at::Tensor& residual, double eps) {
   const FusedShape s = check_fused_out(out, residual_out, input, weight, residual);
-  if (s.rows == 0) return;
+  if (s.rows == 0 || s.hidden == 0) return;
   int64_t r = 0, out_stride = 0, res_out_stride = 0;
   rows_of(out, s.hidden, &r, &out_stride);
   rows_of(residual_out, s.hidden, &r, &res_out_stride);
@@ -332,7 +339,7 @@ ReduceShape check_reduce(const at::Tensor& out, at::TensorList parts, const at::
 void reduce_rms_norm_hip(at::Tensor& out, at::TensorList parts, const at::Tensor& weight, at::Tensor& residual,
                          double eps) {
   const ReduceShape s = check_reduce(out, parts, weight, residual);
-  if (s.rows == 0) return;
+  if (s.rows == 0 || s.hidden == 0) return;
   const void* ptrs[HPRMS_MAX_PARTS];
   for (size_t g = 0; g < parts.size(); ++g) ptrs[g] = parts[g].data_ptr();
   c10::DeviceGuard guard(residual.device());
@@ -393,7 +400,7 @@ MxShape check_mx(const at::Tensor& out, const at::Tensor& scales, const at::Tens
 void rms_norm_mx_hip(at::Tensor& out, at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,
                      at::Tensor& residual, int64_t format, double eps) {
   const MxShape s = check_mx(out, scales, input, weight, residual, format);
-  if (s.f.rows == 0) return;
+  if (s.f.rows == 0 || s.f.hidden == 0) return;
   c10::DeviceGuard guard(input.device());
   hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
   check_status(hprms_fused_add_rmsnorm_mx(out.data_ptr(), scales.data_ptr(), input.data_ptr(), weight.data_ptr(),

@@ -80,6 +80,27 @@ def test_meta_rejects_like_the_reference(args, msg):
         ops.hp_rms_norm(*args, 1e-6)
 
 
+def test_meta_accepts_rows_of_width_zero():
+    """[..., 0] tensors hold no element: every op accepts them (view cannot
+    infer their row count, so the binding counts the leading dims) and a
+    width that does not match the weight is still rejected."""
+    assert ops.hp_rms_norm(t(4, 0), t(0), t(4, 0), 1e-6) is None
+    assert ops.hp_rms_norm(t(2, 3, 0), t(0), t(2, 3, 0), 1e-6) is None
+    assert ops.relu(t(4, 0), t(4, 0)) is None
+    assert ops.rms_norm(t(2, 3, 0), t(2, 3, 0), t(0), 1e-6) is None
+    assert ops.fused_add_rms_norm_out(t(4, 0), t(4, 0), t(4, 0), t(0), t(4, 0), 1e-6) is None
+    assert ops.hp_rms_norm_fp8(t(4, 0, dtype=torch.float8_e4m3fn), t(4, 1, dtype=torch.float32), t(4, 0), t(0),
+                               t(4, 0), 1e-6) is None
+    assert ops.reduce_add_rms_norm(t(4, 0), [t(4, 0), t(4, 0)], t(0), t(4, 0), 1e-6) is None
+    assert ops.hp_rms_norm_mx(t(4, 0, dtype=torch.uint8), t(4, 0, dtype=torch.uint8), t(4, 0), t(0), t(4, 0), 1e-6,
+                              ops.MXFP8) is None
+    with pytest.raises(RuntimeError, match=r"input.size\(-1\) == hidden_dim"):
+        ops.hp_rms_norm(t(4, 8), t(0), t(4, 8), 1e-6)
+    with pytest.raises(RuntimeError, match="scale.numel"):
+        ops.hp_rms_norm_fp8(t(4, 0, dtype=torch.float8_e4m3fn), t(3, 1, dtype=torch.float32), t(4, 0), t(0),
+                            t(4, 0), 1e-6)
+
+
 def test_meta_rejects_rows_that_cannot_be_flattened():
     base = t(4, 8, 256)
     x = base.transpose(0, 1)      # [8, 4, 256]: leading dims do not collapse

@@ -248,6 +248,17 @@ def test_3d_input_and_empty(abi):
     assert_output_close(bits(xd), want_out, torch.bfloat16)
     e = torch.empty(0, 4096, dtype=torch.bfloat16, device=DEV)
     hp_rms_norm_amd.hp_rms_norm(e, w.to(DEV), e.clone(), 1e-6)
+    # rows of width 0: every op returns without a launch
+    z = lambda *s, dt=torch.bfloat16: torch.empty(*s, dtype=dt, device=DEV)  # noqa: E731
+    ops = hp_rms_norm_amd
+    ops.hp_rms_norm(z(4, 0), z(0), z(4, 0), 1e-6)
+    ops.relu(z(2, 3, 0), z(2, 3, 0))
+    ops.rms_norm(z(4, 0), z(4, 0), z(0), 1e-6)
+    ops.fused_add_rms_norm_out(z(4, 0), z(4, 0), z(4, 0), z(0), z(4, 0), 1e-6)
+    ops.hp_rms_norm_fp8(z(4, 0, dt=torch.float8_e4m3fn), z(4, 1, dt=torch.float32), z(4, 0), z(0), z(4, 0), 1e-6)
+    ops.reduce_add_rms_norm(z(4, 0), [z(4, 0)], z(0), z(4, 0), 1e-6)
+    ops.hp_rms_norm_mx(z(4, 0, dt=torch.uint8), z(4, 0, dt=torch.uint8), z(4, 0), z(0), z(4, 0), 1e-6, ops.MXFP4)
+    torch.cuda.synchronize()
 
 
 # ---- size-independent properties at the largest configuration ---------------------------
