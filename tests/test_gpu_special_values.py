@@ -132,3 +132,38 @@ def test_other_forms_special_values(abi, dtype, eps):
                                                        code, threads=8)
         assert_residual_exact(bits(zero), want_res, dtype, "partial-sum residual " + tag)
         assert_output_close(bits(od), want_out, dtype, "partial-sum output " + tag)
+
+
+# eps that swamps the mean square (1, 1e30) or overflows binary32 (1e39, inf):
+# the output goes to zero, NaN where a factor is infinite
+LARGE_EPS = [1.0, 1e30, 1e39, float("inf")]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_large_eps(abi, dtype):
+    """The fused op on the special rows with eps past the mean square, up to
+    infinity, at one shape per kernel kind of the table, the tail variant and
+    the general kernel, and plain RMSNorm at two widths."""
+    code = DT[dtype]
+    for rows, hidden, pad in [c for c in FUSED_CASES if c[1] in (1024, 4096, 16384, 32768, 4097, 70000)]:
+        x, r, w = special_inputs(rows, hidden, dtype, seed=rows + 3 * hidden)
+        for eps in LARGE_EPS:
+            tag = f"large eps {rows}x{hidden}+{pad} {dtype} eps {eps}"
+            print(tag, flush=True)
+            want_out, want_res = oracle_fused(x, r, w, eps, dtype)
+            xd, rd, wd = _on_device(x, pad), _on_device(r, pad), w.to(DEV)
+            abi.fused_add_rmsnorm(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows, hidden, xd.stride(0),
+                                  rd.stride(0), code, eps, _stream())
+            torch.cuda.synchronize()
+            assert_residual_exact(bits(rd), want_res, dtype, "residual " + tag)
+            assert_output_close(bits(xd), want_out, dtype, "output " + tag)
+    for rows, hidden in ((28, 4096), (300, 32768)):
+        x, _, w = special_inputs(rows, hidden, dtype, seed=rows + hidden)
+        xd, wd = x.to(DEV), w.to(DEV)
+        for eps in LARGE_EPS:
+            od = torch.empty_like(xd)
+            abi.rmsnorm(od.data_ptr(), xd.data_ptr(), wd.data_ptr(), rows, hidden, hidden, hidden, code, eps,
+                        _stream())
+            torch.cuda.synchronize()
+            assert_output_close(bits(od), oracle.rmsnorm(bits(x), bits(w), eps, code, threads=8), dtype,
+                                f"plain large eps {rows}x{hidden} {dtype} eps {eps}")

@@ -147,16 +147,18 @@ def pin_special_values(mutation=0):
     """The live torch formula on rows of special values (helpers.SPECIAL_PATTERNS:
     NaN, infinities, zero rows, binary32 overflow of a square and of the sum of
     squares, subnormals), also with a weight of special values
-    (helpers.special_weight), with eps = 0 and 1e-6: the residual bit-exact and the
-    output within 1 ulp, NaN where torch's is NaN (NaN bit patterns are not
-    compared: torch's own differ between its vectorised and scalar paths)."""
+    (helpers.special_weight), with eps = 0 and 1e-6 and with eps that swamps the
+    mean square or overflows binary32 (1, 1e30, 1e39, inf: the output goes to
+    zero, NaN where a factor is infinite): the residual bit-exact and the output
+    within 1 ulp, NaN where torch's is NaN (NaN bit patterns are not compared:
+    torch's own differ between its vectorised and scalar paths)."""
     for code in (BF, HF):
         for hidden, weight in ((300, "plain"), (1024, "plain"), (520, "special")):
             x, r, w = special_inputs(28, hidden, TDT[code], hidden)
             if weight == "special":
                 w = special_weight(w)
             x, r, w = tbits(x), tbits(r), tbits(w)
-            for eps in (0.0, 1e-6):
+            for eps in (0.0, 1e-6, 1.0, 1e30, 1e39, float("inf")):
                 want_out, want_res = torch_formula(x, r, w, eps, code)
                 out, res = oracle.fused_add_rmsnorm(x, w, r, eps, code, mutation=mutation)
                 if oracle.ulp_distance(res, want_res, code).max() != 0:
@@ -278,7 +280,7 @@ def test_oracle_rmsnorm_plain_special_values_match_torch():
     for code in (BF, HF):
         x, r, w = (tbits(t) for t in special_inputs(28, 520, TDT[code], 5))
         s = tbits(tfrom(x, code) + tfrom(r, code))          # the special rows as one input
-        for eps in (0.0, 1e-6):
+        for eps in (0.0, 1e-6, 1e30, float("inf")):
             want = tbits(torch.rms_norm(tfrom(s, code), (520,), weight=tfrom(w, code), eps=eps))
             assert oracle.ulp_distance(oracle.rmsnorm(s, w, eps, code), want, code).max() <= 1, (code, eps)
 
