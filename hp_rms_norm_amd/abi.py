@@ -29,6 +29,7 @@ MX_FP8_E4M3, MX_FP4_E2M1 = 0, 1
 SYMBOLS = (
     "hprms_fused_add_rmsnorm",
     "hprms_fused_add_rmsnorm_fp8",
+    "hprms_fused_add_rmsnorm_fp8_static",
     "hprms_fused_add_rmsnorm_out",
     "hprms_reduce_add_rmsnorm",
     "hprms_fused_add_rmsnorm_mx",
@@ -69,6 +70,7 @@ def _bind(L, bench):
                                                  ctypes.POINTER(Config), vp]
     L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
+    L.hprms_fused_add_rmsnorm_fp8_static.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_out.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_reduce_add_rmsnorm.argtypes = [vp, ctypes.POINTER(vp), ci, vp, vp, i64, i64, i64, i64, i64, ci,
                                            cd, vp]
@@ -84,7 +86,8 @@ def _bind(L, bench):
     L.hprms_last_error.argtypes = []
     L.hprms_abi_version.restype = ci
     names = ["hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
-             "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_out", "hprms_reduce_add_rmsnorm",
+             "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_fp8_static", "hprms_fused_add_rmsnorm_out",
+             "hprms_reduce_add_rmsnorm",
              "hprms_fused_add_rmsnorm_mx", "hprms_streamer", "hprms_select_config", "hprms_select_config_cu",
              "hprms_device_cu_count", "hprms_kernel_configs", "hprms_set_batch_invariant", "hprms_batch_invariant"]
     if bench:
@@ -150,6 +153,12 @@ class Library:
         return self._check(self.lib().hprms_fused_add_rmsnorm_fp8(out_ptr, scale_ptr, input_ptr, weight_ptr,
                                                                   residual_ptr, rows, hidden, out_stride,
                                                                   input_stride, residual_stride, dtype, eps, stream))
+
+    def fused_add_rmsnorm_fp8_static(self, out_ptr, scale_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden,
+                                     out_stride, input_stride, residual_stride, dtype, eps, stream=0):
+        return self._check(self.lib().hprms_fused_add_rmsnorm_fp8_static(
+            out_ptr, scale_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride, input_stride,
+            residual_stride, dtype, eps, stream))
 
     def fused_add_rmsnorm_out(self, out_ptr, residual_out_ptr, input_ptr, residual_ptr, weight_ptr, rows, hidden,
                               out_stride, residual_out_stride, input_stride, residual_stride, dtype, eps, stream=0):
@@ -245,6 +254,7 @@ def last_error():
 
 fused_add_rmsnorm = PRODUCT.fused_add_rmsnorm
 fused_add_rmsnorm_fp8 = PRODUCT.fused_add_rmsnorm_fp8
+fused_add_rmsnorm_fp8_static = PRODUCT.fused_add_rmsnorm_fp8_static
 fused_add_rmsnorm_out = PRODUCT.fused_add_rmsnorm_out
 reduce_add_rmsnorm = PRODUCT.reduce_add_rmsnorm
 fused_add_rmsnorm_mx = PRODUCT.fused_add_rmsnorm_mx

@@ -480,7 +480,8 @@ struct Problem {
   int64_t rows, hidden, x_stride, out_stride, res_stride;
   int dtype;
   double eps;
-  float* scale = nullptr;      // mode 2
+  float* scale = nullptr;      // mode 2: per-row scales, written
+  const float* static_scale = nullptr;  // mode 2: one given scale for every row (then no `scale`)
   void* res_out = nullptr;     // mode 3
   int64_t res_out_stride = 0;  // mode 3
   int nparts = 1;              // mode 4
@@ -545,7 +546,8 @@ int check_problem(const Problem& p) {
       (is_mx(p.mode) && !extent_ok(p.rows, p.mx_scale_stride, 1, p.hidden / 32)))
     return fail(HPRMS_E_RANGE, "%lld rows at these row strides span more than 2^56 bytes", (long long)p.rows);
   if (p.mode == 4 && !p.parts) return fail(HPRMS_E_INVALID, "null parts array");
-  if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) || (p.mode == 2 && !p.scale) ||
+  if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) ||
+      (p.mode == 2 && !p.scale && !p.static_scale) ||
       (p.mode == 3 && !p.res_out) || (is_mx(p.mode) && !p.mx_scales))
     return fail(HPRMS_E_INVALID, "null tensor pointer");
   if (p.mode == 4) {
@@ -846,6 +848,7 @@ int launch_general(const Problem& p, hipStream_t stream) {
   a.eps = (float)p.eps;
   a.q = p.mode == 2 ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
+  a.static_scale = p.static_scale;
   a.q_stride = p.mode == 2 ? p.out_stride : 0;
   const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
   launch_general_kernels(a, p.dtype, p.mode, grid, stream);
@@ -917,6 +920,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   for (int g = 0; g < p.nparts && p.parts; ++g) a.parts[g] = (const uint16_t*)p.parts[g];
   a.q = p.mode == 2 || is_mx(p.mode) ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
+  a.static_scale = p.static_scale;
   a.q_stride = p.mode == 2 || is_mx(p.mode) ? p.out_stride : 0;
   a.mx_scale = (uint8_t*)p.mx_scales;
   a.mx_scale_stride = p.mx_scale_stride;
@@ -986,6 +990,16 @@ int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, cons
                                 int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
   Problem p{2, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
             residual_row_stride, dtype, eps, scale};
+  return run(p, nullptr, stream);
+}
+
+int hprms_fused_add_rmsnorm_fp8_static(void* out, const float* scale, const void* input, const void* weight,
+                                       void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                                       int64_t input_row_stride, int64_t residual_row_stride, int dtype, double eps,
+                                       hipStream_t stream) {
+  Problem p{2, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
+            residual_row_stride, dtype, eps, nullptr};
+  p.static_scale = scale;
   return run(p, nullptr, stream);
 }
 

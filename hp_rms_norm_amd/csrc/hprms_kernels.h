@@ -74,7 +74,9 @@
 // plain RMSNorm (reads `input`, writes `out`, no residual stream); MODE 2 is
 // the fused op with an FP8 output: the 16-bit output y is quantised per row
 // (scale = max(amax|y| / 448, FLT_MIN) to scale[row], q = e4m3fn(clamp(y *
-// (1 / scale))) to q), the residual is updated in place and `input` is only read.
+// (1 / scale))) to q), or, with FusedArgs::static_scale set, with that one
+// given scale for every row (no row maximum, no scale written); the residual
+// is updated in place and `input` is only read.
 // The row maximum is a second DPP/LDS reduction over the 16-bit magnitudes
 // (sign-magnitude bit patterns order like their values, NaN above inf).
 // MODE 3 is the fused op out of place: input and residual are only read, the
@@ -124,6 +126,7 @@ struct FusedArgs {
   int64_t out_stride;
   uint8_t* q;            // MODES 2, 5, 6: quantised output rows
   float* scale;          // MODE 2: per-row scales
+  const float* static_scale;  // MODE 2: one scale for every row, given (null: per-row scales, written)
   int64_t q_stride;      // MODES 2, 5, 6: bytes between quantised rows
   uint16_t* res_out;     // MODE 3: residual output rows
   int64_t res_out_stride;
@@ -762,20 +765,30 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
           }
         }
       }
-      uint32_t mx = group_max_u32<GW>(m2);
-      if constexpr (WPR > 1) {
-        if ((tid & 63) == 0) red[buf][wave] = __builtin_bit_cast(float, mx);
-        __syncthreads();
-        const int w0 = (wave / WPR) * WPR;
+      float isc;
+      const float* const given = opaque(a.static_scale);
+      if (given != nullptr) {
+        // one scale for every row, given by the caller: no row maximum (the
+        // branch is uniform over the workgroup, so no barrier is skipped by
+        // part of it)
+        isc = 1.0f / *given;
+      } else {
+        uint32_t mx = group_max_u32<GW>(m2);
+        if constexpr (WPR > 1) {
+          if ((tid & 63) == 0) red[buf][wave] = __builtin_bit_cast(float, mx);
+          __syncthreads();
+          const int w0 = (wave / WPR) * WPR;
 #pragma unroll
-        for (int j = 0; j < WPR; ++j) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w0 + j]));
-        buf ^= 1;
+          for (int j = 0; j < WPR; ++j)
+            mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w0 + j]));
+          buf ^= 1;
+        }
+        const float amax = F::one((uint16_t)mx);
+        float sc = amax / 448.0f;
+        if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+        isc = 1.0f / sc;
+        if (row_ok && lane == 0) opaque(a.scale)[row0 + rib] = sc;
       }
-      const float amax = F::one((uint16_t)mx);
-      float sc = amax / 448.0f;
-      if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
-      const float isc = 1.0f / sc;
-      if (row_ok && lane == 0) opaque(a.scale)[row0 + rib] = sc;
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         u32x2 q;
@@ -834,6 +847,7 @@ struct GeneralArgs {
   float eps;
   uint8_t* q;        // MODE 2
   float* scale;      // MODE 2
+  const float* static_scale;  // MODE 2: as FusedArgs::static_scale
   int64_t q_stride;  // MODE 2
   uint16_t* res_out;  // MODE 3
   int64_t res_out_stride;
@@ -889,18 +903,23 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
     } else {
       // y is recomputed in each pass from the residual this thread wrote, so
       // both passes see the same bits
-      uint32_t m = 0;
-      for (int64_t j = tid; j < a.hidden; j += 256)
-        m = __builtin_elementwise_max(m, (uint32_t)(F::pack1((F::one(rs[j]) * inv) * F::one(a.w[j])) & 0x7fffu));
-      uint32_t mx = group_max_u32<64>(m);
-      if ((tid & 63) == 0) red[buf][tid >> 6] = __builtin_bit_cast(float, mx);
-      __syncthreads();
-      for (int j = 0; j < 4; ++j) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][j]));
-      buf ^= 1;
-      float sc = F::one((uint16_t)mx) / 448.0f;
-      if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
-      const float isc = 1.0f / sc;
-      if (tid == 0) a.scale[row] = sc;
+      float isc;
+      if (a.static_scale != nullptr) {
+        isc = 1.0f / *a.static_scale;   // one given scale for every row (uniform branch)
+      } else {
+        uint32_t m = 0;
+        for (int64_t j = tid; j < a.hidden; j += 256)
+          m = __builtin_elementwise_max(m, (uint32_t)(F::pack1((F::one(rs[j]) * inv) * F::one(a.w[j])) & 0x7fffu));
+        uint32_t mx = group_max_u32<64>(m);
+        if ((tid & 63) == 0) red[buf][tid >> 6] = __builtin_bit_cast(float, mx);
+        __syncthreads();
+        for (int j = 0; j < 4; ++j) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][j]));
+        buf ^= 1;
+        float sc = F::one((uint16_t)mx) / 448.0f;
+        if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+        isc = 1.0f / sc;
+        if (tid == 0) a.scale[row] = sc;
+      }
       uint8_t* qr = a.q + row * a.q_stride;
       for (int64_t j = tid; j < a.hidden; j += 256) {
         const float y = F::one(F::pack1((F::one(rs[j]) * inv) * F::one(a.w[j])));
@@ -999,16 +1018,21 @@ __global__ __launch_bounds__(BLOCK) void fused_general_reg_kernel(GeneralArgs a)
         xv[k] = F::pack1((sv[k] * inv) * F::one((uint16_t)rv[k]));  // the 16-bit output (0 past the row)
         m = __builtin_elementwise_max(m, xv[k] & 0x7fffu);
       }
-      uint32_t mx = group_max_u32<64>(m);
-      buf ^= 1;
-      if ((tid & 63) == 0) red[buf][wave] = __builtin_bit_cast(float, mx);
-      __syncthreads();
+      float isc;
+      if (a.static_scale != nullptr) {
+        isc = 1.0f / *a.static_scale;   // one given scale for every row (uniform branch)
+      } else {
+        uint32_t mx = group_max_u32<64>(m);
+        buf ^= 1;
+        if ((tid & 63) == 0) red[buf][wave] = __builtin_bit_cast(float, mx);
+        __syncthreads();
 #pragma unroll
-      for (int w = 0; w < NW; ++w) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w]));
-      float sc = F::one((uint16_t)mx) / 448.0f;
-      if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
-      const float isc = 1.0f / sc;
-      if (tid == 0) a.scale[row] = sc;
+        for (int w = 0; w < NW; ++w) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w]));
+        float sc = F::one((uint16_t)mx) / 448.0f;
+        if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+        isc = 1.0f / sc;
+        if (tid == 0) a.scale[row] = sc;
+      }
       const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q + row * a.q_stride, (uint32_t)a.hidden);
 #pragma unroll
       for (int k = 0; k < E; ++k)

@@ -227,6 +227,49 @@ void rms_norm_fp8_meta(at::Tensor& out, at::Tensor& scale, const at::Tensor& inp
   (void)eps;
 }
 
+// ---- FP8 output with one given scale ---------------------------------------------------
+Fp8Shape check_fp8_static(const at::Tensor& out, const at::Tensor& scale, const at::Tensor& input,
+                          const at::Tensor& weight, const at::Tensor& residual) {
+  Fp8Shape s;
+  s.f = check_fused(input, weight, residual);
+  TORCH_CHECK(out.scalar_type() == at::kFloat8_e4m3fn, "out.dtype() == float8_e4m3fn");
+  TORCH_CHECK(scale.scalar_type() == at::kFloat, "scale.dtype() == float32");
+  TORCH_CHECK(scale.numel() == 1, "scale must hold one element (one scale for every row)");
+  TORCH_CHECK(out.dim() == input.dim(), "out.dim() == input.dim()");
+  for (int64_t i = 0; i < input.dim(); ++i) TORCH_CHECK(out.size(i) == input.size(i), "out.size(i) == input.size(i)");
+  TORCH_CHECK(out.stride(-1) == 1, "out.stride(-1) == 1");
+  TORCH_CHECK(out.device() == input.device() && scale.device() == input.device(),
+              "out, scale and input must be on the same device");
+  int64_t orows = 0;
+  rows_of(out, s.f.hidden, &orows, &s.out_stride);
+  if (s.f.rows > 0) {
+    // the FP8 rows are written while input, residual and the scale are read
+    at::assert_no_overlap(out, residual);
+    at::assert_no_overlap(out, input);
+    at::assert_no_overlap(out, scale);
+    at::assert_no_overlap(residual, scale);
+  }
+  return s;
+}
+
+void rms_norm_fp8_static_hip(at::Tensor& out, const at::Tensor& scale, const at::Tensor& input,
+                             const at::Tensor& weight, at::Tensor& residual, double eps) {
+  const Fp8Shape s = check_fp8_static(out, scale, input, weight, residual);
+  if (s.f.rows == 0 || s.f.hidden == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm_fp8_static(out.data_ptr(), scale.data_ptr<float>(), input.data_ptr(),
+                                                  weight.data_ptr(), residual.data_ptr(), s.f.rows, s.f.hidden,
+                                                  s.out_stride, s.f.in_stride, s.f.res_stride, s.f.dtype, eps,
+                                                  stream));
+}
+
+void rms_norm_fp8_static_meta(at::Tensor& out, const at::Tensor& scale, const at::Tensor& input,
+                              const at::Tensor& weight, at::Tensor& residual, double eps) {
+  (void)check_fp8_static(out, scale, input, weight, residual);
+  (void)eps;
+}
+
 // ---- fused op out of place ----------------------------------------------------------
 FusedShape check_fused_out(const at::Tensor& out, const at::Tensor& residual_out, const at::Tensor& input,
                            const at::Tensor& weight, const at::Tensor& residual) {
@@ -459,6 +502,8 @@ TORCH_LIBRARY(hp_rms_norm, m) {
   m.def("rms_norm_plain(Tensor(a!) out, Tensor input, Tensor weight, float eps) -> ()");
   m.def("rms_norm_fp8_quant(Tensor(a!) out, Tensor(b!) scale, Tensor input, Tensor weight, Tensor(c!) residual, "
         "float eps) -> ()");
+  m.def("rms_norm_fp8_static_quant(Tensor(a!) out, Tensor scale, Tensor input, Tensor weight, Tensor(b!) residual, "
+        "float eps) -> ()");
   m.def("rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, Tensor residual, "
         "float eps) -> ()");
   m.def("reduce_add_rms_norm(Tensor(a!) out, Tensor[] parts, Tensor weight, Tensor(b!) residual, float eps) -> ()");
@@ -473,6 +518,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
   m.impl("relu_max0", &relu_max0_hip);
   m.impl("rms_norm_plain", &rms_norm_plain_hip);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_hip);
+  m.impl("rms_norm_fp8_static_quant", &rms_norm_fp8_static_hip);
   m.impl("rms_norm_out", &rms_norm_out_hip);
   m.impl("reduce_add_rms_norm", &reduce_rms_norm_hip);
   m.impl("rms_norm_mx_quant", &rms_norm_mx_hip);
@@ -486,6 +532,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
   m.impl("relu_max0", &stream_meta);
   m.impl("rms_norm_plain", &rms_norm_plain_meta);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_meta);
+  m.impl("rms_norm_fp8_static_quant", &rms_norm_fp8_static_meta);
   m.impl("rms_norm_out", &rms_norm_out_meta);
   m.impl("reduce_add_rms_norm", &reduce_rms_norm_meta);
   m.impl("rms_norm_mx_quant", &rms_norm_mx_meta);

@@ -4,7 +4,8 @@ argument order, in-place semantics and ``None`` return."""
 import torch
 
 __all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "fused_add_rms_norm_out",
-           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "reduce_add_rms_norm", "hp_rms_norm_mx",
+           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "hp_rms_norm_fp8_static", "fused_add_rms_norm_fp8_static",
+           "reduce_add_rms_norm", "hp_rms_norm_mx",
            "fused_add_rms_norm_mxfp8", "fused_add_rms_norm_mxfp4", "MXFP8", "MXFP4",
            "set_batch_invariant", "batch_invariant"]
 
@@ -76,6 +77,24 @@ def fused_add_rms_norm_fp8(input, residual, weight, eps):
     scale = torch.empty(input.shape[:-1] + (1,), dtype=torch.float32, device=input.device)
     torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(q, scale, input, weight, residual, eps)
     return q, scale
+
+
+def hp_rms_norm_fp8_static(output, scale, input, weight, residual, eps):
+    """Fused residual-add + RMSNorm with an FP8 output and one given scale for
+    every row (static per-tensor quantisation): ``residual <- input +
+    residual`` in place; with ``y`` the op's 16-bit output, ``output =
+    float8_e4m3fn(clamp(y * (1 / scale), -448, 448))``.  ``scale``: a float32
+    tensor of one element on the device, only read; ``input`` is only read.
+    No reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_fp8_static_quant.default(output, scale, input, weight, residual, eps)
+
+
+def fused_add_rms_norm_fp8_static(input, residual, weight, scale, eps):
+    """Allocating form of ``hp_rms_norm_fp8_static``: returns ``q``
+    (float8_e4m3fn shaped like ``input``); ``residual`` is updated in place."""
+    q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
+    torch.ops.hp_rms_norm.rms_norm_fp8_static_quant.default(q, scale, input, weight, residual, eps)
+    return q
 
 
 def reduce_add_rms_norm(out, parts, weight, residual, eps):

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 6
+#define HPRMS_ABI_VERSION 7
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -119,6 +119,21 @@ int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, cons
                                 void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
                                 int64_t input_row_stride, int64_t residual_row_stride,
                                 int dtype, double eps, hipStream_t stream);
+
+/*
+ * The same with one scale for every row, given by the caller (static
+ * per-tensor quantisation, the scale calibrated offline for the FP8 GEMM that
+ * follows):
+ *   out[r, :] = e4m3fn(clamp(y * (1 / scale[0]), -448, 448))
+ * `scale` points to one float32 on the device and is only read (a scale of 0
+ * gives +-448 and NaN for y = 0; a NaN scale gives NaN).  No row maximum is
+ * taken and no scale is written.  No counterpart in the reference.
+ */
+int hprms_fused_add_rmsnorm_fp8_static(void* out, const float* scale, const void* input,
+                                       const void* weight, void* residual, int64_t rows,
+                                       int64_t hidden, int64_t out_row_stride,
+                                       int64_t input_row_stride, int64_t residual_row_stride,
+                                       int dtype, double eps, hipStream_t stream);
 
 /*
  * Fused residual-add + RMSNorm out of place: the arithmetic of

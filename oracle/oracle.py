@@ -221,6 +221,21 @@ def fused_add_rmsnorm_fp8(x, w, r, eps, dtype, threads=1):
     return q, sc, ro
 
 
+def fused_add_rmsnorm_fp8_static(x, w, r, eps, dtype, scale, threads=1):
+    """FP8 form with one given scale for every row (static per-tensor
+    quantisation): returns (q uint8 [rows, hidden] of e4m3fn bits, new
+    residual), q = e4m3fn(clamp(y * (1 / scale), -448, 448)) with y the fused
+    op's 16-bit output (fused_add_rmsnorm) and 1 / scale rounded to binary32,
+    the dynamic form's quantisation step (hprms_oracle_fused_add_rmsnorm_fp8)
+    with the scale given instead of taken from the row maximum."""
+    y, res = fused_add_rmsnorm(x, w, r, eps, dtype, threads=threads)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        isc = np.float32(1.0) / np.float32(scale)
+        v = to_f32(y, dtype) * isc
+        v = np.where(v > 448.0, np.float32(448.0), np.where(v < -448.0, np.float32(-448.0), v)).astype(np.float32)
+    return e4m3_from_f32(v), res
+
+
 def e4m3_from_f32(a):
     a = np.ascontiguousarray(a, dtype=np.float32)
     out = np.empty(a.shape, dtype=np.uint8)

@@ -435,6 +435,23 @@ def test_fp8_entry_rejects_bad_arguments():
     assert call(r=0x1000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
 
 
+def test_fp8_static_entry_rejects_bad_arguments():
+    L = abi.lib()
+    ok = dict(out=0x4000, scale=0x5000, x=0x1000, w=0x2000, r=0x3000, so=4096)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.hprms_fused_add_rmsnorm_fp8_static(a["out"], a["scale"], a["x"], a["w"], a["r"], 4, 4096, a["so"],
+                                                    4096, 4096, 0, 1e-6, None)
+    assert call(scale=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
+    assert call(out=0) == abi.HPRMS_E_INVALID
+    assert call(so=100) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
+    assert call(r=0x1000) == abi.HPRMS_E_INVALID and "alias" in abi.last_error()
+    # no rows: validated, nothing launched, null pointers allowed
+    assert L.hprms_fused_add_rmsnorm_fp8_static(0, 0, 0, 0, 0, 0, 4096, 4096, 4096, 4096, 0, 1e-6,
+                                                None) == abi.HPRMS_OK
+
+
 def test_out_of_place_entry_rejects_bad_arguments():
     L = abi.lib()
     ok = dict(out=0x4000, ro=0x5000, x=0x1000, r=0x3000, w=0x2000, so=4096, sro=4096)

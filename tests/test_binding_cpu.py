@@ -162,6 +162,26 @@ def test_fp8_op_schema_and_meta_checks():
         ops.hp_rms_norm_fp8(q, sc, x, t(128), r, 1e-6)
 
 
+def test_fp8_static_op_schema_and_meta_checks():
+    s = str(torch.ops.hp_rms_norm.rms_norm_fp8_static_quant.default._schema)
+    assert s == ("hp_rms_norm::rms_norm_fp8_static_quant(Tensor(a!) out, Tensor scale, Tensor input, Tensor weight, "
+                 "Tensor(b!) residual, float eps) -> ()")
+    x, w, r = t(4, 256), t(256), t(4, 256)
+    q = t(4, 256, dtype=torch.float8_e4m3fn)
+    sc = torch.empty(1, device=M)
+    assert ops.hp_rms_norm_fp8_static(q, sc, x, w, r, 1e-6) is None
+    assert ops.hp_rms_norm_fp8_static(q, torch.empty((), device=M), x, w, r, 1e-6) is None
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        ops.hp_rms_norm_fp8_static(t(4, 256), sc, x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="float32"):
+        ops.hp_rms_norm_fp8_static(q, torch.empty(1, device=M, dtype=torch.float16), x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="one element"):
+        ops.hp_rms_norm_fp8_static(q, torch.empty(4, device=M), x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match=r"input.size\(-1\) == hidden_dim"):
+        ops.hp_rms_norm_fp8_static(q, sc, x, t(128), r, 1e-6)
+    assert ops.fused_add_rms_norm_fp8_static(x, r, w, sc, 1e-6).dtype == torch.float8_e4m3fn
+
+
 def test_out_of_place_and_reduce_schemas():
     s = str(torch.ops.hp_rms_norm.rms_norm_out.default._schema)
     assert s == ("hp_rms_norm::rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, "

@@ -344,6 +344,56 @@ def test_oracle_fp8_quantisation_stage_matches_torch():
         assert oracle.e4m3_ulp_distance(q, tq).max() == 0
 
 
+STATIC_SCALES = [0.01, 1.0, 3.0, 7e-4, 2.0 ** -140, 1e30, 0.0, float("inf"), float("nan")]
+
+
+def torch_quantise_static(y, code, scale):
+    """torch's static per-tensor quantisation of 16-bit outputs y:
+    e4m3fn(clamp(y * reciprocal(scale), -448, 448)) in binary32 on the CPU."""
+    yf = tfrom(y, code).float()
+    q = (yf * torch.reciprocal(torch.tensor(scale, dtype=torch.float32))).clamp(-448.0, 448.0)
+    return q.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_oracle_fp8_static_quantisation_matches_torch():
+    """The static form: the residual is the fused oracle's, and q equals torch's
+    quantisation of the oracle's own 16-bit output with the given scale, bit for
+    bit (NaN where torch's is NaN), on ordinary and special rows and for scales
+    that are ordinary, subnormal, huge, zero, infinite and NaN."""
+    for code in (BF, HF):
+        for i, (rows, hidden, kind) in enumerate([(64, 4096, "bench"), (16, 1000, "reference_test"),
+                                                  (28, 520, "special")]):
+            if kind == "special":
+                x, r, w = (tbits(t) for t in special_inputs(rows, hidden, TDT[code], 11 + i))
+            else:
+                x, r, w = seeded(rows, hidden, code, 500 + i, kind)
+            y, res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, code)
+            for scale in STATIC_SCALES:
+                q, res8 = oracle.fused_add_rmsnorm_fp8_static(x, w, r, 1e-6, code, scale)
+                assert np.array_equal(res8, res), (code, kind, scale)
+                d = oracle.e4m3_ulp_distance(q, torch_quantise_static(y, code, scale))
+                assert d.max() == 0, (code, kind, scale)
+
+
+def test_planted_fp8_static_mistakes_are_rejected():
+    """Two plausible mistakes in the static step, planted in a copy of the
+    oracle's composition, each fail the torch pin above: the reciprocal of the
+    scale rounded to the tensor's 16-bit type, and the clamp to +-448 left out
+    (the e4m3fn cast then gives NaN past 464)."""
+    x, r, w = seeded(64, 4096, BF, 500, "bench")
+    y, _ = oracle.fused_add_rmsnorm(x, w, r, 1e-6, BF)
+    yf = oracle.to_f32(y, BF)
+    for scale in (3.0, 7e-4):
+        want = torch_quantise_static(y, BF, scale)
+        isc = np.float32(1.0) / np.float32(scale)
+        isc16 = oracle.to_f32(oracle.from_f32(np.array([isc], np.float32), BF), BF)[0]
+        rounded = oracle.e4m3_from_f32(np.clip(yf * isc16, -448, 448).astype(np.float32))
+        unclamped = oracle.e4m3_from_f32((yf * isc).astype(np.float32))
+        assert oracle.e4m3_ulp_distance(rounded, want).max() > 0, scale
+        if scale == 7e-4:    # outputs past 448 only with the small scale
+            assert oracle.e4m3_ulp_distance(unclamped, want).max() > 0
+
+
 def test_oracle_fp8_matches_golden(golden):
     for name, c in golden.items():
         if c["kind"] != "fp8":
