@@ -22,7 +22,7 @@ DTYPE_BF16, DTYPE_FP16 = 0, 1
 STREAM_COPY, STREAM_RELU = 0, 1
 MAX_PARTS = 8
 # the `mode` numbering of hprms_select_config / hprms_kernel_configs
-MODE_FUSED, MODE_PLAIN, MODE_FP8, MODE_OUT, MODE_REDUCE, MODE_MXFP8, MODE_MXFP4 = 0, 1, 2, 3, 4, 5, 6
+MODE_FUSED, MODE_PLAIN, MODE_FP8, MODE_OUT, MODE_REDUCE, MODE_MXFP8, MODE_MXFP4, MODE_FP8_GROUP = 0, 1, 2, 3, 4, 5, 6, 7
 MX_FP8_E4M3, MX_FP4_E2M1 = 0, 1
 
 # every symbol the header declares
@@ -30,6 +30,7 @@ SYMBOLS = (
     "hprms_fused_add_rmsnorm",
     "hprms_fused_add_rmsnorm_fp8",
     "hprms_fused_add_rmsnorm_fp8_static",
+    "hprms_fused_add_rmsnorm_fp8_group",
     "hprms_fused_add_rmsnorm_out",
     "hprms_reduce_add_rmsnorm",
     "hprms_fused_add_rmsnorm_mx",
@@ -71,6 +72,7 @@ def _bind(L, bench):
     L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8_static.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
+    L.hprms_fused_add_rmsnorm_fp8_group.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_out.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_reduce_add_rmsnorm.argtypes = [vp, ctypes.POINTER(vp), ci, vp, vp, i64, i64, i64, i64, i64, ci,
                                            cd, vp]
@@ -86,7 +88,8 @@ def _bind(L, bench):
     L.hprms_last_error.argtypes = []
     L.hprms_abi_version.restype = ci
     names = ["hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
-             "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_fp8_static", "hprms_fused_add_rmsnorm_out",
+             "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_fp8_static", "hprms_fused_add_rmsnorm_fp8_group",
+             "hprms_fused_add_rmsnorm_out",
              "hprms_reduce_add_rmsnorm",
              "hprms_fused_add_rmsnorm_mx", "hprms_streamer", "hprms_select_config", "hprms_select_config_cu",
              "hprms_device_cu_count", "hprms_kernel_configs", "hprms_set_batch_invariant", "hprms_batch_invariant"]
@@ -159,6 +162,12 @@ class Library:
         return self._check(self.lib().hprms_fused_add_rmsnorm_fp8_static(
             out_ptr, scale_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride, input_stride,
             residual_stride, dtype, eps, stream))
+
+    def fused_add_rmsnorm_fp8_group(self, out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden,
+                                    out_stride, scale_stride, input_stride, residual_stride, dtype, eps, stream=0):
+        return self._check(self.lib().hprms_fused_add_rmsnorm_fp8_group(
+            out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride, scale_stride,
+            input_stride, residual_stride, dtype, eps, stream))
 
     def fused_add_rmsnorm_out(self, out_ptr, residual_out_ptr, input_ptr, residual_ptr, weight_ptr, rows, hidden,
                               out_stride, residual_out_stride, input_stride, residual_stride, dtype, eps, stream=0):
@@ -255,6 +264,7 @@ def last_error():
 fused_add_rmsnorm = PRODUCT.fused_add_rmsnorm
 fused_add_rmsnorm_fp8 = PRODUCT.fused_add_rmsnorm_fp8
 fused_add_rmsnorm_fp8_static = PRODUCT.fused_add_rmsnorm_fp8_static
+fused_add_rmsnorm_fp8_group = PRODUCT.fused_add_rmsnorm_fp8_group
 fused_add_rmsnorm_out = PRODUCT.fused_add_rmsnorm_out
 reduce_add_rmsnorm = PRODUCT.reduce_add_rmsnorm
 fused_add_rmsnorm_mx = PRODUCT.fused_add_rmsnorm_mx

@@ -198,7 +198,7 @@ bool latency_config(int64_t rows, int64_t nvec, int mode, hprms_config* c) {
                                          {1024, 256, 768, 256, 256},
                                          {1024, 768, 768, 256, 256},
                                          {256, 256, 256, 256, 256}};
-  const int cls = mode == 0 ? 0 : mode == 1 ? 1 : (mode == 2 || mode == 5 || mode == 6) ? 2 : 3;
+  const int cls = mode == 0 ? 0 : mode == 1 ? 1 : (mode == 2 || mode >= 5) ? 2 : 3;
   for (int i = 0; i < 5; ++i) {
     const Row& r = lat[i];
     if (nvec <= r.max_nvec) {
@@ -398,7 +398,7 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, int cus, hp
   if (mode == 1 && plain_config(nvec, c)) return;
   if (mode == 4 && reduce_config(nvec, c)) return;
   if (mode == 2 && fp8_config(nvec, c)) return;
-  if ((mode == 5 || mode == 6) && mx_config(nvec, c)) return;
+  if (mode >= 5 && mx_config(nvec, c)) return;   // MX and the FP8 output with a scale per 128 elements
   *c = hprms_config{1, 0, 0, 0, 0, 0, 3};
   // flags: 3 = non-temporal row loads and stores, +4 = weight loaded late,
   // +24 = sc1 on loads and stores, +128 = residual loads before input loads
@@ -472,7 +472,8 @@ constexpr int64_t kMaxHidden = int64_t(1) << 24;
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
 struct Problem {
-  int mode;  // 0 fused, 1 plain, 2 fused with FP8 output, 3 fused out of place, 4 parts reduced first
+  int mode;  // 0 fused, 1 plain, 2 fused with FP8 output, 3 fused out of place, 4 parts reduced first,
+             // 5 / 6 MX output, 7 FP8 output with a scale per 128 elements
   void* x;    // mode 4: parts[0]
   void* out;  // modes 1, 3, 4: 16-bit output; mode 2: FP8 output
   void* res;
@@ -486,12 +487,16 @@ struct Problem {
   int64_t res_out_stride = 0;  // mode 3
   int nparts = 1;              // mode 4
   const void* const* parts = nullptr;
-  void* mx_scales = nullptr;   // modes 5, 6: E8M0 bytes
+  void* mx_scales = nullptr;   // modes 5, 6: E8M0 bytes; mode 7: float32
   int64_t mx_scale_stride = 0; // bytes
   int64_t* timeline = nullptr; // configurations with flags bit 9 (bench library)
 };
 
 bool is_mx(int mode) { return mode == 5 || mode == 6; }
+// outputs with per-block scales: the MX modes (one E8M0 byte per 32 elements)
+// and mode 7 (one float32 per 128 elements); either way hidden / 32 scale
+// bytes per row
+bool is_blockq(int mode) { return is_mx(mode) || mode == 7; }
 // bytes of quantised output per row (modes 2, 5, 6)
 int64_t q_row_bytes(int mode, int64_t hidden) { return mode == 6 ? hidden / 2 : hidden; }
 
@@ -525,12 +530,18 @@ int check_problem(const Problem& p) {
                 (long long)p.hidden);
   if (is_mx(p.mode) && p.hidden % 32 != 0)
     return fail(HPRMS_E_INVALID, "MX output needs hidden %% 32 == 0 (got %lld)", (long long)p.hidden);
+  if (p.mode == 7 && p.hidden % 128 != 0)
+    return fail(HPRMS_E_INVALID, "FP8 output with a scale per 128 elements needs hidden %% 128 == 0 (got %lld)",
+                (long long)p.hidden);
   if (has_out(p.mode) && p.out_stride < q_row_bytes(p.mode, p.hidden))
     return fail(HPRMS_E_INVALID, "output row stride %lld < %lld", (long long)p.out_stride,
                 (long long)q_row_bytes(p.mode, p.hidden));
   if (is_mx(p.mode) && p.mx_scale_stride < p.hidden / 32)
     return fail(HPRMS_E_INVALID, "scale row stride %lld < hidden / 32 = %lld", (long long)p.mx_scale_stride,
                 (long long)(p.hidden / 32));
+  if (p.mode == 7 && p.mx_scale_stride < p.hidden / 32)   // bytes: 4 per 128 elements
+    return fail(HPRMS_E_INVALID, "scale row stride %lld < hidden / 128 = %lld", (long long)(p.mx_scale_stride / 4),
+                (long long)(p.hidden / 128));
   if (p.mode == 3 && p.res_out_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "residual output row stride %lld < hidden %lld", (long long)p.res_out_stride,
                 (long long)p.hidden);
@@ -538,18 +549,20 @@ int check_problem(const Problem& p) {
     return fail(HPRMS_E_INVALID, "nparts must be in [1, %d] (got %d)", HPRMS_MAX_PARTS, p.nparts);
   if (!(p.eps >= 0.0)) return fail(HPRMS_E_INVALID, "eps must be >= 0");
   if (p.rows == 0) return HPRMS_OK;
-  const int64_t ob = (p.mode == 2 || is_mx(p.mode)) ? 1 : 2;  // bytes per output element
+  const int64_t ob = (p.mode == 2 || is_blockq(p.mode)) ? 1 : 2;  // bytes per output element
   if (!extent_ok(p.rows, p.x_stride, 2, p.hidden) ||
       (has_res(p.mode) && !extent_ok(p.rows, p.res_stride, 2, p.hidden)) ||
       (has_out(p.mode) && !extent_ok(p.rows, p.out_stride, ob, q_row_bytes(p.mode, p.hidden))) ||
       (p.mode == 3 && !extent_ok(p.rows, p.res_out_stride, 2, p.hidden)) ||
-      (is_mx(p.mode) && !extent_ok(p.rows, p.mx_scale_stride, 1, p.hidden / 32)))
+      (is_blockq(p.mode) && !extent_ok(p.rows, p.mx_scale_stride, 1, p.hidden / 32)))
     return fail(HPRMS_E_RANGE, "%lld rows at these row strides span more than 2^56 bytes", (long long)p.rows);
   if (p.mode == 4 && !p.parts) return fail(HPRMS_E_INVALID, "null parts array");
   if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) ||
       (p.mode == 2 && !p.scale && !p.static_scale) ||
-      (p.mode == 3 && !p.res_out) || (is_mx(p.mode) && !p.mx_scales))
+      (p.mode == 3 && !p.res_out) || (is_blockq(p.mode) && !p.mx_scales))
     return fail(HPRMS_E_INVALID, "null tensor pointer");
+  if (p.mode == 7 && ((uintptr_t)p.mx_scales & 3u) != 0)
+    return fail(HPRMS_E_INVALID, "the float32 scales must be 4-byte aligned");
   if (p.mode == 4) {
     for (int g = 0; g < p.nparts; ++g) {
       if (!p.parts[g]) return fail(HPRMS_E_INVALID, "null tensor pointer (part %d)", g);
@@ -591,7 +604,7 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
     if (!aligned16(p.x) || !aligned16(p.w)) return false;
     if (p.x_stride % 8 != 0) return false;
     if (has_res(p.mode) && (!aligned16(p.res) || p.res_stride % 8 != 0)) return false;
-    if (p.mode == 2 || p.mode == 5) {
+    if (p.mode == 2 || p.mode == 5 || p.mode == 7) {
       if (((uintptr_t)p.out & 7u) != 0 || p.out_stride % 8 != 0) return false;
     } else if (p.mode == 6) {
       if (((uintptr_t)p.out & 3u) != 0 || p.out_stride % 4 != 0) return false;
@@ -613,7 +626,9 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   if (has_res(p.mode) && p.res_stride > smax) smax = p.res_stride;
   if (p.mode == 3 && p.res_out_stride > smax) smax = p.res_out_stride;
   // the MX scale rows have their own buffer resource (byte stride)
-  if (is_mx(p.mode) && (rpb - 1) * p.mx_scale_stride + p.hidden / 32 >= (int64_t)kOOB) return false;
+  if (is_blockq(p.mode) && (rpb - 1) * p.mx_scale_stride + p.hidden / 32 >= (int64_t)kOOB) return false;
+  // a 128-element group of mode 7 is 16 adjacent lanes' vectors
+  if (p.mode == 7 && c.lanes_per_row % 16 != 0) return false;
   if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
     return false;
   return true;
@@ -627,7 +642,7 @@ bool needs_unaligned(const Problem& p) {
   if (!rows_aligned128(p.x, p.x_stride * 2)) return true;
   if (has_res(p.mode) && !rows_aligned128(p.res, p.res_stride * 2)) return true;
   if (has_out(p.mode)) {
-    const bool bytes = p.mode == 2 || is_mx(p.mode);  // quantised rows: byte strides
+    const bool bytes = p.mode == 2 || is_blockq(p.mode);  // quantised rows: byte strides
     if (!rows_aligned128(p.out, bytes ? p.out_stride : p.out_stride * 2)) return true;
   }
   if (p.mode == 3 && !rows_aligned128(p.res_out, p.res_out_stride * 2)) return true;
@@ -879,11 +894,11 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   }
   if ((c.flags & 512) && !p.timeline)
     return fail(HPRMS_E_INVALID, "flags bit 9 (timeline) needs hprms_bench_fused_timeline and its buffer");
-  if (is_mx(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
+  if (is_blockq(p.mode) && (c.tier == 3 || !vec_fits(p, c)))
     return fail(HPRMS_E_INVALID,
-                "MX output needs 2-byte aligned input, residual and weight, input and residual row "
+                "%s output needs 2-byte aligned input, residual and weight, input and residual row "
                 "strides below 2^31 elements and a row group's rows (strides times rows per "
-                "workgroup) within 2 GiB");
+                "workgroup) within 2 GiB", is_mx(p.mode) ? "MX" : "group-scaled FP8");
   if (c.tier != 3 && !vec_fits(p, c)) {
     if (forced && forced->tier != 0)
       return fail(HPRMS_E_INVALID,
@@ -913,18 +928,18 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   const int64_t rpb = c.block_threads / c.lanes_per_row;
   FusedArgs a = {};
   const int64_t ngroups = (p.rows + rpb - 1) / rpb;
-  a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x : p.out);
+  a.out = (uint16_t*)(p.mode == 0 || p.mode == 2 || is_blockq(p.mode) ? p.x : p.out);
   a.res_out = (uint16_t*)p.res_out;
   a.res_out_stride = p.res_out_stride;
   a.nparts = p.nparts;
   for (int g = 0; g < p.nparts && p.parts; ++g) a.parts[g] = (const uint16_t*)p.parts[g];
-  a.q = p.mode == 2 || is_mx(p.mode) ? (uint8_t*)p.out : nullptr;
+  a.q = p.mode == 2 || is_blockq(p.mode) ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
   a.static_scale = p.static_scale;
-  a.q_stride = p.mode == 2 || is_mx(p.mode) ? p.out_stride : 0;
+  a.q_stride = p.mode == 2 || is_blockq(p.mode) ? p.out_stride : 0;
   a.mx_scale = (uint8_t*)p.mx_scales;
   a.mx_scale_stride = p.mx_scale_stride;
-  a.out_stride = p.mode == 0 || p.mode == 2 || is_mx(p.mode) ? p.x_stride : p.out_stride;
+  a.out_stride = p.mode == 0 || p.mode == 2 || is_blockq(p.mode) ? p.x_stride : p.out_stride;
   const Phase shift = (c.flags & 64) ? shift_phase(p) : Phase{0, 0};
   const Phase rot = (c.flags & 32) ? rot_phase(p) : Phase{0, 0};
   const uint32_t phases = pack_phases(rot.base, rot.step, shift.base, shift.step);
@@ -1047,6 +1062,20 @@ int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const
   return run(p, nullptr, stream);
 }
 
+int hprms_fused_add_rmsnorm_fp8_group(void* out, float* scales, const void* input, const void* weight,
+                                      void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
+                                      int64_t scale_row_stride, int64_t input_row_stride,
+                                      int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
+  // the kernels take the scale row stride in bytes
+  if (scale_row_stride < 0 || scale_row_stride > (int64_t(1) << 60))
+    return fail(HPRMS_E_INVALID, "scale row stride %lld out of range", (long long)scale_row_stride);
+  Problem p{7, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
+            residual_row_stride, dtype, eps};
+  p.mx_scales = scales;
+  p.mx_scale_stride = scale_row_stride * 4;
+  return run(p, nullptr, stream);
+}
+
 int hprms_rmsnorm(void* out, const void* in, const void* weight, int64_t rows, int64_t hidden,
                   int64_t out_row_stride, int64_t in_row_stride, int dtype, double eps, hipStream_t stream) {
   Problem p{1, const_cast<void*>(in), out, nullptr, weight, rows, hidden, in_row_stride, out_row_stride,
@@ -1059,7 +1088,7 @@ int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, in
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
+  if (mode < 0 || mode > 7) return fail(HPRMS_E_INVALID, "mode must be in [0, 7] (got %d)", mode);
   if (rows < 0 || hidden < 1 || hidden > kMaxHidden) return fail(HPRMS_E_INVALID, "bad rows/hidden");
   if (cu_count < 1 || cu_count > 65536) return fail(HPRMS_E_INVALID, "cu_count must be in [1, 65536] (got %d)", cu_count);
   // the choice for rows on the 128-byte grid; odd widths: the tail variant of
@@ -1129,7 +1158,7 @@ int hprms_streamer(void* out, const void* in, int64_t rows, int64_t hidden, int6
 int hprms_kernel_configs(int dtype, int mode, hprms_config* out, int capacity) {
   if (dtype != HPRMS_DTYPE_BF16 && dtype != HPRMS_DTYPE_FP16)
     return fail(HPRMS_E_INVALID, "dtype must be HPRMS_DTYPE_BF16 or HPRMS_DTYPE_FP16 (got %d)", dtype);
-  if (mode < 0 || mode > 6) return fail(HPRMS_E_INVALID, "mode must be in [0, 6] (got %d)", mode);
+  if (mode < 0 || mode > 7) return fail(HPRMS_E_INVALID, "mode must be in [0, 7] (got %d)", mode);
   if (capacity < 0 || (capacity > 0 && !out)) return fail(HPRMS_E_INVALID, "bad output array");
   int n = 0;
   for (const Registry& r : kRegistries) {

@@ -94,6 +94,11 @@
 // are gfx950 instructions).  A block holding NaN or infinity gets the scale
 // byte 0xFF and unscaled elements.  The
 // residual is updated in place and `input` is only read, as in MODE 2.
+// MODE 7 is the fused op with an FP8 (e4m3fn) output and one float32 scale
+// per 128 consecutive elements of a row (the 16 adjacent lanes of a DPP row
+// at one vector index, so a group's maximum is one 16-lane DPP reduction):
+// scale = max(amax|y| / 448, FLT_MIN) and q = e4m3fn(clamp(y * (1 / scale)))
+// per group, as MODE 2 per row.
 #pragma once
 
 #include "hprms_device.h"
@@ -132,7 +137,7 @@ struct FusedArgs {
   int64_t res_out_stride;
   int32_t nparts;        // MODE 4: number of partial rows summed (x_rows is part 0)
   const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
-  uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes, hidden / 32 per row
+  uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes; MODE 7: float32 scales (hidden / 32 bytes per row)
   int64_t mx_scale_stride;  // bytes between scale rows
   int64_t* timeline;     // FLAGS bit 9 only (bench library): 4 values per workgroup
 };
@@ -167,16 +172,20 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;
   constexpr int NW = BLOCK / 64;
   constexpr int VREG = VPL - LDSV;
-  static_assert(MODE >= 0 && MODE <= 6, "mode");
+  static_assert(MODE >= 0 && MODE <= 7, "mode");
   constexpr bool RES = MODE != 1;                                  // residual stream read
   constexpr bool MX = MODE == 5 || MODE == 6;                      // OCP MX output
+  constexpr bool GQ = MODE == 7;                                   // FP8, one scale per 128 elements
+  constexpr bool BLOCKQ = MX || GQ;                                // per-block scales from DPP maxima
+  static_assert(!GQ || LPR % 16 == 0, "a 128-element group is 16 adjacent lanes' vectors");
   constexpr bool OUT16 = MODE == 1 || MODE == 3 || MODE == 4;      // 16-bit output to `out`
-  constexpr bool TAIL = (FLAGS & 64) != 0 && !MX;                  // shifted rows, head and tail vectors
+  constexpr bool TAIL = (FLAGS & 64) != 0 && !BLOCKQ;              // shifted rows, head and tail vectors
   // rows off the 128-byte grid: each row's lane mapping rotated so that every
   // wave's 1 KiB access starts on a 512-byte boundary (`phases` bits 0-19)
-  // (not the FP8 and MX outputs: the FP8 form's 1024 x 2 tail kernel,
-  // held to 64 VGPRs, would spill, and an MX block must stay one quad's)
-  constexpr bool ROT = (FLAGS & 32) != 0 && !MX && MODE != 2;
+  // (not the FP8 and block-scaled outputs: the FP8 form's 1024 x 2 tail
+  // kernel, held to 64 VGPRs, would spill, and a block must stay one group
+  // of adjacent lanes)
+  constexpr bool ROT = (FLAGS & 32) != 0 && !BLOCKQ && MODE != 2;
   // residual loads issued first (not for the partial-sum form, where it measured 0.1-1.8% slower)
   constexpr bool RFIRST = (FLAGS & 128) != 0 && RES && MODE != 4;
   // FLAGS bit 20 / bit 21 (bench library, with bit 7): the residual-first and
@@ -427,7 +436,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     // (with it the compiler kept 64 x 8's unpacked rows live, 120 -> 189
     // VGPRs), nor does the LDS tier, whose weight loads then trail the row
     // loads (1-1.6% slower at 16K-32K, two builds side by side).
-    // srs/soff: residual stores; ors/ooff: output; xsrs/xsoff: MX scales
+    // srs/soff: residual stores; ors/ooff: output; xsrs/xsoff: block scales (MX, MODE 7)
     if constexpr (MODE >= 2 && LDSV == 0) __builtin_amdgcn_sched_barrier(0);
     __amdgpu_buffer_rsrc_t srs = rrs, ors = xrs, xsrs = xrs;
     uint32_t soff = roff, ooff = xoff, xsoff = 0, esoff = eroff, eooff = exoff;
@@ -440,7 +449,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       soff = srow + lofs + wshift;
       esoff = eok ? srow + eb : kOOB;
     }
-    if constexpr (MODE == 2 || MX) {
+    if constexpr (MODE == 2 || BLOCKQ) {
       constexpr uint32_t QB = MODE == 6 ? 4u : 8u;  // output bytes per 8-element vector
       uint8_t* const qp = opaque(a.q);
       const int64_t qs = opaque(a.q_stride);
@@ -457,6 +466,15 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       xsrs = make_rsrc(sp + row0 * ss, sbytes);
       // one lane of each quad writes its block's scale byte
       xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)ss + (uint32_t)lane / 4u : kOOB;
+    }
+    if constexpr (GQ) {
+      // float32 scales, one per 128 elements; `mx_scale_stride` in bytes
+      uint8_t* const sp = opaque(a.mx_scale);
+      const int64_t ss = opaque(a.mx_scale_stride);
+      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * ss + hidden / 32);
+      xsrs = make_rsrc(sp + row0 * ss, sbytes);
+      // the first lane of each 16 writes its group's scale
+      xsoff = (lane & 15) == 0 ? (uint32_t)rib * (uint32_t)ss + (uint32_t)lane / 4u : kOOB;
     }
     if constexpr (MODE == 1) {
       // no residual: its (preloaded) arguments carry the output rows
@@ -713,6 +731,37 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
           q = cvt_e2m1x2<3>(q, F::lo(y[3]) * mul, F::hi(y[3]) * mul);
           store4<OSAUX>(q, ors, ok ? ooff + k * (LPR * 4u) : kOOB);
         }
+      }
+    } else if constexpr (GQ) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        const u32x4 s = k < VREG ? sv[k < VREG ? k : 0] : spill[(k - VREG) * BLOCK + tid];
+        u32x4 y;
+        uint32_t m2 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          y[j] = F::pack((olo(s[j]) * inv) * F::lo(wv[k][j]), (ohi(s[j]) * inv) * F::hi(wv[k][j]));
+          const uint32_t mag = y[j] & 0x7fff7fffu;
+          m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(mag & 0xffffu, mag >> 16));
+        }
+        // the group's maximum magnitude: the 16 lanes of a DPP row hold its
+        // 16 vectors (sign-magnitude patterns order like their values, NaN
+        // above inf)
+        const float amax = F::one((uint16_t)group_max_u32<16>(m2));
+        float sc = amax / 448.0f;
+        if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
+        const float isc = 1.0f / sc;
+        const bool ok = row_ok && vec_ok[k];
+        // default cache policy, so that L2 merges a row's scales into lines
+        store4<0>(__float_as_uint(sc), xsrs, ok && xsoff != kOOB ? xsoff + (uint32_t)(k * (LPR / 16) * 4) : kOOB);
+        u32x2 q;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t y0 = y[2 * h], y1 = y[2 * h + 1];
+          q[h] = pack_e4m3x4(clamp_e4m3(F::lo(y0) * isc), clamp_e4m3(F::hi(y0) * isc),
+                             clamp_e4m3(F::lo(y1) * isc), clamp_e4m3(F::hi(y1) * isc));
+        }
+        store8<OSAUX>(q, ors, ok ? ooff + k * (LPR * 8u) : kOOB);
       }
     } else if constexpr (MODE != 2) {
 #pragma unroll

@@ -146,7 +146,10 @@ struct FusedEntry {
   HPRMS_MODE1_SHAPES(ENTRY, DT, 1) HPRMS_MODE2_SHAPES(ENTRY, DT, 2)                              \
   HPRMS_FUSED_TAIL_SHAPES(ENTRY, DT, 3) ENTRY(DT, 3, 128, 4, 0, 256, 131) HPRMS_WIDE_ROWS(ENTRY, DT, 3) \
   HPRMS_MODE4_TAIL_SHAPES(ENTRY, DT, 4) ENTRY(DT, 4, 128, 4, 0, 256, 131) ENTRY(DT, 4, 256, 4, 0, 256, 3)
-#define HPRMS_MX_MODES(ENTRY, DT) HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6)
+// the block-scaled outputs: MX (modes 5, 6) and FP8 with a scale per 128
+// elements (mode 7), with the same shapes
+#define HPRMS_MX_MODES(ENTRY, DT) \
+  HPRMS_MX_SHAPES(ENTRY, DT, 5) HPRMS_MX_SHAPES(ENTRY, DT, 6) HPRMS_MX_SHAPES(ENTRY, DT, 7)
 
 // The shapes with sc1 bits among the lists of modes 0, 1, 3 and 4 (their
 // off-grid variants keep them for calls past the Infinity Cache)

@@ -270,6 +270,59 @@ void rms_norm_fp8_static_meta(at::Tensor& out, const at::Tensor& scale, const at
   (void)eps;
 }
 
+// ---- FP8 output with a scale per 128 elements -------------------------------------------
+struct GroupShape {
+  FusedShape f;
+  int64_t out_stride, scale_stride;
+};
+
+GroupShape check_fp8_group(const at::Tensor& out, const at::Tensor& scales, const at::Tensor& input,
+                           const at::Tensor& weight, const at::Tensor& residual) {
+  GroupShape s;
+  s.f = check_fused(input, weight, residual);
+  TORCH_CHECK(s.f.hidden % 128 == 0, "the FP8 output with a scale per 128 elements needs hidden_dim % 128 == 0");
+  TORCH_CHECK(out.scalar_type() == at::kFloat8_e4m3fn, "out.dtype() == float8_e4m3fn");
+  TORCH_CHECK(scales.scalar_type() == at::kFloat, "scales.dtype() == float32");
+  for (const at::Tensor* t : {&out, &scales}) {
+    TORCH_CHECK(t->dim() == input.dim(), "out and scales must have input.dim() dimensions");
+    for (int64_t i = 0; i + 1 < input.dim(); ++i)
+      TORCH_CHECK(t->size(i) == input.size(i), "out and scales must match input in the leading dimensions");
+    TORCH_CHECK(t->stride(-1) == 1, "out and scales must be contiguous in the last dimension");
+    TORCH_CHECK(t->device() == input.device(), "out, scales and input must be on the same device");
+  }
+  TORCH_CHECK(out.size(-1) == s.f.hidden, "out.size(-1) == hidden_dim");
+  TORCH_CHECK(scales.size(-1) == s.f.hidden / 128, "scales.size(-1) must be hidden / 128 = ", s.f.hidden / 128);
+  int64_t r = 0;
+  rows_of(out, s.f.hidden, &r, &s.out_stride);
+  rows_of(scales, s.f.hidden / 128, &r, &s.scale_stride);
+  if (s.f.rows > 0) {
+    at::assert_no_overlap(out, scales);
+    at::assert_no_overlap(out, residual);
+    at::assert_no_overlap(out, input);
+    at::assert_no_overlap(scales, residual);
+    at::assert_no_overlap(scales, input);
+  }
+  return s;
+}
+
+void rms_norm_fp8_group_hip(at::Tensor& out, at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,
+                            at::Tensor& residual, double eps) {
+  const GroupShape s = check_fp8_group(out, scales, input, weight, residual);
+  if (s.f.rows == 0 || s.f.hidden == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm_fp8_group(out.data_ptr(), scales.data_ptr<float>(), input.data_ptr(),
+                                                 weight.data_ptr(), residual.data_ptr(), s.f.rows, s.f.hidden,
+                                                 s.out_stride, s.scale_stride, s.f.in_stride, s.f.res_stride,
+                                                 s.f.dtype, eps, stream));
+}
+
+void rms_norm_fp8_group_meta(at::Tensor& out, at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,
+                             at::Tensor& residual, double eps) {
+  (void)check_fp8_group(out, scales, input, weight, residual);
+  (void)eps;
+}
+
 // ---- fused op out of place ----------------------------------------------------------
 FusedShape check_fused_out(const at::Tensor& out, const at::Tensor& residual_out, const at::Tensor& input,
                            const at::Tensor& weight, const at::Tensor& residual) {
@@ -504,6 +557,8 @@ TORCH_LIBRARY(hp_rms_norm, m) {
         "float eps) -> ()");
   m.def("rms_norm_fp8_static_quant(Tensor(a!) out, Tensor scale, Tensor input, Tensor weight, Tensor(b!) residual, "
         "float eps) -> ()");
+  m.def("rms_norm_fp8_group_quant(Tensor(a!) out, Tensor(b!) scales, Tensor input, Tensor weight, "
+        "Tensor(c!) residual, float eps) -> ()");
   m.def("rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, Tensor residual, "
         "float eps) -> ()");
   m.def("reduce_add_rms_norm(Tensor(a!) out, Tensor[] parts, Tensor weight, Tensor(b!) residual, float eps) -> ()");
@@ -519,6 +574,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
   m.impl("rms_norm_plain", &rms_norm_plain_hip);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_hip);
   m.impl("rms_norm_fp8_static_quant", &rms_norm_fp8_static_hip);
+  m.impl("rms_norm_fp8_group_quant", &rms_norm_fp8_group_hip);
   m.impl("rms_norm_out", &rms_norm_out_hip);
   m.impl("reduce_add_rms_norm", &reduce_rms_norm_hip);
   m.impl("rms_norm_mx_quant", &rms_norm_mx_hip);
@@ -533,6 +589,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
   m.impl("rms_norm_plain", &rms_norm_plain_meta);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_meta);
   m.impl("rms_norm_fp8_static_quant", &rms_norm_fp8_static_meta);
+  m.impl("rms_norm_fp8_group_quant", &rms_norm_fp8_group_meta);
   m.impl("rms_norm_out", &rms_norm_out_meta);
   m.impl("reduce_add_rms_norm", &reduce_rms_norm_meta);
   m.impl("rms_norm_mx_quant", &rms_norm_mx_meta);

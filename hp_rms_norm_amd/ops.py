@@ -5,6 +5,7 @@ import torch
 
 __all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "fused_add_rms_norm_out",
            "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "hp_rms_norm_fp8_static", "fused_add_rms_norm_fp8_static",
+           "hp_rms_norm_fp8_group", "fused_add_rms_norm_fp8_group",
            "reduce_add_rms_norm", "hp_rms_norm_mx",
            "fused_add_rms_norm_mxfp8", "fused_add_rms_norm_mxfp4", "MXFP8", "MXFP4",
            "set_batch_invariant", "batch_invariant"]
@@ -95,6 +96,27 @@ def fused_add_rms_norm_fp8_static(input, residual, weight, scale, eps):
     q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
     torch.ops.hp_rms_norm.rms_norm_fp8_static_quant.default(q, scale, input, weight, residual, eps)
     return q
+
+
+def hp_rms_norm_fp8_group(output, scales, input, weight, residual, eps):
+    """Fused residual-add + RMSNorm with an FP8 output and one float32 scale
+    per 128 consecutive elements of a row (per-token-group quantisation, 1 x
+    128 groups): ``residual <- input + residual`` in place; with ``y`` the op's
+    16-bit output, per group ``scales = max(amax|y| / 448, FLT_MIN)`` and
+    ``output = float8_e4m3fn(clamp(y * (1 / scales), -448, 448))``.
+    ``output``: float8_e4m3fn shaped like ``input``; ``scales``: float32
+    ``[..., H // 128]``.  ``input`` is only read.  Needs ``H % 128 == 0``.  No
+    reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_fp8_group_quant.default(output, scales, input, weight, residual, eps)
+
+
+def fused_add_rms_norm_fp8_group(input, residual, weight, eps):
+    """Allocating form of ``hp_rms_norm_fp8_group``: returns ``(q, scales)``;
+    ``residual`` is updated in place."""
+    q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
+    scales = torch.empty(input.shape[:-1] + (input.shape[-1] // 128,), dtype=torch.float32, device=input.device)
+    torch.ops.hp_rms_norm.rms_norm_fp8_group_quant.default(q, scales, input, weight, residual, eps)
+    return q, scales
 
 
 def reduce_add_rms_norm(out, parts, weight, residual, eps):

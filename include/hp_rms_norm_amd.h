@@ -200,6 +200,28 @@ int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const
                                hipStream_t stream);
 
 /*
+ * Fused residual-add + RMSNorm with an FP8 (OCP e4m3fn) output and one
+ * float32 scale per 128 consecutive elements of a row (per-token-group
+ * quantisation, 1 x 128 groups, the activation format of block-scaled FP8
+ * GEMMs):
+ *   residual[r, :] <- rne16(f32(input) + f32(residual))        (in place)
+ *   y              =  the 16-bit output of hprms_fused_add_rmsnorm
+ *   per group g of 128 consecutive elements of row r:
+ *     scales[r, g] =  max(max |y| / 448, FLT_MIN)   (NaN if the group holds a NaN)
+ *     out          =  e4m3fn(clamp(y * (1 / scales[r, g]), -448, 448))
+ * `out` is [rows, hidden] bytes with its row stride in bytes; `scales` is
+ * [rows, hidden / 128] float32, 4-byte aligned, with its row stride in
+ * elements.  `input` is only read.  Needs hidden % 128 == 0 and the same
+ * layouts as hprms_fused_add_rmsnorm_mx (no general-tier fallback); other
+ * calls return HPRMS_E_INVALID.  No counterpart in the reference.
+ */
+int hprms_fused_add_rmsnorm_fp8_group(void* out, float* scales, const void* input, const void* weight,
+                                      void* residual, int64_t rows, int64_t hidden,
+                                      int64_t out_row_stride, int64_t scale_row_stride,
+                                      int64_t input_row_stride, int64_t residual_row_stride,
+                                      int dtype, double eps, hipStream_t stream);
+
+/*
  * Kernel configuration of the fused add+RMSNorm family.  Used by the tuning
  * sweep and by tests that exercise every tier at every shape; normal callers
  * use hprms_fused_add_rmsnorm(), which picks the configuration from the
@@ -243,7 +265,8 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  * `mode` (0: hprms_fused_add_rmsnorm, 1: hprms_rmsnorm, 2:
  * hprms_fused_add_rmsnorm_fp8, 3: hprms_fused_add_rmsnorm_out, 4:
  * hprms_reduce_add_rmsnorm, 5 / 6: hprms_fused_add_rmsnorm_mx with
- * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1) on a device of 256 CUs (a whole
+ * HPRMS_MX_FP8_E4M3 / HPRMS_MX_FP4_E2M1, 7: hprms_fused_add_rmsnorm_fp8_group,
+ * which takes the MX modes' shapes) on a device of 256 CUs (a whole
  * MI355X), written to *config; tier 3 when only the general kernel fits
  * hidden.  It is the choice for contiguous rows on the 128-byte grid (for
  * hidden % 8 != 0: the tail variant of the choice for rows off it).  A call's
@@ -268,7 +291,7 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  *     place of the LDS tier's 256 x 8, and adds bit 14 to 512 x 2-3 and
  *     1024 x 2 (modes 0, 3; from 1024 rows), 512 x 3 (mode 4; from 1024 rows)
  *     and 512 x 2-4 and 1024 x 3 (mode 1; from 384 rows).
- *   - Calls of modes 0, 2, 4, 5 and 6 on the grid with rows * hidden <= 2^24
+ *   - Calls of modes 0, 2, 4, 5, 6 and 7 on the grid with rows * hidden <= 2^24
  *     whose configuration carries the sc1 bits run the same shape with flags
  *     (flags & ~24) | 32: the unaligned variant without sc1 (rows off a
  *     512-byte boundary are then rotated, as above).

@@ -236,6 +236,31 @@ def fused_add_rmsnorm_fp8_static(x, w, r, eps, dtype, scale, threads=1):
     return e4m3_from_f32(v), res
 
 
+def fused_add_rmsnorm_fp8_group(x, w, r, eps, dtype, threads=1, group=128, floor=True):
+    """FP8 form with one scale per `group` (128) consecutive elements of a
+    row: returns (q uint8 [rows, hidden] of e4m3fn bits, scales float32
+    [rows, hidden // group], new residual).  Per group, scale = max(amax|y| /
+    448, FLT_MIN) (NaN if the group holds a NaN) and q = e4m3fn(clamp(y * (1 /
+    scale), -448, 448)) with y the fused op's 16-bit output: the per-row step
+    of hprms_oracle_fused_add_rmsnorm_fp8 applied to each group.  `group` and
+    `floor` (the FLT_MIN floor) exist for the tests that plant mistakes."""
+    y, res = fused_add_rmsnorm(x, w, r, eps, dtype, threads=threads)
+    rows, hidden = y.shape
+    if hidden % group:
+        raise ValueError(f"hidden {hidden} is not a multiple of the group size {group}")
+    yf = to_f32(y, dtype).reshape(rows, hidden // group, group)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        amax = np.max(np.abs(yf), axis=-1)                       # NaN propagates
+        sc = (amax / np.float32(448.0)).astype(np.float32)
+        if floor:
+            tiny = np.float32(np.finfo(np.float32).tiny)
+            sc = np.where(sc < tiny, tiny, sc).astype(np.float32)  # NaN compares false and stays
+        isc = (np.float32(1.0) / sc).astype(np.float32)
+        v = yf * isc[..., None]
+        v = np.where(v > 448.0, np.float32(448.0), np.where(v < -448.0, np.float32(-448.0), v)).astype(np.float32)
+    return e4m3_from_f32(v).reshape(rows, hidden), sc, res
+
+
 def e4m3_from_f32(a):
     a = np.ascontiguousarray(a, dtype=np.float32)
     out = np.empty(a.shape, dtype=np.uint8)

@@ -50,11 +50,17 @@ int main(void) {
   EXPECT(hprms_fused_add_rmsnorm(NULL, NULL, NULL, 0, 4096, 4096, 4096, HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
   EXPECT(hprms_fused_add_rmsnorm_fp8(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 4096, 4096, HPRMS_DTYPE_FP16,
                                      1e-6, NULL) == HPRMS_OK);
+  EXPECT(hprms_fused_add_rmsnorm_fp8_static(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 4096, 4096,
+                                            HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
+  EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 32, 4096, 4096,
+                                           HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
+  EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4000, 4000, 32, 4000, 4000,
+                                           HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_E_INVALID);
   EXPECT(hprms_reduce_add_rmsnorm(NULL, NULL, 3, NULL, NULL, 0, 4096, 4096, 4096, 4096, HPRMS_DTYPE_BF16, 1e-6,
                                   NULL) == HPRMS_OK);
 
   /* the table: every mode has a vector-tier kernel covering H = 4096 */
-  for (mode = 0; mode <= 6; ++mode) {
+  for (mode = 0; mode <= 7; ++mode) {
     int n;
     EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, mode, &c) == HPRMS_OK);
     EXPECT(c.tier == 1 || c.tier == 2);
@@ -62,7 +68,7 @@ int main(void) {
     n = hprms_kernel_configs(HPRMS_DTYPE_BF16, mode, NULL, 0);
     EXPECT(n > 0);
   }
-  EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, 7, &c) == HPRMS_E_INVALID);
+  EXPECT(hprms_select_config(4096, 4096, HPRMS_DTYPE_BF16, 8, &c) == HPRMS_E_INVALID);
   /* hidden % 8 != 0: the same shape with a tail vector (flags bit 6); below 8 elements, the general kernel */
   EXPECT(hprms_select_config(4096, 4097, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 1 && (c.flags & 96) == 96);
   EXPECT(hprms_select_config(4096, 15, HPRMS_DTYPE_BF16, 0, &c) == HPRMS_OK && c.tier == 1 && (c.flags & 96) == 96);

@@ -253,9 +253,9 @@ def test_row_rules_scale_with_the_cu_count():
     bf = abi.DTYPE_BF16
     hiddens = (512, 1024, 1032, 2048, 2056, 3072, 4096, 5120, 6144, 8192, 8191, 12289, 16384, 16391, 32768)
     rowss = (1, 8, 32, 100, 128, 129, 256, 300, 400, 512, 640, 768, 1000, 1024, 1280, 2048, 4096, 8192)
-    for mode in range(7):
+    for mode in range(8):
         for hidden in hiddens:
-            if mode >= 5 and hidden % 32:
+            if (mode >= 5 and hidden % 32) or (mode == 7 and hidden % 128):
                 continue
             for rows in rowss:
                 assert abi.select_config(rows, hidden, bf, mode, cus=256).as_tuple() == \
@@ -293,7 +293,7 @@ def test_row_groups_in_runs_per_xcd_at_two_pitches():
                 c = abi.select_config(rows, hidden, dtype)
                 assert (c.flags >> 16) & 7 == v and c.flags & 0xffff == (131 if hidden == 4096 else 7), c.as_tuple()
             assert not abi.select_config(first - 1, hidden, dtype).flags >> 16
-            for mode in range(1, 7):
+            for mode in range(1, 8):
                 assert not abi.select_config(first, hidden, dtype, mode).flags >> 16, mode
             assert not abi.select_config(first, hidden + 1, dtype).flags >> 16   # odd width: the tail variant
         for hidden in (1024, 2048, 3072, 5120, 6144, 7168, 9216, 12288, 16384, 24576, 28672, 32768):
@@ -341,7 +341,7 @@ def test_table_covers_every_hidden_with_a_built_kernel():
     up, and launch nothing)."""
     L = abi.lib()
     built = {(dt, m): {c.as_tuple() for c in abi.kernel_configs(dt, m)}
-             for dt in (abi.DTYPE_BF16, abi.DTYPE_FP16) for m in range(7)}
+             for dt in (abi.DTYPE_BF16, abi.DTYPE_FP16) for m in range(8)}
     for dtype, rows in ((abi.DTYPE_BF16, 4096), (abi.DTYPE_FP16, 4096), (abi.DTYPE_BF16, 1), (abi.DTYPE_FP16, 256)):
         for hidden in list(range(8, 70000, 8)) + [1, 3, 7, 9, 15, 1001, 4097, 65535, 65537, 65543, 65545]:
             c = abi.select_config(rows, hidden, dtype)
@@ -352,8 +352,8 @@ def test_table_covers_every_hidden_with_a_built_kernel():
             assert (c.flags & 96) == (96 if hidden % 8 else 0)
             assert c.lanes_per_row * c.vec_per_lane >= hidden // 8
             assert c.block_threads % c.lanes_per_row == 0
-            for mode in range(7):
-                if mode >= 5 and hidden % 32:
+            for mode in range(8):
+                if (mode >= 5 and hidden % 32) or (mode == 7 and hidden % 128):
                     continue
                 cm = abi.select_config(rows, hidden, dtype, mode)
                 t = cm.as_tuple()
@@ -409,7 +409,7 @@ def test_config_entry_rejects_unbuilt_and_misfit_configs():
 
 def test_every_built_config_is_well_formed():
     for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
-        for mode in range(7):
+        for mode in range(8):
             cfgs = abi.kernel_configs(dtype, mode)
             assert cfgs
             for c in cfgs:
@@ -509,6 +509,31 @@ def test_plain_c_caller_compiles_links_and_runs(tmp_path):
     assert p.returncode == 0 and "ok" in p.stdout, p.stdout + p.stderr
 
 
+def test_fp8_group_entry_rejects_bad_arguments():
+    L = abi.lib()
+    ok = dict(out=0x4000, sc=0x5000, x=0x1000, w=0x2000, r=0x3000, h=4096, so=4096, ss=32)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.hprms_fused_add_rmsnorm_fp8_group(a["out"], a["sc"], a["x"], a["w"], a["r"], a.get("rows", 4),
+                                                   a["h"], a["so"], a["ss"], a["h"], a["h"], 0, 1e-6, None)
+    assert call(h=4160, so=4160, ss=33) == abi.HPRMS_E_INVALID and "128" in abi.last_error()
+    assert call(so=2048) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
+    assert call(ss=31) == abi.HPRMS_E_INVALID and "scale row stride" in abi.last_error()
+    assert call(ss=-1) == abi.HPRMS_E_INVALID and "scale row stride" in abi.last_error()
+    assert call(sc=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
+    assert call(sc=0x5002) == abi.HPRMS_E_INVALID and "4-byte aligned" in abi.last_error()
+    # outputs and rows off the 16-byte grid take the unaligned variants; odd addresses are refused
+    assert call(out=0x4002, rows=0) == abi.HPRMS_OK and call(x=0x1008, rows=0) == abi.HPRMS_OK
+    assert call(x=0x1001) == abi.HPRMS_E_INVALID and "aligned" in abi.last_error()
+    # every width the form accepts maps to a vector-tier shape whose 128-element groups are
+    # 16 adjacent lanes
+    for hidden in range(128, 65536 + 1, 128):
+        for rows in (1, 300, 1024, 4096):
+            c = abi.select_config(rows, hidden, abi.DTYPE_BF16, abi.MODE_FP8_GROUP)
+            assert c.tier in (1, 2) and c.lanes_per_row % 16 == 0, (hidden, rows, c.as_tuple())
+
+
 def test_mx_entry_rejects_bad_arguments():
     L = abi.lib()
     ok = dict(out=0x4000, sc=0x5000, x=0x1000, w=0x2000, r=0x3000, h=4096, so=2048, ss=128, fmt=abi.MX_FP4_E2M1)
@@ -582,7 +607,7 @@ def test_bench_library_is_apart_from_the_product():
     for n in extra:
         assert hasattr(bench, n), n
         assert not hasattr(abi.lib(), n), f"{n} must not be in the product library"
-    for mode in range(7):
+    for mode in range(8):
         for dt in (abi.DTYPE_BF16, abi.DTYPE_FP16):
             prod = {c.as_tuple() for c in abi.kernel_configs(dt, mode)}
             more = {c.as_tuple() for c in abi.BENCH.kernel_configs(dt, mode)}
@@ -655,6 +680,6 @@ def test_product_library_holds_exactly_the_reachable_kernels():
     """libhprms.so instantiates the kernels its tables can choose and no
     other (the tuning shapes live in the bench library)."""
     for dtype in (abi.DTYPE_BF16, abi.DTYPE_FP16):
-        for mode in range(7):
+        for mode in range(8):
             built = {c.as_tuple() for c in abi.kernel_configs(dtype, mode)}
             assert built == _reachable(dtype, mode), (dtype, mode, sorted(built ^ _reachable(dtype, mode)))

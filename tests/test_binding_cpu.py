@@ -182,6 +182,28 @@ def test_fp8_static_op_schema_and_meta_checks():
     assert ops.fused_add_rms_norm_fp8_static(x, r, w, sc, 1e-6).dtype == torch.float8_e4m3fn
 
 
+def test_fp8_group_op_schema_and_meta_checks():
+    s = str(torch.ops.hp_rms_norm.rms_norm_fp8_group_quant.default._schema)
+    assert s == ("hp_rms_norm::rms_norm_fp8_group_quant(Tensor(a!) out, Tensor(b!) scales, Tensor input, "
+                 "Tensor weight, Tensor(c!) residual, float eps) -> ()")
+    x, w, r = t(4, 512), t(512), t(4, 512)
+    q = t(4, 512, dtype=torch.float8_e4m3fn)
+    sc = torch.empty(4, 4, device=M)
+    assert ops.hp_rms_norm_fp8_group(q, sc, x, w, r, 1e-6) is None
+    q2, sc2 = ops.fused_add_rms_norm_fp8_group(t(2, 3, 512), t(2, 3, 512), w, 1e-6)
+    assert q2.shape == (2, 3, 512) and q2.dtype == torch.float8_e4m3fn and sc2.shape == (2, 3, 4)
+    assert sc2.dtype == torch.float32
+    with pytest.raises(RuntimeError, match="128"):
+        ops.hp_rms_norm_fp8_group(t(4, 320, dtype=torch.float8_e4m3fn), torch.empty(4, 2, device=M), t(4, 320),
+                                  t(320), t(4, 320), 1e-6)
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        ops.hp_rms_norm_fp8_group(t(4, 512), sc, x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="float32"):
+        ops.hp_rms_norm_fp8_group(q, torch.empty(4, 4, device=M, dtype=torch.float16), x, w, r, 1e-6)
+    with pytest.raises(RuntimeError, match="hidden / 128"):
+        ops.hp_rms_norm_fp8_group(q, torch.empty(4, 16, device=M), x, w, r, 1e-6)
+
+
 def test_out_of_place_and_reduce_schemas():
     s = str(torch.ops.hp_rms_norm.rms_norm_out.default._schema)
     assert s == ("hp_rms_norm::rms_norm_out(Tensor(a!) out, Tensor(b!) residual_out, Tensor input, Tensor weight, "

@@ -1,0 +1,148 @@
+"""GPU parity of the fused add+RMSNorm with an FP8 (OCP e4m3fn) output and one
+float32 scale per 128 consecutive elements of a row (per-token-group
+quantisation, 1 x 128 groups).
+
+Pins: the residual is bit-exact against the oracle; q and the scales equal,
+bit for bit, torch's per-group quantisation of the 16-bit output the same
+kernel family produces for the same inputs (the 16-bit op run with this
+form's lane mapping); against the CPU oracle q is within one FP8 step and the
+scales within one 16-bit ulp of the group maximum.  `input` is not modified.
+NaN encodings differ (hardware 0xFF, torch 0x7F): NaN compares equal to NaN.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, assert_residual_exact, bits, make_inputs, special_inputs
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    assert torch.cuda.is_available(), "the gpu tests need a HIP device"
+    import hp_rms_norm_amd
+    return hp_rms_norm_amd
+
+
+def torch_quantise_group(y):
+    """torch's per-group quantisation of y on the CPU (binary32)."""
+    yf = y.detach().cpu().float()
+    rows, hidden = yf.shape
+    g = yf.view(rows, hidden // 128, 128)
+    sc = torch.clamp(g.abs().amax(-1, keepdim=True) / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (g * (1.0 / sc)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(rows, hidden).view(torch.uint8).numpy(), sc.view(rows, -1).numpy()
+
+
+def q_bits(q):
+    return q.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def same_floats(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32)) or np.array_equal(a, b, equal_nan=True)
+
+
+def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6, special=False):
+    from hp_rms_norm_amd import abi
+    if special:
+        x, r, w = special_inputs(rows, hidden, dtype, seed)
+    else:
+        x, r, w = make_inputs(rows, hidden, dtype, seed, dist)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    q, sc = ops.fused_add_rms_norm_fp8_group(xd, rd, wd, eps)
+    # the same inputs through the 16-bit op with this form's lane mapping
+    # (the same fp32 reduction order, hence the same y)
+    cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_FP8_GROUP)
+    assert cfg.tier in (1, 2), cfg.as_tuple()
+    y, r16 = x.to(DEV), r.to(DEV)
+    abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
+                                eps, torch.cuda.current_stream().cuda_stream, cfg)
+    torch.cuda.synchronize()
+    tag = f"{rows}x{hidden} {dtype} seed {seed}"
+    assert torch.equal(xd.cpu().view(torch.int16), x.view(torch.int16)), "input modified " + tag
+    assert torch.equal(rd.view(torch.int16), r16.view(torch.int16)), "residual differs from the 16-bit op " + tag
+    tq, tsc = torch_quantise_group(y)
+    assert same_floats(sc.cpu().numpy(), tsc), "scales " + tag
+    d = oracle.e4m3_ulp_distance(q_bits(q), tq)
+    assert d.max() == 0, f"q differs from torch's quantisation of y: {tag}"
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8_group(bits(x), bits(w), bits(r), eps, DT[dtype],
+                                                       threads=min(16, oracle.max_threads()))
+    assert_residual_exact(bits(rd), ores, dtype, "residual " + tag)
+    assert oracle.e4m3_ulp_distance(q_bits(q).reshape(oq.shape), oq).max() <= 1, tag
+    np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7, equal_nan=True, err_msg=tag)
+
+
+@pytest.mark.parametrize("rows,hidden,dtype", [
+    (4096, 4096, torch.bfloat16), (4096, 8192, torch.bfloat16), (4096, 16384, torch.bfloat16),
+    (4096, 32768, torch.bfloat16), (4096, 5120, torch.float16), (4096, 7168, torch.float16),
+    (1, 4096, torch.bfloat16), (32, 8192, torch.bfloat16), (512, 4096, torch.bfloat16)],
+    ids=lambda v: str(v).replace("torch.", ""))
+def test_fp8_group_baseline_shapes(ops, rows, hidden, dtype):
+    print("fp8 group case", rows, hidden, dtype, flush=True)
+    run_case(ops, rows, hidden, dtype, seed=rows + hidden, dist="outliers" if rows <= 512 else "bench")
+
+
+def test_fp8_group_every_table_entry(ops):
+    """H at every breakpoint of the table this form takes (and one group
+    below), with 1100 rows (the bandwidth rows) and 7 rows (the latency
+    rows), both dtypes at a few."""
+    for hidden in (128, 256, 512, 640, 1024, 1152, 2048, 3072, 3200, 4096, 5120, 6144, 8192, 12288, 16384, 16256,
+                   24576, 32768, 65536):
+        for rows in (1100, 7):
+            print("fp8 group table", rows, hidden, flush=True)
+            run_case(ops, rows, hidden, torch.bfloat16, seed=hidden + rows)
+    for hidden in (1024, 4096, 16384):
+        run_case(ops, 300, hidden, torch.float16, seed=hidden + 1)
+
+
+def test_fp8_group_special_rows(ops):
+    """Rows of special values (NaN, infinities, zero rows with eps = 0,
+    binary32 overflow of the sum of squares, subnormals): a group holding NaN
+    gets a NaN scale and NaN codes, a zero group the scale FLT_MIN and zero
+    codes, as torch's quantisation of y."""
+    for rows, hidden in ((28, 1024), (300, 4096), (40, 32768)):
+        for eps in (0.0, 1e-6):
+            print("fp8 group special", rows, hidden, eps, flush=True)
+            run_case(ops, rows, hidden, torch.bfloat16, seed=rows + hidden, eps=eps, special=True)
+
+
+def test_fp8_group_strided_misaligned_output_and_scales(ops):
+    from hp_rms_norm_amd import abi
+    rows, hidden, eps, dtype = 40, 2048, 1e-6, torch.bfloat16
+    x, r, w = make_inputs(rows, hidden, dtype, 79)
+    oq, osc, ores = oracle.fused_add_rmsnorm_fp8_group(bits(x), bits(w), bits(r), eps, oracle.BF16)
+    for offset, pad, spad in ((0, 64, 0), (1, 3, 5)):
+        xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+        buf = torch.zeros(rows, hidden + pad + offset, dtype=torch.uint8, device=DEV)
+        qv = buf[:, offset:offset + hidden]
+        sbuf = torch.full((rows, hidden // 128 + spad), -1.0, dtype=torch.float32, device=DEV)
+        sv = sbuf[:, :hidden // 128]
+        abi.fused_add_rmsnorm_fp8_group(qv.data_ptr(), sv.data_ptr(), xd.data_ptr(), wd.data_ptr(), rd.data_ptr(),
+                                        rows, hidden, qv.stride(0), sv.stride(0), hidden, hidden, abi.DTYPE_BF16, eps,
+                                        torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(rd), ores, dtype)
+        assert oracle.e4m3_ulp_distance(qv.cpu().numpy(), oq).max() <= 1
+        np.testing.assert_allclose(sv.cpu().numpy(), osc, rtol=2.0 ** -7)
+        assert not buf[:, :offset].any() and not buf[:, offset + hidden:].any()
+        assert (sbuf[:, hidden // 128:] == -1.0).all()
+
+
+def test_fp8_group_of_one_group_rows_equals_the_per_row_form(ops):
+    """With H = 128 a row is one group: q and the scales equal the per-row FP8
+    form's (which takes another lane mapping, hence the comparison through y:
+    both quantise their own y, and the two y agree within 1 ulp)."""
+    rows, hidden = 512, 128
+    x, r, w = make_inputs(rows, hidden, torch.bfloat16, 81)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    q, sc = ops.fused_add_rms_norm_fp8_group(xd, rd, wd, 1e-6)
+    xd2, rd2 = x.to(DEV), r.to(DEV)
+    q1, sc1 = ops.fused_add_rms_norm_fp8(xd2, rd2, wd, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(rd.view(torch.int16), rd2.view(torch.int16))
+    assert oracle.e4m3_ulp_distance(q_bits(q), q_bits(q1)).max() <= 1
+    np.testing.assert_allclose(sc.cpu().numpy().reshape(-1), sc1.cpu().numpy().reshape(-1), rtol=2.0 ** -7)

@@ -394,6 +394,51 @@ def test_planted_fp8_static_mistakes_are_rejected():
             assert oracle.e4m3_ulp_distance(unclamped, want).max() > 0
 
 
+def torch_quantise_group(y, code, group=128):
+    """torch's per-token-group quantisation of 16-bit outputs y (binary32 on
+    the CPU): per `group` elements, scale = clamp(amax / 448, min=FLT_MIN),
+    q = e4m3fn(clamp(y * (1 / scale), -448, 448))."""
+    yf = tfrom(y, code).float()
+    rows, hidden = yf.shape
+    g = yf.view(rows, hidden // group, group)
+    sc = torch.clamp(g.abs().amax(-1, keepdim=True) / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (g * (1.0 / sc)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(rows, hidden).view(torch.uint8).numpy(), sc.view(rows, -1).numpy()
+
+
+def test_oracle_fp8_group_matches_torch():
+    """The FP8 output with a scale per 128 elements: the residual is the fused
+    oracle's, and q and the scales equal torch's per-group quantisation of the
+    oracle's own 16-bit output bit for bit (NaN where torch's is NaN), on
+    ordinary rows, rows with an outlier and rows of special values."""
+    for code in (BF, HF):
+        for i, (rows, hidden, kind) in enumerate([(64, 4096, "bench"), (32, 1024, "outliers"), (28, 640, "special")]):
+            if kind == "special":
+                x, r, w = (tbits(t) for t in special_inputs(rows, hidden, TDT[code], 21 + i))
+            else:
+                x, r, w = seeded(rows, hidden, code, 600 + i, kind)
+            y, res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, code)
+            q, sc, resg = oracle.fused_add_rmsnorm_fp8_group(x, w, r, 1e-6, code)
+            assert np.array_equal(resg, res), (code, kind)
+            tq, tsc = torch_quantise_group(y, code)
+            assert np.array_equal(sc.view(np.uint32), tsc.view(np.uint32)) or \
+                np.array_equal(sc, tsc, equal_nan=True), (code, kind)
+            assert oracle.e4m3_ulp_distance(q, tq).max() == 0, (code, kind)
+
+
+def test_planted_fp8_group_mistakes_are_rejected():
+    """Groups of 32 (an MX block) instead of 128, and the FLT_MIN floor of the
+    scale left out (a zero group then gives NaN codes), each fail the torch pin
+    above on rows that include zero rows."""
+    x, r, w = (tbits(t) for t in special_inputs(28, 640, torch.bfloat16, 21))
+    y, _ = oracle.fused_add_rmsnorm(x, w, r, 1e-6, BF)
+    tq, tsc = torch_quantise_group(y, BF)
+    q32, sc32, _ = oracle.fused_add_rmsnorm_fp8_group(x, w, r, 1e-6, BF, group=32)
+    assert oracle.e4m3_ulp_distance(q32, tq).max() > 0
+    qnf, scnf, _ = oracle.fused_add_rmsnorm_fp8_group(x, w, r, 1e-6, BF, floor=False)
+    assert oracle.e4m3_ulp_distance(qnf, tq).max() > 0 or not np.array_equal(scnf, tsc, equal_nan=True)
+
+
 def test_oracle_fp8_matches_golden(golden):
     for name, c in golden.items():
         if c["kind"] != "fp8":
