@@ -1072,6 +1072,24 @@ def run_extra(torch, ops, args):
         del sets, qs
         torch.cuda.empty_cache()
     out["fp8_static_output_bf16"] = fp8s
+    # the FP8 output with one float32 scale per 128 elements (per-token-group quantisation)
+    fp8g = []
+    for h in (4096, 8192, 16384, 32768):
+        n = cold_sets(B, h)
+        sets = [make_set(torch, B, h, torch.bfloat16, 7300 + i, "cuda:0") for i in range(n)]
+        w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
+        qs = [torch.empty(B, h, dtype=torch.float8_e4m3fn, device="cuda:0") for _ in range(n)]
+        sc = torch.empty(B, h // 128, dtype=torch.float32, device="cuda:0")
+
+        def call(i, sets=sets, qs=qs, sc=sc, w=w):
+            ops.hp_rms_norm_fp8_group(qs[i], sc, sets[i][0], w, sets[i][1], EPS)
+        us = time_rotating(torch, call, n, steps, args.warmup)
+        nbytes = 7 * B * h + 2 * h + 4 * B * (h // 128)
+        fp8g.append({"rows": B, "hidden": h, "us_per_call": round(us, 2),
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_call": nbytes})
+        del sets, qs
+        torch.cuda.empty_cache()
+    out["fp8_group128_output_bf16"] = fp8g
     # OCP MX outputs (MXFP8 / MXFP4): reads x, r; writes r, the elements and one scale byte per 32
     mx = []
     for fmt, name in ((ops.MXFP8, "mxfp8"), (ops.MXFP4, "mxfp4")):

@@ -341,7 +341,7 @@ def test_torch_compile_functionalises_the_in_place_op(abi):
 
 
 def test_torch_compile_with_the_other_ops(abi):
-    """The out-of-place, plain, FP8 (per row and static) / MX and partial-sum ops through
+    """The out-of-place, plain, FP8 (per row, static, per group) / MX and partial-sum ops through
     torch.compile (aot_eager, fullgraph): their alias annotations and Meta
     kernels let functionalisation see every write; bit-for-bit equal to eager."""
     import hp_rms_norm_amd as h
@@ -354,12 +354,14 @@ def test_torch_compile_with_the_other_ops(abi):
         q8, s8 = h.fused_add_rms_norm_fp8(x, r8, w, 1e-6)
         rs = r.clone()
         qs = h.fused_add_rms_norm_fp8_static(x, rs, w, s1, 1e-6)
+        rg = r.clone()
+        qg, sg = h.fused_add_rms_norm_fp8_group(x, rg, w, 1e-6)
         r4 = r.clone()
         q4, s4 = h.fused_add_rms_norm_mxfp4(x, r4, w, 1e-6)
         rp, o2 = r.clone(), torch.empty_like(x)
         h.reduce_add_rms_norm(o2, [x, p1], w, rp, 1e-6)
-        return (out, res, plain, q8.view(torch.uint8), s8, r8, qs.view(torch.uint8), rs, q4.view(torch.uint8),
-                s4.view(torch.uint8), r4, o2, rp)
+        return (out, res, plain, q8.view(torch.uint8), s8, r8, qs.view(torch.uint8), rs, qg.view(torch.uint8), sg,
+                rg, q4.view(torch.uint8), s4.view(torch.uint8), r4, o2, rp)
 
     x, r, w = (t.to(DEV) for t in make_inputs(96, 2048, torch.bfloat16, 22))
     p1 = torch.randn(96, 2048, device=DEV).to(torch.bfloat16)
