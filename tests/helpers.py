@@ -159,3 +159,59 @@ def as_dispatched(abi, cfg, hidden):
     c = abi.Config(*cfg.as_tuple())
     c.flags = (c.flags & ~24) | 32
     return c
+
+
+# ---- FP8 outputs against the oracle's 16-bit output ----------------------------------------
+# The 16-bit output y is held to one ulp of the oracle's; an FP8 output quantises the kernel's
+# own y, so against the oracle it is pinned as "the quantisation of some y within one ulp of the
+# oracle's", element by element.  (One ulp of a subnormal y is a factor of two, which a group's
+# or a row's small scale turns into several FP8 steps; a fixed step bound would not hold there.)
+def ulp_neighbours(a):
+    """(below, a, above): each 16-bit pattern and its neighbours one ulp down
+    and up on the ordered line (-0 taken as +0)."""
+    a = np.asarray(a, np.uint16).astype(np.int32)
+    mag = a & 0x7FFF
+    o = np.where((a & 0x8000) != 0, -mag, mag)
+
+    def back(v):
+        return np.where(v >= 0, v, 0x8000 | (-v)).astype(np.uint16)
+    return back(o - 1), a.astype(np.uint16), back(o + 1)
+
+
+def _e4m3_of(y_bits, isc, dtype):
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = oracle.to_f32(y_bits, DT[dtype]) * np.asarray(isc, np.float32)
+        v = np.where(v > 448.0, np.float32(448.0), np.where(v < -448.0, np.float32(-448.0), v)).astype(np.float32)
+    return oracle.e4m3_from_f32(v)
+
+
+def assert_fp8_from_y_within_one_ulp(q, y_oracle, isc, dtype, what="q"):
+    """q (e4m3fn bytes, shaped like y_oracle) equals e4m3fn(clamp(y * isc)) for
+    y one of y_oracle's 16-bit neighbours or itself, at every element; `isc`
+    (the reciprocal of the kernel's scale) broadcasts against y_oracle."""
+    q = np.asarray(q, np.uint8).reshape(np.shape(y_oracle))
+    ok = np.zeros(q.shape, bool)
+    for yc in ulp_neighbours(y_oracle):
+        ok |= oracle.e4m3_ulp_distance(q, _e4m3_of(yc, isc, dtype)) == 0
+    bad = np.argwhere(~ok)
+    assert bad.size == 0, f"{what}: {len(bad)} elements are no quantisation of a y within 1 ulp; first {bad[0]}"
+
+
+def assert_group_scales(scales, y_oracle, group, dtype, what="scales"):
+    """Each scale is max(amax / 448, FLT_MIN) for an amax within one ulp of the
+    largest |y| of the oracle's group of `group` elements (a kernel's y within
+    one ulp of the oracle's moves the maximum by at most that), NaN where the
+    group holds NaN."""
+    y = np.asarray(y_oracle, np.uint16)
+    rows = y.shape[0]
+    mag = (y & 0x7FFF).reshape(rows, -1, group).max(axis=-1)        # NaN patterns order above inf
+    tiny = np.float32(np.finfo(np.float32).tiny)
+    got = np.asarray(scales, np.float32).reshape(mag.shape)
+    ok = np.zeros(mag.shape, bool)
+    for m in ulp_neighbours(mag):
+        with np.errstate(invalid="ignore"):
+            sc = (oracle.to_f32(m & 0x7FFF, DT[dtype]) / np.float32(448.0)).astype(np.float32)
+            sc = np.where(sc < tiny, tiny, sc).astype(np.float32)
+        ok |= (got.view(np.uint32) == sc.view(np.uint32)) | (np.isnan(got) & np.isnan(sc))
+    bad = np.argwhere(~ok)
+    assert bad.size == 0, f"{what}: {len(bad)} scales off; first {bad[0]}: {got[tuple(bad[0])]}"

@@ -5,15 +5,18 @@ quantisation, 1 x 128 groups).
 Pins: the residual is bit-exact against the oracle; q and the scales equal,
 bit for bit, torch's per-group quantisation of the 16-bit output the same
 kernel family produces for the same inputs (the 16-bit op run with this
-form's lane mapping); against the CPU oracle q is within one FP8 step and the
-scales within one 16-bit ulp of the group maximum.  `input` is not modified.
+form's lane mapping); against the CPU oracle q is the quantisation of a y
+within one 16-bit ulp of the oracle's output and the scales those of a group
+maximum within one ulp of the oracle's (one ulp of a subnormal y is a factor
+of two, so no fixed FP8 step bound holds there).  `input` is not modified.
 NaN encodings differ (hardware 0xFF, torch 0x7F): NaN compares equal to NaN.
 """
 import numpy as np
 import pytest
 import torch
 
-from helpers import DT, assert_residual_exact, bits, make_inputs, special_inputs
+from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_residual_exact, bits,
+                     make_inputs, special_inputs)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -69,11 +72,14 @@ def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6, special=Fal
     assert same_floats(sc.cpu().numpy(), tsc), "scales " + tag
     d = oracle.e4m3_ulp_distance(q_bits(q), tq)
     assert d.max() == 0, f"q differs from torch's quantisation of y: {tag}"
-    oq, osc, ores = oracle.fused_add_rmsnorm_fp8_group(bits(x), bits(w), bits(r), eps, DT[dtype],
-                                                       threads=min(16, oracle.max_threads()))
+    oy, ores = oracle.fused_add_rmsnorm(bits(x), bits(w), bits(r), eps, DT[dtype],
+                                        threads=min(16, oracle.max_threads()))
     assert_residual_exact(bits(rd), ores, dtype, "residual " + tag)
-    assert oracle.e4m3_ulp_distance(q_bits(q).reshape(oq.shape), oq).max() <= 1, tag
-    np.testing.assert_allclose(sc.cpu().numpy(), osc, rtol=2.0 ** -7, equal_nan=True, err_msg=tag)
+    scales = sc.cpu().numpy()
+    assert_group_scales(scales, oy, 128, dtype, "scales " + tag)
+    with np.errstate(divide="ignore"):
+        assert_fp8_from_y_within_one_ulp(q_bits(q), oy, np.repeat(np.float32(1.0) / scales, 128, axis=1), dtype,
+                                         "q " + tag)
 
 
 @pytest.mark.parametrize("rows,hidden,dtype", [
@@ -114,7 +120,7 @@ def test_fp8_group_strided_misaligned_output_and_scales(ops):
     from hp_rms_norm_amd import abi
     rows, hidden, eps, dtype = 40, 2048, 1e-6, torch.bfloat16
     x, r, w = make_inputs(rows, hidden, dtype, 79)
-    oq, osc, ores = oracle.fused_add_rmsnorm_fp8_group(bits(x), bits(w), bits(r), eps, oracle.BF16)
+    oy, ores = oracle.fused_add_rmsnorm(bits(x), bits(w), bits(r), eps, oracle.BF16)
     for offset, pad, spad in ((0, 64, 0), (1, 3, 5)):
         xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
         buf = torch.zeros(rows, hidden + pad + offset, dtype=torch.uint8, device=DEV)
@@ -126,8 +132,10 @@ def test_fp8_group_strided_misaligned_output_and_scales(ops):
                                         torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         assert_residual_exact(bits(rd), ores, dtype)
-        assert oracle.e4m3_ulp_distance(qv.cpu().numpy(), oq).max() <= 1
-        np.testing.assert_allclose(sv.cpu().numpy(), osc, rtol=2.0 ** -7)
+        scales = sv.cpu().numpy()
+        assert_group_scales(scales, oy, 128, dtype)
+        assert_fp8_from_y_within_one_ulp(qv.cpu().numpy(), oy, np.repeat(np.float32(1.0) / scales, 128, axis=1),
+                                         dtype)
         assert not buf[:, :offset].any() and not buf[:, offset + hidden:].any()
         assert (sbuf[:, hidden // 128:] == -1.0).all()
 
