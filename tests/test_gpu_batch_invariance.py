@@ -73,7 +73,7 @@ def test_in_place_rows_do_not_depend_on_the_row_count(abi, invariant, dtype):
                                        f"{diff[0][0]}, element {diff[1][0]})")
 
 
-@pytest.mark.parametrize("form", ["plain", "out_of_place", "reduce", "fp8", "mxfp4"])
+@pytest.mark.parametrize("form", ["plain", "out_of_place", "reduce", "fp8", "fp8_static", "fp8_group", "mxfp4"])
 def test_other_forms_do_not_depend_on_the_row_count(abi, invariant, form):
     dtype = torch.bfloat16
     code = DT[dtype]
@@ -105,6 +105,19 @@ def test_other_forms_do_not_depend_on_the_row_count(abi, invariant, form):
                 sc = torch.empty(n, dtype=torch.float32, device=DEV)
                 abi.fused_add_rmsnorm_fp8(q.data_ptr(), sc.data_ptr(), xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), n,
                                           hidden, hidden, hidden, hidden, code, 1e-6, st)
+                outs = [q, sc, rd]
+            elif form == "fp8_static":
+                q = torch.empty((n, hidden), dtype=torch.uint8, device=DEV)
+                sc = torch.full((1,), 0.02, dtype=torch.float32, device=DEV)
+                abi.fused_add_rmsnorm_fp8_static(q.data_ptr(), sc.data_ptr(), xd.data_ptr(), wd.data_ptr(),
+                                                 rd.data_ptr(), n, hidden, hidden, hidden, hidden, code, 1e-6, st)
+                outs = [q, rd]
+            elif form == "fp8_group":
+                q = torch.empty((n, hidden), dtype=torch.uint8, device=DEV)
+                sc = torch.empty((n, hidden // 128), dtype=torch.float32, device=DEV)
+                abi.fused_add_rmsnorm_fp8_group(q.data_ptr(), sc.data_ptr(), xd.data_ptr(), wd.data_ptr(),
+                                                rd.data_ptr(), n, hidden, hidden, hidden // 128, hidden, hidden, code,
+                                                1e-6, st)
                 outs = [q, sc, rd]
             else:
                 q = torch.empty((n, hidden // 2), dtype=torch.uint8, device=DEV)
