@@ -91,6 +91,32 @@ def fp8_case(name, rows, hidden, dtype, eps, seed, special=None):
     return name, meta, arrs
 
 
+def fp8_static_case(name, rows, hidden, dtype, eps, seed, scale, special=None):
+    """The fused op's output quantised with one given scale for every row, as
+    torch evaluates it: q = e4m3fn(clamp(y * reciprocal(scale), -448, 448))."""
+    name, meta, arrs = fused_case(name, rows, hidden, dtype, eps, "bench", seed, special)
+    y = torch.from_numpy(arrs["out"].view(np.int16)).view(dtype).float()
+    q = (y * torch.reciprocal(torch.tensor(scale, dtype=torch.float32))).clamp(-448.0, 448.0)
+    meta["kind"] = "fp8_static"
+    meta["scale"] = scale
+    arrs["q"] = q.to(torch.float8_e4m3fn).view(torch.uint8).numpy().copy()
+    return name, meta, arrs
+
+
+def fp8_group_case(name, rows, hidden, dtype, eps, seed, special=None):
+    """The fused op's output quantised with one scale per 128 consecutive
+    elements, as torch evaluates it: per group scale = max(amax|y| / 448,
+    FLT_MIN), q = e4m3fn(clamp(y * (1 / scale), -448, 448))."""
+    name, meta, arrs = fused_case(name, rows, hidden, dtype, eps, "bench", seed, special)
+    y = torch.from_numpy(arrs["out"].view(np.int16)).view(dtype).float().view(rows, hidden // 128, 128)
+    scale = torch.clamp(y.abs().amax(-1, keepdim=True) / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (y * (1.0 / scale)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    meta["kind"] = "fp8_group"
+    arrs["q"] = q.view(rows, hidden).view(torch.uint8).numpy().copy()
+    arrs["scale"] = scale.view(rows, -1).numpy().copy()
+    return name, meta, arrs
+
+
 def sp_fp8_rows(x, r, w):
     x[0].zero_(); r[0].zero_()             # all-zero row: scale = FLT_MIN, q = 0
     x[1, 3] = float("nan")                 # NaN row: NaN scale, NaN outputs
@@ -126,6 +152,11 @@ def main():
         fp8_case("fp8_bf16_4x4096", 4, 4096, bf, 1e-6, 15),
         fp8_case("fp8_fp16_3x5120", 3, 5120, hf, 1e-6, 16),
         fp8_case("fp8_bf16_4x1000_tail", 4, 1000, bf, 1e-6, 17, sp_fp8_rows),
+        fp8_static_case("fp8_static_bf16_4x4096", 4, 4096, bf, 1e-6, 19, 0.02),
+        fp8_static_case("fp8_static_fp16_3x1000_tail", 3, 1000, hf, 1e-6, 20, 0.01, sp_fp8_rows),
+        fp8_group_case("fp8_group_bf16_4x4096", 4, 4096, bf, 1e-6, 21),
+        fp8_group_case("fp8_group_fp16_3x5120", 3, 5120, hf, 1e-6, 22),
+        fp8_group_case("fp8_group_bf16_4x1024_special", 4, 1024, bf, 1e-6, 23, sp_fp8_rows),
         stream_case("stream_bf16_3x384", 3, 384, bf, 13),
         stream_case("stream_fp16_2x1000", 2, 1000, hf, 14),
     ]

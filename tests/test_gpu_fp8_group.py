@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_residual_exact, bits,
-                     make_inputs, special_inputs)
+                     from_bits, make_inputs, special_inputs)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -80,6 +80,29 @@ def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6, special=Fal
     with np.errstate(divide="ignore"):
         assert_fp8_from_y_within_one_ulp(q_bits(q), oy, np.repeat(np.float32(1.0) / scales, 128, axis=1), dtype,
                                          "q " + tag)
+
+
+def test_fp8_group_golden_through_torch_op(ops, golden):
+    """torch's per-group quantisation of torch's own 16-bit output (golden
+    vectors): the residual bit-exact, the scales those of a group maximum
+    within one ulp of torch's, q the quantisation of a y within one 16-bit ulp
+    of torch's output."""
+    n = 0
+    for name, c in golden.items():
+        if c["kind"] != "fp8_group":
+            continue
+        dtype = torch.bfloat16 if c["dtype"] == "bf16" else torch.float16
+        x, r, w = (from_bits(c[k], dtype).to(DEV) for k in ("x", "r", "w"))
+        q, sc = ops.fused_add_rms_norm_fp8_group(x, r, w, c["eps"])
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(r), c["res"], dtype, name)
+        scales = sc.cpu().numpy()
+        assert_group_scales(scales, c["out"], 128, dtype, name)
+        with np.errstate(divide="ignore"):
+            isc = np.repeat(np.float32(1.0) / scales, 128, axis=1)
+        assert_fp8_from_y_within_one_ulp(q_bits(q), c["out"], isc, dtype, name)
+        n += 1
+    assert n >= 3
 
 
 @pytest.mark.parametrize("rows,hidden,dtype", [

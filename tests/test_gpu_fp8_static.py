@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DT, assert_fp8_from_y_within_one_ulp, assert_residual_exact, bits, make_inputs, special_inputs
+from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_residual_exact, bits, from_bits, make_inputs,
+                     special_inputs)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -66,6 +67,24 @@ def run_case(ops, rows, hidden, dtype, seed, scale, dist="bench", eps=1e-6, spec
     with np.errstate(divide="ignore", over="ignore"):
         isc = np.float32(1.0) / np.float32(scale)
     assert_fp8_from_y_within_one_ulp(q_bits(q), oy, isc, dtype, "q " + tag)
+
+
+def test_fp8_static_golden_through_torch_op(ops, golden):
+    """torch's static quantisation of torch's own 16-bit output (golden
+    vectors): the residual bit-exact, q the quantisation of a y within one
+    16-bit ulp of torch's output."""
+    n = 0
+    for name, c in golden.items():
+        if c["kind"] != "fp8_static":
+            continue
+        dtype = torch.bfloat16 if c["dtype"] == "bf16" else torch.float16
+        x, r, w = (from_bits(c[k], dtype).to(DEV) for k in ("x", "r", "w"))
+        q = ops.fused_add_rms_norm_fp8_static(x, r, w, torch.tensor([c["scale"]], device=DEV), c["eps"])
+        torch.cuda.synchronize()
+        assert_residual_exact(bits(r), c["res"], dtype, name)
+        assert_fp8_from_y_within_one_ulp(q_bits(q), c["out"], np.float32(1.0) / np.float32(c["scale"]), dtype, name)
+        n += 1
+    assert n >= 2
 
 
 @pytest.mark.parametrize("rows,hidden,dtype", [

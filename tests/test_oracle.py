@@ -375,6 +375,40 @@ def test_oracle_fp8_static_quantisation_matches_torch():
                 assert d.max() == 0, (code, kind, scale)
 
 
+def test_oracle_fp8_static_and_group_match_golden(golden):
+    """The torch-made golden vectors of the static and per-group FP8 forms: the
+    residual bit-exact; where the oracle's 16-bit output equals torch's (every
+    element for the static form, every element of a group for the per-group
+    form) q and the scales equal torch's bit for bit, and everywhere q is the
+    quantisation of a y within one 16-bit ulp of torch's output."""
+    from helpers import assert_fp8_from_y_within_one_ulp, assert_group_scales
+    seen = set()
+    for name, c in golden.items():
+        if c["kind"] not in ("fp8_static", "fp8_group"):
+            continue
+        seen.add(c["kind"])
+        code = BF if c["dtype"] == "bf16" else HF
+        dt = TDT[code]
+        y, _ = oracle.fused_add_rmsnorm(c["x"], c["w"], c["r"], c["eps"], code)
+        same = oracle.ulp_distance(y, c["out"], code) == 0
+        if c["kind"] == "fp8_static":
+            q, res = oracle.fused_add_rmsnorm_fp8_static(c["x"], c["w"], c["r"], c["eps"], code, c["scale"])
+            isc = np.float32(1.0) / np.float32(c["scale"])
+            assert np.array_equal(q[same], c["q"][same]), name
+        else:
+            q, sc, res = oracle.fused_add_rmsnorm_fp8_group(c["x"], c["w"], c["r"], c["eps"], code)
+            gsame = same.reshape(same.shape[0], -1, 128).all(-1)
+            assert np.array_equal(sc[gsame], c["scale"][gsame], equal_nan=True), name
+            assert_group_scales(sc, c["out"], 128, dt, name)
+            with np.errstate(divide="ignore"):
+                isc = np.repeat(np.float32(1.0) / sc, 128, axis=1)
+            eq = oracle.e4m3_ulp_distance(q, c["q"]) == 0
+            assert eq[np.repeat(gsame, 128, axis=1)].all(), name
+        assert oracle.ulp_distance(res, c["res"], code).max() == 0, name
+        assert_fp8_from_y_within_one_ulp(q, c["out"], isc, dt, name)
+    assert seen == {"fp8_static", "fp8_group"}
+
+
 def test_planted_fp8_static_mistakes_are_rejected():
     """Two plausible mistakes in the static step, planted in a copy of the
     oracle's composition, each fail the torch pin above: the reciprocal of the
