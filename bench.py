@@ -1080,13 +1080,20 @@ def run_extra(torch, ops, args):
         w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
         qs = [torch.empty(B, h, dtype=torch.float8_e4m3fn, device="cuda:0") for _ in range(n)]
         sc = torch.empty(B, h // 128, dtype=torch.float32, device="cuda:0")
+        # the column-major (token-minor) scale layout some block-scaled GEMMs read
+        sc_cols = torch.empty(h // 128, B, dtype=torch.float32, device="cuda:0").t()
 
         def call(i, sets=sets, qs=qs, sc=sc, w=w):
             ops.hp_rms_norm_fp8_group(qs[i], sc, sets[i][0], w, sets[i][1], EPS)
+
+        def call_cols(i, sets=sets, qs=qs, sc=sc_cols, w=w):
+            ops.hp_rms_norm_fp8_group(qs[i], sc, sets[i][0], w, sets[i][1], EPS)
         us = time_rotating(torch, call, n, steps, args.warmup)
+        us_cols = time_rotating(torch, call_cols, n, steps, args.warmup)
         nbytes = 7 * B * h + 2 * h + 4 * B * (h // 128)
         fp8g.append({"rows": B, "hidden": h, "us_per_call": round(us, 2),
-                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_call": nbytes})
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_call": nbytes,
+                     "us_per_call_column_major_scales": round(us_cols, 2)})
         del sets, qs
         torch.cuda.empty_cache()
     out["fp8_group128_output_bf16"] = fp8g

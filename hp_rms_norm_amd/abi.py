@@ -72,7 +72,8 @@ def _bind(L, bench):
     L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8_static.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
-    L.hprms_fused_add_rmsnorm_fp8_group.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
+    L.hprms_fused_add_rmsnorm_fp8_group.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, ci, cd,
+                                                    vp]
     L.hprms_fused_add_rmsnorm_out.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_reduce_add_rmsnorm.argtypes = [vp, ctypes.POINTER(vp), ci, vp, vp, i64, i64, i64, i64, i64, ci,
                                            cd, vp]
@@ -164,10 +165,11 @@ class Library:
             residual_stride, dtype, eps, stream))
 
     def fused_add_rmsnorm_fp8_group(self, out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden,
-                                    out_stride, scale_stride, input_stride, residual_stride, dtype, eps, stream=0):
+                                    out_stride, scale_stride, scale_group_stride, input_stride, residual_stride,
+                                    dtype, eps, stream=0):
         return self._check(self.lib().hprms_fused_add_rmsnorm_fp8_group(
             out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride, scale_stride,
-            input_stride, residual_stride, dtype, eps, stream))
+            scale_group_stride, input_stride, residual_stride, dtype, eps, stream))
 
     def fused_add_rmsnorm_out(self, out_ptr, residual_out_ptr, input_ptr, residual_ptr, weight_ptr, rows, hidden,
                               out_stride, residual_out_stride, input_stride, residual_stride, dtype, eps, stream=0):

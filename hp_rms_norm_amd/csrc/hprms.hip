@@ -489,6 +489,7 @@ struct Problem {
   const void* const* parts = nullptr;
   void* mx_scales = nullptr;   // modes 5, 6: E8M0 bytes; mode 7: float32
   int64_t mx_scale_stride = 0; // bytes
+  int64_t mx_group_stride = 4; // mode 7: bytes between a row's consecutive scales
   int64_t* timeline = nullptr; // configurations with flags bit 9 (bench library)
 };
 
@@ -497,6 +498,27 @@ bool is_mx(int mode) { return mode == 5 || mode == 6; }
 // and mode 7 (one float32 per 128 elements); either way hidden / 32 scale
 // bytes per row
 bool is_blockq(int mode) { return is_mx(mode) || mode == 7; }
+
+// Mode 7's scale (row r, group g) sits at byte r * mx_scale_stride + g *
+// mx_group_stride.  Bytes one row's scales span: (groups - 1) * group stride
+// + 4 (hidden / 32 for rows of scales).
+int64_t group_extent(const Problem& p) { return (p.hidden / 128 - 1) * p.mx_group_stride + 4; }
+
+// The scales form rows (each row's groups inside the gap to the next row) or
+// columns (each group's rows inside the gap to the next group), so no two
+// (row, group) pairs share a scale; interleaved layouts are refused.  Strides in bytes, at most 2^42 (the entry
+// point's bound), groups at most kMaxHidden / 128 = 2^17, so no product
+// here passes 2^59.
+bool group_scales_disjoint(const Problem& p) {
+  const int64_t groups = p.hidden / 128, rs = p.mx_scale_stride, gs = p.mx_group_stride;
+  if (rs < 0 || gs < 0) return false;
+  const bool rows_of_scales = (groups <= 1 || gs >= 4) && (p.rows <= 1 || rs >= (groups - 1) * gs + 4);
+  // (rows - 1) * rs + 4 <= gs <= 2^42, so rows past 2^42 / rs never fit
+  const bool columns = (p.rows <= 1 || rs >= 4) &&
+                       (groups <= 1 || (p.rows - 1 <= (int64_t(1) << 42) / (rs > 0 ? rs : 1) &&
+                                        gs >= (p.rows - 1) * rs + 4));
+  return rows_of_scales || columns;
+}
 // bytes of quantised output per row (modes 2, 5, 6)
 int64_t q_row_bytes(int mode, int64_t hidden) { return mode == 6 ? hidden / 2 : hidden; }
 
@@ -539,9 +561,12 @@ int check_problem(const Problem& p) {
   if (is_mx(p.mode) && p.mx_scale_stride < p.hidden / 32)
     return fail(HPRMS_E_INVALID, "scale row stride %lld < hidden / 32 = %lld", (long long)p.mx_scale_stride,
                 (long long)(p.hidden / 32));
-  if (p.mode == 7 && p.mx_scale_stride < p.hidden / 32)   // bytes: 4 per 128 elements
-    return fail(HPRMS_E_INVALID, "scale row stride %lld < hidden / 128 = %lld", (long long)(p.mx_scale_stride / 4),
-                (long long)(p.hidden / 128));
+  if (p.mode == 7 && !group_scales_disjoint(p))
+    return fail(HPRMS_E_INVALID,
+                "scale strides (row %lld, group %lld) lay the scales out neither as rows (row stride > "
+                "(hidden / 128 - 1) * group stride, group stride >= 1) nor as columns (group stride > "
+                "(rows - 1) * row stride, row stride >= 1)",
+                (long long)(p.mx_scale_stride / 4), (long long)(p.mx_group_stride / 4));
   if (p.mode == 3 && p.res_out_stride < p.hidden)
     return fail(HPRMS_E_INVALID, "residual output row stride %lld < hidden %lld", (long long)p.res_out_stride,
                 (long long)p.hidden);
@@ -554,7 +579,8 @@ int check_problem(const Problem& p) {
       (has_res(p.mode) && !extent_ok(p.rows, p.res_stride, 2, p.hidden)) ||
       (has_out(p.mode) && !extent_ok(p.rows, p.out_stride, ob, q_row_bytes(p.mode, p.hidden))) ||
       (p.mode == 3 && !extent_ok(p.rows, p.res_out_stride, 2, p.hidden)) ||
-      (is_blockq(p.mode) && !extent_ok(p.rows, p.mx_scale_stride, 1, p.hidden / 32)))
+      (is_mx(p.mode) && !extent_ok(p.rows, p.mx_scale_stride, 1, p.hidden / 32)) ||
+      (p.mode == 7 && !extent_ok(p.rows, p.mx_scale_stride, 1, group_extent(p))))
     return fail(HPRMS_E_RANGE, "%lld rows at these row strides span more than 2^56 bytes", (long long)p.rows);
   if (p.mode == 4 && !p.parts) return fail(HPRMS_E_INVALID, "null parts array");
   if (!p.x || !p.w || (has_res(p.mode) && !p.res) || (has_out(p.mode) && !p.out) ||
@@ -626,7 +652,8 @@ bool vec_fits(const Problem& p, const hprms_config& c) {
   if (has_res(p.mode) && p.res_stride > smax) smax = p.res_stride;
   if (p.mode == 3 && p.res_out_stride > smax) smax = p.res_out_stride;
   // the MX scale rows have their own buffer resource (byte stride)
-  if (is_blockq(p.mode) && (rpb - 1) * p.mx_scale_stride + p.hidden / 32 >= (int64_t)kOOB) return false;
+  if (is_mx(p.mode) && (rpb - 1) * p.mx_scale_stride + p.hidden / 32 >= (int64_t)kOOB) return false;
+  if (p.mode == 7 && (rpb - 1) * p.mx_scale_stride + group_extent(p) >= (int64_t)kOOB) return false;
   // a 128-element group of mode 7 is 16 adjacent lanes' vectors
   if (p.mode == 7 && c.lanes_per_row % 16 != 0) return false;
   if (((rpb - 1) * smax + p.hidden) * 2 + 16 * (int64_t)c.lanes_per_row * c.vec_per_lane >= (int64_t)kOOB)
@@ -939,6 +966,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   a.q_stride = p.mode == 2 || is_blockq(p.mode) ? p.out_stride : 0;
   a.mx_scale = (uint8_t*)p.mx_scales;
   a.mx_scale_stride = p.mx_scale_stride;
+  a.mx_group_stride = p.mx_group_stride;
   a.out_stride = p.mode == 0 || p.mode == 2 || is_blockq(p.mode) ? p.x_stride : p.out_stride;
   const Phase shift = (c.flags & 64) ? shift_phase(p) : Phase{0, 0};
   const Phase rot = (c.flags & 32) ? rot_phase(p) : Phase{0, 0};
@@ -1064,15 +1092,19 @@ int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const
 
 int hprms_fused_add_rmsnorm_fp8_group(void* out, float* scales, const void* input, const void* weight,
                                       void* residual, int64_t rows, int64_t hidden, int64_t out_row_stride,
-                                      int64_t scale_row_stride, int64_t input_row_stride,
-                                      int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
-  // the kernels take the scale row stride in bytes
-  if (scale_row_stride < 0 || scale_row_stride > (int64_t(1) << 60))
-    return fail(HPRMS_E_INVALID, "scale row stride %lld out of range", (long long)scale_row_stride);
+                                      int64_t scale_row_stride, int64_t scale_group_stride,
+                                      int64_t input_row_stride, int64_t residual_row_stride, int dtype, double eps,
+                                      hipStream_t stream) {
+  // the kernels take the scale strides in bytes
+  if (scale_row_stride < 0 || scale_row_stride > (int64_t(1) << 40) || scale_group_stride < 0 ||
+      scale_group_stride > (int64_t(1) << 40))
+    return fail(HPRMS_E_INVALID, "scale strides (row %lld, group %lld) out of range [0, 2^40]",
+                (long long)scale_row_stride, (long long)scale_group_stride);
   Problem p{7, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
             residual_row_stride, dtype, eps};
   p.mx_scales = scales;
   p.mx_scale_stride = scale_row_stride * 4;
+  p.mx_group_stride = scale_group_stride * 4;
   return run(p, nullptr, stream);
 }
 

@@ -98,7 +98,9 @@
 // per 128 consecutive elements of a row (the 16 adjacent lanes of a DPP row
 // at one vector index, so a group's maximum is one 16-lane DPP reduction):
 // scale = max(amax|y| / 448, FLT_MIN) and q = e4m3fn(clamp(y * (1 / scale)))
-// per group, as MODE 2 per row.
+// per group, as MODE 2 per row.  The scales sit at a row stride and a group
+// stride of their own, so rows of scales and the column-major (token-minor)
+// layout of block-scaled GEMMs are written alike.
 #pragma once
 
 #include "hprms_device.h"
@@ -139,6 +141,7 @@ struct FusedArgs {
   const uint16_t* parts[HPRMS_MAX_PARTS];  // MODE 4: parts[g] has row stride x_stride
   uint8_t* mx_scale;     // MODES 5, 6: E8M0 scale bytes; MODE 7: float32 scales (hidden / 32 bytes per row)
   int64_t mx_scale_stride;  // bytes between scale rows
+  int64_t mx_group_stride;  // MODE 7: bytes between a row's consecutive scales (4: rows of scales)
   int64_t* timeline;     // FLAGS bit 9 only (bench library): 4 values per workgroup
 };
 
@@ -440,6 +443,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     if constexpr (MODE >= 2 && LDSV == 0) __builtin_amdgcn_sched_barrier(0);
     __amdgpu_buffer_rsrc_t srs = rrs, ors = xrs, xsrs = xrs;
     uint32_t soff = roff, ooff = xoff, xsoff = 0, esoff = eroff, eooff = exoff;
+    uint32_t gs = 4;  // MODE 7: bytes between a row's consecutive scales
     if constexpr (MODE == 3) {
       uint16_t* const ro = opaque(a.res_out);
       const int64_t rs = opaque(a.res_out_stride);
@@ -468,13 +472,16 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
       xsoff = (lane & 3) == 0 ? (uint32_t)rib * (uint32_t)ss + (uint32_t)lane / 4u : kOOB;
     }
     if constexpr (GQ) {
-      // float32 scales, one per 128 elements; `mx_scale_stride` in bytes
+      // float32 scales, one per 128 elements; scale (row, group) at byte
+      // row * mx_scale_stride + group * mx_group_stride (row-major scales:
+      // group stride 4; column-major: row stride 4)
       uint8_t* const sp = opaque(a.mx_scale);
       const int64_t ss = opaque(a.mx_scale_stride);
-      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * ss + hidden / 32);
+      gs = (uint32_t)opaque(a.mx_group_stride);
+      const uint32_t sbytes = (uint32_t)((int64_t)(nrows - 1) * ss + (int64_t)(hidden / 128 - 1) * gs + 4);
       xsrs = make_rsrc(sp + row0 * ss, sbytes);
       // the first lane of each 16 writes its group's scale
-      xsoff = (lane & 15) == 0 ? (uint32_t)rib * (uint32_t)ss + (uint32_t)lane / 4u : kOOB;
+      xsoff = (lane & 15) == 0 ? (uint32_t)rib * (uint32_t)ss + (uint32_t)(lane / 16) * gs : kOOB;
     }
     if constexpr (MODE == 1) {
       // no residual: its (preloaded) arguments carry the output rows
@@ -753,7 +760,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         const float isc = 1.0f / sc;
         const bool ok = row_ok && vec_ok[k];
         // default cache policy, so that L2 merges a row's scales into lines
-        store4<0>(__float_as_uint(sc), xsrs, ok && xsoff != kOOB ? xsoff + (uint32_t)(k * (LPR / 16) * 4) : kOOB);
+        store4<0>(__float_as_uint(sc), xsrs, ok && xsoff != kOOB ? xsoff + (uint32_t)(k * (LPR / 16)) * gs : kOOB);
         u32x2 q;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {

@@ -273,7 +273,7 @@ void rms_norm_fp8_static_meta(at::Tensor& out, const at::Tensor& scale, const at
 // ---- FP8 output with a scale per 128 elements -------------------------------------------
 struct GroupShape {
   FusedShape f;
-  int64_t out_stride, scale_stride;
+  int64_t out_stride, scale_stride, scale_group_stride;
 };
 
 GroupShape check_fp8_group(const at::Tensor& out, const at::Tensor& scales, const at::Tensor& input,
@@ -287,14 +287,24 @@ GroupShape check_fp8_group(const at::Tensor& out, const at::Tensor& scales, cons
     TORCH_CHECK(t->dim() == input.dim(), "out and scales must have input.dim() dimensions");
     for (int64_t i = 0; i + 1 < input.dim(); ++i)
       TORCH_CHECK(t->size(i) == input.size(i), "out and scales must match input in the leading dimensions");
-    TORCH_CHECK(t->stride(-1) == 1, "out and scales must be contiguous in the last dimension");
     TORCH_CHECK(t->device() == input.device(), "out, scales and input must be on the same device");
   }
+  TORCH_CHECK(out.stride(-1) == 1, "out must be contiguous in the last dimension");
   TORCH_CHECK(out.size(-1) == s.f.hidden, "out.size(-1) == hidden_dim");
   TORCH_CHECK(scales.size(-1) == s.f.hidden / 128, "scales.size(-1) must be hidden / 128 = ", s.f.hidden / 128);
   int64_t r = 0;
   rows_of(out, s.f.hidden, &r, &s.out_stride);
-  rows_of(scales, s.f.hidden / 128, &r, &s.scale_stride);
+  // scales: rows of scales or the column-major (token-minor) layout; the
+  // leading dimensions must flatten to one row stride, and the C ABI rejects
+  // strides under which two (row, group) pairs share a scale
+  TORCH_CHECK(at::has_internal_overlap(scales) != at::MemOverlap::Yes, "scales must not overlap themselves");
+  s.scale_stride = 0;
+  s.scale_group_stride = 1;
+  if (s.f.hidden > 0) {
+    const at::Tensor flat = scales.view({-1, s.f.hidden / 128});
+    s.scale_stride = flat.size(0) <= 1 ? s.f.hidden / 128 : flat.stride(0);
+    s.scale_group_stride = flat.size(1) <= 1 ? 1 : flat.stride(1);
+  }
   if (s.f.rows > 0) {
     at::assert_no_overlap(out, scales);
     at::assert_no_overlap(out, residual);
@@ -313,8 +323,8 @@ void rms_norm_fp8_group_hip(at::Tensor& out, at::Tensor& scales, const at::Tenso
   hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
   check_status(hprms_fused_add_rmsnorm_fp8_group(out.data_ptr(), scales.data_ptr<float>(), input.data_ptr(),
                                                  weight.data_ptr(), residual.data_ptr(), s.f.rows, s.f.hidden,
-                                                 s.out_stride, s.scale_stride, s.f.in_stride, s.f.res_stride,
-                                                 s.f.dtype, eps, stream));
+                                                 s.out_stride, s.scale_stride, s.scale_group_stride,
+                                                 s.f.in_stride, s.f.res_stride, s.f.dtype, eps, stream));
 }
 
 void rms_norm_fp8_group_meta(at::Tensor& out, at::Tensor& scales, const at::Tensor& input, const at::Tensor& weight,

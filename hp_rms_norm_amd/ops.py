@@ -105,16 +105,30 @@ def hp_rms_norm_fp8_group(output, scales, input, weight, residual, eps):
     16-bit output, per group ``scales = max(amax|y| / 448, FLT_MIN)`` and
     ``output = float8_e4m3fn(clamp(y * (1 / scales), -448, 448))``.
     ``output``: float8_e4m3fn shaped like ``input``; ``scales``: float32
-    ``[..., H // 128]``.  ``input`` is only read.  Needs ``H % 128 == 0``.  No
-    reference counterpart."""
+    ``[..., H // 128]`` with any strides under which its leading dimensions
+    flatten to one row stride and no two elements share memory: rows of
+    scales, or the column-major (token-minor) layout that some block-scaled
+    GEMMs read, e.g. ``torch.empty(H // 128, T).t()``.  ``input`` is only
+    read.  Needs ``H % 128 == 0``.  No reference counterpart."""
     torch.ops.hp_rms_norm.rms_norm_fp8_group_quant.default(output, scales, input, weight, residual, eps)
 
 
-def fused_add_rms_norm_fp8_group(input, residual, weight, eps):
+def fused_add_rms_norm_fp8_group(input, residual, weight, eps, column_major_scales=False, scale_row_align=1):
     """Allocating form of ``hp_rms_norm_fp8_group``: returns ``(q, scales)``;
-    ``residual`` is updated in place."""
+    ``residual`` is updated in place.  ``column_major_scales``: the scales are
+    laid out token-minor (element ``(t, g)`` at ``g * T' + t``, where ``T'``
+    is the token count rounded up to a multiple of ``scale_row_align``, e.g.
+    4 for 16-byte aligned columns); the returned tensor is the ``[..., H //
+    128]`` view of that storage."""
     q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
-    scales = torch.empty(input.shape[:-1] + (input.shape[-1] // 128,), dtype=torch.float32, device=input.device)
+    groups = input.shape[-1] // 128
+    if column_major_scales:
+        tokens = input.numel() // input.shape[-1] if input.shape[-1] else 0
+        padded = -(-tokens // scale_row_align) * scale_row_align
+        store = torch.empty(groups, padded, dtype=torch.float32, device=input.device)
+        scales = store[:, :tokens].t().view(input.shape[:-1] + (groups,))
+    else:
+        scales = torch.empty(input.shape[:-1] + (groups,), dtype=torch.float32, device=input.device)
     torch.ops.hp_rms_norm.rms_norm_fp8_group_quant.default(q, scales, input, weight, residual, eps)
     return q, scales
 

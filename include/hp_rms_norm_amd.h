@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define HPRMS_ABI_VERSION 7
+#define HPRMS_ABI_VERSION 8
 
 /* element types (the reference accepts exactly these two:
  * hp_rms_norm/csrc/cuda/hp_rms_norm.cu:29-49) */
@@ -209,17 +209,27 @@ int hprms_fused_add_rmsnorm_mx(void* out, void* scales, const void* input, const
  *   per group g of 128 consecutive elements of row r:
  *     scales[r, g] =  max(max |y| / 448, FLT_MIN)   (NaN if the group holds a NaN)
  *     out          =  e4m3fn(clamp(y * (1 / scales[r, g]), -448, 448))
- * `out` is [rows, hidden] bytes with its row stride in bytes; `scales` is
- * [rows, hidden / 128] float32, 4-byte aligned, with its row stride in
- * elements.  `input` is only read.  Needs hidden % 128 == 0 and the same
- * layouts as hprms_fused_add_rmsnorm_mx (no general-tier fallback); other
- * calls return HPRMS_E_INVALID.  No counterpart in the reference.
+ * `out` is [rows, hidden] bytes with its row stride in bytes.  `scales` is
+ * float32, 4-byte aligned; scales[r, g] sits at element
+ * r * scale_row_stride + g * scale_group_stride: rows of scales
+ * (scale_group_stride 1, scale_row_stride >= hidden / 128) or the
+ * column-major, token-minor layout some block-scaled GEMMs read
+ * (scale_row_stride 1, scale_group_stride >= rows, e.g. rows rounded up to a
+ * multiple of 4).  Any strides in [0, 2^40] under which no two (row, group)
+ * pairs share a scale are taken: the scales form rows (scale_row_stride >
+ * (hidden / 128 - 1) * scale_group_stride, scale_group_stride >= 1) or
+ * columns (scale_group_stride > (rows - 1) * scale_row_stride,
+ * scale_row_stride >= 1).  `input` is only read.  Needs hidden % 128 == 0
+ * and the same layouts as hprms_fused_add_rmsnorm_mx (no general-tier
+ * fallback; a row group's scales, too, within 2 GiB); other calls return
+ * HPRMS_E_INVALID.  No counterpart in the reference.
  */
 int hprms_fused_add_rmsnorm_fp8_group(void* out, float* scales, const void* input, const void* weight,
                                       void* residual, int64_t rows, int64_t hidden,
                                       int64_t out_row_stride, int64_t scale_row_stride,
-                                      int64_t input_row_stride, int64_t residual_row_stride,
-                                      int dtype, double eps, hipStream_t stream);
+                                      int64_t scale_group_stride, int64_t input_row_stride,
+                                      int64_t residual_row_stride, int dtype, double eps,
+                                      hipStream_t stream);
 
 /*
  * Kernel configuration of the fused add+RMSNorm family.  Used by the tuning

@@ -52,9 +52,9 @@ int main(void) {
                                      1e-6, NULL) == HPRMS_OK);
   EXPECT(hprms_fused_add_rmsnorm_fp8_static(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 4096, 4096,
                                             HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
-  EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 32, 4096, 4096,
+  EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 32, 1, 4096, 4096,
                                            HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
-  EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4000, 4000, 32, 4000, 4000,
+  EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4000, 4000, 32, 1, 4000, 4000,
                                            HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_E_INVALID);
   EXPECT(hprms_reduce_add_rmsnorm(NULL, NULL, 3, NULL, NULL, 0, 4096, 4096, 4096, 4096, HPRMS_DTYPE_BF16, 1e-6,
                                   NULL) == HPRMS_OK);

@@ -511,16 +511,27 @@ def test_plain_c_caller_compiles_links_and_runs(tmp_path):
 
 def test_fp8_group_entry_rejects_bad_arguments():
     L = abi.lib()
-    ok = dict(out=0x4000, sc=0x5000, x=0x1000, w=0x2000, r=0x3000, h=4096, so=4096, ss=32)
+    ok = dict(out=0x4000, sc=0x5000, x=0x1000, w=0x2000, r=0x3000, h=4096, so=4096, ss=32, gs=1)
 
     def call(**kw):
         a = dict(ok, **kw)
         return L.hprms_fused_add_rmsnorm_fp8_group(a["out"], a["sc"], a["x"], a["w"], a["r"], a.get("rows", 4),
-                                                   a["h"], a["so"], a["ss"], a["h"], a["h"], 0, 1e-6, None)
+                                                   a["h"], a["so"], a["ss"], a["gs"], a["h"], a["h"], 0, 1e-6, None)
     assert call(h=4160, so=4160, ss=33) == abi.HPRMS_E_INVALID and "128" in abi.last_error()
     assert call(so=2048) == abi.HPRMS_E_INVALID and "output row stride" in abi.last_error()
-    assert call(ss=31) == abi.HPRMS_E_INVALID and "scale row stride" in abi.last_error()
-    assert call(ss=-1) == abi.HPRMS_E_INVALID and "scale row stride" in abi.last_error()
+    # scale strides that lay the scales out neither as rows nor as columns: rows of scales
+    # that overlap, groups that collide, columns (rows = 4) that overlap, and (3, 8), which
+    # interleaves rows and groups without a collision
+    for ss, gs in ((31, 1), (0, 1), (32, 0), (62, 2), (1, 3), (2, 6), (1, 1), (3, 8)):
+        assert call(ss=ss, gs=gs) == abi.HPRMS_E_INVALID and "neither as rows" in abi.last_error(), (ss, gs)
+    for ss, gs in ((-1, 1), (32, -1), (32, 1 << 41), (1 << 41, 1)):
+        assert call(ss=ss, gs=gs) == abi.HPRMS_E_INVALID and "out of range" in abi.last_error(), (ss, gs)
+    # one row, or one group: the other stride is free
+    assert call(rows=0, ss=0, gs=0, h=128, so=128) == abi.HPRMS_OK
+    # a row group's scales must fit one buffer resource (H = 128: 64 rows per workgroup,
+    # the column-major group stride spans 2^29 floats)
+    assert call(rows=0, h=256, so=256, ss=1, gs=1 << 29) == abi.HPRMS_E_INVALID and "2 GiB" in abi.last_error()
+    assert call(rows=0, h=256, so=256, ss=1, gs=1 << 20) == abi.HPRMS_OK
     assert call(sc=0) == abi.HPRMS_E_INVALID and "null" in abi.last_error()
     assert call(sc=0x5002) == abi.HPRMS_E_INVALID and "4-byte aligned" in abi.last_error()
     # outputs and rows off the 16-byte grid take the unaligned variants; odd addresses are refused

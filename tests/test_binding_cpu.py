@@ -202,6 +202,13 @@ def test_fp8_group_op_schema_and_meta_checks():
         ops.hp_rms_norm_fp8_group(q, torch.empty(4, 4, device=M, dtype=torch.float16), x, w, r, 1e-6)
     with pytest.raises(RuntimeError, match="hidden / 128"):
         ops.hp_rms_norm_fp8_group(q, torch.empty(4, 16, device=M), x, w, r, 1e-6)
+    # column-major scales (a transposed view) pass the checks; scales that overlap themselves do not
+    assert ops.hp_rms_norm_fp8_group(q, torch.empty(4, 4, device=M).t(), x, w, r, 1e-6) is None
+    q3, sc3 = ops.fused_add_rms_norm_fp8_group(t(2, 3, 512), t(2, 3, 512), w, 1e-6, column_major_scales=True,
+                                               scale_row_align=4)
+    assert sc3.shape == (2, 3, 4) and sc3.stride() == (3, 1, 8)
+    with pytest.raises(RuntimeError, match="overlap themselves"):
+        ops.hp_rms_norm_fp8_group(q, torch.empty(1, 4, device=M).expand(4, 4), x, w, r, 1e-6)
 
 
 def test_out_of_place_and_reduce_schemas():

@@ -116,8 +116,8 @@ def test_other_forms_do_not_depend_on_the_row_count(abi, invariant, form):
                 q = torch.empty((n, hidden), dtype=torch.uint8, device=DEV)
                 sc = torch.empty((n, hidden // 128), dtype=torch.float32, device=DEV)
                 abi.fused_add_rmsnorm_fp8_group(q.data_ptr(), sc.data_ptr(), xd.data_ptr(), wd.data_ptr(),
-                                                rd.data_ptr(), n, hidden, hidden, hidden // 128, hidden, hidden, code,
-                                                1e-6, st)
+                                                rd.data_ptr(), n, hidden, hidden, hidden // 128, 1, hidden, hidden,
+                                                code, 1e-6, st)
                 outs = [q, sc, rd]
             else:
                 q = torch.empty((n, hidden // 2), dtype=torch.uint8, device=DEV)

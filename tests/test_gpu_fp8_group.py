@@ -151,8 +151,8 @@ def test_fp8_group_strided_misaligned_output_and_scales(ops):
         sbuf = torch.full((rows, hidden // 128 + spad), -1.0, dtype=torch.float32, device=DEV)
         sv = sbuf[:, :hidden // 128]
         abi.fused_add_rmsnorm_fp8_group(qv.data_ptr(), sv.data_ptr(), xd.data_ptr(), wd.data_ptr(), rd.data_ptr(),
-                                        rows, hidden, qv.stride(0), sv.stride(0), hidden, hidden, abi.DTYPE_BF16, eps,
-                                        torch.cuda.current_stream().cuda_stream)
+                                        rows, hidden, qv.stride(0), sv.stride(0), 1, hidden, hidden, abi.DTYPE_BF16,
+                                        eps, torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         assert_residual_exact(bits(rd), ores, dtype)
         scales = sv.cpu().numpy()
@@ -177,3 +177,61 @@ def test_fp8_group_of_one_group_rows_equals_the_per_row_form(ops):
     assert torch.equal(rd.view(torch.int16), rd2.view(torch.int16))
     assert oracle.e4m3_ulp_distance(q_bits(q), q_bits(q1)).max() <= 1
     np.testing.assert_allclose(sc.cpu().numpy().reshape(-1), sc1.cpu().numpy().reshape(-1), rtol=2.0 ** -7)
+
+
+@pytest.mark.parametrize("rows,hidden,pad", [(4096, 4096, 0), (4093, 7168, 3), (1, 4096, 3), (37, 128, 0),
+                                             (300, 16384, 1), (2049, 32768, 3)])
+def test_fp8_group_column_major_scales_through_the_abi(ops, rows, hidden, pad):
+    """Scales in the column-major (token-minor) layout: scale (r, g) at element
+    g * (rows + pad) + r of a [groups, rows + pad] buffer; the same q, scales
+    and residual as the row-major call, bit for bit (the layout does not change
+    the kernel's shape), and the padding columns untouched."""
+    from hp_rms_norm_amd import abi
+    print("fp8 group column-major", rows, hidden, pad, flush=True)
+    x, r, w = make_inputs(rows, hidden, torch.bfloat16, rows + hidden)
+    st = torch.cuda.current_stream().cuda_stream
+    ng = hidden // 128
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    q = torch.empty(rows, hidden, dtype=torch.uint8, device=DEV)
+    sb = torch.full((ng, rows + pad), -1.0, dtype=torch.float32, device=DEV)
+    abi.fused_add_rmsnorm_fp8_group(q.data_ptr(), sb.data_ptr(), xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), rows,
+                                    hidden, hidden, 1, rows + pad, hidden, hidden, abi.DTYPE_BF16, 1e-6, st)
+    xd2, rd2 = x.to(DEV), r.to(DEV)
+    q2 = torch.empty(rows, hidden, dtype=torch.uint8, device=DEV)
+    s2 = torch.empty(rows, ng, dtype=torch.float32, device=DEV)
+    abi.fused_add_rmsnorm_fp8_group(q2.data_ptr(), s2.data_ptr(), xd2.data_ptr(), wd.data_ptr(), rd2.data_ptr(), rows,
+                                    hidden, hidden, ng, 1, hidden, hidden, abi.DTYPE_BF16, 1e-6, st)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(rd.view(torch.int16), rd2.view(torch.int16))
+    assert same_floats(sb[:, :rows].t().cpu().numpy(), s2.cpu().numpy())
+    assert (sb[:, rows:] == -1.0).all()
+    oy, ores = oracle.fused_add_rmsnorm(bits(x), bits(w), bits(r), 1e-6, oracle.BF16,
+                                        threads=min(16, oracle.max_threads()))
+    assert_residual_exact(bits(rd), ores, torch.bfloat16)
+    scales = sb[:, :rows].t().cpu().numpy()
+    assert_group_scales(scales, oy, 128, torch.bfloat16)
+    assert_fp8_from_y_within_one_ulp(q_bits(q), oy, np.repeat(np.float32(1.0) / scales, 128, axis=1), torch.bfloat16)
+
+
+def test_fp8_group_column_major_scales_through_the_torch_op(ops):
+    """The allocating form with column-major scales, 16-byte aligned columns
+    (tokens rounded up to a multiple of 4), on a [batch, seq, H] input; and the
+    in-place form given a transposed view: both equal the row-major form."""
+    b, s_, hidden = 3, 343, 5120
+    x, r, w = make_inputs(b * s_, hidden, torch.bfloat16, 91)
+    x, r = x.view(b, s_, hidden), r.view(b, s_, hidden)
+    wd = w.to(DEV)
+    xd, rd = x.to(DEV), r.to(DEV)
+    q, sc = ops.fused_add_rms_norm_fp8_group(xd, rd, wd, 1e-6, column_major_scales=True, scale_row_align=4)
+    assert sc.shape == (b, s_, hidden // 128) and sc.stride(-1) == -(-b * s_ // 4) * 4 and sc.stride(1) == 1
+    xd2, rd2 = x.to(DEV), r.to(DEV)
+    q2, sc2 = ops.fused_add_rms_norm_fp8_group(xd2, rd2, wd, 1e-6)
+    xd3, rd3 = x.to(DEV), r.to(DEV)
+    q3 = torch.empty_like(q)
+    sc3 = torch.full((hidden // 128, b * s_), -1.0, device=DEV)
+    ops.hp_rms_norm_fp8_group(q3, sc3.t().view(b, s_, hidden // 128), xd3, wd, rd3, 1e-6)
+    torch.cuda.synchronize()
+    for qq, ss, rr in ((q, sc, rd), (q3, sc3.t().view(b, s_, -1), rd3)):
+        assert torch.equal(qq.view(torch.uint8), q2.view(torch.uint8))
+        assert same_floats(ss.cpu().numpy(), sc2.cpu().numpy())
+        assert torch.equal(rr.view(torch.int16), rd2.view(torch.int16))

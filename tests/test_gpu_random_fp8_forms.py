@@ -4,7 +4,8 @@ against the CPU oracle: the residual bit-exact, q the quantisation of a y
 within one 16-bit ulp of the oracle's output, the per-group scales those of a
 group maximum within one ulp of the oracle's, the bytes around every written
 region untouched.  Widths cover the table's rows (any width for the static
-form, multiples of 128 for the per-group form), row counts from 1 to a few
+form, multiples of 128 for the per-group form, whose scales are rows or
+columns), row counts from 1 to a few
 thousand, row strides and offsets that move rows off the 16- and 128-byte
 grids, both dtypes, eps 0 and 1e-6, and rows of special values.  Each case is
 printed before it runs.
@@ -83,17 +84,26 @@ def run_case(abi, i, c):
             isc = np.float32(1.0) / np.float32(c["scale"])
     else:
         ng = hidden // 128
-        sb = torch.full((rows, offs[3] + ng + pads[3]), -1.0, dtype=torch.float32, device=DEV)
-        sv = sb[:, offs[3]:offs[3] + ng]
+        colmajor = random.Random(i).random() < 0.4
+        if colmajor:
+            # column-major scales: [groups, rows + pad] with the rows at an offset
+            t += " (column-major scales)"
+            sb = torch.full((ng, offs[3] + rows + pads[3]), -1.0, dtype=torch.float32, device=DEV)
+            sv = sb[:, offs[3]:offs[3] + rows].t()
+        else:
+            sb = torch.full((rows, offs[3] + ng + pads[3]), -1.0, dtype=torch.float32, device=DEV)
+            sv = sb[:, offs[3]:offs[3] + ng]
         abi.fused_add_rmsnorm_fp8_group(q.data_ptr(), sv.data_ptr(), xv.data_ptr(), wd.data_ptr(), rv.data_ptr(),
-                                        rows, hidden, qb.stride(0), sb.stride(0), xv.stride(0), rv.stride(0), code,
-                                        eps, st)
+                                        rows, hidden, qb.stride(0), sv.stride(0), sv.stride(1), xv.stride(0),
+                                        rv.stride(0), code, eps, st)
         torch.cuda.synchronize()
         scales = sv.cpu().numpy()
         assert_group_scales(scales, oy, 128, dtype, "scales " + t)
         with np.errstate(divide="ignore"):
             isc = np.repeat(np.float32(1.0) / scales, 128, axis=1)
-        assert (sb[:, :offs[3]] == -1.0).all() and (sb[:, offs[3] + ng:] == -1.0).all(), "scales outside " + t
+        written = torch.zeros_like(sb, dtype=torch.bool)
+        (written[:, offs[3]:offs[3] + rows] if colmajor else written[:, offs[3]:offs[3] + ng]).fill_(True)
+        assert (sb[~written] == -1.0).all(), "scales outside " + t
     assert_residual_exact(bits(rv), ores, dtype, "residual " + t)
     assert np.array_equal(bits(xv), bits(x)), "input modified " + t
     assert_fp8_from_y_within_one_ulp(q.contiguous().cpu().numpy(), oy, isc, dtype, "q " + t)
