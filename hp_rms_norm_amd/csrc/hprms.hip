@@ -55,6 +55,8 @@ const FusedEntry kFused[] = {
     HPRMS_ALL_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16)
     HPRMS_MX_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16)
     HPRMS_MX_MODES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16)
+    HPRMS_QUANT_RUNS(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16)
+    HPRMS_QUANT_RUNS(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16)
 #ifdef HPRMS_BENCH_BUILD
     HPRMS_OTHER_MODE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_OTHER_MODE_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_FP16, 0)
@@ -450,20 +452,39 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, int cus, hp
 // at 64 KiB (H = 32768) runs of 8 ranged from 3.6% faster to 4% slower with
 // the row count.  The order only changes which workgroup takes a row, so the
 // bits are the same.
+// The quantised outputs (modes 2, 5, 6, 7) at 16 KiB rows with their table
+// kernel (512 x 2), runs of 32: 0.7-1.1% faster at 4096 rows (three
+// interleaved trials), and 6% for mode 7 with column-major scales.  Those
+// scales are 4-byte stores, 32 rows to a 128-byte line; with one row per
+// workgroup the 32 rows of a line otherwise go to all 8 XCDs, and each XCD's
+// L2 writes its part of the line back on its own.  Mode 7 with column-major
+// scales also takes runs of 32 at 8 KiB rows (256 x 2): 2.6-3.5% faster;
+// there the other quantised outputs and mode 7 with rows of scales were
+// within 0.5% either way, so left out.  At 32 and 64 KiB rows (1024 lanes,
+// one row per workgroup) runs of 8-64 were 3-11% slower in mode 7.
 struct RunsRow {
+  unsigned modes;       // bit m: mode m
+  bool scale_columns;   // mode 7 with column-major scales only
   int64_t pitch_bytes;
   int lpr, vpl, block, flags, v;
   int64_t min_rows;  // on 256 CUs
 };
-constexpr RunsRow kRuns[] = {{8192, 256, 2, 256, 131, 5, 4096}, {16384, 512, 2, 512, 7, 6, 2048}};
+constexpr unsigned kQuantModes = 1u << 2 | 1u << 5 | 1u << 6 | 1u << 7;
+constexpr RunsRow kRuns[] = {{1u, false, 8192, 256, 2, 256, 131, 5, 4096},
+                             {1u, false, 16384, 512, 2, 512, 7, 6, 2048},
+                             {kQuantModes, false, 16384, 512, 2, 512, 7, 5, 4096},
+                             {1u << 7, true, 8192, 256, 2, 256, 7, 5, 4096}};
 
-// flags bits 16-18 for configuration c of the in-place op (mode 0) on rows
-// `pitch_bytes` apart in both streams, on the 128-byte grid; 0 for others
-int xcd_runs_flags(int mode, int64_t rows, int64_t pitch_bytes, int cus, const hprms_config& c) {
-  if (mode != 0 || c.tier != 1 || c.lds_vec_per_lane != 0) return 0;
+// flags bits 16-18 for configuration c of mode `mode` on rows `pitch_bytes`
+// apart in both input streams, on the 128-byte grid (scale_columns: mode 7's
+// scales are column-major); 0 for others
+int xcd_runs_flags(int mode, int64_t rows, int64_t pitch_bytes, int cus, const hprms_config& c,
+                   bool scale_columns) {
+  if (c.tier != 1 || c.lds_vec_per_lane != 0) return 0;
   for (const RunsRow& r : kRuns)
-    if (r.pitch_bytes == pitch_bytes && r.lpr == c.lanes_per_row && r.vpl == c.vec_per_lane &&
-        r.block == c.block_threads && r.flags == c.flags && rows_at_ref(rows, cus) >= r.min_rows)
+    if (((r.modes >> mode) & 1u) && (!r.scale_columns || scale_columns) && r.pitch_bytes == pitch_bytes &&
+        r.lpr == c.lanes_per_row && r.vpl == c.vec_per_lane && r.block == c.block_threads && r.flags == c.flags &&
+        rows_at_ref(rows, cus) >= r.min_rows)
       return r.v << 16;
   return 0;
 }
@@ -916,7 +937,9 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
       c.flags = unaligned_flags(p, c.flags);
       tail_shape(p, cus, &c);
     } else if (!off_grid && p.x_stride == p.res_stride) {
-      c.flags |= xcd_runs_flags(p.mode, p.rows, p.x_stride * 2, cus, c);
+      // mode 7's scales in columns: one float per row, each group a column
+      const bool scale_columns = p.mode == 7 && p.mx_scale_stride == 4 && p.hidden > 128;
+      c.flags |= xcd_runs_flags(p.mode, p.rows, p.x_stride * 2, cus, c, scale_columns);
     }
   }
   if ((c.flags & 512) && !p.timeline)
@@ -1126,7 +1149,7 @@ int hprms_select_config_cu(int64_t rows, int64_t hidden, int dtype, int mode, in
   // the choice for rows on the 128-byte grid; odd widths: the tail variant of
   // the choice for rows off it
   table_config(rows, hidden, mode, hidden % 8 == 0, cu_count, config);
-  if (hidden % 8 == 0) config->flags |= xcd_runs_flags(mode, rows, hidden * 2, cu_count, *config);
+  if (hidden % 8 == 0) config->flags |= xcd_runs_flags(mode, rows, hidden * 2, cu_count, *config, false);
   if (hidden % 8 != 0) {
     if (config->tier != 3 && hidden >= 8 && mode <= 4) {
       Problem p{mode, nullptr, nullptr, nullptr, nullptr, rows, hidden, hidden, hidden, hidden, dtype, 0.0};

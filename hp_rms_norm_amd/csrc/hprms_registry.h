@@ -106,6 +106,13 @@ struct FusedEntry {
   X(DT, MODE, 128, 6, 0, 128, 135) X(DT, MODE, 128, 7, 0, 128, 135) X(DT, MODE, 128, 8, 0, 128, 135)
 // the in-place op's rows with their row groups in runs per XCD (hprms.hip, kRuns)
 #define HPRMS_RUNS_ROWS(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131 | 327680) X(DT, MODE, 512, 2, 0, 512, 7 | 393216)
+// the quantised outputs' rows with runs of 32 row groups per XCD (hprms.hip,
+// kRuns; aligned registry only): 16 KiB rows in modes 2, 5, 6, 7, and 8 KiB
+// rows in mode 7 (column-major scales)
+#define HPRMS_QUANT_RUNS(X, DT)                                                                    \
+  X(DT, 2, 512, 2, 0, 512, 7 | 327680) X(DT, 5, 512, 2, 0, 512, 7 | 327680)                       \
+  X(DT, 6, 512, 2, 0, 512, 7 | 327680) X(DT, 7, 512, 2, 0, 512, 7 | 327680)                       \
+  X(DT, 7, 256, 2, 0, 256, 7 | 327680)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
   HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE) HPRMS_PAIR_ROWS(X, DT, MODE) HPRMS_RUNS_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)

@@ -260,9 +260,10 @@ typedef struct {
                                with aligned loads into LDS, where shifted rows read it;
                                bit 15 (partial sums, the latency rows): every part's loads
                                issued before the first part is added;
-                               bits 16-18, V > 0 (the in-place op at two row pitches):
-                               each XCD takes runs of 2^V consecutive row groups rather
-                               than every 8th (the same results) */
+                               bits 16-18, V > 0 (the in-place op and the quantised
+                               outputs at some row pitches): each XCD takes runs of 2^V
+                               consecutive row groups rather than every 8th (the same
+                               results) */
 } hprms_config;
 
 int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residual,
@@ -306,10 +307,12 @@ int hprms_fused_add_rmsnorm_config(void* input, const void* weight, void* residu
  *     (flags & ~24) | 32: the unaligned variant without sc1 (rows off a
  *     512-byte boundary are then rotated, as above).
  *   - Mode 0 reports bits 16-18 (row groups in runs per XCD) for hidden 4096
- *     from 4096 rows and hidden 8192 from 2048 rows; calls take them when
- *     their input and residual rows are on the grid with that pitch (8 KiB,
- *     16 KiB) and the table's shape.  Every variant above takes its row
- *     groups in the default order.
+ *     from 4096 rows and hidden 8192 from 2048 rows, and modes 2, 5, 6 and 7
+ *     for hidden 8192 from 4096 rows; calls take them when their input and
+ *     residual rows are on the grid with that pitch (8 KiB, 16 KiB) and the
+ *     table's shape.  Mode 7 with column-major scales (row stride 1) also
+ *     takes them for hidden 4096 from 4096 rows.  Every variant above takes
+ *     its row groups in the default order.
  * Pure function of its arguments; touches no device. */
 int hprms_select_config(int64_t rows, int64_t hidden, int dtype, int mode, hprms_config* config);
 

@@ -223,3 +223,16 @@ def assert_group_scales(scales, y_oracle, group, dtype, what="scales"):
         ok |= (got.view(np.uint32) == sc.view(np.uint32)) | (np.isnan(got) & np.isnan(sc))
     bad = np.argwhere(~ok)
     assert bad.size == 0, f"{what}: {len(bad)} scales off; first {bad[0]}: {got[tuple(bad[0])]}"
+
+
+def lane_mapping(abi, cfg):
+    """`cfg` without the row-order bits (xcd_xor, bit 10; runs per XCD, bits
+    16-18): the same lanes, vectors and flags, so the same result for every
+    row, with the row groups in the default order.  The 16-bit op that tests
+    run with a quantised form's configuration has no run variants of the
+    quantised forms' shapes."""
+    if cfg is None or cfg.tier == 3:
+        return cfg
+    c = abi.Config(*cfg.as_tuple())
+    c.flags &= ~(1024 | (7 << 16))
+    return c

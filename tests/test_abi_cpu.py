@@ -360,10 +360,11 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 assert t in built[(dtype, mode)], (hidden, mode, t)
                 # the choice for rows off the grid (odd widths report it: the tail
                 # variant, with the sc1 bits the dispatch keeps) in its unaligned and
-                # tail variants, with and without sc1
+                # tail variants, with and without sc1; rows off the grid keep the default
+                # row-group order (no runs per XCD, bits 16-18)
                 hw = hidden + (1 if hidden % 8 == 0 and mode <= 4 else 0)
                 off = abi.select_config(rows, hw, dtype, mode).as_tuple()
-                u = (off[6] & ~(24 | 64 | 16384)) | 32
+                u = (off[6] & ~(24 | 64 | 16384 | (7 << 16))) | 32
                 if mode in (0, 3, 4) and off[1] == 1024 and off[2] in (2, 3):
                     u &= ~4   # the weight loaded late by the tail variant only
                 assert off[:6] + (u,) in built[(dtype, mode)], (hidden, mode, off)
@@ -385,10 +386,11 @@ def test_table_covers_every_hidden_with_a_built_kernel():
                 assert rc == abi.HPRMS_OK, (hidden, c.as_tuple(), abi.last_error())
                 # the bench library also has the FP8 and partial-sum tables' choices as
                 # fused (mode 0) kernels, so the 16-bit op can be run with the same lane
-                # mapping (the partial sums' part prefetch has no in-place form)
+                # mapping (the partial sums' part prefetch has no in-place form; the tests
+                # run it in the default row-group order, which changes no row's result)
                 for other in (2, 4):
                     c8 = abi.select_config(rows, hidden, dtype, other)
-                    c8.flags &= ~32768
+                    c8.flags &= ~(32768 | (7 << 16))
                     assert c8.lanes_per_row * c8.vec_per_lane * 8 >= hidden
                     rc = abi.BENCH.lib().hprms_fused_add_rmsnorm_config(0, 0, 0, 0, hidden, hidden, hidden,
                                                                         dtype, 1e-6, ctypes.byref(c8), None)
@@ -665,6 +667,8 @@ def _reachable(dtype, mode):
                 continue
             shape = (c.tier, c.lanes_per_row, c.vec_per_lane, c.lds_vec_per_lane, c.block_threads, 0)
             out.add(shape + (c.flags,))
+            if mode == 7 and nvec == 512 and rows >= 4096 and c.flags == 7 and shape[1:5] == (256, 2, 0, 256):
+                out.add(shape + (7 | 5 << 16,))   # column-major scales at 8 KiB rows: runs of 32 per XCD
             c.flags &= ~(7 << 16)   # the variants keep the default row-group order
             if c.flags & 24:
                 out.add(shape + ((c.flags & ~24) | 32,))

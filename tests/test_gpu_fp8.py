@@ -13,8 +13,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_residual_exact, bits,
-                     from_bits, make_inputs)
+from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_residual_exact, bits, from_bits,
+                     lane_mapping, make_inputs)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -49,7 +49,7 @@ def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6):
     # (the same fp32 reduction order, hence the same y); the bench library
     # holds that shape for the 16-bit op where the FP8 table has a row of its own
     from hp_rms_norm_amd import abi
-    cfg = abi.select_config(rows, hidden, DT[dtype], 2)
+    cfg = lane_mapping(abi, abi.select_config(rows, hidden, DT[dtype], 2))
     y, r16 = x.to(DEV), r.to(DEV)
     abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
                                 eps, torch.cuda.current_stream().cuda_stream, None if cfg.tier == 3 else cfg)

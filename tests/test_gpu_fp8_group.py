@@ -15,8 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_residual_exact, bits,
-                     from_bits, make_inputs, special_inputs)
+from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_residual_exact, bits, from_bits,
+                     lane_mapping, make_inputs, special_inputs)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -59,7 +59,7 @@ def run_case(ops, rows, hidden, dtype, seed, dist="bench", eps=1e-6, special=Fal
     q, sc = ops.fused_add_rms_norm_fp8_group(xd, rd, wd, eps)
     # the same inputs through the 16-bit op with this form's lane mapping
     # (the same fp32 reduction order, hence the same y)
-    cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_FP8_GROUP)
+    cfg = lane_mapping(abi, abi.select_config(rows, hidden, DT[dtype], abi.MODE_FP8_GROUP))
     assert cfg.tier in (1, 2), cfg.as_tuple()
     y, r16 = x.to(DEV), r.to(DEV)
     abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],

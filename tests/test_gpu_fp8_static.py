@@ -13,8 +13,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_residual_exact, bits, from_bits, make_inputs,
-                     special_inputs)
+from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_residual_exact, bits, from_bits, lane_mapping,
+                     make_inputs, special_inputs)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -49,7 +49,7 @@ def run_case(ops, rows, hidden, dtype, seed, scale, dist="bench", eps=1e-6, spec
     q = ops.fused_add_rms_norm_fp8_static(xd, rd, wd, sd, eps)
     # the same inputs through the 16-bit op with the FP8 kernel's lane mapping
     # (the same fp32 reduction order, hence the same y)
-    cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_FP8)
+    cfg = lane_mapping(abi, abi.select_config(rows, hidden, DT[dtype], abi.MODE_FP8))
     y, r16 = x.to(DEV), r.to(DEV)
     abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
                                 eps, torch.cuda.current_stream().cuda_stream, None if cfg.tier == 3 else cfg)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DT, assert_residual_exact, bits, make_inputs
+from helpers import DT, assert_residual_exact, bits, lane_mapping, make_inputs
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -54,7 +54,7 @@ def run_case(ops, rows, hidden, dtype, elem, seed, dist="bench", eps=1e-6, w=Non
     xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
     fn = ops.fused_add_rms_norm_mxfp8 if elem == oracle.MXFP8 else ops.fused_add_rms_norm_mxfp4
     q, sc = fn(xd, rd, wd, eps)
-    cfg = abi.select_config(rows, hidden, DT[dtype], 5 if elem == oracle.MXFP8 else 6)
+    cfg = lane_mapping(abi, abi.select_config(rows, hidden, DT[dtype], 5 if elem == oracle.MXFP8 else 6))
     y, r16 = x.to(DEV), r.to(DEV)
     abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
                                 eps, torch.cuda.current_stream().cuda_stream, cfg)
@@ -159,7 +159,7 @@ def test_mx_dequantises_close_to_the_16_bit_output(ops):
     rows, hidden = 4096, 8192
     x, r, w = (t.to(DEV) for t in make_inputs(rows, hidden, torch.bfloat16, 21))
     # y from the 16-bit op with the MX kernel's lane mapping (the same reduction order)
-    cfg = abi.select_config(rows, hidden, abi.DTYPE_BF16, abi.MODE_MXFP4)
+    cfg = lane_mapping(abi, abi.select_config(rows, hidden, abi.DTYPE_BF16, abi.MODE_MXFP4))
     y, r16 = x.clone(), r.clone()
     abi.BENCH.fused_add_rmsnorm(y.data_ptr(), w.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, abi.DTYPE_BF16,
                                 1e-6, torch.cuda.current_stream().cuda_stream, cfg)

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DT, assert_output_close, assert_residual_exact, bits, make_inputs, oracle_fused
+from helpers import DT, assert_output_close, assert_residual_exact, bits, lane_mapping, make_inputs, oracle_fused
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -195,7 +195,8 @@ def test_random_layouts_mx(abi, case):
         abi.fused_add_rmsnorm_mx(q.data_ptr(), s.data_ptr(), xv.data_ptr(), wv.data_ptr(), rv.data_ptr(), rows, hidden,
                                  qb.stride(0), sb.stride(0), stride(xv), stride(rv), fmt, DT[dtype], EPS, _stream())
         # the 16-bit output of the same shape (in place, contiguous copies)
-        cfg = abi.select_config(rows, hidden, DT[dtype], abi.MODE_MXFP8 if fmt == abi.MX_FP8_E4M3 else abi.MODE_MXFP4)
+        mode = abi.MODE_MXFP8 if fmt == abi.MX_FP8_E4M3 else abi.MODE_MXFP4
+        cfg = lane_mapping(abi, abi.select_config(rows, hidden, DT[dtype], mode))
         y, r16, wd = x.to(DEV), r.to(DEV), w.to(DEV)
         abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, DT[dtype],
                                     EPS, _stream(), cfg)

@@ -22,7 +22,8 @@ import pytest
 import torch
 
 from helpers import (DT, assert_fp8_from_y_within_one_ulp, assert_group_scales, assert_output_close,
-                     assert_residual_exact, bits, make_inputs, oracle_fused, special_inputs, special_weight)
+                     assert_residual_exact, bits, lane_mapping, make_inputs, oracle_fused, special_inputs,
+                     special_weight)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -146,7 +147,8 @@ def run_case(abi, i, c):
         q, s_ = qb[:, offs[2]:offs[2] + qw], sb[:, offs[3]:offs[3] + hidden // 32]
         abi.fused_add_rmsnorm_mx(q.data_ptr(), s_.data_ptr(), xv.data_ptr(), wv.data_ptr(), rv.data_ptr(), rows,
                                  hidden, qb.stride(0), sb.stride(0), xv.stride(0), rv.stride(0), fmt, code, eps, st)
-        cfg = abi.select_config(rows, hidden, code, abi.MODE_MXFP8 if mode == 5 else abi.MODE_MXFP4)
+        cfg = lane_mapping(abi, abi.select_config(rows, hidden, code,
+                                                  abi.MODE_MXFP8 if mode == 5 else abi.MODE_MXFP4))
         y, r16, wd = x.to(DEV), r.to(DEV), w.to(DEV)
         abi.BENCH.fused_add_rmsnorm(y.data_ptr(), wd.data_ptr(), r16.data_ptr(), rows, hidden, hidden, hidden, code,
                                     eps, st, cfg)
