@@ -71,6 +71,7 @@ const FusedEntry kFused[] = {
     HPRMS_ALT_ORDER_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_STREAM_POLICY_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
     HPRMS_SHARED_UNPACK_SHAPES(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16, 0)
+    HPRMS_QUANT_RUNS_AB(HPRMS_FUSED_ENTRY, HPRMS_DTYPE_BF16)
 #endif
 };
 
@@ -453,15 +454,16 @@ void table_config(int64_t rows, int64_t hidden, int mode, bool grid, int cus, hp
 // the row count.  The order only changes which workgroup takes a row, so the
 // bits are the same.
 // The quantised outputs (modes 2, 5, 6, 7) at 16 KiB rows with their table
-// kernel (512 x 2), runs of 32: 0.7-1.1% faster at 4096 rows (three
-// interleaved trials), and 6% for mode 7 with column-major scales.  Those
+// kernel (512 x 2), runs of 32: 0.3-1.1% faster at 4096 rows (seven
+// interleaved trials), and 5.7% for mode 7 with column-major scales.  Those
 // scales are 4-byte stores, 32 rows to a 128-byte line; with one row per
 // workgroup the 32 rows of a line otherwise go to all 8 XCDs, and each XCD's
 // L2 writes its part of the line back on its own.  Mode 7 with column-major
-// scales also takes runs of 32 at 8 KiB rows (256 x 2): 2.6-3.5% faster;
-// there the other quantised outputs and mode 7 with rows of scales were
-// within 0.5% either way, so left out.  At 32 and 64 KiB rows (1024 lanes,
-// one row per workgroup) runs of 8-64 were 3-11% slower in mode 7.
+// scales also takes runs of 32 at 8 KiB rows (256 x 2): 2.2-3.5% faster;
+// there modes 2, 5 and 6 were within 0.4% either way, and mode 7 with rows
+// of scales from 1.1% faster to 0.5% slower over two boxes, so left out.  At
+// 32 and 64 KiB rows (1024 lanes, one row per workgroup) runs of 8-64 were
+// 3-13% slower in mode 7.
 struct RunsRow {
   unsigned modes;       // bit m: mode m
   bool scale_columns;   // mode 7 with column-major scales only
@@ -1240,6 +1242,33 @@ int hprms_bench_fused_timeline(void* input, const void* weight, void* residual, 
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
   Problem p{0, input, input, residual, weight, rows, hidden, hidden, hidden, hidden, dtype, eps, nullptr};
   p.timeline = timeline;
+  return run(p, config, stream);
+}
+
+// Bench library only: a quantised output (mode 2: per-row FP8 scales; 5 / 6:
+// MXFP8 / MXFP4, hidden / 32 scale bytes per row; 7: float32 scales per 128
+// elements at (scale_row_stride, scale_group_stride) elements) on contiguous
+// input, residual and output rows, with a forced configuration: the table's
+// shape with and without runs of row groups per XCD, timed side by side.
+int hprms_bench_quant_config(int mode, void* out, void* scales, int64_t scale_row_stride,
+                             int64_t scale_group_stride, void* input, const void* weight, void* residual,
+                             int64_t rows, int64_t hidden, int dtype, double eps, const hprms_config* config,
+                             hipStream_t stream) {
+  if (!config) return fail(HPRMS_E_INVALID, "config is null");
+  if (mode != 2 && mode != 5 && mode != 6 && mode != 7)
+    return fail(HPRMS_E_INVALID, "mode must be 2, 5, 6 or 7 (got %d)", mode);
+  if (scale_row_stride < 0 || scale_row_stride > (int64_t(1) << 40) || scale_group_stride < 0 ||
+      scale_group_stride > (int64_t(1) << 40))
+    return fail(HPRMS_E_INVALID, "scale strides out of range [0, 2^40]");
+  Problem p{mode, input, out, residual, weight, rows, hidden, hidden, q_row_bytes(mode, hidden), hidden, dtype, eps,
+            nullptr};
+  if (mode == 2) {
+    p.scale = (float*)scales;
+  } else {
+    p.mx_scales = scales;
+    p.mx_scale_stride = mode == 7 ? scale_row_stride * 4 : scale_row_stride;
+    p.mx_group_stride = scale_group_stride * 4;
+  }
   return run(p, config, stream);
 }
 #endif
