@@ -335,9 +335,10 @@ def main():
                     help="only an A/B at every H of the sweep: the table's shape with its row groups in each "
                          "xcd_runs order (runs of 1, 2, ..., 128 per XCD; flags bits 16-18) against the table")
     ap.add_argument("--ab-runs", default="", metavar="H,H,...",
-                    help="only an A/B of the quantised outputs (FP8 per row, MXFP8, MXFP4, FP8 per 128 elements "
-                         "with rows or columns of scales) at (--ab-rows, H) bf16: the table's shape in the default "
-                         "row-group order against runs of 32 row groups per XCD, and the dispatch's own choice")
+                    help="only an A/B of the fused op's other forms (plain, out of place, FP8 per row, MXFP8, "
+                         "MXFP4, FP8 per 128 elements with rows or columns of scales) at (--ab-rows, H) bf16: the "
+                         "table's shape in the default row-group order against runs of 32 and 64 row groups per "
+                         "XCD, and the dispatch's own choice")
     ap.add_argument("--hot", action="store_true",
                     help="with --ab: one buffer set, the same every call (resident in the Infinity Cache)")
     ap.add_argument("--ab-rows", type=int, default=B, metavar="ROWS",
@@ -594,65 +595,81 @@ def ab_trials(torch, abi, op, specs, hot, off=0, pad=0, trials=7, rows=B):
 
 
 def ab_runs_leg(torch, abi, ops, hiddens, rows=B, trials=7):
-    """The quantised outputs at (rows, H) bf16, cold: the table's shape with
-    its row groups in the default order, in runs of 32 per XCD (flags bits
-    16-18 = 5), and the dispatch's own choice (through the torch ops), timed in
-    `trials` interleaved rounds (order reversed every other round).  One JSON
-    line per form and H: the median µs of each and the runs / default ratio."""
+    """The fused op's other forms at (rows, H) bf16, cold: the table's shape
+    with its row groups in the default order, in runs of 32 and of 64 per XCD
+    (flags bits 16-18 = 5, 6; where the bench library builds them), and the
+    dispatch's own choice (through the torch ops), timed in `trials`
+    interleaved rounds (order reversed every other round).  One JSON line per
+    form and H: the median µs of each and each run length's ratio to the
+    default order."""
     stream = torch.cuda.current_stream().cuda_stream
-    forms = (("fp8", 2), ("mxfp8", 5), ("mxfp4", 6), ("group128_rows", 7), ("group128_columns", 7))
+    forms = (("plain", 1), ("out_of_place", 3), ("fp8", 2), ("mxfp8", 5), ("mxfp4", 6), ("group128_rows", 7),
+             ("group128_columns", 7))
     for h in hiddens:
         n = cold_sets(rows, h)
         sets = [make_set(torch, rows, h, torch.bfloat16, 7700 + i, "cuda:0") for i in range(n)]
         w = make_weight(torch, h, torch.bfloat16, 1, "cuda:0")
         q8 = [torch.empty(rows, h, dtype=torch.uint8, device="cuda:0") for _ in range(n)]
         q4 = [torch.empty(rows, h // 2, dtype=torch.uint8, device="cuda:0") for _ in range(n)]
+        o16 = [torch.empty(rows, h, dtype=torch.bfloat16, device="cuda:0") for _ in range(n)]
+        ro16 = [torch.empty(rows, h, dtype=torch.bfloat16, device="cuda:0") for _ in range(n)]
         s_row = torch.empty(rows, dtype=torch.float32, device="cuda:0")
         s_mx = torch.empty(rows, h // 32, dtype=torch.uint8, device="cuda:0")
         s_g = torch.empty(rows, h // 128, dtype=torch.float32, device="cuda:0")
         s_gc = torch.empty(h // 128, rows, dtype=torch.float32, device="cuda:0")
         for name, mode in forms:
-            q = q4 if mode == 6 else q8
+            out = q4 if mode == 6 else o16 if mode in (1, 3) else q8
+            aux = [ro16[i] for i in range(n)] if mode == 3 else [None] * n
             sc, ss, gs = {2: (s_row, 0, 0), 5: (s_mx, h // 32, 1), 6: (s_mx, h // 32, 1)}.get(
                 mode, (s_gc, 1, rows) if name.endswith("columns") else (s_g, h // 128, 1))
 
-            def table(i, q=q, sc=sc, mode=mode, name=name):
+            def table(i, out=out, aux=aux, sc=sc, mode=mode, name=name):
                 x, r = sets[i]
-                if mode == 2:
-                    ops.hp_rms_norm_fp8(q[i].view(torch.float8_e4m3fn), sc, x, w, r, EPS)
+                if mode == 1:
+                    ops.rms_norm(out[i], x, w, EPS)
+                elif mode == 3:
+                    ops.fused_add_rms_norm_out(out[i], aux[i], x, w, r, EPS)
+                elif mode == 2:
+                    ops.hp_rms_norm_fp8(out[i].view(torch.float8_e4m3fn), sc, x, w, r, EPS)
                 elif mode in (5, 6):
-                    ops.hp_rms_norm_mx(q[i], sc, x, w, r, EPS, ops.MXFP8 if mode == 5 else ops.MXFP4)
+                    ops.hp_rms_norm_mx(out[i], sc, x, w, r, EPS, ops.MXFP8 if mode == 5 else ops.MXFP4)
                 else:
-                    ops.hp_rms_norm_fp8_group(q[i].view(torch.float8_e4m3fn), sc.t() if name.endswith("columns")
+                    ops.hp_rms_norm_fp8_group(out[i].view(torch.float8_e4m3fn), sc.t() if name.endswith("columns")
                                               else sc, x, w, r, EPS)
 
-            def forced(cfg, q=q, sc=sc, ss=ss, gs=gs, mode=mode):
-                return lambda i: abi.BENCH.bench_quant_config(mode, q[i].data_ptr(), sc.data_ptr(), ss, gs,
-                                                              sets[i][0].data_ptr(), w.data_ptr(),
-                                                              sets[i][1].data_ptr(), rows, h, abi.DTYPE_BF16, EPS,
-                                                              cfg, stream)
+            def forced(cfg, out=out, aux=aux, sc=sc, ss=ss, gs=gs, mode=mode):
+                def call(i):
+                    a = aux[i].data_ptr() if mode == 3 else 0 if mode == 1 else sc.data_ptr()
+                    abi.BENCH.bench_form_config(mode, out[i].data_ptr(), a, ss, gs, sets[i][0].data_ptr(),
+                                                w.data_ptr(), sets[i][1].data_ptr(), rows, h, abi.DTYPE_BF16, EPS,
+                                                cfg, stream)
+                return call
             base = abi.select_config(rows, h, abi.DTYPE_BF16, mode)
             built = {c.as_tuple() for c in abi.BENCH.kernel_configs(abi.DTYPE_BF16, mode)}
             default = abi.Config(*base.as_tuple())
             default.flags &= ~(7 << 16)
-            runs = abi.Config(*default.as_tuple())
-            runs.flags |= 5 << 16
-            if runs.as_tuple() not in built:
+            calls = [("default", forced(default))]
+            for v in (5, 6):
+                c = abi.Config(*default.as_tuple())
+                c.flags |= v << 16
+                if c.as_tuple() in built:
+                    calls.append((f"runs{1 << v}", forced(c)))
+            if len(calls) == 1:
                 print(json.dumps({"ab_runs": name, "hidden": h, "rows": rows, "shape": default.as_tuple(),
                                   "skipped": "no runs variant built for this shape"}), flush=True)
                 continue
-            calls = [("default", forced(default)), ("runs32", forced(runs)), ("table", table)]
+            calls.append(("table", table))
             res = {k: [] for k, _ in calls}
             for t in range(trials):
                 for k, call in (calls if t % 2 == 0 else calls[::-1]):
                     res[k].append(time_rotating(torch, call, n, max(40, 2 * n), 3))
             med = {k: round(statistics.median(v), 2) for k, v in res.items()}
             print(json.dumps({"ab_runs": name, "hidden": h, "rows": rows, "shape": default.as_tuple()[1:5],
-                              "flags": default.flags, "us": med, "runs_over_default": round(med["runs32"] /
-                                                                                             med["default"], 4),
+                              "flags": default.flags, "us": med,
+                              "over_default": {k: round(med[k] / med["default"], 4) for k in med if k != "default"},
                               "spread": {k: round((max(v) - min(v)) / statistics.median(v), 4)
                                          for k, v in res.items()}}), flush=True)
-        del sets, q8, q4
+        del sets, q8, q4, o16, ro16
         torch.cuda.empty_cache()
 
 

@@ -103,9 +103,9 @@ def _bind(L, bench):
         L.hprms_ceil_skeleton.argtypes = [vp, vp, i64, i64, ci, ci, ci, ci, vp]
         L.hprms_ceil_streams.argtypes = [ci, vp, vp, vp, vp, i64, vp]
         L.hprms_ceil_flat.argtypes = [ci, ci, ci, ci, vp, vp, i64, vp]
-        L.hprms_bench_quant_config.argtypes = [ci, vp, vp, i64, i64, vp, vp, vp, i64, i64, ci, cd,
-                                               ctypes.POINTER(Config), vp]
-        names += ["hprms_bench_fused_timeline", "hprms_bench_quant_config", "hprms_ceil_empty", "hprms_ceil_read", "hprms_ceil_write",
+        L.hprms_bench_form_config.argtypes = [ci, vp, vp, i64, i64, vp, vp, vp, i64, i64, ci, cd,
+                                              ctypes.POINTER(Config), vp]
+        names += ["hprms_bench_fused_timeline", "hprms_bench_form_config", "hprms_ceil_empty", "hprms_ceil_read", "hprms_ceil_write",
                   "hprms_ceil_copy", "hprms_ceil_skeleton", "hprms_ceil_streams", "hprms_ceil_flat"]
     for name in names:
         getattr(L, name).restype = ci
@@ -242,14 +242,14 @@ class Library:
                                                                  dtype, eps, ctypes.byref(config), timeline_ptr,
                                                                  stream))
 
-    def bench_quant_config(self, mode, out_ptr, scales_ptr, scale_stride, scale_group_stride, input_ptr, weight_ptr,
-                           residual_ptr, rows, hidden, dtype, eps, config, stream=0):
-        """Bench library only: a quantised output (mode 2, 5, 6 or 7) on
-        contiguous rows with a forced configuration."""
-        return self._check(self.lib().hprms_bench_quant_config(mode, out_ptr, scales_ptr, scale_stride,
-                                                               scale_group_stride, input_ptr, weight_ptr,
-                                                               residual_ptr, rows, hidden, dtype, eps,
-                                                               ctypes.byref(config), stream))
+    def bench_form_config(self, mode, out_ptr, aux_ptr, aux_stride, aux_group_stride, input_ptr, weight_ptr,
+                          residual_ptr, rows, hidden, dtype, eps, config, stream=0):
+        """Bench library only: a form of the op (mode 1, 2, 3, 5, 6 or 7) on
+        contiguous rows with a forced configuration; `aux` is the residual
+        output (mode 3) or the scales."""
+        return self._check(self.lib().hprms_bench_form_config(mode, out_ptr, aux_ptr, aux_stride, aux_group_stride,
+                                                              input_ptr, weight_ptr, residual_ptr, rows, hidden,
+                                                              dtype, eps, ctypes.byref(config), stream))
 
     def kernel_configs(self, dtype, mode=0):
         """Every vector-tier configuration built for (dtype, mode)."""

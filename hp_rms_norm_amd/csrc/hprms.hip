@@ -1245,29 +1245,34 @@ int hprms_bench_fused_timeline(void* input, const void* weight, void* residual, 
   return run(p, config, stream);
 }
 
-// Bench library only: a quantised output (mode 2: per-row FP8 scales; 5 / 6:
-// MXFP8 / MXFP4, hidden / 32 scale bytes per row; 7: float32 scales per 128
-// elements at (scale_row_stride, scale_group_stride) elements) on contiguous
-// input, residual and output rows, with a forced configuration: the table's
-// shape with and without runs of row groups per XCD, timed side by side.
-int hprms_bench_quant_config(int mode, void* out, void* scales, int64_t scale_row_stride,
-                             int64_t scale_group_stride, void* input, const void* weight, void* residual,
-                             int64_t rows, int64_t hidden, int dtype, double eps, const hprms_config* config,
-                             hipStream_t stream) {
+// Bench library only: one of the fused op's other forms on contiguous rows
+// with a forced configuration, to time the table's shape against its
+// variants (the row-group order).  mode 1: `out` <- plain RMSNorm of `input`
+// (no residual); 3: `out` and `aux` (the residual output) out of place; 2:
+// FP8 with per-row scales in `aux`; 5 / 6: MXFP8 / MXFP4, hidden / 32 scale
+// bytes per row in `aux`; 7: float32 scales per 128 elements in `aux` at
+// (aux_row_stride, aux_group_stride) elements.
+int hprms_bench_form_config(int mode, void* out, void* aux, int64_t aux_row_stride, int64_t aux_group_stride,
+                            void* input, const void* weight, void* residual, int64_t rows, int64_t hidden,
+                            int dtype, double eps, const hprms_config* config, hipStream_t stream) {
   if (!config) return fail(HPRMS_E_INVALID, "config is null");
-  if (mode != 2 && mode != 5 && mode != 6 && mode != 7)
-    return fail(HPRMS_E_INVALID, "mode must be 2, 5, 6 or 7 (got %d)", mode);
-  if (scale_row_stride < 0 || scale_row_stride > (int64_t(1) << 40) || scale_group_stride < 0 ||
-      scale_group_stride > (int64_t(1) << 40))
+  if (mode != 1 && mode != 2 && mode != 3 && mode != 5 && mode != 6 && mode != 7)
+    return fail(HPRMS_E_INVALID, "mode must be 1, 2, 3, 5, 6 or 7 (got %d)", mode);
+  if (aux_row_stride < 0 || aux_row_stride > (int64_t(1) << 40) || aux_group_stride < 0 ||
+      aux_group_stride > (int64_t(1) << 40))
     return fail(HPRMS_E_INVALID, "scale strides out of range [0, 2^40]");
-  Problem p{mode, input, out, residual, weight, rows, hidden, hidden, q_row_bytes(mode, hidden), hidden, dtype, eps,
-            nullptr};
+  const bool quant = mode == 2 || mode >= 5;
+  Problem p{mode, input, out, mode == 1 ? nullptr : residual, weight, rows, hidden, hidden,
+            quant ? q_row_bytes(mode, hidden) : hidden, mode == 1 ? 0 : hidden, dtype, eps, nullptr};
   if (mode == 2) {
-    p.scale = (float*)scales;
-  } else {
-    p.mx_scales = scales;
-    p.mx_scale_stride = mode == 7 ? scale_row_stride * 4 : scale_row_stride;
-    p.mx_group_stride = scale_group_stride * 4;
+    p.scale = (float*)aux;
+  } else if (mode == 3) {
+    p.res_out = aux;
+    p.res_out_stride = hidden;
+  } else if (mode >= 5) {
+    p.mx_scales = aux;
+    p.mx_scale_stride = mode == 7 ? aux_row_stride * 4 : aux_row_stride;
+    p.mx_group_stride = aux_group_stride * 4;
   }
   return run(p, config, stream);
 }

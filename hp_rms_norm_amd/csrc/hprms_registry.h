@@ -114,11 +114,17 @@ struct FusedEntry {
   X(DT, 6, 512, 2, 0, 512, 7 | 327680) X(DT, 7, 512, 2, 0, 512, 7 | 327680)                       \
   X(DT, 7, 256, 2, 0, 256, 7 | 327680)
 // bench library: the same runs where the table leaves them out (modes 2, 5, 6
-// at 8 KiB rows; mode 7 at 32 and 64 KiB rows), for bench.py --ab-runs
+// at 8 KiB rows; mode 7 at 32 and 64 KiB rows), and runs of 32 and 64 for the
+// plain RMSNorm (mode 1) and the op out of place (mode 3) at 8 and 16 KiB
+// rows, for bench.py --ab-runs
 #define HPRMS_QUANT_RUNS_AB(X, DT)                                                                 \
   X(DT, 2, 256, 2, 0, 256, 7 | 327680) X(DT, 5, 256, 2, 0, 256, 7 | 327680)                       \
   X(DT, 6, 256, 2, 0, 256, 7 | 327680) X(DT, 7, 1024, 2, 0, 1024, 31 | 327680)                    \
-  X(DT, 7, 1024, 4, 0, 1024, 159 | 327680)
+  X(DT, 7, 1024, 4, 0, 1024, 159 | 327680)                                                        \
+  X(DT, 1, 64, 8, 0, 256, 3 | 327680) X(DT, 1, 64, 8, 0, 256, 3 | 393216)                         \
+  X(DT, 1, 512, 2, 0, 512, 31 | 327680) X(DT, 1, 512, 2, 0, 512, 31 | 393216)                     \
+  X(DT, 3, 128, 4, 0, 256, 131 | 327680) X(DT, 3, 128, 4, 0, 256, 131 | 393216)                   \
+  X(DT, 3, 512, 2, 0, 512, 7 | 327680) X(DT, 3, 512, 2, 0, 512, 7 | 393216)
 #define HPRMS_MODE0_SHAPES(X, DT, MODE) HPRMS_FUSED_SHAPES(X, DT, MODE) X(DT, MODE, 256, 2, 0, 256, 131) \
   HPRMS_WIDE_ROWS(X, DT, MODE) HPRMS_WAVE_ROWS(X, DT, MODE) HPRMS_PAIR_ROWS(X, DT, MODE) HPRMS_RUNS_ROWS(X, DT, MODE)
 // rows off the 128-byte grid at 3K < H <= 4K keep 128 x 4 in place (hprms.hip, inplace_config)

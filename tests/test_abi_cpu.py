@@ -615,7 +615,7 @@ def test_bench_library_is_apart_from_the_product():
     bench = abi.BENCH.lib()
     for n in declared_functions():
         assert hasattr(bench, n), n
-    extra = ("hprms_bench_fused_timeline", "hprms_bench_quant_config", "hprms_ceil_empty", "hprms_ceil_read",
+    extra = ("hprms_bench_fused_timeline", "hprms_bench_form_config", "hprms_ceil_empty", "hprms_ceil_read",
              "hprms_ceil_write", "hprms_ceil_copy", "hprms_ceil_skeleton", "hprms_ceil_streams", "hprms_ceil_flat")
     for n in extra:
         assert hasattr(bench, n), n
@@ -649,21 +649,24 @@ def test_bench_entry_points_reject_bad_arguments():
                                                           abi.DTYPE_BF16, 1e-6, ctypes.byref(c),
                                                           None) == abi.HPRMS_E_INVALID
     assert "timeline" in abi.BENCH.last_error()
-    # the quantised outputs with a forced configuration: modes 2, 5, 6, 7 only, a built shape,
+    # the other forms with a forced configuration: modes 1, 2, 3, 5, 6, 7 only, a built shape,
     # and mode 7's scale layout checked as in the product entry (rows = 0 launches nothing)
     q = abi.Config(1, 512, 2, 0, 512, 0, 7 | 5 << 16)
     rest = (0x1000, 0x2000, 0x3000, 0, 8192, abi.DTYPE_BF16, 1e-6)
-    for mode, ss, gs in ((2, 0, 0), (5, 256, 1), (6, 256, 1), (7, 1, 64), (7, 64, 1)):
-        rc = L.hprms_bench_quant_config(mode, 0x4000, 0x5000, ss, gs, *rest, ctypes.byref(q), None)
+    for mode, ss, gs in ((2, 0, 0), (5, 256, 1), (6, 256, 1), (7, 1, 64), (7, 64, 1), (3, 0, 0)):
+        rc = L.hprms_bench_form_config(mode, 0x4000, 0x5000, ss, gs, *rest, ctypes.byref(q), None)
         assert rc == abi.HPRMS_OK, (mode, abi.BENCH.last_error())
     args = (0x4000, 0x5000, 1, 64) + rest
-    assert L.hprms_bench_quant_config(0, *args, ctypes.byref(q), None) == abi.HPRMS_E_INVALID
-    assert L.hprms_bench_quant_config(7, *args, None, None) == abi.HPRMS_E_INVALID
+    assert L.hprms_bench_form_config(0, *args, ctypes.byref(q), None) == abi.HPRMS_E_INVALID
+    assert L.hprms_bench_form_config(4, *args, ctypes.byref(q), None) == abi.HPRMS_E_INVALID
+    plain = abi.Config(1, 512, 2, 0, 512, 0, 31 | 6 << 16)
+    assert L.hprms_bench_form_config(1, 0x4000, 0, 0, 0, *rest, ctypes.byref(plain), None) == abi.HPRMS_OK
+    assert L.hprms_bench_form_config(7, *args, None, None) == abi.HPRMS_E_INVALID
     bad = abi.Config(1, 512, 2, 0, 512, 0, 7 | 3 << 16)
-    assert L.hprms_bench_quant_config(7, *args, ctypes.byref(bad), None) == abi.HPRMS_E_INVALID
+    assert L.hprms_bench_form_config(7, *args, ctypes.byref(bad), None) == abi.HPRMS_E_INVALID
     assert "no kernel built" in abi.BENCH.last_error()
-    assert L.hprms_bench_quant_config(7, 0x4000, 0x5000, 1, 1, *args[4:], ctypes.byref(q), None) == abi.HPRMS_OK
-    assert L.hprms_bench_quant_config(7, 0x4000, 0x5000, 1, -1, *args[4:], ctypes.byref(q), None) == \
+    assert L.hprms_bench_form_config(7, 0x4000, 0x5000, 1, 1, *args[4:], ctypes.byref(q), None) == abi.HPRMS_OK
+    assert L.hprms_bench_form_config(7, 0x4000, 0x5000, 1, -1, *args[4:], ctypes.byref(q), None) == \
         abi.HPRMS_E_INVALID
 
 
