@@ -8,7 +8,7 @@
                        the ceiling kernels (hprms_ceiling.hip)
 
 All land next to this file, so they travel with the source tree.  Run
-``python hp_rms_norm_amd/build.py [all|product|kernels|torch|oracle]`` (or
+``python hp_rms_norm_amd/build.py [all|product|kernels|torch|oracle|tests]`` (or
 ``__graft_entry__.build()``; ``product``, the two product libraries, is what
 ``pip install`` builds) -- as a script, not with ``-m``: importing it through
 the package would run the package's __init__, which needs the libraries this
@@ -117,10 +117,19 @@ def build_oracle():
         _run(["make", "-s", "-B", "-C", oracle_dir])
 
 
+def build_test_programs():
+    """tests/c_gpu_caller (gcc): the C ABI driven from a plain C program on
+    the GPU, checked against the oracle; test infrastructure."""
+    tests_dir = os.path.join(ROOT, "tests")
+    if os.path.exists(os.path.join(tests_dir, "Makefile")) and shutil.which("gcc"):
+        _run(["make", "-s", "-B", "-C", tests_dir])
+
+
 def build_all():
     build_kernels()
     build_torch_binding()
     build_oracle()
+    build_test_programs()
 
 
 def build_product():
@@ -133,4 +142,4 @@ if __name__ == "__main__":
     what = sys.argv[1:] or ["all"]
     for w in what:
         {"all": build_all, "product": build_product, "kernels": build_kernels, "torch": build_torch_binding,
-         "oracle": build_oracle}[w]()
+         "oracle": build_oracle, "tests": build_test_programs}[w]()

@@ -511,6 +511,20 @@ def test_plain_c_caller_compiles_links_and_runs(tmp_path):
     assert p.returncode == 0 and "ok" in p.stdout, p.stdout + p.stderr
 
 
+def test_gpu_c_caller_is_built_and_links():
+    """tests/c_gpu_caller (built with the libraries) loads libhprms.so, the
+    oracle and the HIP runtime; without a device it stops with status 2 and
+    says so, before any case runs."""
+    import subprocess
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is present: tests/test_gpu_c_caller.py runs the program there")
+    exe = os.path.join(ROOT, "tests", "c_gpu_caller")
+    assert os.path.exists(exe), "tests/c_gpu_caller is not built: run __graft_entry__.build()"
+    p = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert p.returncode == 2 and "case " not in p.stdout, p.stdout + p.stderr
+    assert "hipGetDeviceCount" in p.stderr or "no HIP device" in p.stderr, p.stderr
+
+
 def test_fp8_group_entry_rejects_bad_arguments():
     L = abi.lib()
     ok = dict(out=0x4000, sc=0x5000, x=0x1000, w=0x2000, r=0x3000, h=4096, so=4096, ss=32, gs=1)
