@@ -348,8 +348,11 @@ def main():
                          "into rows of H + OFF + PAD elements (rows off the 128-byte grid take the "
                          "configurations' off-grid variants)")
     ap.add_argument("--profile-op", default="fused",
-                    choices=("fused", "fp8", "plain", "mxfp8", "mxfp4", "copy", "relu"),
-                    help="with --profile: the 16-bit fused op, its FP8 / MX-output forms, plain RMSNorm, "
+                    choices=("fused", "fp8", "plain", "mxfp8", "mxfp4", "group_rows", "group_columns", "copy",
+                             "relu"),
+                    help="with --profile: the 16-bit fused op, its FP8 / MX-output forms (group_rows / "
+                         "group_columns: FP8 with a scale per 128 elements, rows or column-major scales; "
+                         "with --profile-config, forced through the bench library), plain RMSNorm, "
                          "or the streamer (the reference's relu = copy, and the true ReLU)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -707,6 +710,24 @@ def profile_driver(torch, abi, op, args):
 
         def op(x, w, r, eps):  # noqa: F811  (MX output; the input row is only read)
             hp_rms_norm_amd.hp_rms_norm_mx(q, sc, x, w, r, eps, fmt)
+    if args.profile_op in ("group_rows", "group_columns"):
+        # FP8 with a scale per 128 elements, rows of scales or column-major ones; with
+        # --profile-config, that configuration forced through the bench library
+        import hp_rms_norm_amd
+        q = torch.empty(B, hidden, dtype=torch.float8_e4m3fn, device="cuda:0")
+        cols = args.profile_op == "group_columns"
+        sc = torch.empty(hidden // 128, B, dtype=torch.float32, device="cuda:0").t() if cols else \
+            torch.empty(B, hidden // 128, dtype=torch.float32, device="cuda:0")
+        gcfg = cfg if args.profile_config else None
+        gstream = torch.cuda.current_stream().cuda_stream
+
+        def op(x, w, r, eps):  # noqa: F811  (the input row is only read)
+            if gcfg is None:
+                hp_rms_norm_amd.hp_rms_norm_fp8_group(q, sc, x, w, r, eps)
+            else:
+                abi.BENCH.bench_form_config(7, q.data_ptr(), sc.data_ptr(), sc.stride(0), sc.stride(1),
+                                            x.data_ptr(), w.data_ptr(), r.data_ptr(), x.shape[0], x.shape[1],
+                                            abi.DTYPE_BF16, eps, gcfg, gstream)
     if args.profile_op in ("copy", "relu"):
         import hp_rms_norm_amd
         stream_fn = hp_rms_norm_amd.relu if args.profile_op == "copy" else hp_rms_norm_amd.relu_max0
