@@ -31,6 +31,7 @@ SYMBOLS = (
     "hprms_fused_add_rmsnorm_fp8",
     "hprms_fused_add_rmsnorm_fp8_static",
     "hprms_fused_add_rmsnorm_fp8_group",
+    "hprms_fused_add_rmsnorm_fp8_ub",
     "hprms_fused_add_rmsnorm_out",
     "hprms_reduce_add_rmsnorm",
     "hprms_fused_add_rmsnorm_mx",
@@ -72,6 +73,7 @@ def _bind(L, bench):
     L.hprms_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8_static.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
+    L.hprms_fused_add_rmsnorm_fp8_ub.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, cd, vp]
     L.hprms_fused_add_rmsnorm_fp8_group.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, ci, cd,
                                                     vp]
     L.hprms_fused_add_rmsnorm_out.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, cd, vp]
@@ -90,6 +92,7 @@ def _bind(L, bench):
     L.hprms_abi_version.restype = ci
     names = ["hprms_fused_add_rmsnorm", "hprms_fused_add_rmsnorm_config", "hprms_rmsnorm",
              "hprms_fused_add_rmsnorm_fp8", "hprms_fused_add_rmsnorm_fp8_static", "hprms_fused_add_rmsnorm_fp8_group",
+             "hprms_fused_add_rmsnorm_fp8_ub",
              "hprms_fused_add_rmsnorm_out",
              "hprms_reduce_add_rmsnorm",
              "hprms_fused_add_rmsnorm_mx", "hprms_streamer", "hprms_select_config", "hprms_select_config_cu",
@@ -165,6 +168,12 @@ class Library:
         return self._check(self.lib().hprms_fused_add_rmsnorm_fp8_static(
             out_ptr, scale_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride, input_stride,
             residual_stride, dtype, eps, stream))
+
+    def fused_add_rmsnorm_fp8_ub(self, out_ptr, scale_ptr, scale_ub_ptr, input_ptr, weight_ptr, residual_ptr, rows,
+                                 hidden, out_stride, input_stride, residual_stride, dtype, eps, stream=0):
+        return self._check(self.lib().hprms_fused_add_rmsnorm_fp8_ub(
+            out_ptr, scale_ptr, scale_ub_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden, out_stride,
+            input_stride, residual_stride, dtype, eps, stream))
 
     def fused_add_rmsnorm_fp8_group(self, out_ptr, scales_ptr, input_ptr, weight_ptr, residual_ptr, rows, hidden,
                                     out_stride, scale_stride, scale_group_stride, input_stride, residual_stride,
@@ -278,6 +287,7 @@ fused_add_rmsnorm = PRODUCT.fused_add_rmsnorm
 fused_add_rmsnorm_fp8 = PRODUCT.fused_add_rmsnorm_fp8
 fused_add_rmsnorm_fp8_static = PRODUCT.fused_add_rmsnorm_fp8_static
 fused_add_rmsnorm_fp8_group = PRODUCT.fused_add_rmsnorm_fp8_group
+fused_add_rmsnorm_fp8_ub = PRODUCT.fused_add_rmsnorm_fp8_ub
 fused_add_rmsnorm_out = PRODUCT.fused_add_rmsnorm_out
 reduce_add_rmsnorm = PRODUCT.reduce_add_rmsnorm
 fused_add_rmsnorm_mx = PRODUCT.fused_add_rmsnorm_mx

@@ -506,6 +506,7 @@ struct Problem {
   double eps;
   float* scale = nullptr;      // mode 2: per-row scales, written
   const float* static_scale = nullptr;  // mode 2: one given scale for every row (then no `scale`)
+  const float* scale_ub = nullptr;      // mode 2, per-row scales: upper bound on the row maximum
   void* res_out = nullptr;     // mode 3
   int64_t res_out_stride = 0;  // mode 3
   int nparts = 1;              // mode 4
@@ -914,6 +915,7 @@ int launch_general(const Problem& p, hipStream_t stream) {
   a.q = p.mode == 2 ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
   a.static_scale = p.static_scale;
+  a.scale_ub = p.scale_ub;
   a.q_stride = p.mode == 2 ? p.out_stride : 0;
   const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
   launch_general_kernels(a, p.dtype, p.mode, grid, stream);
@@ -988,6 +990,7 @@ int run(const Problem& p, const hprms_config* forced, hipStream_t stream) {
   a.q = p.mode == 2 || is_blockq(p.mode) ? (uint8_t*)p.out : nullptr;
   a.scale = p.scale;
   a.static_scale = p.static_scale;
+  a.scale_ub = p.scale_ub;
   a.q_stride = p.mode == 2 || is_blockq(p.mode) ? p.out_stride : 0;
   a.mx_scale = (uint8_t*)p.mx_scales;
   a.mx_scale_stride = p.mx_scale_stride;
@@ -1058,6 +1061,17 @@ int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, cons
                                 int64_t residual_row_stride, int dtype, double eps, hipStream_t stream) {
   Problem p{2, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
             residual_row_stride, dtype, eps, scale};
+  return run(p, nullptr, stream);
+}
+
+int hprms_fused_add_rmsnorm_fp8_ub(void* out, float* scale, const float* scale_ub, const void* input,
+                                   const void* weight, void* residual, int64_t rows, int64_t hidden,
+                                   int64_t out_row_stride, int64_t input_row_stride, int64_t residual_row_stride,
+                                   int dtype, double eps, hipStream_t stream) {
+  Problem p{2, const_cast<void*>(input), out, residual, weight, rows, hidden, input_row_stride, out_row_stride,
+            residual_row_stride, dtype, eps, scale};
+  p.scale_ub = scale_ub;
+  if (!scale_ub && rows > 0) return fail(HPRMS_E_INVALID, "null tensor pointer (scale_ub)");
   return run(p, nullptr, stream);
 }
 

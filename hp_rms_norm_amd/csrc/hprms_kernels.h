@@ -134,6 +134,7 @@ struct FusedArgs {
   uint8_t* q;            // MODES 2, 5, 6: quantised output rows
   float* scale;          // MODE 2: per-row scales
   const float* static_scale;  // MODE 2: one scale for every row, given (null: per-row scales, written)
+  const float* scale_ub;      // MODE 2, per-row scales: upper bound on the row maximum (null: none)
   int64_t q_stride;      // MODES 2, 5, 6: bytes between quantised rows
   uint16_t* res_out;     // MODE 3: residual output rows
   int64_t res_out_stride;
@@ -839,7 +840,11 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
             mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w0 + j]));
           buf ^= 1;
         }
-        const float amax = F::one((uint16_t)mx);
+        float amax = F::one((uint16_t)mx);
+        // an upper bound on the row maximum, given by the caller (a NaN
+        // maximum stays NaN; a NaN bound bounds nothing)
+        const float* const ub = opaque(a.scale_ub);
+        if (ub != nullptr && amax > *ub) amax = *ub;
         float sc = amax / 448.0f;
         if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
         isc = 1.0f / sc;
@@ -904,6 +909,7 @@ struct GeneralArgs {
   uint8_t* q;        // MODE 2
   float* scale;      // MODE 2
   const float* static_scale;  // MODE 2: as FusedArgs::static_scale
+  const float* scale_ub;      // MODE 2: as FusedArgs::scale_ub
   int64_t q_stride;  // MODE 2
   uint16_t* res_out;  // MODE 3
   int64_t res_out_stride;
@@ -971,7 +977,9 @@ __global__ __launch_bounds__(256) void fused_general_kernel(GeneralArgs a) {
         __syncthreads();
         for (int j = 0; j < 4; ++j) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][j]));
         buf ^= 1;
-        float sc = F::one((uint16_t)mx) / 448.0f;
+        float amax = F::one((uint16_t)mx);
+        if (a.scale_ub != nullptr && amax > *a.scale_ub) amax = *a.scale_ub;  // the caller's upper bound
+        float sc = amax / 448.0f;
         if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
         isc = 1.0f / sc;
         if (tid == 0) a.scale[row] = sc;
@@ -1084,7 +1092,9 @@ __global__ __launch_bounds__(BLOCK) void fused_general_reg_kernel(GeneralArgs a)
         __syncthreads();
 #pragma unroll
         for (int w = 0; w < NW; ++w) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(uint32_t, red[buf][w]));
-        float sc = F::one((uint16_t)mx) / 448.0f;
+        float amax = F::one((uint16_t)mx);
+        if (a.scale_ub != nullptr && amax > *a.scale_ub) amax = *a.scale_ub;  // the caller's upper bound
+        float sc = amax / 448.0f;
         if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
         isc = 1.0f / sc;
         if (tid == 0) a.scale[row] = sc;

@@ -227,6 +227,35 @@ void rms_norm_fp8_meta(at::Tensor& out, at::Tensor& scale, const at::Tensor& inp
   (void)eps;
 }
 
+// ---- FP8 output with per-row scales bounded above ------------------------------------
+Fp8Shape check_fp8_ub(const at::Tensor& out, const at::Tensor& scale, const at::Tensor& input,
+                      const at::Tensor& weight, const at::Tensor& residual, const at::Tensor& scale_ub) {
+  const Fp8Shape s = check_fp8(out, scale, input, weight, residual);
+  TORCH_CHECK(scale_ub.scalar_type() == at::kFloat, "scale_ub.dtype() == float32");
+  TORCH_CHECK(scale_ub.numel() == 1, "scale_ub must hold one element");
+  TORCH_CHECK(scale_ub.device() == input.device(), "scale_ub and input must be on the same device");
+  if (s.f.rows > 0) at::assert_no_overlap(scale, scale_ub);
+  return s;
+}
+
+void rms_norm_fp8_ub_hip(at::Tensor& out, at::Tensor& scale, const at::Tensor& input, const at::Tensor& weight,
+                         at::Tensor& residual, const at::Tensor& scale_ub, double eps) {
+  const Fp8Shape s = check_fp8_ub(out, scale, input, weight, residual, scale_ub);
+  if (s.f.rows == 0 || s.f.hidden == 0) return;
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStream(input.device().index()).stream();
+  check_status(hprms_fused_add_rmsnorm_fp8_ub(out.data_ptr(), scale.data_ptr<float>(), scale_ub.data_ptr<float>(),
+                                              input.data_ptr(), weight.data_ptr(), residual.data_ptr(), s.f.rows,
+                                              s.f.hidden, s.out_stride, s.f.in_stride, s.f.res_stride, s.f.dtype,
+                                              eps, stream));
+}
+
+void rms_norm_fp8_ub_meta(at::Tensor& out, at::Tensor& scale, const at::Tensor& input, const at::Tensor& weight,
+                          at::Tensor& residual, const at::Tensor& scale_ub, double eps) {
+  (void)check_fp8_ub(out, scale, input, weight, residual, scale_ub);
+  (void)eps;
+}
+
 // ---- FP8 output with one given scale ---------------------------------------------------
 Fp8Shape check_fp8_static(const at::Tensor& out, const at::Tensor& scale, const at::Tensor& input,
                           const at::Tensor& weight, const at::Tensor& residual) {
@@ -565,6 +594,8 @@ TORCH_LIBRARY(hp_rms_norm, m) {
   m.def("rms_norm_plain(Tensor(a!) out, Tensor input, Tensor weight, float eps) -> ()");
   m.def("rms_norm_fp8_quant(Tensor(a!) out, Tensor(b!) scale, Tensor input, Tensor weight, Tensor(c!) residual, "
         "float eps) -> ()");
+  m.def("rms_norm_fp8_quant_ub(Tensor(a!) out, Tensor(b!) scale, Tensor input, Tensor weight, Tensor(c!) residual, "
+        "Tensor scale_ub, float eps) -> ()");
   m.def("rms_norm_fp8_static_quant(Tensor(a!) out, Tensor scale, Tensor input, Tensor weight, Tensor(b!) residual, "
         "float eps) -> ()");
   m.def("rms_norm_fp8_group_quant(Tensor(a!) out, Tensor(b!) scales, Tensor input, Tensor weight, "
@@ -583,6 +614,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, CUDA, m) {
   m.impl("relu_max0", &relu_max0_hip);
   m.impl("rms_norm_plain", &rms_norm_plain_hip);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_hip);
+  m.impl("rms_norm_fp8_quant_ub", &rms_norm_fp8_ub_hip);
   m.impl("rms_norm_fp8_static_quant", &rms_norm_fp8_static_hip);
   m.impl("rms_norm_fp8_group_quant", &rms_norm_fp8_group_hip);
   m.impl("rms_norm_out", &rms_norm_out_hip);
@@ -598,6 +630,7 @@ TORCH_LIBRARY_IMPL(hp_rms_norm, Meta, m) {
   m.impl("relu_max0", &stream_meta);
   m.impl("rms_norm_plain", &rms_norm_plain_meta);
   m.impl("rms_norm_fp8_quant", &rms_norm_fp8_meta);
+  m.impl("rms_norm_fp8_quant_ub", &rms_norm_fp8_ub_meta);
   m.impl("rms_norm_fp8_static_quant", &rms_norm_fp8_static_meta);
   m.impl("rms_norm_fp8_group_quant", &rms_norm_fp8_group_meta);
   m.impl("rms_norm_out", &rms_norm_out_meta);

@@ -4,7 +4,8 @@ argument order, in-place semantics and ``None`` return."""
 import torch
 
 __all__ = ["hp_rms_norm", "relu", "relu_max0", "rms_norm", "fused_add_rms_norm", "fused_add_rms_norm_out",
-           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "hp_rms_norm_fp8_static", "fused_add_rms_norm_fp8_static",
+           "hp_rms_norm_fp8", "fused_add_rms_norm_fp8", "hp_rms_norm_fp8_ub", "hp_rms_norm_fp8_static",
+           "fused_add_rms_norm_fp8_static",
            "hp_rms_norm_fp8_group", "fused_add_rms_norm_fp8_group",
            "reduce_add_rms_norm", "hp_rms_norm_mx",
            "fused_add_rms_norm_mxfp8", "fused_add_rms_norm_mxfp4", "MXFP8", "MXFP4",
@@ -70,14 +71,28 @@ def hp_rms_norm_fp8(output, scale, input, weight, residual, eps):
     torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(output, scale, input, weight, residual, eps)
 
 
-def fused_add_rms_norm_fp8(input, residual, weight, eps):
+def fused_add_rms_norm_fp8(input, residual, weight, eps, scale_ub=None):
     """Allocating form of ``hp_rms_norm_fp8``: returns ``(q, scale)`` with
     ``q`` float8_e4m3fn shaped like ``input`` and ``scale`` float32 of shape
-    ``input.shape[:-1] + (1,)``; ``residual`` is updated in place."""
+    ``input.shape[:-1] + (1,)``; ``residual`` is updated in place.
+    ``scale_ub``: an optional one-element float32 device tensor bounding each
+    row's maximum (``hp_rms_norm_fp8_ub``)."""
     q = torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device)
     scale = torch.empty(input.shape[:-1] + (1,), dtype=torch.float32, device=input.device)
-    torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(q, scale, input, weight, residual, eps)
+    if scale_ub is None:
+        torch.ops.hp_rms_norm.rms_norm_fp8_quant.default(q, scale, input, weight, residual, eps)
+    else:
+        torch.ops.hp_rms_norm.rms_norm_fp8_quant_ub.default(q, scale, input, weight, residual, scale_ub, eps)
     return q, scale
+
+
+def hp_rms_norm_fp8_ub(output, scale, input, weight, residual, scale_ub, eps):
+    """``hp_rms_norm_fp8`` with an upper bound on each row's maximum (the
+    activation scale bound of FP8 row-wise checkpoints): ``scale = max(min(
+    amax|y|, scale_ub) / 448, FLT_MIN)``, ``output`` as before with that
+    scale.  ``scale_ub``: one float32 on the device, read by the kernel; a
+    row holding NaN keeps a NaN scale.  No reference counterpart."""
+    torch.ops.hp_rms_norm.rms_norm_fp8_quant_ub.default(output, scale, input, weight, residual, scale_ub, eps)
 
 
 def hp_rms_norm_fp8_static(output, scale, input, weight, residual, eps):

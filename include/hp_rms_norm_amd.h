@@ -121,6 +121,20 @@ int hprms_fused_add_rmsnorm_fp8(void* out, float* scale, const void* input, cons
                                 int dtype, double eps, hipStream_t stream);
 
 /*
+ * hprms_fused_add_rmsnorm_fp8 with an upper bound on each row's maximum
+ * (the activation scale bound of FP8 row-wise checkpoints):
+ *   scale[r] = max(min(max_j |y[r, j]|, *scale_ub) / 448, FLT_MIN)
+ * and out as above with that scale.  `scale_ub` is one float32 in device
+ * memory, read by the kernel (so a captured graph sees later values); a row
+ * containing NaN keeps a NaN scale, and a NaN bound bounds nothing.  No
+ * counterpart in the reference.
+ */
+int hprms_fused_add_rmsnorm_fp8_ub(void* out, float* scale, const float* scale_ub, const void* input,
+                                   const void* weight, void* residual, int64_t rows, int64_t hidden,
+                                   int64_t out_row_stride, int64_t input_row_stride,
+                                   int64_t residual_row_stride, int dtype, double eps, hipStream_t stream);
+
+/*
  * The same with one scale for every row, given by the caller (static
  * per-tensor quantisation, the scale calibrated offline for the FP8 GEMM that
  * follows):

@@ -221,6 +221,34 @@ def fused_add_rmsnorm_fp8(x, w, r, eps, dtype, threads=1):
     return q, sc, ro
 
 
+def fused_add_rmsnorm_fp8_ub(x, w, r, eps, dtype, scale_ub, threads=1, bound_scale=False):
+    """FP8 form with per-row scales whose row maximum is bounded above (the
+    activation scale bound of FP8 row-wise checkpoints): returns (q uint8
+    [rows, hidden] of e4m3fn bits, scale float32 [rows], new residual).  With
+    amax the row's max |y| (NaN if the row holds a NaN), amax' = scale_ub
+    where amax > scale_ub (a NaN bound bounds nothing), scale = max(amax' /
+    448, FLT_MIN) and q = e4m3fn(clamp(y * (1 / scale), -448, 448)): the
+    quantisation step of hprms_oracle_fused_add_rmsnorm_fp8 with the bounded
+    maximum.  `bound_scale` (bounding the scale by scale_ub instead of the
+    maximum) exists for the test that plants that mistake."""
+    y, res = fused_add_rmsnorm(x, w, r, eps, dtype, threads=threads)
+    yf = to_f32(y, dtype)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        amax = np.abs(yf).max(axis=1).astype(np.float32)
+        ub = np.float32(scale_ub)
+        if not bound_scale:
+            amax = np.where(amax > ub, ub, amax).astype(np.float32)
+        sc = (amax / np.float32(448.0)).astype(np.float32)
+        if bound_scale:
+            sc = np.where(sc > ub, ub, sc).astype(np.float32)
+        tiny = np.float32(np.finfo(np.float32).tiny)
+        sc = np.where(sc < tiny, tiny, sc).astype(np.float32)
+        isc = (np.float32(1.0) / sc).astype(np.float32)
+        v = (yf * isc[:, None]).astype(np.float32)
+        v = np.where(v > 448.0, np.float32(448.0), np.where(v < -448.0, np.float32(-448.0), v)).astype(np.float32)
+    return e4m3_from_f32(v), sc, res
+
+
 def fused_add_rmsnorm_fp8_static(x, w, r, eps, dtype, scale, threads=1):
     """FP8 form with one given scale for every row (static per-tensor
     quantisation): returns (q uint8 [rows, hidden] of e4m3fn bits, new

@@ -52,6 +52,11 @@ int main(void) {
                                      1e-6, NULL) == HPRMS_OK);
   EXPECT(hprms_fused_add_rmsnorm_fp8_static(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 4096, 4096,
                                             HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
+  EXPECT(hprms_fused_add_rmsnorm_fp8_ub(NULL, NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 4096, 4096,
+                                        HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
+  EXPECT(hprms_fused_add_rmsnorm_fp8_ub(x, x, NULL, x, w, r, 4, 4096, 4096, 4096, 4096, HPRMS_DTYPE_BF16, 1e-6,
+                                        NULL) == HPRMS_E_INVALID);
+  EXPECT(strstr(hprms_last_error(), "scale_ub") != NULL);
   EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4096, 4096, 32, 1, 4096, 4096,
                                            HPRMS_DTYPE_BF16, 1e-6, NULL) == HPRMS_OK);
   EXPECT(hprms_fused_add_rmsnorm_fp8_group(NULL, NULL, NULL, NULL, NULL, 0, 4000, 4000, 32, 1, 4000, 4000,

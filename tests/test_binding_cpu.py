@@ -182,6 +182,22 @@ def test_fp8_static_op_schema_and_meta_checks():
     assert ops.fused_add_rms_norm_fp8_static(x, r, w, sc, 1e-6).dtype == torch.float8_e4m3fn
 
 
+def test_fp8_ub_op_schema_and_meta_checks():
+    s = str(torch.ops.hp_rms_norm.rms_norm_fp8_quant_ub.default._schema)
+    assert s == ("hp_rms_norm::rms_norm_fp8_quant_ub(Tensor(a!) out, Tensor(b!) scale, Tensor input, "
+                 "Tensor weight, Tensor(c!) residual, Tensor scale_ub, float eps) -> ()")
+    x, w, r = t(4, 512), t(512), t(4, 512)
+    q = t(4, 512, dtype=torch.float8_e4m3fn)
+    sc, ub = torch.empty(4, 1, device=M), torch.empty(1, device=M)
+    assert ops.hp_rms_norm_fp8_ub(q, sc, x, w, r, ub, 1e-6) is None
+    q2, sc2 = ops.fused_add_rms_norm_fp8(t(2, 3, 512), t(2, 3, 512), w, 1e-6, scale_ub=ub)
+    assert q2.shape == (2, 3, 512) and sc2.shape == (2, 3, 1)
+    with pytest.raises(RuntimeError, match="scale_ub must hold one element"):
+        ops.hp_rms_norm_fp8_ub(q, sc, x, w, r, torch.empty(2, device=M), 1e-6)
+    with pytest.raises(RuntimeError, match="scale_ub.dtype"):
+        ops.hp_rms_norm_fp8_ub(q, sc, x, w, r, torch.empty(1, device=M, dtype=torch.float16), 1e-6)
+
+
 def test_fp8_group_op_schema_and_meta_checks():
     s = str(torch.ops.hp_rms_norm.rms_norm_fp8_group_quant.default._schema)
     assert s == ("hp_rms_norm::rms_norm_fp8_group_quant(Tensor(a!) out, Tensor(b!) scales, Tensor input, "

@@ -344,6 +344,71 @@ def test_oracle_fp8_quantisation_stage_matches_torch():
         assert oracle.e4m3_ulp_distance(q, tq).max() == 0
 
 
+def torch_quantise_ub(y, code, scale_ub):
+    """torch's per-row quantisation of 16-bit outputs y with the row maximum
+    bounded above (binary32 on the CPU): amax' = amax where not amax >
+    scale_ub, else scale_ub (torch.where keeps a NaN maximum, and a NaN bound
+    bounds nothing), scale = clamp(amax' / 448, min=FLT_MIN)."""
+    yf = tfrom(y, code).float()
+    amax = yf.abs().amax(-1, keepdim=True)
+    ub = torch.tensor(scale_ub, dtype=torch.float32)
+    amax = torch.where(amax > ub, ub, amax)
+    sc = torch.clamp(amax / 448.0, min=torch.finfo(torch.float32).tiny)
+    q = (yf * (1.0 / sc)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).numpy(), sc.view(-1).numpy()
+
+
+UB_BOUNDS = [0.5, 2.0, 3.5, 1e-30, 1e30, float("inf"), 0.0, float("nan")]
+
+
+def test_oracle_fp8_ub_matches_torch_and_the_unbounded_form():
+    """The bounded form: q and the scales equal torch's bounded quantisation of
+    the oracle's own 16-bit output bit for bit (NaN where torch's is), on
+    ordinary and special rows and bounds that bound most rows, some, none
+    (huge, infinite, NaN) and all down to the FLT_MIN floor (tiny, zero); with
+    a bound no row reaches, they equal the unbounded C oracle's bit for bit;
+    and every bounded row's scale is exactly max(bound / 448, FLT_MIN)."""
+    tiny = np.float32(np.finfo(np.float32).tiny)
+    for code in (BF, HF):
+        for i, (rows, hidden, kind) in enumerate([(64, 4096, "bench"), (16, 1000, "reference_test"),
+                                                  (28, 520, "special")]):
+            if kind == "special":
+                x, r, w = (tbits(t) for t in special_inputs(rows, hidden, TDT[code], 31 + i))
+            else:
+                x, r, w = seeded(rows, hidden, code, 700 + i, kind)
+            y, res = oracle.fused_add_rmsnorm(x, w, r, 1e-6, code)
+            q0, sc0, _ = oracle.fused_add_rmsnorm_fp8(x, w, r, 1e-6, code)
+            amax = np.abs(oracle.to_f32(y, code)).max(axis=1)
+            for ub in UB_BOUNDS:
+                q, sc, res8 = oracle.fused_add_rmsnorm_fp8_ub(x, w, r, 1e-6, code, ub)
+                assert np.array_equal(res8, res), (code, kind, ub)
+                tq, tsc = torch_quantise_ub(y, code, ub)
+                assert np.array_equal(sc.view(np.uint32), tsc.view(np.uint32)) or \
+                    np.array_equal(sc, tsc, equal_nan=True), (code, kind, ub)
+                assert oracle.e4m3_ulp_distance(q, tq).max() == 0, (code, kind, ub)
+                with np.errstate(invalid="ignore"):
+                    bounded = amax > np.float32(ub)
+                    free = ~bounded
+                want = max(np.float32(np.float32(ub) / np.float32(448.0)), tiny)
+                assert (sc[bounded] == want).all(), (code, kind, ub)
+                assert np.array_equal(sc[free], sc0[free], equal_nan=True), (code, kind, ub)
+                if free.any():
+                    assert oracle.e4m3_ulp_distance(q[free], q0[free]).max() == 0, (code, kind, ub)
+                if ub in (1e30, float("inf"), float("nan")):
+                    assert not bounded.any()
+
+
+def test_planted_fp8_ub_mistake_is_rejected():
+    """Bounding the scale by the bound instead of the row maximum (scale =
+    min(amax / 448, bound)), planted in the oracle, fails the torch pin."""
+    x, r, w = seeded(64, 4096, BF, 700, "bench")
+    y, _ = oracle.fused_add_rmsnorm(x, w, r, 1e-6, BF)
+    for ub in (0.5, 2.0, 3.5):
+        q, sc, _ = oracle.fused_add_rmsnorm_fp8_ub(x, w, r, 1e-6, BF, ub, bound_scale=True)
+        tq, tsc = torch_quantise_ub(y, BF, ub)
+        assert not np.array_equal(sc, tsc) or oracle.e4m3_ulp_distance(q, tq).max() > 0, ub
+
+
 STATIC_SCALES = [0.01, 1.0, 3.0, 7e-4, 2.0 ** -140, 1e30, 0.0, float("inf"), float("nan")]
 
 
