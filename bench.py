@@ -1155,9 +1155,15 @@ def run_extra(torch, ops, args):
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / ncalls
+        # the same with each row's maximum bounded above (a bound most rows reach)
+        ub = torch.tensor([2.0], dtype=torch.float32, device="cuda:0")
+
+        def call_ub(i, qs=qs, sets=sets, w=w, sc=sc, ub=ub):
+            ops.hp_rms_norm_fp8_ub(qs[i], sc, sets[i][0], w, sets[i][1], ub, EPS)
+        us_ub = time_rotating(torch, call_ub, n, steps, args.warmup)
         nbytes = 7 * B * h + 2 * h + 4 * B
         fp8.append({"rows": B, "hidden": h, "us_per_call": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                    "bytes_per_call": nbytes})
+                    "bytes_per_call": nbytes, "us_per_call_scale_ub": round(us_ub, 2)})
         del sets, qs
         torch.cuda.empty_cache()
     out["fp8_output_bf16"] = fp8
