@@ -445,6 +445,14 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     __amdgpu_buffer_rsrc_t srs = rrs, ors = xrs, xsrs = xrs;
     uint32_t soff = roff, ooff = xoff, xsoff = 0, esoff = eroff, eooff = exoff;
     uint32_t gs = 4;  // MODE 7: bytes between a row's consecutive scales
+    // MODE 2: the caller's upper bound on the row maximum, loaded while the
+    // row loads are in flight rather than after the row sum (NaN when there
+    // is none: a NaN bound bounds nothing)
+    float ubound = __builtin_nanf("");
+    if constexpr (MODE == 2) {
+      const float* const ub = opaque(a.scale_ub);
+      if (ub != nullptr) ubound = *ub;
+    }
     if constexpr (MODE == 3) {
       uint16_t* const ro = opaque(a.res_out);
       const int64_t rs = opaque(a.res_out_stride);
@@ -841,10 +849,7 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
           buf ^= 1;
         }
         float amax = F::one((uint16_t)mx);
-        // an upper bound on the row maximum, given by the caller (a NaN
-        // maximum stays NaN; a NaN bound bounds nothing)
-        const float* const ub = opaque(a.scale_ub);
-        if (ub != nullptr && amax > *ub) amax = *ub;
+        if (amax > ubound) amax = ubound;  // the caller's bound (a NaN maximum stays NaN)
         float sc = amax / 448.0f;
         if (sc < 1.17549435e-38f) sc = 1.17549435e-38f;  // FLT_MIN; NaN stays NaN
         isc = 1.0f / sc;
