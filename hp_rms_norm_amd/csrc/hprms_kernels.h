@@ -445,13 +445,18 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
     __amdgpu_buffer_rsrc_t srs = rrs, ors = xrs, xsrs = xrs;
     uint32_t soff = roff, ooff = xoff, xsoff = 0, esoff = eroff, eooff = exoff;
     uint32_t gs = 4;  // MODE 7: bytes between a row's consecutive scales
-    // MODE 2: the caller's upper bound on the row maximum, loaded while the
-    // row loads are in flight rather than after the row sum (NaN when there
-    // is none: a NaN bound bounds nothing)
+    // MODE 2: the caller's upper bound on the row maximum, or the one given
+    // scale, loaded while the row loads are in flight rather than when the
+    // output phase needs it (no bound: NaN, which bounds nothing)
     float ubound = __builtin_nanf("");
+    float given_scale = 0.0f;
+    bool has_given = false;
     if constexpr (MODE == 2) {
       const float* const ub = opaque(a.scale_ub);
       if (ub != nullptr) ubound = *ub;
+      const float* const given = opaque(a.static_scale);
+      has_given = given != nullptr;
+      if (has_given) given_scale = *given;
     }
     if constexpr (MODE == 3) {
       uint16_t* const ro = opaque(a.res_out);
@@ -831,12 +836,11 @@ void fused_vec_kernel(const uint16_t* x_rows,  // input rows (MODE 0: also the o
         }
       }
       float isc;
-      const float* const given = opaque(a.static_scale);
-      if (given != nullptr) {
+      if (has_given) {
         // one scale for every row, given by the caller: no row maximum (the
         // branch is uniform over the workgroup, so no barrier is skipped by
         // part of it)
-        isc = 1.0f / *given;
+        isc = 1.0f / given_scale;
       } else {
         uint32_t mx = group_max_u32<GW>(m2);
         if constexpr (WPR > 1) {
