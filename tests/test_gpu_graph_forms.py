@@ -1,9 +1,10 @@
 """Every form captured in one HIP graph: the plain RMSNorm, the out-of-place
 and partial-sum forms, and the quantised outputs (FP8 with a scale per row,
-one given scale, scales per 128 elements in the column-major layout, MXFP8,
-MXFP4).  None allocates or issues a memset, so each replay, with fresh inputs
-copied into the captured buffers and eager work and synchronisations between
-replays, must give the eager call's bytes exactly.
+one given scale, per-row scales under a bound that changes between replays,
+scales per 128 elements in the column-major layout, MXFP8, MXFP4).  None
+allocates or issues a memset, so each replay, with fresh inputs copied into
+the captured buffers and eager work and synchronisations between replays,
+must give the eager call's bytes exactly.
 """
 import pytest
 import torch
@@ -32,6 +33,7 @@ def buffers(ops):
         "reduce": [e(n, h)],
         "fp8": [e(n, h, dt=torch.float8_e4m3fn), e(n, dt=torch.float32)],
         "fp8_static": [e(n, h, dt=torch.float8_e4m3fn)],
+        "fp8_ub": [e(n, h, dt=torch.float8_e4m3fn), e(n, dt=torch.float32)],
         # column-major scales with 4 padding columns, which no call writes
         "fp8_group": [e(n, h, dt=torch.float8_e4m3fn), e(h // 128, n + 4, dt=torch.float32).fill_(-1.0)],
         "mxfp8": [e(n, h, dt=torch.uint8), e(n, h // 32, dt=torch.uint8)],
@@ -39,11 +41,12 @@ def buffers(ops):
     }
 
 
-FORMS = ("plain", "out", "reduce", "fp8", "fp8_static", "fp8_group", "mxfp8", "mxfp4")
+FORMS = ("plain", "out", "reduce", "fp8", "fp8_static", "fp8_ub", "fp8_group", "mxfp8", "mxfp4")
 
 
-def run_form(ops, form, x, r, p1, w, sc, bufs):
-    """One call of `form` on inputs x, r (p1: the second partial sum)."""
+def run_form(ops, form, x, r, p1, w, sc, bufs, ub=None):
+    """One call of `form` on inputs x, r (p1: the second partial sum; ub: the
+    bounded FP8 form's bound, a one-element device tensor)."""
     b = bufs[form]
     if form == "plain":
         ops.rms_norm(b[0], x, w, EPS)
@@ -55,6 +58,8 @@ def run_form(ops, form, x, r, p1, w, sc, bufs):
         ops.hp_rms_norm_fp8(b[0], b[1], x, w, r, EPS)
     elif form == "fp8_static":
         ops.hp_rms_norm_fp8_static(b[0], sc, x, w, r, EPS)
+    elif form == "fp8_ub":
+        ops.hp_rms_norm_fp8_ub(b[0], b[1], x, w, r, ub, EPS)
     elif form == "fp8_group":
         ops.hp_rms_norm_fp8_group(b[0], b[1][:, :ROWS].t(), x, w, r, EPS)
     elif form == "mxfp8":
@@ -79,6 +84,7 @@ def test_every_form_in_one_hip_graph(ops):
     _, _, _, w = fresh(0)
     wd = w.to(DEV)
     sc = torch.tensor([0.02], dtype=torch.float32, device=DEV)
+    ub = torch.tensor([2.0], dtype=torch.float32, device=DEV)   # read by the kernel at each replay
     bufs = buffers(ops)
     # captured inputs: one (x, r, second part) per form
     ins = {f: [torch.empty(ROWS, HIDDEN, dtype=torch.bfloat16, device=DEV) for _ in range(3)] for f in FORMS}
@@ -89,16 +95,17 @@ def test_every_form_in_one_hip_graph(ops):
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for f in FORMS:  # warm-up outside the graph
-            run_form(ops, f, *ins[f], wd, sc, bufs)
+            run_form(ops, f, *ins[f], wd, sc, bufs, ub)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for f in FORMS:
-            run_form(ops, f, *ins[f], wd, sc, bufs)
+            run_form(ops, f, *ins[f], wd, sc, bufs, ub)
     eager_bufs = buffers(ops)
     for rep in range(3):
         print("graph replay", rep, flush=True)
+        ub.fill_((2.0, 3.0, 1.5)[rep])   # a new bound: the replay reads it from device memory
         data = {}
         for k, f in enumerate(FORMS):
             x, r, p1, _ = fresh(1000 * rep + 10 * k + 1)
@@ -110,7 +117,7 @@ def test_every_form_in_one_hip_graph(ops):
         got = {f: snapshot(f, ins[f][0], ins[f][1], bufs) for f in FORMS}
         for f in FORMS:
             x, r, p1 = (v.to(DEV) for v in data[f])
-            run_form(ops, f, x, r, p1, wd, sc, eager_bufs)
+            run_form(ops, f, x, r, p1, wd, sc, eager_bufs, ub)
             torch.cuda.synchronize()
             want = snapshot(f, x, r, eager_bufs)
             assert len(got[f]) == len(want)
